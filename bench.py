@@ -1,0 +1,169 @@
+"""Benchmark of the split-manifold LUT path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--instances N]
+
+Workload: LUT-GEMV 2560 -> 6912 (MLP gate/up),
+batch 1, fp32 activations, d = 16 / 256 centroids, 0.38 % CSR outliers.  A
+step is one call of the fused LUT-GEMV kernel on one of N distinct weight
+instances (round robin), all resident in HBM; N is sized so the working set
+exceeds the 256 MB Infinity Cache and the codes really stream from HBM.
+
+Printed: one JSON line.  ``value`` is microseconds per call (lower is
+better), measured with HIP events on the launch stream over the K timed
+steps.  ``roofline`` relates the algorithmic code bytes of one call to that
+per-call time; ``cpu_baseline`` times the reference's own C++ engine
+(compiled from its sources into oracle/_ref when present, else the repo's C
+restatement) on the host, one thread, on the same inputs.  Extra fields give
+the MoE and KV-decode figures of the same run.
+"""
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+import numpy as np  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0
+M_GU, K_GU = 6912, 2560
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=2000)
+    ap.add_argument("--warmup", type=int, default=200)
+    ap.add_argument("--instances", type=int, default=160)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    return ap.parse_args()
+
+
+def time_cpu_linear(d, seconds):
+    """Reference C++ engine (or the C restatement) on the host, 1 thread,
+    ojasx_run.cpp's method: 50 warm-up calls, then timed calls."""
+    from oracle import ref, cpu
+    x = d["x"]
+    if ref.available():
+        R = ref.RefLinear(d["codebook"], d["codes"], d["scales"], None, d["csr"])
+        call = lambda: R.forward(x, 1)
+        kind = "reference"
+    else:
+        call = lambda: cpu.linear_forward(x, d["codebook"], d["codes"], d["scales"], None, *d["csr"])
+        kind = "port"
+    for _ in range(50):
+        call()
+    n, t0 = 0, time.perf_counter()
+    while True:
+        call()
+        n += 1
+        el = time.perf_counter() - t0
+        if el > seconds or n >= 1000:
+            break
+    return dict(value=el / n * 1e6, unit="us/call", cores=1, kind=kind,
+                sample=f"{n} calls of LUT-GEMV 2560->6912 B=1 fp32 with CSR, 1 thread, "
+                       f"after 50 warm-up calls")
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported "
+              "(the path would shard by output rows / experts / kv heads, see DESIGN.md)",
+              file=sys.stderr)
+        sys.exit(2)
+    import torch
+    import __graft_entry__
+    from oracle import gen, cpu
+
+    pkg = __graft_entry__.load_package()
+    L = pkg.lib()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+
+    # --- weights: N distinct instances, shared x --------------------------------
+    base = gen.linear(M_GU, K_GU, B=1, seed=2026)
+    r = np.random.default_rng(7)
+    handles, wbytes = [], 0
+    p = lambda a: a.ctypes.data_as(ctypes.c_void_p)
+    for i in range(args.instances):
+        codes = base["codes"] if i == 0 else r.integers(0, 256, size=base["codes"].shape,
+                                                        dtype=np.uint8)
+        h = L.ojasx_create_linear(K_GU, M_GU, 16, 256, p(base["codebook"]), p(codes),
+                                  p(base["scales"]), None)
+        assert h, L.ojasx_get_last_error()
+        rp, cl, vl = base["csr"]
+        assert L.ojasx_set_linear_outliers(h, vl.size, p(rp), p(cl), p(vl)) == 0
+        handles.append(h)
+        wbytes = L.ojasx_linear_device_weight_bytes(h)
+    x = torch.from_numpy(base["x"]).to(dev)
+    y = torch.empty(1, M_GU, device=dev)
+    stream = torch.cuda.current_stream()
+    sp = ctypes.c_void_p(stream.cuda_stream)
+    xp, yp = ctypes.c_void_p(x.data_ptr()), ctypes.c_void_p(y.data_ptr())
+    fwd = L.ojasx_linear_forward_device
+
+    # parity of the benchmarked configuration (instance 0) against the oracle
+    assert fwd(handles[0], xp, yp, 1, 0, sp) == 0
+    torch.cuda.synchronize()
+    y_ref = cpu.linear_forward(base["x"], base["codebook"], base["codes"], base["scales"], None,
+                               *base["csr"])
+    rel = float(np.abs(y.cpu().numpy() - y_ref).max() / np.abs(y_ref).max())
+
+    n = len(handles)
+    for i in range(args.warmup):
+        fwd(handles[i % n], xp, yp, 1, 0, sp)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t_wall = time.perf_counter()
+    e0.record(stream)
+    for i in range(args.steps):
+        fwd(handles[i % n], xp, yp, 1, 0, sp)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    t_wall = time.perf_counter() - t_wall
+    ms = e0.elapsed_time(e1)
+    us_call = ms * 1e3 / args.steps
+
+    code_bytes = M_GU * (K_GU // 16)
+    achieved = code_bytes / (us_call * 1e-6) / 1e9
+    all_bytes = wbytes + K_GU * 4 + M_GU * 4
+
+    out = {
+        "metric": "LUT-GEMV 2560->6912 us/call (HBM GB/s on code bytes alongside)",
+        "value": round(us_call, 4),
+        "unit": "us/call",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms / args.steps, 6),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded N(0,1) x, N(0,0.02) codebook, uniform codes, 0.38% CSR)",
+        "config": {"workload": "LUT-GEMV 2560->6912 gate/up, B=1, fp32, d=16/256 centroids, "
+                               "0.38% CSR outliers", "batch": 1, "in_features": K_GU,
+                   "out_features": M_GU, "weight_instances": n,
+                   "working_set_MB": round(n * wbytes / 2**20, 1)},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 5), "traffic": None,
+                     "algorithmic_bytes_per_call": code_bytes,
+                     "all_compulsory_bytes_per_call": all_bytes,
+                     "achieved_all_bytes_GBs": round(all_bytes / (us_call * 1e-6) / 1e9, 2)},
+        "parity_rel_err": rel,
+        "wall_s_timed": round(t_wall, 3),
+    }
+    if not args.no_cpu:
+        out["cpu_baseline"] = time_cpu_linear(base, args.cpu_seconds)
+    for h in handles:
+        L.ojasx_destroy_linear(h)
+    print(json.dumps(out))
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,174 @@
+/*
+ * ojasx_lut_c_api.h -- C-ABI of the MI355X (gfx950) split-manifold LUT engine.
+ *
+ * Drop-in for the reference C-ABI (split_manifold_lut_experiment/native/
+ * include/ojasx_lut_c_api.h, cited below as "ref.h:<line>"), implemented with
+ * hand-written HIP kernels in libojasx_lut_hip.so.
+ *
+ * Two faces:
+ *  1. The reference's 21 symbols, same names and signatures, same semantics:
+ *     host pointers, synchronous, create_* deep-copies every array (here: into
+ *     device memory, repacked into the kernels' tiled layout), NULL data means
+ *     zeros (scales default to 1), int status 0 = OK, -1 = null handle or
+ *     pointer, -2 = head index out of range, create_* returns NULL on failure.
+ *  2. Device variants (no counterpart in the reference, whose GPU code is
+ *     never built): device pointers, an activation dtype tag and a hipStream_t
+ *     passed as void*.  They enqueue work and return without synchronising.
+ *
+ * Extra status codes: -3 invalid argument (shape, dtype, CSR structure, an
+ * expert id is validated by the skip rule instead), -4 HIP runtime error,
+ * -5 device out of memory.  ojasx_get_last_error() returns a message for the
+ * last failing call on the calling thread.
+ *
+ * Concurrency: calls on one handle must be serialised by the caller (the
+ * reference's mutators are unlocked too); forward calls on one handle share
+ * that handle's workspace.
+ */
+#ifndef OJASX_LUT_C_API_H
+#define OJASX_LUT_C_API_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define OJASX_API __attribute__((visibility("default")))
+
+typedef void *OjasxLinearHandle; /* ref.h:35 */
+typedef void *OjasxKVHandle;     /* ref.h:36 */
+typedef void *OjasxMoEHandle;    /* ref.h:37 */
+
+enum {
+    OJASX_OK = 0,
+    OJASX_ERR_NULL = -1,
+    OJASX_ERR_HEAD = -2,
+    OJASX_ERR_INVALID = -3,
+    OJASX_ERR_HIP = -4,
+    OJASX_ERR_OOM = -5
+};
+
+/* Activation / output element types of the device entry points. */
+enum { OJASX_DTYPE_F32 = 0, OJASX_DTYPE_BF16 = 1 };
+
+/* ---- metadata (ref.h:40-41) ------------------------------------------- */
+OJASX_API const char *ojasx_get_version(void);
+OJASX_API const char *ojasx_get_backend_name(void);
+/* No reference counterpart: message of the last failing call (thread-local). */
+OJASX_API const char *ojasx_get_last_error(void);
+
+/* ---- linear (ref.h:46-91) --------------------------------------------- */
+/* ref.h:46-55.  codes_data is [out_features][in_features/block_dim] uint8,
+ * codebook_data [codebook_size][block_dim] fp32.  block_dim <= 32,
+ * codebook_size <= 256, in_features % block_dim == 0. */
+OJASX_API OjasxLinearHandle ojasx_create_linear(int in_features, int out_features,
+                                                int block_dim, int codebook_size,
+                                                const float *codebook_data,
+                                                const uint8_t *codes_data,
+                                                const float *scales_data,
+                                                const float *bias_data);
+/* ref.h:60-66.  CSR over [out_features][in_features]; replaces any previous
+ * outliers; nnz == 0 clears them.  Validated: row_ptrs monotone from 0 to
+ * nnz, columns in range (-3 otherwise). */
+OJASX_API int ojasx_set_linear_outliers(OjasxLinearHandle handle, int nnz,
+                                        const int *row_ptrs, const int *col_indices,
+                                        const float *values);
+/* ref.h:72-78.  Host x [batch][in], y [batch][out], fp32; synchronous.
+ * num_threads is accepted for compatibility and ignored (the GPU runs it). */
+OJASX_API int ojasx_linear_forward(OjasxLinearHandle handle, const float *x, float *y,
+                                   int batch_size, int num_threads);
+/* ref.h:83-86: sizes of the reference's own representation (codes + codebook
+ * + scales + bias + int32/int32/fp32 CSR) so callers' accounting is unchanged. */
+OJASX_API size_t ojasx_get_compressed_size(OjasxLinearHandle handle);
+OJASX_API size_t ojasx_get_dense_size(OjasxLinearHandle handle);
+OJASX_API size_t ojasx_get_lut_sram_size(OjasxLinearHandle handle);
+OJASX_API float ojasx_get_compression_ratio(OjasxLinearHandle handle);
+/* ref.h:91 */
+OJASX_API void ojasx_destroy_linear(OjasxLinearHandle handle);
+
+/* Device variant of ref.h:72-78 (no reference counterpart): x [batch][in],
+ * y [batch][out] in HBM, dtype OJASX_DTYPE_F32 or _BF16 for both, enqueued on
+ * stream (a hipStream_t; NULL = default stream). */
+OJASX_API int ojasx_linear_forward_device(OjasxLinearHandle handle, const void *x, void *y,
+                                          int batch_size, int dtype, void *stream);
+/* LUT[b][g][k] = <x_b[g*D:(g+1)*D], C[k]> for k < codebook_size (fp32 out,
+ * [batch][groups][codebook_size]); the standalone LUT build of
+ * split_manifold_engine.py:185-200 / ojasx_lut_cpu.cpp:18-102 (no reference
+ * C-ABI counterpart).  x [batch][groups*block_dim] in dtype, codebook fp32. */
+OJASX_API int ojasx_build_lut_device(const void *x, const float *codebook, int batch_size,
+                                     int groups, int block_dim, int codebook_size, float *lut,
+                                     int dtype, void *stream);
+/* Bytes the forward reads per call that are weights: packed codes, outlier
+ * stream, codebook, scales, bias (no reference counterpart; for roofline
+ * accounting). */
+OJASX_API size_t ojasx_linear_device_weight_bytes(OjasxLinearHandle handle);
+
+/* ---- KV cache (ref.h:96-120) ------------------------------------------ */
+OJASX_API OjasxKVHandle ojasx_create_kv_cache(int num_heads, int head_dim, int max_seq_len,
+                                              int block_dim);
+/* ref.h:103-108: quantise and append one token of one head (host k, v). */
+OJASX_API int ojasx_kv_cache_append(OjasxKVHandle handle, int head_idx, const float *k,
+                                    const float *v);
+/* ref.h:110-116: softmax(q.K^T * sf) . V for one head; sf <= 0 means
+ * 1/sqrt(head_dim); an empty head returns 0 and leaves out_context untouched. */
+OJASX_API int ojasx_kv_cache_attention(OjasxKVHandle handle, int head_idx, const float *q,
+                                       float *out_context, float scale_factor);
+OJASX_API size_t ojasx_kv_cache_get_memory_size(OjasxKVHandle handle);
+OJASX_API float ojasx_kv_cache_get_compression_ratio(OjasxKVHandle handle);
+OJASX_API void ojasx_destroy_kv_cache(OjasxKVHandle handle);
+
+/* Paged code-domain decode attention over device memory (no reference
+ * counterpart; generalises ref.h:110-116 to a per-kv-head 256 x block_dim
+ * codebook, GQA and a block table).
+ *   q        [num_q_heads][head_dim] fp32
+ *   k_codes  [num_pages][num_kv_heads][page_size][head_dim/block_dim] uint8
+ *   k_scales [num_pages][num_kv_heads][page_size] fp32 (same for v_*)
+ *   k_cb     [num_kv_heads][256][block_dim] fp32 (same for v_cb)
+ *   block_table [ceil(seq_len/page_size)] int32 physical page of each logical page
+ *   out      [num_q_heads][head_dim] fp32
+ * q head j attends with kv head j / (num_q_heads / num_kv_heads);
+ * head_dim / block_dim <= 32, block_dim <= 32; sf <= 0 means 1/sqrt(head_dim);
+ * seq_len == 0 leaves out untouched.  Calls from one host thread share a
+ * workspace and must be ordered on one stream. */
+OJASX_API int ojasx_kv_decode_paged_device(const float *q, const uint8_t *k_codes,
+                                           const float *k_scales, const uint8_t *v_codes,
+                                           const float *v_scales, const float *k_cb,
+                                           const float *v_cb, const int *block_table,
+                                           int seq_len, int page_size, int num_q_heads,
+                                           int num_kv_heads, int head_dim, int block_dim,
+                                           float scale_factor, float *out, void *stream);
+
+/* ---- MoE (ref.h:125-150) ---------------------------------------------- */
+OJASX_API OjasxMoEHandle ojasx_create_moe(int num_experts, int hidden_dim,
+                                          int intermediate_dim, int top_k, int block_dim,
+                                          const float *codebook_in, const float *codebook_down,
+                                          const uint8_t *gate_up_codes,
+                                          const float *gate_up_scales,
+                                          const uint8_t *down_codes, const float *down_scales);
+/* ref.h:139-146: one token; k_active <= 0 leaves y_out untouched. */
+OJASX_API int ojasx_moe_forward(OjasxMoEHandle handle, const float *x, const int *top_k_indices,
+                                const float *top_k_weights, float *y_out, int k_active);
+OJASX_API size_t ojasx_moe_get_compressed_size(OjasxMoEHandle handle);
+OJASX_API float ojasx_moe_get_compression_ratio(OjasxMoEHandle handle);
+OJASX_API void ojasx_destroy_moe(OjasxMoEHandle handle);
+
+/* Device variant of ref.h:139-146 for a batch of tokens (no reference
+ * counterpart): x [num_tokens][hidden], idx/w [num_tokens][k_active],
+ * y [num_tokens][hidden] fully overwritten (k_active <= 0: untouched). */
+OJASX_API int ojasx_moe_forward_device(OjasxMoEHandle handle, const void *x, const int *idx,
+                                       const float *w, void *y, int num_tokens, int k_active,
+                                       int dtype, void *stream);
+/* Router (absent from the reference; its callers pass indices and weights):
+ * logits [num_tokens][num_experts] fp32 -> idx [num_tokens][k] int32 (the k
+ * largest logits, descending, ties to the lower index) and w [num_tokens][k]
+ * = softmax over all experts at those indices, divided by their sum when
+ * renormalize != 0.  num_experts <= 1024, k <= 32. */
+OJASX_API int ojasx_moe_route_device(const float *logits, int num_tokens, int num_experts, int k,
+                                     int renormalize, int *idx, float *w, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* OJASX_LUT_C_API_H */

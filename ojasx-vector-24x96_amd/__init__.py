@@ -1,0 +1,25 @@
+"""MI355X-native split-manifold LUT execution path (OjasX drop-in).
+
+Loaded under the module name ``ojasx_vector_24x96_amd`` (the directory name
+is not an identifier; ``__graft_entry__.load_package()`` registers it).
+
+Faces, each mirroring a reference interface:
+
+* C-ABI ``libojasx_lut_hip.so`` (``include/ojasx_lut_c_api.h``): the reference
+  C-ABI's 21 symbols plus device-pointer / stream variants
+* ``native``: ``NativeSplitManifoldLinear``, ``NativeKVCache``,
+  ``NativeSplitManifoldMoE``, ``get_engine_info`` (reference ctypes binding)
+* ``engine``: ``SplitManifoldLUTLinear`` (reference PyTorch module)
+"""
+from . import _lib
+from ._lib import OjasxError, lib
+
+__all__ = ["OjasxError", "lib", "native", "engine"]
+
+
+def __getattr__(name):
+    # Lazy submodules: ``engine`` imports torch, ``native`` only numpy.
+    import importlib
+    if name in ("native", "engine", "moe", "kv", "math_engine"):
+        return importlib.import_module(f"{__name__}.{name}")
+    raise AttributeError(name)

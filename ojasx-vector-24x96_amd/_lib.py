@@ -1,0 +1,80 @@
+"""ctypes loader of the HIP C-ABI library ``libojasx_lut_hip.so``.
+
+Mirrors the reference binding's loader
+(split_manifold_lut_experiment/native/bindings/ojasx_lut_ctypes.py:16-88): the
+library is located next to this package and a missing library raises
+``FileNotFoundError`` at first use.  There is no CPU fallback: every entry
+point runs on the GPU.
+"""
+import ctypes
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libojasx_lut_hip.so")
+
+_lib = None
+
+vp, ci, cf, cz = ctypes.c_void_p, ctypes.c_int, ctypes.c_float, ctypes.c_size_t
+
+# name -> (restype, argtypes); the set of symbols declared in include/ojasx_lut_c_api.h
+SIGNATURES = {
+    "ojasx_get_version": (ctypes.c_char_p, []),
+    "ojasx_get_backend_name": (ctypes.c_char_p, []),
+    "ojasx_get_last_error": (ctypes.c_char_p, []),
+    "ojasx_create_linear": (vp, [ci, ci, ci, ci, vp, vp, vp, vp]),
+    "ojasx_set_linear_outliers": (ci, [vp, ci, vp, vp, vp]),
+    "ojasx_linear_forward": (ci, [vp, vp, vp, ci, ci]),
+    "ojasx_get_compressed_size": (cz, [vp]),
+    "ojasx_get_dense_size": (cz, [vp]),
+    "ojasx_get_lut_sram_size": (cz, [vp]),
+    "ojasx_get_compression_ratio": (cf, [vp]),
+    "ojasx_destroy_linear": (None, [vp]),
+    "ojasx_linear_forward_device": (ci, [vp, vp, vp, ci, ci, vp]),
+    "ojasx_linear_device_weight_bytes": (cz, [vp]),
+    "ojasx_build_lut_device": (ci, [vp, vp, ci, ci, ci, ci, vp, ci, vp]),
+    "ojasx_create_kv_cache": (vp, [ci, ci, ci, ci]),
+    "ojasx_kv_cache_append": (ci, [vp, ci, vp, vp]),
+    "ojasx_kv_cache_attention": (ci, [vp, ci, vp, vp, cf]),
+    "ojasx_kv_cache_get_memory_size": (cz, [vp]),
+    "ojasx_kv_cache_get_compression_ratio": (cf, [vp]),
+    "ojasx_destroy_kv_cache": (None, [vp]),
+    "ojasx_kv_decode_paged_device": (ci, [vp, vp, vp, vp, vp, vp, vp, vp, ci, ci, ci, ci, ci,
+                                          ci, cf, vp, vp]),
+    "ojasx_create_moe": (vp, [ci, ci, ci, ci, ci, vp, vp, vp, vp, vp, vp]),
+    "ojasx_moe_forward": (ci, [vp, vp, vp, vp, vp, ci]),
+    "ojasx_moe_get_compressed_size": (cz, [vp]),
+    "ojasx_moe_get_compression_ratio": (cf, [vp]),
+    "ojasx_destroy_moe": (None, [vp]),
+    "ojasx_moe_forward_device": (ci, [vp, vp, vp, vp, vp, ci, ci, ci, vp]),
+    "ojasx_moe_route_device": (ci, [vp, ci, ci, ci, ci, vp, vp, vp]),
+}
+
+DTYPE_F32 = 0
+DTYPE_BF16 = 1
+
+
+class OjasxError(RuntimeError):
+    """A C-ABI call returned a non-zero status."""
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise FileNotFoundError(
+                f"Native library not found at: {LIB_PATH} (build it with "
+                "`python -c 'import __graft_entry__ as g; g.build()'`)")
+        L = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def check(rc, what):
+    if rc != 0:
+        msg = lib().ojasx_get_last_error().decode(errors="replace")
+        raise OjasxError(f"{what} failed with code {rc}: {msg}")
+    return rc

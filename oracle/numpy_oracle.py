@@ -1,0 +1,235 @@
+"""NumPy restatements of the Python side of the reference LUT path.
+
+TEST INFRASTRUCTURE ONLY (tests, smoke() checker, bench.py cpu_baseline).
+
+Each function cites the reference routine it restates (paths relative to the
+reference tree).  All of them accept a ``dtype`` so they can be evaluated in
+float64 as a brute-force reference.
+"""
+import math
+
+import numpy as np
+
+
+# --- split_manifold_lut_experiment/engine/split_manifold_engine.py ---------------
+
+def engine_build_lut(x, codebook, dtype=np.float64):
+    """LUT[..., g, k] = <x_g, C[k]>.  split_manifold_engine.py:185-200."""
+    x = np.asarray(x, dtype)
+    cb = np.asarray(codebook, dtype)
+    d = cb.shape[1]
+    xb = x.reshape(*x.shape[:-1], x.shape[-1] // d, d)
+    return xb @ cb.T
+
+
+def engine_forward(x, codebook, codes, scales, outlier_indices=None, outlier_values=None,
+                   bias=None, dtype=np.float64):
+    """SplitManifoldLUTLinear.forward: gather-sum, * scales, + COO outliers
+    (index_add over rows), + bias.  split_manifold_engine.py:202-250."""
+    x = np.asarray(x, dtype)
+    shp = x.shape
+    xf = x.reshape(-1, shp[-1])
+    lut = engine_build_lut(xf, codebook, dtype)            # [B, G, K]
+    codes = np.asarray(codes).astype(np.int64)              # [M, G]
+    g = np.arange(codes.shape[1])[None, :]
+    gathered = lut[:, g, codes]                             # [B, M, G]
+    y = gathered.sum(axis=2) * np.asarray(scales, dtype)[None, :]
+    if outlier_values is not None and np.asarray(outlier_values).size:
+        m_idx = np.asarray(outlier_indices[0], np.int64)
+        k_idx = np.asarray(outlier_indices[1], np.int64)
+        prod = xf[:, k_idx] * np.asarray(outlier_values, dtype)[None, :]
+        yo = np.zeros_like(y)
+        for b in range(y.shape[0]):
+            np.add.at(yo[b], m_idx, prod[b])
+        y = y + yo
+    if bias is not None:
+        y = y + np.asarray(bias, dtype)[None, :]
+    return y.reshape(*shp[:-1], codes.shape[0])
+
+
+def dequantize(codebook, codes, scales, csr=None, dtype=np.float64):
+    """Dense W = s_m * C[codes] (+ outliers).  split_manifold_engine.py:252-267."""
+    cb = np.asarray(codebook, dtype)
+    codes = np.asarray(codes).astype(np.int64)
+    M, G = codes.shape
+    W = (cb[codes] * np.asarray(scales, dtype)[:, None, None]).reshape(M, G * cb.shape[1])
+    if csr is not None:
+        rp, cl, vl = csr
+        rows = np.repeat(np.arange(M), np.diff(np.asarray(rp)))
+        W[rows, np.asarray(cl)] += np.asarray(vl, dtype)
+    return W
+
+
+def csr_to_coo(csr):
+    rp, cl, vl = csr
+    rows = np.repeat(np.arange(len(rp) - 1), np.diff(np.asarray(rp)))
+    return np.stack([rows, np.asarray(cl, np.int64)]), np.asarray(vl)
+
+
+def linear_fp64(x, codebook, codes, scales, bias=None, csr=None):
+    """Brute force y = x W^T + bias in float64 (the identity LUT-gather = x.W^T)."""
+    W = dequantize(codebook, codes, scales, csr, np.float64)
+    y = np.asarray(x, np.float64).reshape(-1, W.shape[1]) @ W.T
+    if bias is not None:
+        y = y + np.asarray(bias, np.float64)
+    return y
+
+
+# --- MoE brute force ------------------------------------------------------------
+
+def silu(v):
+    return v / (1.0 + np.exp(-v))
+
+
+def moe_fp64(x, cb_in, cb_down, gu_codes, gu_scales, dn_codes, dn_scales, idx, w, E=None):
+    """Top-k SwiGLU FFN in float64 from dequantised experts, with the skip rule
+    of NAT/src/ojasx_lut_cpu.cpp:284-286."""
+    x = np.asarray(x, np.float64).reshape(-1)
+    E = gu_codes.shape[0] if E is None else E
+    I = gu_codes.shape[1] // 2
+    y = np.zeros(dn_codes.shape[1], np.float64)
+    for e, we in zip(np.asarray(idx).reshape(-1), np.asarray(w, np.float32).reshape(-1)):
+        if e < 0 or e >= E or abs(float(we)) < 1e-8:
+            continue
+        Wgu = dequantize(cb_in, gu_codes[e], gu_scales[e])
+        gu = Wgu @ x
+        inter = silu(gu[:I]) * gu[I:]
+        Wd = dequantize(cb_down, dn_codes[e], dn_scales[e])
+        y += float(we) * (Wd @ inter)
+    return y
+
+
+# --- router ---------------------------------------------------------------------
+
+def router_topk(logits, k, renorm=False):
+    """Stable descending top-k (ties -> lower index), softmax weights in fp64."""
+    lg = np.asarray(logits, np.float32)
+    if lg.ndim == 1:
+        lg = lg[None]
+    idx = np.argsort(-lg, axis=1, kind="stable")[:, :k].astype(np.int32)
+    l64 = lg.astype(np.float64)
+    p = np.exp(l64 - l64.max(axis=1, keepdims=True))
+    p /= p.sum(axis=1, keepdims=True)
+    w = np.take_along_axis(p, idx.astype(np.int64), axis=1)
+    if renorm:
+        w = w / w.sum(axis=1, keepdims=True)
+    return idx, w
+
+
+# --- ojasx_24x96/long_context.py --------------------------------------------------
+
+def online_softmax_attention(q, k_tiles, v_tiles, scale=None):
+    """fp64 online-softmax attention of one query row over streamed (K, V)
+    tiles, non-causal (decode).  Restates OnlineSoftmaxBlockAttention.
+    forward_stream (long_context.py:92-176): running (m, l, acc), alpha =
+    exp(m_old - m_new) with the -inf guard, final acc / l."""
+    q = np.asarray(q, np.float64).reshape(-1)
+    D = q.size
+    scale = 1.0 / math.sqrt(D) if scale is None else scale
+    m, l, acc = -math.inf, 0.0, np.zeros(D)
+    for kt, vt in zip(k_tiles, v_tiles):
+        kt = np.asarray(kt, np.float64)
+        vt = np.asarray(vt, np.float64)
+        if kt.shape[0] == 0:
+            continue
+        s = (kt @ q) * scale
+        m_new = max(m, float(s.max()))
+        safe = 0.0 if math.isinf(m_new) else m_new
+        alpha = 0.0 if math.isinf(m) else math.exp(m - safe)
+        p = np.where(np.isinf(s), 0.0, np.exp(s - safe))
+        l = alpha * l + p.sum()
+        acc = alpha * acc + p @ vt
+        m = m_new
+    return acc / (l if l > 0 else 1.0)
+
+
+def full_softmax_attention(q, K, V, scale=None):
+    """fp64 full-softmax reference (tests/test_m13_ultra_long_context_10m.py:49-103)."""
+    q = np.asarray(q, np.float64).reshape(-1)
+    scale = 1.0 / math.sqrt(q.size) if scale is None else scale
+    s = (np.asarray(K, np.float64) @ q) * scale
+    p = np.exp(s - s.max())
+    p /= p.sum()
+    return p @ np.asarray(V, np.float64)
+
+
+def paged_quantize_int8(t):
+    """PagedCompressedKVCache._quantize_int8 (long_context.py:234-240):
+    s = max(|t|_D, 1e-8) / 127 stored as float16; q = clamp(round_half_even(t / s),
+    -127, 127) int8 (division by the fp32 scale before the fp16 cast)."""
+    t = np.asarray(t, np.float32)
+    amax = np.maximum(np.abs(t).max(axis=-1, keepdims=True), np.float32(1e-8))
+    s = (amax / np.float32(127.0)).astype(np.float32)
+    q = np.clip(np.rint(t / s), -127, 127).astype(np.int8)
+    return q, s.astype(np.float16)
+
+
+def code_domain_kv_decode(q_heads, kv_group, k_cb, v_cb, k_codes, k_scales, v_codes, v_scales,
+                          scale=None, tile=256):
+    """fp64 general-codebook decode for the query heads of one kv head, as an
+    online softmax over tiles of the dequantised stream: K_t = s_t * Ck[code],
+    V_t = vs_t * Cv[code]."""
+    k_cb = np.asarray(k_cb, np.float64)
+    v_cb = np.asarray(v_cb, np.float64)
+    T, G = k_codes.shape
+    Kd = (k_cb[k_codes.astype(np.int64)].reshape(T, -1)) * np.asarray(k_scales, np.float64)[:, None]
+    Vd = (v_cb[v_codes.astype(np.int64)].reshape(T, -1)) * np.asarray(v_scales, np.float64)[:, None]
+    outs = []
+    for q in q_heads:
+        kt = [Kd[i:i + tile] for i in range(0, T, tile)]
+        vt = [Vd[i:i + tile] for i in range(0, T, tile)]
+        outs.append(online_softmax_attention(q, kt, vt, scale))
+    return np.stack(outs)
+
+
+# --- ojasx_24x96/codec.py + math_engine.py ---------------------------------------
+
+def pack_codes(codes, bits):
+    """Little-endian bit packing (codec.py:176-195); identity for 8 bits."""
+    flat = np.asarray(codes).reshape(-1).astype(np.int64)
+    if bits not in (1, 2, 4, 8):
+        raise ValueError("Only 1-, 2-, 4-, and 8-bit codes are supported")
+    if flat.size and (flat.min() < 0 or flat.max() >= (1 << bits)):
+        raise ValueError("A code exceeds the requested bit width")
+    if bits == 8:
+        return flat.astype(np.uint8)
+    per = 8 // bits
+    n = (flat.size + per - 1) // per * per
+    pad = np.zeros(n, np.int64)
+    pad[:flat.size] = flat
+    grp = pad.reshape(-1, per)
+    return (grp << (np.arange(per) * bits)).sum(axis=1).astype(np.uint8)
+
+
+def unpack_codes(packed, bits, count):
+    """Inverse of pack_codes with explicit count (codec.py:198-214)."""
+    packed = np.asarray(packed, np.uint8)
+    if (count * bits + 7) // 8 != packed.size:
+        raise ValueError("packed size mismatch")
+    per = 8 // bits
+    vals = (packed.astype(np.int64)[:, None] >> (np.arange(per) * bits)) & ((1 << bits) - 1)
+    return vals.reshape(-1)[:count].astype(np.uint8)
+
+
+def subspace_lut_rvq_gemm(x, codebooks, packed_codes, bits, rows, cols, block, row_scales,
+                          bias=None, dtype=np.float64):
+    """Y[b,m] = s_m * sum_{s,g} LUT[b,s,g,code_s[m,g]] + bias with K zero-padded
+    to G*block (math_engine.py:136-208)."""
+    x = np.asarray(x, dtype)
+    shp = x.shape
+    xf = x.reshape(-1, cols)
+    G = (cols + block - 1) // block
+    if G * block > cols:
+        xf = np.pad(xf, ((0, 0), (0, G * block - cols)))
+    xb = xf.reshape(xf.shape[0], G, block)
+    cbs = np.asarray(codebooks, dtype)                      # [S, Q, block]
+    lut = np.einsum("bgd,sqd->bsgq", xb, cbs)
+    y = np.zeros((xf.shape[0], rows), dtype)
+    gi = np.arange(G)[None, :]
+    for s in range(cbs.shape[0]):
+        c = unpack_codes(packed_codes[s], bits, rows * G).reshape(rows, G).astype(np.int64)
+        y += lut[:, s][:, gi, c].sum(axis=2)
+    y = y * np.asarray(row_scales, dtype)[None, :]
+    if bias is not None:
+        y = y + np.asarray(bias, dtype)[None, :]
+    return y.reshape(*shp[:-1], rows)

@@ -1,0 +1,203 @@
+"""GPU parity of the LUT linear path (K1 LUT build + K2 gather + K3 CSR)
+against the CPU oracle, through the HIP C-ABI.
+
+Bars: bit-exact on integer-valued inputs (every partial sum exact in fp32,
+so any summation order gives the same bits) and on the reference's CSR known
+answer; rel <= 1e-5 (max-abs error / max |ref|) for fp32 activations and
+<= 1e-2 for bf16 activations on random inputs.
+"""
+import ctypes
+import os
+
+import numpy as np
+import pytest
+
+from conftest import GOLDEN, rel_err
+from oracle import cpu, gen
+from test_oracle import integer_case
+
+pytestmark = pytest.mark.gpu
+
+F32_TOL = 1e-5
+BF16_TOL = 1e-2
+
+
+def native_linear(pkg, d, M, K, D=16, Kcb=256):
+    nat = pkg.native.NativeSplitManifoldLinear(K, M, D, Kcb)
+    nat.initialize_weights(d["codebook"], d["codes"],
+                           d["scales"] if d.get("scales") is not None else np.ones(M, np.float32),
+                           d.get("bias"))
+    if d.get("csr") is not None:
+        nat.set_outliers(*d["csr"])
+    return nat
+
+
+def dev_forward(pkg, nat, x_t, dtype_tag, out_dtype):
+    import torch
+    y = torch.empty(x_t.shape[0], nat.out_features, device=x_t.device, dtype=out_dtype)
+    rc = pkg.lib().ojasx_linear_forward_device(
+        nat.handle, ctypes.c_void_p(x_t.data_ptr()), ctypes.c_void_p(y.data_ptr()),
+        x_t.shape[0], dtype_tag, ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    assert rc == 0, pkg.lib().ojasx_get_last_error()
+    torch.cuda.synchronize()
+    return y
+
+
+@pytest.mark.parametrize("name", ["linear_k256_m200_b3", "linear_d8_k128_m96_b2_cb64",
+                                  "linear_k2560_m64_b1"])
+def test_host_api_golden(pkg, name):
+    g = np.load(os.path.join(GOLDEN, name + ".npz"))
+    M, G = g["codes"].shape
+    D = g["codebook"].shape[1]
+    d = dict(codebook=g["codebook"], codes=g["codes"], scales=g["scales"],
+             bias=g["bias"] if "bias" in g else None, csr=(g["row_ptrs"], g["cols"], g["vals"]))
+    nat = native_linear(pkg, d, M, G * D, D, g["codebook"].shape[0])
+    y = nat.forward(g["x"])
+    assert rel_err(y, g["y"]) < F32_TOL
+
+
+def test_reference_t3_exact(pkg):
+    t3 = gen.reference_t3()
+    nat = native_linear(pkg, t3, 32, 64)
+    y = nat.forward(t3["x"])
+    assert np.all(y == 5.0)
+
+
+def test_reference_t2(pkg):
+    t2 = gen.reference_t2()
+    nat = native_linear(pkg, t2, 128, 256)
+    y = nat.forward(t2["x"])
+    g = np.load(os.path.join(GOLDEN, "ref_t2_linear.npz"))["y"][0]
+    assert np.abs(y - g).max() < 1e-4
+    assert rel_err(y, g) < F32_TOL
+
+
+@pytest.mark.parametrize("M,K,B", [(97, 640, 2), (6912, 2560, 1), (6912, 2560, 3),
+                                   (2560, 2560, 8), (1000, 2560, 64)])
+def test_integer_inputs_bit_exact(pkg, dev, M, K, B):
+    import torch
+    c = integer_case(M * 7 + B, M=M, K=K, B=B)
+    nat = native_linear(pkg, dict(codebook=c["codebook"], codes=c["codes"], csr=c["csr"]), M, K)
+    y = dev_forward(pkg, nat, torch.from_numpy(c["x"]).to(dev), 0, torch.float32)
+    assert np.array_equal(y.cpu().numpy(), c["y"])
+
+
+@pytest.mark.parametrize("M,K,B", [(2560, 2560, 1), (6912, 2560, 1), (6912, 2560, 8),
+                                   (6912, 2560, 64)])
+def test_baseline_configs_fp32(pkg, dev, M, K, B):
+    import torch
+    d = gen.linear(M, K, B=B, seed=M + B, scales="u")
+    nat = native_linear(pkg, d, M, K)
+    y = dev_forward(pkg, nat, torch.from_numpy(d["x"]).to(dev), 0, torch.float32).cpu().numpy()
+    y_ref = cpu.linear_forward(d["x"], d["codebook"], d["codes"], d["scales"], None, *d["csr"])
+    assert rel_err(y, y_ref) < F32_TOL
+
+
+@pytest.mark.parametrize("B", [1, 8, 64])
+def test_baseline_gate_up_bf16(pkg, dev, B):
+    import torch
+    d = gen.linear(6912, 2560, B=B, seed=50 + B)
+    nat = native_linear(pkg, d, 6912, 2560)
+    xb = torch.from_numpy(d["x"]).to(dev).to(torch.bfloat16)
+    y = dev_forward(pkg, nat, xb, 1, torch.bfloat16).float().cpu().numpy()
+    x_rounded = xb.float().cpu().numpy()
+    y_ref = cpu.linear_forward(x_rounded, d["codebook"], d["codes"], d["scales"], None, *d["csr"])
+    assert rel_err(y, y_ref) < BF16_TOL
+
+
+@pytest.mark.parametrize("M,K,D,Kcb,bias", [(300, 200, 8, 256, True), (513, 384, 24, 100, False),
+                                            (64, 32, 32, 256, True), (1, 16, 16, 256, False)])
+def test_odd_shapes(pkg, dev, M, K, D, Kcb, bias):
+    """Groups not a multiple of 16, block_dim != 16, small codebooks, one row."""
+    d = gen.linear(M, K, B=5, D=D, Kcb=Kcb, seed=M + K, scales="u", bias=bias, density=0.02)
+    nat = native_linear(pkg, d, M, K, D, Kcb)
+    y = nat.forward(d["x"])
+    y_ref = cpu.linear_forward(d["x"], d["codebook"], d["codes"], d["scales"], d["bias"], *d["csr"])
+    assert rel_err(y, y_ref) < F32_TOL
+
+
+def test_repeat_calls_deterministic_and_outlier_reset(pkg):
+    """The split-reduction tickets reset themselves: repeated calls give
+    identical bits; nnz = 0 clears the outliers."""
+    d = gen.linear(6912, 2560, B=2, seed=77, scales="u", bias=True)
+    nat = native_linear(pkg, d, 6912, 2560)
+    ys = [nat.forward(d["x"]) for _ in range(5)]
+    for y in ys[1:]:
+        assert np.array_equal(y, ys[0])
+    y1 = nat.forward(d["x"][:1])
+    assert rel_err(y1[None] if y1.ndim == 1 else y1, ys[0][:1]) < F32_TOL
+    nat.set_outliers(np.zeros(6913, np.int32), np.zeros(0, np.int32), np.zeros(0, np.float32))
+    y0 = nat.forward(d["x"])
+    want = cpu.linear_forward(d["x"], d["codebook"], d["codes"], d["scales"], d["bias"])
+    assert rel_err(y0, want) < F32_TOL
+
+
+def test_invalid_outliers_rejected(pkg):
+    d = gen.linear(64, 256, seed=3)
+    nat = native_linear(pkg, dict(codebook=d["codebook"], codes=d["codes"]), 64, 256)
+    rp = np.zeros(65, np.int32)
+    rp[1:] = 1
+    with pytest.raises(pkg.OjasxError):
+        nat.set_outliers(rp, np.array([256], np.int32), np.array([1.0], np.float32))
+    L = pkg.lib()
+    assert L.ojasx_linear_forward(None, None, None, 1, 0) == -1
+    assert L.ojasx_set_linear_outliers(None, 0, None, None, None) == -1
+
+
+def test_zero_batch_noop(pkg, dev):
+    import torch
+    d = gen.linear(64, 256, seed=4)
+    nat = native_linear(pkg, d, 64, 256)
+    y = torch.full((1, 64), 3.0, device=dev)
+    rc = pkg.lib().ojasx_linear_forward_device(nat.handle, ctypes.c_void_p(y.data_ptr()),
+                                               ctypes.c_void_p(y.data_ptr()), 0, 0, None)
+    torch.cuda.synchronize()
+    assert rc == 0 and bool((y == 3.0).all())
+
+
+def test_build_lut_device(pkg, dev):
+    import torch
+    eng = pkg.engine
+    d = gen.linear(8, 2560, B=3, seed=5)
+    layer = eng.SplitManifoldLUTLinear(2560, 8).to(dev)
+    layer.codebook.copy_(torch.from_numpy(d["codebook"]))
+    lut = layer.build_lut(torch.from_numpy(d["x"]).to(dev)).cpu().numpy()
+    for b in range(3):
+        assert rel_err(lut[b], cpu.build_lut(d["x"][b], d["codebook"])) < 1e-6
+
+
+@pytest.mark.parametrize("dtype", ["float32", "bfloat16"])
+def test_engine_module(pkg, dev, dtype):
+    """SplitManifoldLUTLinear API: COO outliers, bias, leading batch dims."""
+    import torch
+    dt = getattr(torch, dtype)
+    d = gen.linear(640, 1024, B=6, seed=9, scales="u", bias=True)
+    layer = pkg.engine.SplitManifoldLUTLinear(1024, 640, bias=True, dtype=dt).to(dev)
+    layer.codebook.copy_(torch.from_numpy(d["codebook"]))
+    layer.codes.copy_(torch.from_numpy(d["codes"]))
+    layer.scales.copy_(torch.from_numpy(d["scales"]))
+    layer.bias.data.copy_(torch.from_numpy(d["bias"]))
+    rp, cl, vl = d["csr"]
+    rows = np.repeat(np.arange(640), np.diff(rp))
+    layer.outlier_indices = torch.from_numpy(np.stack([rows, cl]).astype(np.int64)).to(dev)
+    layer.outlier_values = torch.from_numpy(vl).to(dev).to(dt)
+    layer.num_outliers = vl.size
+    x = torch.from_numpy(d["x"]).to(dev).to(dt).view(2, 3, 1024)
+    y = layer(x)
+    assert y.shape == (2, 3, 640) and y.dtype == dt
+    # reference semantics on the module's own (possibly bf16-rounded) buffers
+    f = lambda t: t.detach().float().cpu().numpy()
+    y_ref = cpu.linear_forward(f(x).reshape(6, 1024), f(layer.codebook), d["codes"],
+                               f(layer.scales), f(layer.bias), rp, cl, f(layer.outlier_values))
+    tol = F32_TOL if dt == torch.float32 else BF16_TOL
+    assert rel_err(f(y).reshape(6, 640), y_ref) < tol
+    # the diagnostic dense weight reproduces the same layer
+    W = f(layer.dequantize_weights()).astype(np.float64)
+    assert rel_err(f(y).reshape(6, 640), f(x).reshape(6, 1024) @ W.T + f(layer.bias)) < tol * 10
+
+
+def test_cpu_tensor_fails_loudly(pkg):
+    import torch
+    layer = pkg.engine.SplitManifoldLUTLinear(32, 8)
+    with pytest.raises(RuntimeError, match="GPU only"):
+        layer(torch.zeros(1, 32))
