@@ -57,9 +57,23 @@ class OjasxError(RuntimeError):
     """A C-ABI call returned a non-zero status."""
 
 
+def _bind_torch_runtime():
+    """Load PyTorch's HIP runtime before the library.  torch ships its own
+    libamdhip64 (soname libamdhip64.so.7, needed by name libamdhip64.so); if
+    the system one were loaded first the process would hold two HIP runtimes
+    and torch streams and allocations would not be valid in our calls.  With
+    torch loaded first, the library's libamdhip64.so.7 dependency resolves to
+    torch's copy: one runtime per process."""
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
+
+
 def lib():
     global _lib
     if _lib is None:
+        _bind_torch_runtime()
         if not os.path.exists(LIB_PATH):
             raise FileNotFoundError(
                 f"Native library not found at: {LIB_PATH} (build it with "

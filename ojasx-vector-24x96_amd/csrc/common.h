@@ -38,6 +38,15 @@ int upload(DevBuf &buf, const void *host, size_t n);  // ensure + memcpy
 
 inline size_t round_up(size_t v, size_t m) { return (v + m - 1) / m * m; }
 
+// Raise a kernel's dynamic-LDS limit when a launch needs more than the 64 KB
+// default (gfx950 has 160 KB per workgroup).  `granted` caches the last value.
+inline int ensure_dyn_lds(const void *fn, size_t bytes, size_t *granted) {
+    if (bytes <= 65536 || bytes <= *granted) return OJASX_OK;
+    OJX_HIP(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes));
+    *granted = bytes;
+    return OJASX_OK;
+}
+
 // ---- device helpers ------------------------------------------------------
 __device__ __forceinline__ float load_act(const float *p, size_t i) { return p[i]; }
 __device__ __forceinline__ float load_act(const __hip_bfloat16 *p, size_t i) {
@@ -46,6 +55,49 @@ __device__ __forceinline__ float load_act(const __hip_bfloat16 *p, size_t i) {
 __device__ __forceinline__ void store_act(float *p, size_t i, float v) { p[i] = v; }
 __device__ __forceinline__ void store_act(__hip_bfloat16 *p, size_t i, float v) {
     p[i] = __float2bfloat16(v);
+}
+
+// Copy n activations (converted to fp32) from global memory to LDS with all
+// of a thread's loads in flight before the first LDS store: loads and stores
+// use clamped indices, so the code is branch-free (out-of-range lanes rewrite
+// the last element with its own value) and the loop body is
+// one memory round trip for up to NT*4*16 elements (fp32 rows use 16-byte
+// loads when 16-byte aligned).  Runtime-trip-count copy loops otherwise
+// serialise one round trip per element a thread copies.
+template <int NT>
+__device__ __forceinline__ void stage_to_lds(float *dst, const float *src, int n) {
+    constexpr int U = 16;
+    if (((reinterpret_cast<uintptr_t>(src) & 15) == 0) && (n & 3) == 0) {
+        const float4 *s4 = reinterpret_cast<const float4 *>(src);
+        const int n4 = n >> 2;
+        for (int b = threadIdx.x; b < n4; b += NT * U) {
+            float4 v[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u) v[u] = s4[min(b + u * NT, n4 - 1)];
+#pragma unroll
+            for (int u = 0; u < U; ++u) reinterpret_cast<float4 *>(dst)[min(b + u * NT, n4 - 1)] = v[u];
+        }
+        return;
+    }
+    for (int b = threadIdx.x; b < n; b += NT * U) {
+        float v[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) v[u] = src[min(b + u * NT, n - 1)];
+#pragma unroll
+        for (int u = 0; u < U; ++u) dst[min(b + u * NT, n - 1)] = v[u];
+    }
+}
+
+template <int NT>
+__device__ __forceinline__ void stage_to_lds(float *dst, const __hip_bfloat16 *src, int n) {
+    constexpr int U = 16;
+    for (int b = threadIdx.x; b < n; b += NT * U) {
+        float v[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) v[u] = __bfloat162float(src[min(b + u * NT, n - 1)]);
+#pragma unroll
+        for (int u = 0; u < U; ++u) dst[min(b + u * NT, n - 1)] = v[u];
+    }
 }
 
 // Exclusive prefix sum over the 64 lanes of a wave of a value < 256.

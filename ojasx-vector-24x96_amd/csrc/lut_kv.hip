@@ -269,12 +269,9 @@ int kv_decode(const float *q, const uint8_t *kc, const float *ks, const uint8_t 
     KVParams p{q, kc, vc, ks, vs, kcb, vcb, bt, wk.o.as<float>(), wk.ml.as<float>(), T, P, Hq,
                Hkv, hd, D, G, Tc, RS, n_chunks, sf};
     const size_t lds = ((size_t)RS * G * 256 * 2 + 256 * D + (size_t)RS * Tc + kNT) * 4;
-    static bool attr = false;
-    if (!attr) {
-        OJX_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(&kv_decode_chunk_kernel),
-                                    hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
-        attr = true;
-    }
+    static size_t granted = 0;
+    rc = ensure_dyn_lds(reinterpret_cast<const void *>(&kv_decode_chunk_kernel), lds, &granted);
+    if (rc) return rc;
     hipLaunchKernelGGL(kv_decode_chunk_kernel, dim3(n_chunks, Hkv, nz), dim3(kNT), lds, st, p);
     hipLaunchKernelGGL(kv_merge_kernel, dim3(Hq), dim3(128), 0, st, wk.o.as<float>(),
                        wk.ml.as<float>(), n_chunks, hd, out);

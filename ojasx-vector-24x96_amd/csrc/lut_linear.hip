@@ -1,32 +1,30 @@
 // lut_linear.hip -- split-manifold LUT linear layer on gfx950.
 //
 // Computes, for every token b and output row m,
-//   y[b,m] = s_m * sum_g LUT_b[g, codes[m,g]] + bias[m] + sum_j val_j * x[b,col_j]
-// with LUT_b[g,k] = <x_b[gD:(g+1)D], C[k]>, the formula of
+//   y[b,m] = (s_m * sum_g LUT_b[g, codes[m,g]] + bias[m]) + sum_j val_j * x[b,col_j]
+// with LUT_b[g,k] = <x_b[gD:(g+1)D], C[k]>, the formula and epilogue order of
 // split_manifold_lut_experiment/native/src/ojasx_lut_cpu.cpp:18-206 (LUT build
-// :18-102, row gather :160-184, epilogue :178-182, CSR outliers :104-130) and
-// of split_manifold_lut_experiment/engine/split_manifold_engine.py:185-250.
+// :18-102, row gather :160-184, epilogue :178-182, CSR outliers :104-130,
+// added after the epilogue and not scaled) and of
+// split_manifold_lut_experiment/engine/split_manifold_engine.py:185-250.
 //
-// Design (one kernel per call, K1+K2+K3 fused):
-//  * Work tile = (row block of 256*RPT rows) x (slice of 16 groups) x (BT
-//    tokens).  A workgroup owns a row block, a contiguous run of slices and a
-//    token chunk.  For each slice it stages x for the slice's 16*D columns in
-//    LDS, builds the slice's LUT (BT x 16 x 256 fp32, 16 KB per token) in LDS
-//    from the 256 x D codebook (thread k owns centroid k), then every thread
-//    gathers and sums the 16 LUT entries of each of its rows.
-//  * Codes are repacked at handle creation into slice-major tiles
-//    [S][Mp][16]: a thread reads its row's 16 codes of a slice with one 16-byte
-//    load and a wave reads 1 KB contiguous.
-//  * CSR outliers are re-bucketed at set_outliers() by (slice, row): a uint8
-//    count per (slice,row), a uint32 base per (slice, 64-row group) and
-//    (slice-local uint16 column, fp32 value) entries.  A lane finds its
-//    entries by a wave prefix sum of the counts and reads x from the LDS
-//    slice, so the outlier add is fused into the gather pass.
-//  * When the row's slices are split over several workgroups, each writes a
-//    partial (s_m * sum + outlier part) and the last workgroup to finish a row
-//    block (atomic ticket) sums the partials in slice order and adds bias:
-//    one launch, deterministic result.  The ticket counter is reset by that
-//    workgroup, so the workspace needs no clearing between calls.
+// Two kernels per call and no cross-workgroup synchronisation.  At batch 1
+// both are latency-bound (1.1 MB of codes is ~0.14 us of HBM time against a
+// ~1.3 us kernel floor), so each issues every independent load first and
+// keeps the chain of dependent memory round trips to two:
+//  K1 lut_build: the LUT of every token, LUT[b][g][k] for all 256 centroids,
+//     into a workspace (workgroup = (1 group, 1 token), thread k owns
+//     centroid k): x and the codebook, then one store.
+//  K2 lut_gather: workgroup = 64 output rows x up to 4 tokens; lane = row, the
+//     4 waves take interleaved 16-group slices.  Round trip 1: a lane reads
+//     its row's 16 codes of each of its slices with one 16-byte load each (a
+//     wave reads 1 KB contiguous from the slice-major tiles [S][Mp][16]),
+//     together with scale, bias, CSR row bounds and x (staged in LDS).  Round
+//     trip 2: the 16 LUT entries per slice and token from the L2-resident
+//     LUT, and -- wave 0 -- the row's CSR outlier entries (32 per batch).
+//     The four wave partials are summed in LDS in wave order and the epilogue
+//     applies scale, bias and the outlier sum in the reference's order:
+//     deterministic results.
 #include <algorithm>
 #include <cstring>
 #include <vector>
@@ -38,181 +36,181 @@ namespace ojx {
 namespace {
 constexpr int kNT = 256;        // threads per workgroup (4 waves)
 constexpr int kGS = 16;         // groups per slice: 16 code bytes per row
-constexpr int kRowAlign = 1024; // rows padded to the largest row block
+constexpr int kRowAlign = 1024; // rows padded for the tile layout
 constexpr int kCB = 256;        // centroids in the (zero-padded) codebook
+constexpr int kRows = 64;       // rows per gather workgroup (one per lane)
+constexpr int kWaves = kNT / 64;
+constexpr int kOB = 32;         // outlier entries loaded per batch
+constexpr size_t kXLdsBytes = 48 * 1024;  // x staged in LDS up to this size
 }  // namespace
 
-struct LinParams {
-    const uint8_t *codes;    // [S][Mp][16]
-    const uint8_t *ocnt;     // [S][Mp]
-    const uint32_t *obase;   // [S][Mp/64]
-    const uint16_t *ocol;    // [nnz] slice-local column
-    const float *oval;       // [nnz]
-    const float *codebook;   // [256][D]
-    const float *scales;     // [M]
-    const float *bias;       // [M] or null
-    const void *x;           // [B][K]
-    void *y;                 // [B][M]
-    float *partial;          // [n_splits][B][Mp]
-    unsigned *counters;      // [n_rb][token chunks]
-    int K, M, Mp, D, S, B, spw, n_splits, has_out;
+struct GatherParams {
+    const uint8_t *codes;   // [S][Mp][16]
+    const float *lut;       // [B][Gp][256]
+    const float *scales;    // [M]
+    const float *bias;      // [M] or null
+    const int *rowp;        // [M+1] CSR row pointers (null: no outliers)
+    const int *col;         // [nnz]
+    const float *val;       // [nnz]
+    const void *x;          // [B][K]
+    void *y;                // [B][M]
+    int K, M, Mp, S, Gp, B, nnz, x_lds;
 };
 
-template <int BT, int RPT, int DT, typename T>
-__global__ __launch_bounds__(kNT) void lut_gemv_kernel(LinParams p) {
+// K1: LUT of token b for group blockIdx.x (zero for padded groups >= G).
+template <int DT, typename T>
+__global__ __launch_bounds__(kCB) void lut_build_kernel(const T *__restrict__ x,
+                                                      const float *__restrict__ cb, int K, int D,
+                                                      int G, int Gp, float *__restrict__ lut) {
     constexpr int DMAX = DT > 0 ? DT : 32;
-    const int D = DT > 0 ? DT : p.D;
-    const int slice_cols = kGS * D;
-    extern __shared__ float smem[];
-    float *lut = smem;                     // [BT][16][256]
-    float *xs = smem + BT * kGS * kCB;     // [BT][16*D]
-    __shared__ int s_last;
+    const int Dr = DT > 0 ? DT : D;
+    __shared__ float xs[32];
+    const int b = blockIdx.y, g = blockIdx.x, k = threadIdx.x;
+    float c[DMAX];
+#pragma unroll
+    for (int d = 0; d < DMAX; ++d) c[d] = d < Dr ? cb[k * Dr + d] : 0.f;
+    if (k < Dr) xs[k] = g < G ? load_act(x, (size_t)b * K + (size_t)g * Dr + k) : 0.f;
+    __syncthreads();
+    float dot = 0.f;
+#pragma unroll
+    for (int d = 0; d < DMAX; ++d)
+        if (d < Dr) dot = fmaf(xs[d], c[d], dot);
+    lut[((size_t)b * Gp + g) * kCB + k] = dot;
+}
 
-    const int tid = threadIdx.x;
-    const int rb = blockIdx.x / p.n_splits;
-    const int sp = blockIdx.x - rb * p.n_splits;
+// K2 + K3: gather-accumulate, outliers and epilogue, one row per lane.
+// Loads are issued branch-free (clamped indices, results masked at use) so
+// the compiler can keep them all in flight: round trip 1 = codes, scale,
+// bias, CSR row bounds, x; round trip 2 = LUT entries and outlier entries.
+template <int BT, typename T>
+__global__ __launch_bounds__(kNT) void lut_gather_kernel(GatherParams p) {
+    extern __shared__ float xs[];                 // [BT][K] when p.x_lds
+    __shared__ float red[kWaves][BT][kRows];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int m = blockIdx.x * kRows + lane;      // < Mp: codes need no clamp
+    const int mr = min(m, p.M - 1);               // clamped row for [M] arrays
     const int t0 = blockIdx.y * BT;
-    const int s0 = sp * p.spw;
-    const int s1 = min(p.S, s0 + p.spw);
+    const int nt = min(BT, p.B - t0);
+    const bool outl = p.rowp != nullptr;
     const T *__restrict__ x = static_cast<const T *>(p.x);
-    const int row0 = rb * kNT * RPT + tid;
 
-    float cb[DMAX];
+    // ---- round trip 1
+    uint4 cv[4];
 #pragma unroll
-    for (int d = 0; d < DMAX; ++d) cb[d] = (d < D) ? p.codebook[tid * D + d] : 0.f;
+    for (int i = 0; i < 4; ++i) {
+        const int s = min(w + i * kWaves, p.S - 1);
+        cv[i] = *reinterpret_cast<const uint4 *>(p.codes + ((size_t)s * p.Mp + m) * kGS);
+    }
+    const float sc = p.scales[mr];
+    const float bs = p.bias ? p.bias[mr] : 0.f;
+    int j0 = 0, j1 = 0;
+    if (outl) {
+        j0 = p.rowp[mr];
+        j1 = p.rowp[mr + 1];
+    }
+    if (outl && p.x_lds) stage_to_lds<kNT>(xs, x + (size_t)t0 * p.K, nt * p.K);
 
-    float acc[BT][RPT], oac[BT][RPT];
+    // ---- round trip 2: first batch of outlier entries, LUT entries
+    int oc[kOB];
+    float ov[kOB];
+    if (outl) {
 #pragma unroll
-    for (int t = 0; t < BT; ++t)
-#pragma unroll
-        for (int j = 0; j < RPT; ++j) acc[t][j] = oac[t][j] = 0.f;
-
-    for (int s = s0; s < s1; ++s) {
-        uint4 cv[RPT];
-        int oc[RPT];
-#pragma unroll
-        for (int j = 0; j < RPT; ++j) {
-            const size_t r = (size_t)s * p.Mp + row0 + j * kNT;
-            cv[j] = *reinterpret_cast<const uint4 *>(p.codes + r * kGS);
-            oc[j] = p.has_out ? p.ocnt[r] : 0;
+        for (int u = 0; u < kOB; ++u) {
+            const int j = min(j0 + u, p.nnz - 1);
+            oc[u] = p.col[j];
+            ov[u] = p.val[j];
         }
-        for (int i = tid; i < BT * slice_cols; i += kNT) {
-            const int t = i / slice_cols;
-            const int c = i - t * slice_cols;
-            const int tok = t0 + t;
-            const int col = s * slice_cols + c;
-            xs[i] = (tok < p.B && col < p.K) ? load_act(x, (size_t)tok * p.K + col) : 0.f;
+    }
+    float acc[BT];
+#pragma unroll
+    for (int t = 0; t < BT; ++t) acc[t] = 0.f;
+    for (int s0 = w;; s0 += kWaves * 4) {
+        // (token, slice) pairs, 4 at a time: 64 LUT loads in flight, then the
+        // adds (per token, slices ascending).
+#pragma unroll
+        for (int q0 = 0; q0 < BT * 4; q0 += 4) {
+            float lv[4][kGS];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int t = (q0 + q) >> 2, i = (q0 + q) & 3;
+                const int s = min(s0 + i * kWaves, p.S - 1);
+                const int tt = min(t, nt - 1);
+                const float *L = p.lut + ((size_t)(t0 + tt) * p.Gp + s * kGS) * kCB;
+                const uint32_t w4[4] = {cv[i].x, cv[i].y, cv[i].z, cv[i].w};
+#pragma unroll
+                for (int g = 0; g < kGS; ++g)
+                    lv[q][g] = L[g * kCB + ((w4[g >> 2] >> ((g & 3) * 8)) & 0xffu)];
+            }
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int t = (q0 + q) >> 2, i = (q0 + q) & 3;
+                if (s0 + i * kWaves < p.S) {
+                    float a = acc[t];
+#pragma unroll
+                    for (int g = 0; g < kGS; ++g) a += lv[q][g];
+                    acc[t] = a;
+                }
+            }
         }
-        __syncthreads();
+        const int nx = s0 + kWaves * 4;
+        if (nx >= p.S) break;
+        // further slices (K > 64 groups * 4 waves): next batch of codes
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int s = min(nx + i * kWaves, p.S - 1);
+            cv[i] = *reinterpret_cast<const uint4 *>(p.codes + ((size_t)s * p.Mp + m) * kGS);
+        }
+    }
+#pragma unroll
+    for (int t = 0; t < BT; ++t) red[w][t][lane] = acc[t];
+    __syncthreads();
+    if (w != 0 || m >= p.M) return;
 
-        // K1: LUT[t][g][k = tid] = <x_t,g , C[k]>
+    // Outliers in CSR order (x from LDS when staged).
+    // First batch branch-free: entries past the row's end add an exact 0.
+    float oac[BT];
+#pragma unroll
+    for (int t = 0; t < BT; ++t) oac[t] = 0.f;
+    if (outl) {
+        const int n0 = j1 - j0;
 #pragma unroll
         for (int t = 0; t < BT; ++t) {
-#pragma unroll 4
-            for (int g = 0; g < kGS; ++g) {
-                const float *xg = xs + t * slice_cols + g * D;
-                float dot = 0.f;
+            const int tt = min(t, nt - 1);
+            float xv[kOB];
 #pragma unroll
-                for (int d = 0; d < DMAX; ++d)
-                    if (d < D) dot = fmaf(xg[d], cb[d], dot);
-                lut[(t * kGS + g) * kCB + tid] = dot;
-            }
+            for (int u = 0; u < kOB; ++u)
+                xv[u] = p.x_lds ? xs[tt * p.K + oc[u]] : load_act(x, (size_t)(t0 + tt) * p.K + oc[u]);
+            float o = 0.f;
+#pragma unroll
+            for (int u = 0; u < kOB; ++u) o += u < n0 ? ov[u] * xv[u] : 0.f;
+            oac[t] = o;
         }
-        __syncthreads();
-
-        // K2: gather-accumulate, groups in ascending order
+        // rows with more than kOB outliers (rare): the rest in CSR order
+        for (int j = j0 + kOB; j < j1; ++j) {
+            const int c = p.col[j];
+            const float v = p.val[j];
 #pragma unroll
-        for (int j = 0; j < RPT; ++j) {
-            const uint32_t w4[4] = {cv[j].x, cv[j].y, cv[j].z, cv[j].w};
-#pragma unroll
-            for (int t = 0; t < BT; ++t) {
-                const float *L = lut + t * kGS * kCB;
-                float a = acc[t][j];
-#pragma unroll
-                for (int g = 0; g < kGS; ++g) {
-                    const uint32_t code = (w4[g >> 2] >> ((g & 3) * 8)) & 0xffu;
-                    a += L[g * kCB + code];
-                }
-                acc[t][j] = a;
-            }
+            for (int t = 0; t < BT; ++t)
+                if (t < nt)
+                    oac[t] += v * (p.x_lds ? xs[t * p.K + c] : load_act(x, (size_t)(t0 + t) * p.K + c));
         }
-
-        // K3: outliers of this slice (x from the LDS slice)
-        if (p.has_out) {
-#pragma unroll
-            for (int j = 0; j < RPT; ++j) {
-                const int c = oc[j];
-                const int off = wave_excl_scan_u8(c);
-                if (c) {
-                    const int m = row0 + j * kNT;
-                    const size_t base =
-                        (size_t)p.obase[(size_t)s * (p.Mp >> 6) + (m >> 6)] + off;
-                    for (int e = 0; e < c; ++e) {
-                        const int col = p.ocol[base + e];
-                        const float v = p.oval[base + e];
-#pragma unroll
-                        for (int t = 0; t < BT; ++t) oac[t][j] += v * xs[t * slice_cols + col];
-                    }
-                }
-            }
-        }
-        __syncthreads();
     }
-
     T *y = static_cast<T *>(p.y);
-    const bool split = p.n_splits > 1;
 #pragma unroll
     for (int t = 0; t < BT; ++t) {
-        const int tok = t0 + t;
-        if (tok >= p.B) break;
+        if (t >= nt) break;
+        float a = red[0][t][lane];
 #pragma unroll
-        for (int j = 0; j < RPT; ++j) {
-            const int m = row0 + j * kNT;
-            if (m >= p.M) continue;
-            const float sc = p.scales[m];
-            if (!split) {
-                float r = acc[t][j] * sc;
-                if (p.bias) r += p.bias[m];
-                r += oac[t][j];
-                store_act(y, (size_t)tok * p.M + m, r);
-            } else {
-                p.partial[((size_t)sp * p.B + tok) * p.Mp + m] = acc[t][j] * sc + oac[t][j];
-            }
-        }
-    }
-    if (!split) return;
-
-    // Ticket: the last workgroup of this (row block, token chunk) reduces.
-    __threadfence();
-    __syncthreads();
-    if (tid == 0) {
-        unsigned *ctr = p.counters + (size_t)rb * gridDim.y + blockIdx.y;
-        const unsigned old = atomicAdd(ctr, 1u);
-        s_last = (old == (unsigned)(p.n_splits - 1));
-        if (s_last) atomicExch(ctr, 0u);
-    }
-    __syncthreads();
-    if (!s_last) return;
-    __threadfence();
-#pragma unroll
-    for (int t = 0; t < BT; ++t) {
-        const int tok = t0 + t;
-        if (tok >= p.B) break;
-#pragma unroll
-        for (int j = 0; j < RPT; ++j) {
-            const int m = row0 + j * kNT;
-            if (m >= p.M) continue;
-            float r = 0.f;
-            for (int q = 0; q < p.n_splits; ++q)
-                r += p.partial[((size_t)q * p.B + tok) * p.Mp + m];
-            if (p.bias) r += p.bias[m];
-            store_act(y, (size_t)tok * p.M + m, r);
-        }
+        for (int q = 1; q < kWaves; ++q) a += red[q][t][lane];
+        float r = a * sc;
+        if (p.bias) r += bs;
+        r += oac[t];
+        store_act(y, (size_t)(t0 + t) * p.M + m, r);
     }
 }
 
-// Standalone LUT build: one workgroup per (group, token), thread k computes
-// LUT[b][g][k] = sum_d x[b][g*D+d] * C[k][d].
+// Standalone LUT build with a codebook of Kcb rows: one workgroup per
+// (group, token), thread k computes LUT[b][g][k].
 template <typename T>
 __global__ __launch_bounds__(kCB) void build_lut_kernel(const T *__restrict__ x,
                                                       const float *__restrict__ cb, int G, int D,
@@ -232,45 +230,70 @@ struct Linear {
     int K = 0, M = 0, D = 0, Kcb = 0, G = 0, S = 0, Mp = 0;
     bool has_bias = false;
     size_t nnz = 0;
-    DevBuf codes, codebook, scales, bias, ocnt, obase, ocol, oval;
-    DevBuf partial, counters, xstage, ystage;
-    size_t counters_n = 0;
+    DevBuf codes, codebook, scales, bias, rowp, col, val;
+    DevBuf lut, xstage, ystage;
     ~Linear() {
-        for (DevBuf *b : {&codes, &codebook, &scales, &bias, &ocnt, &obase, &ocol, &oval,
-                          &partial, &counters, &xstage, &ystage})
+        for (DevBuf *b : {&codes, &codebook, &scales, &bias, &rowp, &col, &val, &lut, &xstage,
+                          &ystage})
             b->release();
     }
 };
 
 namespace {
 
-template <int BT, int RPT, int DT, typename T>
-int launch_t(const LinParams &p, int grid_x, int grid_y, hipStream_t st) {
-    const size_t lds = (size_t)BT * kGS * kCB * 4 + (size_t)BT * kGS * (DT > 0 ? DT : p.D) * 4;
-    static bool attr_set = false;
-    if (!attr_set) {
-        OJX_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(&lut_gemv_kernel<BT, RPT, DT, T>),
-                                    hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
-        attr_set = true;
-    }
-    hipLaunchKernelGGL((lut_gemv_kernel<BT, RPT, DT, T>), dim3(grid_x, grid_y), dim3(kNT), lds, st, p);
-    OJX_HIP(hipGetLastError());
+template <int BT, typename T>
+int launch_gather(const GatherParams &gp, dim3 grid, size_t lds, hipStream_t st) {
+    static size_t granted = 0;
+    int rc = ensure_dyn_lds(reinterpret_cast<const void *>(&lut_gather_kernel<BT, T>), lds, &granted);
+    if (rc) return rc;
+    hipLaunchKernelGGL((lut_gather_kernel<BT, T>), grid, dim3(kNT), lds, st, gp);
     return OJASX_OK;
 }
 
-template <int BT, typename T>
-int launch_bt(const LinParams &p, int gx, int gy, hipStream_t st) {
-    return p.D == 16 ? launch_t<BT, 1, 16, T>(p, gx, gy, st) : launch_t<BT, 1, 0, T>(p, gx, gy, st);
-}
-
 template <typename T>
-int launch_dtype(const LinParams &p, int bt, int gx, int gy, hipStream_t st) {
+int launch(Linear *L, const void *x, void *y, int B, hipStream_t st) {
+    const int Gp = L->S * kGS;
+    dim3 g1(Gp, B);
+    if (L->D == 16)
+        hipLaunchKernelGGL((lut_build_kernel<16, T>), g1, dim3(kCB), 0, st,
+                           static_cast<const T *>(x), L->codebook.as<float>(), L->K, L->D, L->G,
+                           Gp, L->lut.as<float>());
+    else
+        hipLaunchKernelGGL((lut_build_kernel<0, T>), g1, dim3(kCB), 0, st,
+                           static_cast<const T *>(x), L->codebook.as<float>(), L->K, L->D, L->G,
+                           Gp, L->lut.as<float>());
+
+    const int bt = B >= 3 ? 4 : B;
+    GatherParams gp{};
+    gp.codes = L->codes.as<uint8_t>();
+    gp.lut = L->lut.as<float>();
+    gp.scales = L->scales.as<float>();
+    gp.bias = L->has_bias ? L->bias.as<float>() : nullptr;
+    gp.rowp = L->nnz ? L->rowp.as<int>() : nullptr;
+    gp.col = L->col.as<int>();
+    gp.val = L->val.as<float>();
+    gp.x = x;
+    gp.y = y;
+    gp.K = L->K;
+    gp.M = L->M;
+    gp.Mp = L->Mp;
+    gp.S = L->S;
+    gp.Gp = Gp;
+    gp.B = B;
+    gp.nnz = (int)L->nnz;
+    const size_t xbytes = (size_t)bt * L->K * sizeof(float);
+    gp.x_lds = L->nnz && xbytes <= kXLdsBytes;
+    const size_t lds = gp.x_lds ? xbytes : 0;
+    dim3 g2((L->M + kRows - 1) / kRows, (B + bt - 1) / bt);
+    int rc;
     switch (bt) {
-        case 1: return launch_bt<1, T>(p, gx, gy, st);
-        case 2: return launch_bt<2, T>(p, gx, gy, st);
-        case 4: return launch_bt<4, T>(p, gx, gy, st);
-        default: return launch_bt<8, T>(p, gx, gy, st);
+        case 1: rc = launch_gather<1, T>(gp, g2, lds, st); break;
+        case 2: rc = launch_gather<2, T>(gp, g2, lds, st); break;
+        default: rc = launch_gather<4, T>(gp, g2, lds, st); break;
     }
+    if (rc) return rc;
+    OJX_HIP(hipGetLastError());
+    return OJASX_OK;
 }
 
 int forward(Linear *L, const void *x, void *y, int B, int dtype, hipStream_t st) {
@@ -279,62 +302,24 @@ int forward(Linear *L, const void *x, void *y, int B, int dtype, hipStream_t st)
         set_error("unsupported dtype %d", dtype);
         return OJASX_ERR_INVALID;
     }
-    const int bt = B >= 8 ? 8 : B >= 3 ? 4 : B;
-    const int chunks = (B + bt - 1) / bt;
-    const int n_rb = (L->M + kNT - 1) / kNT;
-    // Split the slices of a row over enough workgroups to fill the chip.
-    const int base = n_rb * chunks;
-    const int want = std::max(1, std::min(L->S, (512 + base - 1) / base));
-    const int spw = (L->S + want - 1) / want;
-    const int n_splits = (L->S + spw - 1) / spw;
-
-    LinParams p{};
-    p.codes = L->codes.as<uint8_t>();
-    p.ocnt = L->ocnt.as<uint8_t>();
-    p.obase = L->obase.as<uint32_t>();
-    p.ocol = L->ocol.as<uint16_t>();
-    p.oval = L->oval.as<float>();
-    p.codebook = L->codebook.as<float>();
-    p.scales = L->scales.as<float>();
-    p.bias = L->has_bias ? L->bias.as<float>() : nullptr;
-    p.x = x;
-    p.y = y;
-    p.K = L->K;
-    p.M = L->M;
-    p.Mp = L->Mp;
-    p.D = L->D;
-    p.S = L->S;
-    p.B = B;
-    p.spw = spw;
-    p.n_splits = n_splits;
-    p.has_out = L->nnz > 0;
-    if (n_splits > 1) {
-        int rc = L->partial.ensure((size_t)n_splits * B * L->Mp * sizeof(float));
-        if (rc) return rc;
-        const size_t nctr = (size_t)n_rb * chunks;
-        if (nctr > L->counters_n) {
-            rc = L->counters.ensure(nctr * sizeof(unsigned));
-            if (rc) return rc;
-            OJX_HIP(hipMemset(L->counters.ptr, 0, nctr * sizeof(unsigned)));
-            L->counters_n = nctr;
-        }
-        p.partial = L->partial.as<float>();
-        p.counters = L->counters.as<unsigned>();
+    if (B > 65535) {
+        set_error("batch %d exceeds 65535", B);
+        return OJASX_ERR_INVALID;
     }
-    const int gx = n_rb * n_splits;
-    return dtype == OJASX_DTYPE_F32 ? launch_dtype<float>(p, bt, gx, chunks, st)
-                                    : launch_dtype<__hip_bfloat16>(p, bt, gx, chunks, st);
+    const int Gp = L->S * kGS;
+    int rc = L->lut.ensure((size_t)B * Gp * kCB * sizeof(float));
+    if (rc) return rc;
+    return dtype == OJASX_DTYPE_F32 ? launch<float>(L, x, y, B, st)
+                                    : launch<__hip_bfloat16>(L, x, y, B, st);
 }
 
 }  // namespace
 
-// Exposed for the stacked / MoE code paths and tests of the launch heuristics.
 int linear_forward(void *h, const void *x, void *y, int B, int dtype, hipStream_t st) {
     return forward(static_cast<Linear *>(h), x, y, B, dtype, st);
 }
 
 }  // namespace ojx
-
 using ojx::Linear;
 
 extern "C" {
@@ -406,54 +391,19 @@ OJASX_API int ojasx_set_linear_outliers(OjasxLinearHandle handle, int nnz, const
         set_error("row_ptrs must run from 0 to nnz");
         return OJASX_ERR_INVALID;
     }
-    const int slice_cols = kGS * L->D;
-    std::vector<uint32_t> cnt((size_t)L->S * L->Mp, 0);
-    for (int m = 0; m < L->M; ++m) {
+    for (int m = 0; m < L->M; ++m)
         if (row_ptrs[m + 1] < row_ptrs[m]) {
             set_error("row_ptrs not monotone at row %d", m);
             return OJASX_ERR_INVALID;
         }
-        for (int j = row_ptrs[m]; j < row_ptrs[m + 1]; ++j) {
-            const int c = col_indices[j];
-            if (c < 0 || c >= L->K) {
-                set_error("outlier column %d out of range", c);
-                return OJASX_ERR_INVALID;
-            }
-            if (++cnt[(size_t)(c / slice_cols) * L->Mp + m] > 255) {
-                set_error("more than 255 outliers in one row slice");
-                return OJASX_ERR_INVALID;
-            }
+    for (int j = 0; j < nnz; ++j)
+        if (col_indices[j] < 0 || col_indices[j] >= L->K) {
+            set_error("outlier column %d out of range", col_indices[j]);
+            return OJASX_ERR_INVALID;
         }
-    }
-    // Entry order: slice, row, CSR order.  base[s][grp] = first entry of the
-    // 64-row group grp in slice s.
-    const int ngrp = L->Mp / 64;
-    std::vector<uint32_t> start((size_t)L->S * L->Mp);
-    std::vector<uint32_t> base((size_t)L->S * ngrp);
-    uint32_t off = 0;
-    for (int s = 0; s < L->S; ++s)
-        for (int m = 0; m < L->Mp; ++m) {
-            const size_t i = (size_t)s * L->Mp + m;
-            if ((m & 63) == 0) base[(size_t)s * ngrp + (m >> 6)] = off;
-            start[i] = off;
-            off += cnt[i];
-        }
-    std::vector<uint16_t> col((size_t)nnz);
-    std::vector<float> val((size_t)nnz);
-    std::vector<uint8_t> cnt8(cnt.size());
-    for (size_t i = 0; i < cnt.size(); ++i) cnt8[i] = (uint8_t)cnt[i];
-    for (int m = 0; m < L->M; ++m)
-        for (int j = row_ptrs[m]; j < row_ptrs[m + 1]; ++j) {
-            const int c = col_indices[j];
-            const int s = c / slice_cols;
-            const uint32_t at = start[(size_t)s * L->Mp + m]++;
-            col[at] = (uint16_t)(c - s * slice_cols);
-            val[at] = values[j];
-        }
-    int rc = upload(L->ocnt, cnt8.data(), cnt8.size());
-    if (!rc) rc = upload(L->obase, base.data(), base.size() * sizeof(uint32_t));
-    if (!rc) rc = upload(L->ocol, col.data(), col.size() * sizeof(uint16_t));
-    if (!rc) rc = upload(L->oval, val.data(), val.size() * sizeof(float));
+    int rc = upload(L->rowp, row_ptrs, (size_t)(L->M + 1) * sizeof(int));
+    if (!rc) rc = upload(L->col, col_indices, (size_t)nnz * sizeof(int));
+    if (!rc) rc = upload(L->val, values, (size_t)nnz * sizeof(float));
     if (rc) return rc;
     L->nnz = (size_t)nnz;
     return OJASX_OK;
@@ -545,8 +495,7 @@ OJASX_API size_t ojasx_linear_device_weight_bytes(OjasxLinearHandle handle) {
     const Linear *L = static_cast<const Linear *>(handle);
     size_t b = (size_t)L->M * L->G + (size_t)L->Kcb * L->D * 4 + (size_t)L->M * 4;
     if (L->has_bias) b += (size_t)L->M * 4;
-    if (L->nnz)
-        b += L->nnz * 6 + (size_t)L->S * L->M + (size_t)L->S * (L->Mp / 64) * 4;
+    if (L->nnz) b += L->nnz * 8 + (size_t)(L->M + 1) * 4;
     return b;
 }
 

@@ -1,0 +1,146 @@
+"""GPU parity of the top-k MoE path (K4) and the router, through the C-ABI.
+
+Bars: router indices bit-exact (ties to the lower index); router weights
+rel <= 1e-6; MoE outputs rel <= 1e-5 (fp32) / 1e-2 (bf16 activations)
+against the CPU oracle (itself bit-exact with the reference engine).
+"""
+import ctypes
+import os
+
+import numpy as np
+import pytest
+
+from conftest import GOLDEN, rel_err
+from oracle import cpu, gen
+
+pytestmark = pytest.mark.gpu
+
+
+def vp(t):
+    return ctypes.c_void_p(t.data_ptr())
+
+
+def make_native(pkg, m, E, H, I, k=10):
+    nat = pkg.native.NativeSplitManifoldMoE(E, H, I, k, m["cb_in"].shape[1])
+    nat.initialize_weights(m["cb_in"], m["cb_down"], m["gu_codes"], m["gu_scales"],
+                           m["dn_codes"], m["dn_scales"])
+    return nat
+
+
+def test_host_api_golden_skip_rules(pkg):
+    g = np.load(os.path.join(GOLDEN, "moe_e32_h128_i64.npz"))
+    nat = make_native(pkg, g, 32, 128, 64, 6)
+    y = nat.forward(g["x"], g["idx"], g["w"])
+    assert rel_err(y, g["y"]) < 1e-5
+
+
+def test_host_api_reference_t6(pkg):
+    t6 = gen.reference_t6()
+    nat = make_native(pkg, t6, 512, 256, 64)
+    y = nat.forward(t6["x"], t6["idx"], t6["w"])
+    want = np.load(os.path.join(GOLDEN, "ref_t6_moe.npz"))["y"]
+    assert rel_err(y, want) < 1e-5
+
+
+def test_k_active_zero_leaves_output(pkg):
+    g = np.load(os.path.join(GOLDEN, "moe_e32_h128_i64.npz"))
+    nat = make_native(pkg, g, 32, 128, 64, 6)
+    y = np.full(128, 7.0, np.float32)
+    p = lambda a: a.ctypes.data_as(ctypes.c_void_p)
+    x, idx, w = (np.ascontiguousarray(g[n]) for n in ("x", "idx", "w"))
+    assert pkg.lib().ojasx_moe_forward(nat.handle, p(x), p(idx), p(w), p(y), 0) == 0
+    assert np.all(y == 7.0)
+
+
+def route(pkg, logits_t, k, renorm):
+    import torch
+    T, E = logits_t.shape
+    idx = torch.empty(T, k, dtype=torch.int32, device=logits_t.device)
+    w = torch.empty(T, k, dtype=torch.float32, device=logits_t.device)
+    rc = pkg.lib().ojasx_moe_route_device(vp(logits_t), T, E, k, int(renorm), vp(idx), vp(w),
+                                          None)
+    assert rc == 0
+    torch.cuda.synchronize()
+    return idx, w
+
+
+@pytest.mark.parametrize("renorm", [False, True])
+def test_router_bit_exact_indices(pkg, dev, renorm):
+    import torch
+    m = gen.moe(E=512, H=16, I=16, T=16, seed=30)
+    lg = m["logits"].copy()
+    lg[3, [7, 300, 301]] = 5.0                       # ties at the top
+    lg[4, :] = 0.25                                  # all equal
+    idx, w = route(pkg, torch.from_numpy(lg).to(dev), 10, renorm)
+    i_ref, w_ref = cpu.router_topk(lg, 10, renorm)
+    assert np.array_equal(idx.cpu().numpy(), i_ref)
+    assert rel_err(w.cpu().numpy(), w_ref) < 1e-6
+
+
+@pytest.fixture(scope="module")
+def baseline_moe(pkg):
+    m = gen.moe(E=512, H=2048, I=768, T=16, seed=2024, scales="u")
+    nat = make_native(pkg, m, 512, 2048, 768)
+    return m, nat
+
+
+@pytest.mark.parametrize("T", [1, 16])
+def test_baseline_moe_fp32(pkg, dev, baseline_moe, T):
+    import torch
+    m, nat = baseline_moe
+    logits = torch.from_numpy(m["logits"][:T]).to(dev)
+    idx, w = route(pkg, logits, 10, False)
+    x = torch.from_numpy(m["x"][:T]).to(dev)
+    y = torch.empty(T, 2048, device=dev)
+    rc = pkg.lib().ojasx_moe_forward_device(nat.handle, vp(x), vp(idx), vp(w), vp(y), T, 10, 0,
+                                            None)
+    assert rc == 0
+    torch.cuda.synchronize()
+    idx_h, w_h = idx.cpu().numpy(), w.cpu().numpy()
+    i_ref, _ = cpu.router_topk(m["logits"][:T], 10)
+    assert np.array_equal(idx_h, i_ref)
+    for t in range(T):
+        want = cpu.moe_forward(m["x"][t], m["cb_in"], m["cb_down"], m["gu_codes"], m["gu_scales"],
+                               m["dn_codes"], m["dn_scales"], idx_h[t], w_h[t])
+        assert rel_err(y[t].cpu().numpy(), want) < 1e-5, t
+
+
+def test_baseline_moe_bf16(pkg, dev, baseline_moe):
+    import torch
+    m, nat = baseline_moe
+    T = 4
+    idx, w = route(pkg, torch.from_numpy(m["logits"][:T]).to(dev), 10, True)
+    x = torch.from_numpy(m["x"][:T]).to(dev).to(torch.bfloat16)
+    y = torch.empty(T, 2048, device=dev, dtype=torch.bfloat16)
+    rc = pkg.lib().ojasx_moe_forward_device(nat.handle, vp(x), vp(idx), vp(w), vp(y), T, 10, 1,
+                                            None)
+    assert rc == 0
+    torch.cuda.synchronize()
+    xr = x.float().cpu().numpy()
+    for t in range(T):
+        want = cpu.moe_forward(xr[t], m["cb_in"], m["cb_down"], m["gu_codes"], m["gu_scales"],
+                               m["dn_codes"], m["dn_scales"], idx[t].cpu().numpy(),
+                               w[t].cpu().numpy())
+        assert rel_err(y[t].float().cpu().numpy(), want) < 1e-2
+
+
+def test_repeat_deterministic_and_skips(pkg, dev, baseline_moe):
+    """Skipped slots (id out of range, |w| < 1e-8) and repeated experts within a
+    token; repeated calls return identical bits."""
+    import torch
+    m, nat = baseline_moe
+    idx = np.array([[5, 600, 5, 9, -3, 11, 12, 13, 14, 15]], np.int32)
+    w = np.array([[0.2, 0.3, 0.1, 1e-9, 0.1, 0.05, 0.05, 0.05, 0.1, 0.05]], np.float32)
+    it, wt = torch.from_numpy(idx).to(dev), torch.from_numpy(w).to(dev)
+    x = torch.from_numpy(m["x"][:1]).to(dev)
+    ys = []
+    for _ in range(3):
+        y = torch.empty(1, 2048, device=dev)
+        assert pkg.lib().ojasx_moe_forward_device(nat.handle, vp(x), vp(it), vp(wt), vp(y), 1, 10,
+                                                  0, None) == 0
+        torch.cuda.synchronize()
+        ys.append(y.cpu().numpy())
+    want = cpu.moe_forward(m["x"][0], m["cb_in"], m["cb_down"], m["gu_codes"], m["gu_scales"],
+                           m["dn_codes"], m["dn_scales"], idx[0], w[0])
+    assert rel_err(ys[0][0], want) < 1e-5
+    assert all(np.array_equal(ys[0], yy) for yy in ys[1:])
