@@ -15,16 +15,17 @@
 //  K1 lut_build: the LUT of every token, LUT[b][g][k] for all 256 centroids,
 //     into a workspace (workgroup = (1 group, 1 token), thread k owns
 //     centroid k): x and the codebook, then one store.
-//  K2 lut_gather: workgroup = 64 output rows x up to 4 tokens; lane = row, the
-//     4 waves take interleaved 16-group slices.  Round trip 1: a lane reads
-//     its row's 16 codes of each of its slices with one 16-byte load each (a
-//     wave reads 1 KB contiguous from the slice-major tiles [S][Mp][16]),
-//     together with scale, bias, CSR row bounds and x (staged in LDS).  Round
-//     trip 2: the 16 LUT entries per slice and token from the L2-resident
-//     LUT, and -- wave 0 -- the row's CSR outlier entries (32 per batch).
-//     The four wave partials are summed in LDS in wave order and the epilogue
-//     applies scale, bias and the outlier sum in the reference's order:
-//     deterministic results.
+//  K2 lut_gather: workgroup = 32 output rows x 8 slice groups x up to 4
+//     tokens (216 workgroups at 6912 rows: every CU busy; 16- and 64-row
+//     variants measured slower).  Thread (q, r) owns row r and the 16-group
+//     slices q, q+8, ...  Round trip 1: its rows' 16 codes per slice with one
+//     16-byte load each (a wave reads contiguous 512-byte runs of the
+//     slice-major tiles [S][Mp][16]), the CSR row bounds and x (staged in
+//     LDS).  Round trip 2: the 16 LUT entries per slice and token from the
+//     L2-resident LUT and the thread's share of the row's CSR entries.  The
+//     slice-group partials (manifold and outlier sums) are reduced in LDS in
+//     a fixed order and the epilogue applies (s_m * sum + bias) + outliers in
+//     the reference's order: deterministic results.
 #include <algorithm>
 #include <cstring>
 #include <vector>
@@ -38,8 +39,7 @@ constexpr int kNT = 256;        // threads per workgroup (4 waves)
 constexpr int kGS = 16;         // groups per slice: 16 code bytes per row
 constexpr int kRowAlign = 1024; // rows padded for the tile layout
 constexpr int kCB = 256;        // centroids in the (zero-padded) codebook
-constexpr int kRows = 64;       // rows per gather workgroup (one per lane)
-constexpr int kWaves = kNT / 64;
+constexpr int kRows = 32;       // rows per gather workgroup
 constexpr int kOB = 32;         // outlier entries loaded per batch
 constexpr size_t kXLdsBytes = 48 * 1024;  // x staged in LDS up to this size
 }  // namespace
@@ -78,31 +78,38 @@ __global__ __launch_bounds__(kCB) void lut_build_kernel(const T *__restrict__ x,
     lut[((size_t)b * Gp + g) * kCB + k] = dot;
 }
 
-// K2 + K3: gather-accumulate, outliers and epilogue, one row per lane.
-// Loads are issued branch-free (clamped indices, results masked at use) so
-// the compiler can keep them all in flight: round trip 1 = codes, scale,
-// bias, CSR row bounds, x; round trip 2 = LUT entries and outlier entries.
-template <int BT, typename T>
+// K2 + K3: gather-accumulate, outliers and epilogue.  Workgroup = R rows x
+// QG = 256/R slice groups: thread (q, r) owns row r and slices q, q+QG, ...;
+// a wave holds two (or more) slice groups of consecutive rows, so its code
+// loads are contiguous 16-byte rows.  A row's CSR entries are split over its
+// QG threads (entry j0 + q + QG*u).  Loads are branch-free (clamped indices,
+// results masked at use) so each thread's loads of a round trip are all in
+// flight together; partial sums are reduced over the slice groups in LDS in
+// a fixed order.
+template <int R, int BT, typename T>
 __global__ __launch_bounds__(kNT) void lut_gather_kernel(GatherParams p) {
-    extern __shared__ float xs[];                 // [BT][K] when p.x_lds
-    __shared__ float red[kWaves][BT][kRows];
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    const int m = blockIdx.x * kRows + lane;      // < Mp: codes need no clamp
-    const int mr = min(m, p.M - 1);               // clamped row for [M] arrays
+    constexpr int QG = kNT / R;
+    constexpr int NSB = 2;                // slices per thread per batch
+    constexpr int NU = (kOB + QG - 1) / QG;  // outlier entries per thread in batch 1
+    extern __shared__ float xs[];         // [BT][K] when p.x_lds
+    __shared__ float red[2][QG][BT][R];
+    const int tid = threadIdx.x;
+    const int r = tid % R, q = tid / R;
+    const int m = blockIdx.x * R + r;     // < Mp: codes need no clamp
+    const int mr = min(m, p.M - 1);
     const int t0 = blockIdx.y * BT;
     const int nt = min(BT, p.B - t0);
     const bool outl = p.rowp != nullptr;
     const T *__restrict__ x = static_cast<const T *>(p.x);
+    const int nsq = q < p.S ? (p.S - 1 - q) / QG + 1 : 0;   // slices of this thread
 
-    // ---- round trip 1
-    uint4 cv[4];
+    // ---- round trip 1: codes of the first batch, row bounds, x
+    uint4 cv[NSB];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int s = min(w + i * kWaves, p.S - 1);
+    for (int i = 0; i < NSB; ++i) {
+        const int s = min(q + QG * i, p.S - 1);
         cv[i] = *reinterpret_cast<const uint4 *>(p.codes + ((size_t)s * p.Mp + m) * kGS);
     }
-    const float sc = p.scales[mr];
-    const float bs = p.bias ? p.bias[mr] : 0.f;
     int j0 = 0, j1 = 0;
     if (outl) {
         j0 = p.rowp[mr];
@@ -110,13 +117,13 @@ __global__ __launch_bounds__(kNT) void lut_gather_kernel(GatherParams p) {
     }
     if (outl && p.x_lds) stage_to_lds<kNT>(xs, x + (size_t)t0 * p.K, nt * p.K);
 
-    // ---- round trip 2: first batch of outlier entries, LUT entries
-    int oc[kOB];
-    float ov[kOB];
+    // ---- round trip 2: outlier entries of this thread, LUT entries
+    int oc[NU];
+    float ov[NU];
     if (outl) {
 #pragma unroll
-        for (int u = 0; u < kOB; ++u) {
-            const int j = min(j0 + u, p.nnz - 1);
+        for (int u = 0; u < NU; ++u) {
+            const int j = min(j0 + q + QG * u, p.nnz - 1);
             oc[u] = p.col[j];
             ov[u] = p.val[j];
         }
@@ -124,69 +131,61 @@ __global__ __launch_bounds__(kNT) void lut_gather_kernel(GatherParams p) {
     float acc[BT];
 #pragma unroll
     for (int t = 0; t < BT; ++t) acc[t] = 0.f;
-    for (int s0 = w;; s0 += kWaves * 4) {
-        // (token, slice) pairs, 4 at a time: 64 LUT loads in flight, then the
-        // adds (per token, slices ascending).
+    for (int i0 = 0; i0 < nsq; i0 += NSB) {
+        float lv[NSB][BT][kGS];
 #pragma unroll
-        for (int q0 = 0; q0 < BT * 4; q0 += 4) {
-            float lv[4][kGS];
+        for (int i = 0; i < NSB; ++i) {
+            const int s = min(q + QG * (i0 + i), p.S - 1);
+            const uint32_t w4[4] = {cv[i].x, cv[i].y, cv[i].z, cv[i].w};
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const int t = (q0 + q) >> 2, i = (q0 + q) & 3;
-                const int s = min(s0 + i * kWaves, p.S - 1);
+            for (int t = 0; t < BT; ++t) {
                 const int tt = min(t, nt - 1);
                 const float *L = p.lut + ((size_t)(t0 + tt) * p.Gp + s * kGS) * kCB;
-                const uint32_t w4[4] = {cv[i].x, cv[i].y, cv[i].z, cv[i].w};
 #pragma unroll
                 for (int g = 0; g < kGS; ++g)
-                    lv[q][g] = L[g * kCB + ((w4[g >> 2] >> ((g & 3) * 8)) & 0xffu)];
+                    lv[i][t][g] = L[g * kCB + ((w4[g >> 2] >> ((g & 3) * 8)) & 0xffu)];
             }
+        }
+        if (i0 + NSB < nsq) {  // next batch of codes
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const int t = (q0 + q) >> 2, i = (q0 + q) & 3;
-                if (s0 + i * kWaves < p.S) {
+            for (int i = 0; i < NSB; ++i) {
+                const int s = min(q + QG * (i0 + NSB + i), p.S - 1);
+                cv[i] = *reinterpret_cast<const uint4 *>(p.codes + ((size_t)s * p.Mp + m) * kGS);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < NSB; ++i) {
+            if (i0 + i < nsq) {
+#pragma unroll
+                for (int t = 0; t < BT; ++t) {
                     float a = acc[t];
 #pragma unroll
-                    for (int g = 0; g < kGS; ++g) a += lv[q][g];
+                    for (int g = 0; g < kGS; ++g) a += lv[i][t][g];
                     acc[t] = a;
                 }
             }
         }
-        const int nx = s0 + kWaves * 4;
-        if (nx >= p.S) break;
-        // further slices (K > 64 groups * 4 waves): next batch of codes
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int s = min(nx + i * kWaves, p.S - 1);
-            cv[i] = *reinterpret_cast<const uint4 *>(p.codes + ((size_t)s * p.Mp + m) * kGS);
-        }
     }
-#pragma unroll
-    for (int t = 0; t < BT; ++t) red[w][t][lane] = acc[t];
-    __syncthreads();
-    if (w != 0 || m >= p.M) return;
-
-    // Outliers in CSR order (x from LDS when staged).
-    // First batch branch-free: entries past the row's end add an exact 0.
     float oac[BT];
 #pragma unroll
     for (int t = 0; t < BT; ++t) oac[t] = 0.f;
     if (outl) {
+        if (p.x_lds) __syncthreads();
         const int n0 = j1 - j0;
 #pragma unroll
         for (int t = 0; t < BT; ++t) {
             const int tt = min(t, nt - 1);
-            float xv[kOB];
-#pragma unroll
-            for (int u = 0; u < kOB; ++u)
-                xv[u] = p.x_lds ? xs[tt * p.K + oc[u]] : load_act(x, (size_t)(t0 + tt) * p.K + oc[u]);
             float o = 0.f;
 #pragma unroll
-            for (int u = 0; u < kOB; ++u) o += u < n0 ? ov[u] * xv[u] : 0.f;
+            for (int u = 0; u < NU; ++u) {
+                const float xv = p.x_lds ? xs[tt * p.K + oc[u]]
+                                         : load_act(x, (size_t)(t0 + tt) * p.K + oc[u]);
+                o += q + QG * u < n0 ? ov[u] * xv : 0.f;
+            }
             oac[t] = o;
         }
-        // rows with more than kOB outliers (rare): the rest in CSR order
-        for (int j = j0 + kOB; j < j1; ++j) {
+        // entries beyond the first QG*NU of a row (rare)
+        for (int j = j0 + q + QG * NU; j < j1; j += QG) {
             const int c = p.col[j];
             const float v = p.val[j];
 #pragma unroll
@@ -195,17 +194,29 @@ __global__ __launch_bounds__(kNT) void lut_gather_kernel(GatherParams p) {
                     oac[t] += v * (p.x_lds ? xs[t * p.K + c] : load_act(x, (size_t)(t0 + t) * p.K + c));
         }
     }
+#pragma unroll
+    for (int t = 0; t < BT; ++t) {
+        red[0][q][t][r] = acc[t];
+        red[1][q][t][r] = oac[t];
+    }
+    __syncthreads();
+    if (q != 0 || m >= p.M) return;
+    const float sc = p.scales[m];
+    const float bs = p.bias ? p.bias[m] : 0.f;
     T *y = static_cast<T *>(p.y);
 #pragma unroll
     for (int t = 0; t < BT; ++t) {
         if (t >= nt) break;
-        float a = red[0][t][lane];
+        float a = red[0][0][t][r], o = red[1][0][t][r];
 #pragma unroll
-        for (int q = 1; q < kWaves; ++q) a += red[q][t][lane];
-        float r = a * sc;
-        if (p.bias) r += bs;
-        r += oac[t];
-        store_act(y, (size_t)(t0 + t) * p.M + m, r);
+        for (int k = 1; k < QG; ++k) {
+            a += red[0][k][t][r];
+            o += red[1][k][t][r];
+        }
+        float v = a * sc;
+        if (p.bias) v += bs;
+        v += o;
+        store_act(y, (size_t)(t0 + t) * p.M + m, v);
     }
 }
 
@@ -242,11 +253,14 @@ struct Linear {
 namespace {
 
 template <int BT, typename T>
-int launch_gather(const GatherParams &gp, dim3 grid, size_t lds, hipStream_t st) {
+int launch_gather(const GatherParams &gp, int M, dim3 grid_y, size_t lds, hipStream_t st) {
+    constexpr int R = kRows;
     static size_t granted = 0;
-    int rc = ensure_dyn_lds(reinterpret_cast<const void *>(&lut_gather_kernel<BT, T>), lds, &granted);
+    const void *fn = reinterpret_cast<const void *>(&lut_gather_kernel<R, BT, T>);
+    int rc = ensure_dyn_lds(fn, lds, &granted);
     if (rc) return rc;
-    hipLaunchKernelGGL((lut_gather_kernel<BT, T>), grid, dim3(kNT), lds, st, gp);
+    dim3 grid((M + R - 1) / R, grid_y.y);
+    hipLaunchKernelGGL((lut_gather_kernel<R, BT, T>), grid, dim3(kNT), lds, st, gp);
     return OJASX_OK;
 }
 
@@ -284,12 +298,12 @@ int launch(Linear *L, const void *x, void *y, int B, hipStream_t st) {
     const size_t xbytes = (size_t)bt * L->K * sizeof(float);
     gp.x_lds = L->nnz && xbytes <= kXLdsBytes;
     const size_t lds = gp.x_lds ? xbytes : 0;
-    dim3 g2((L->M + kRows - 1) / kRows, (B + bt - 1) / bt);
+    dim3 g2(1, (B + bt - 1) / bt);
     int rc;
     switch (bt) {
-        case 1: rc = launch_gather<1, T>(gp, g2, lds, st); break;
-        case 2: rc = launch_gather<2, T>(gp, g2, lds, st); break;
-        default: rc = launch_gather<4, T>(gp, g2, lds, st); break;
+        case 1: rc = launch_gather<1, T>(gp, L->M, g2, lds, st); break;
+        case 2: rc = launch_gather<2, T>(gp, L->M, g2, lds, st); break;
+        default: rc = launch_gather<4, T>(gp, L->M, g2, lds, st); break;
     }
     if (rc) return rc;
     OJX_HIP(hipGetLastError());
