@@ -40,6 +40,7 @@ def parse():
     ap.add_argument("--instances", type=int, default=160)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-extra", action="store_true", help="skip the MoE and KV figures")
     return ap.parse_args()
 
 
@@ -67,6 +68,115 @@ def time_cpu_linear(d, seconds):
     return dict(value=el / n * 1e6, unit="us/call", cores=1, kind=kind,
                 sample=f"{n} calls of LUT-GEMV 2560->6912 B=1 fp32 with CSR, 1 thread, "
                        f"after 50 warm-up calls")
+
+
+def bench_moe(pkg, torch, steps, warmup, cpu_seconds, do_cpu):
+    """512-expert top-10 MoE layer (H 2048, I 768), T = 1 and 16 tokens.  Two
+    expert banks (2 x 151 MB, above the 256 MB Infinity Cache) alternate and
+    every step has its own routing, so routed experts' codes come from HBM."""
+    from oracle import gen, ref
+    L = pkg.lib()
+    vp = ctypes.c_void_p
+    p = lambda a: a.ctypes.data_as(vp)
+    E, H, I, K = 512, 2048, 768, 10
+    banks = []
+    for seed in (11, 12):
+        m = gen.moe(E=E, H=H, I=I, T=16, seed=seed)
+        h = L.ojasx_create_moe(E, H, I, K, 16, p(m["cb_in"]), p(m["cb_down"]), p(m["gu_codes"]),
+                               p(m["gu_scales"]), p(m["dn_codes"]), p(m["dn_scales"]))
+        assert h, L.ojasx_get_last_error()
+        banks.append((h, m))
+    dev = torch.device("cuda:0")
+    st = torch.cuda.current_stream()
+    sp = vp(st.cuda_stream)
+    res = {}
+    per_expert = 2 * I * (H // 16) + H * (I // 16)
+    for T in (1, 16):
+        nsteps = steps
+        r = np.random.default_rng(T)
+        logits = torch.from_numpy(r.normal(size=(nsteps, T, E)).astype(np.float32)).to(dev)
+        idx = torch.empty(nsteps, T, K, dtype=torch.int32, device=dev)
+        w = torch.empty(nsteps, T, K, dtype=torch.float32, device=dev)
+        for i in range(nsteps):
+            assert L.ojasx_moe_route_device(vp(logits[i].data_ptr()), T, E, K, 0,
+                                            vp(idx[i].data_ptr()), vp(w[i].data_ptr()), sp) == 0
+        torch.cuda.synchronize()
+        distinct = np.array([len(np.unique(a)) for a in idx.cpu().numpy().reshape(nsteps, -1)])
+        x = torch.from_numpy(banks[0][1]["x"][:T]).to(dev)
+        y = torch.empty(T, H, device=dev)
+        fwd = lambda i: L.ojasx_moe_forward_device(banks[i % 2][0], vp(x.data_ptr()),
+                                                   vp(idx[i].data_ptr()), vp(w[i].data_ptr()),
+                                                   vp(y.data_ptr()), T, K, 0, sp)
+        for i in range(min(warmup, nsteps)):
+            fwd(i)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(st)
+        for i in range(nsteps):
+            fwd(i)
+        e1.record(st)
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / nsteps
+        code_bytes = float(distinct.mean()) * per_expert
+        res[f"T{T}"] = {"us_per_call": round(us, 3), "distinct_experts_mean": float(distinct.mean()),
+                        "code_bytes_per_call": int(code_bytes),
+                        "achieved_GBs": round(code_bytes / (us * 1e-6) / 1e9, 2),
+                        "frac_of_8TBs": round(code_bytes / (us * 1e-6) / 8e12, 5)}
+    if do_cpu and ref.available():
+        m = banks[0][1]
+        R = ref.RefMoE(m["cb_in"], m["cb_down"], m["gu_codes"], m["gu_scales"], m["dn_codes"],
+                       m["dn_scales"])
+        ii = idx[0, 0].cpu().numpy()
+        ww = w[0, 0].cpu().numpy()
+        for _ in range(3):
+            R.forward(m["x"][0], ii, ww)
+        n, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < cpu_seconds and n < 100:
+            R.forward(m["x"][0], ii, ww)
+            n += 1
+        res["cpu_reference_T1_us"] = round((time.perf_counter() - t0) / n * 1e6, 2)
+        res["cpu_reference_sample"] = f"{n} single-token calls, 1 thread (reference engine)"
+    for h, _ in banks:
+        L.ojasx_destroy_moe(h)
+    return res
+
+
+def bench_kv(pkg, torch, steps):
+    """Paged code-domain decode: 8 kv / 32 q heads, head_dim 128, page 16."""
+    from oracle import gen
+    L = pkg.lib()
+    vp = ctypes.c_void_p
+    dev = torch.device("cuda:0")
+    st = torch.cuda.current_stream()
+    res = {}
+    for T in (2048, 32768):
+        d = gen.kv(H_kv=8, H_q=32, T=T, seed=5, shuffle_pages=True)
+        t = {k: torch.from_numpy(np.ascontiguousarray(d[k])).to(dev)
+             for k in ("q", "k_codes", "k_scales", "v_codes", "v_scales", "k_cb", "v_cb",
+                       "block_table")}
+        out = torch.empty(32, 128, device=dev)
+        call = lambda: L.ojasx_kv_decode_paged_device(
+            vp(t["q"].data_ptr()), vp(t["k_codes"].data_ptr()), vp(t["k_scales"].data_ptr()),
+            vp(t["v_codes"].data_ptr()), vp(t["v_scales"].data_ptr()), vp(t["k_cb"].data_ptr()),
+            vp(t["v_cb"].data_ptr()), vp(t["block_table"].data_ptr()), T, 16, 32, 8, 128, 16,
+            -1.0, vp(out.data_ptr()), vp(st.cuda_stream))
+        for _ in range(20):
+            call()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        n = max(50, steps // 4)
+        e0.record(st)
+        for _ in range(n):
+            call()
+        e1.record(st)
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / n
+        code_bytes = 2 * T * 8 * 8
+        all_bytes = code_bytes + 2 * T * 8 * 4
+        res[f"T{T}"] = {"us_per_call": round(us, 3), "code_bytes": code_bytes,
+                        "achieved_code_GBs": round(code_bytes / (us * 1e-6) / 1e9, 2),
+                        "achieved_all_GBs": round(all_bytes / (us * 1e-6) / 1e9, 2)}
+    return res
 
 
 def main():
@@ -162,6 +272,10 @@ def main():
         out["cpu_baseline"] = time_cpu_linear(base, args.cpu_seconds)
     for h in handles:
         L.ojasx_destroy_linear(h)
+    if not args.no_extra:
+        out["moe_512x_top10"] = bench_moe(pkg, torch, min(args.steps, 400), args.warmup,
+                                          args.cpu_seconds / 2, not args.no_cpu)
+        out["kv_decode_gqa4"] = bench_kv(pkg, torch, args.steps)
     print(json.dumps(out))
 
 

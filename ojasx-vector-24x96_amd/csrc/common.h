@@ -36,6 +36,11 @@ struct DevBuf {
 
 int upload(DevBuf &buf, const void *host, size_t n);  // ensure + memcpy
 
+// LUT[b][g][k] = <x_b[gD:(g+1)D], C[k]> for g < Gp (0 for g >= G) and all 256
+// centroids of the zero-padded codebook cb [256][D]; x [B][K] in dtype.
+int launch_lut_build(const void *x, const float *cb, int B, int K, int D, int G, int Gp,
+                     float *lut, int dtype, hipStream_t st);
+
 inline size_t round_up(size_t v, size_t m) { return (v + m - 1) / m * m; }
 
 // Raise a kernel's dynamic-LDS limit when a launch needs more than the 64 KB
@@ -64,9 +69,8 @@ __device__ __forceinline__ void store_act(__hip_bfloat16 *p, size_t i, float v) 
 // one memory round trip for up to NT*4*16 elements (fp32 rows use 16-byte
 // loads when 16-byte aligned).  Runtime-trip-count copy loops otherwise
 // serialise one round trip per element a thread copies.
-template <int NT>
+template <int NT, int U = 16>
 __device__ __forceinline__ void stage_to_lds(float *dst, const float *src, int n) {
-    constexpr int U = 16;
     if (((reinterpret_cast<uintptr_t>(src) & 15) == 0) && (n & 3) == 0) {
         const float4 *s4 = reinterpret_cast<const float4 *>(src);
         const int n4 = n >> 2;
@@ -88,9 +92,8 @@ __device__ __forceinline__ void stage_to_lds(float *dst, const float *src, int n
     }
 }
 
-template <int NT>
+template <int NT, int U = 16>
 __device__ __forceinline__ void stage_to_lds(float *dst, const __hip_bfloat16 *src, int n) {
-    constexpr int U = 16;
     for (int b = threadIdx.x; b < n; b += NT * U) {
         float v[U];
 #pragma unroll

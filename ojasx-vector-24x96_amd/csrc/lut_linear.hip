@@ -333,6 +333,23 @@ int linear_forward(void *h, const void *x, void *y, int B, int dtype, hipStream_
     return forward(static_cast<Linear *>(h), x, y, B, dtype, st);
 }
 
+int launch_lut_build(const void *x, const float *cb, int B, int K, int D, int G, int Gp,
+                     float *lut, int dtype, hipStream_t st) {
+    dim3 g(Gp, B);
+    const bool d16 = D == 16;
+    if (dtype == OJASX_DTYPE_F32) {
+        const float *xf = static_cast<const float *>(x);
+        if (d16) hipLaunchKernelGGL((lut_build_kernel<16, float>), g, dim3(kCB), 0, st, xf, cb, K, D, G, Gp, lut);
+        else hipLaunchKernelGGL((lut_build_kernel<0, float>), g, dim3(kCB), 0, st, xf, cb, K, D, G, Gp, lut);
+    } else {
+        const __hip_bfloat16 *xb = static_cast<const __hip_bfloat16 *>(x);
+        if (d16) hipLaunchKernelGGL((lut_build_kernel<16, __hip_bfloat16>), g, dim3(kCB), 0, st, xb, cb, K, D, G, Gp, lut);
+        else hipLaunchKernelGGL((lut_build_kernel<0, __hip_bfloat16>), g, dim3(kCB), 0, st, xb, cb, K, D, G, Gp, lut);
+    }
+    OJX_HIP(hipGetLastError());
+    return OJASX_OK;
+}
+
 }  // namespace ojx
 using ojx::Linear;
 

@@ -4,24 +4,25 @@
 //   gate_i = sg_e[i]   * sum_g LUT_in[g, gu_codes[e][i][g]]
 //   up_i   = sg_e[I+i] * sum_g LUT_in[g, gu_codes[e][I+i][g]]
 //   inter_i = silu(gate_i) * up_i,             silu(v) = v / (1 + exp(-v))
-//   y[t][h] += w * sd_e[h] * sum_g LUT_down[g, dn_codes[e][h][g]]   (j ascending)
+//   y[t][h] = sum_j w * (sd_e[h] * sum_g LUT_down[g, dn_codes[e][h][g]])   (j ascending)
 // the computation of split_manifold_lut_experiment/native/src/
 // ojasx_lut_cpu.cpp:213-365, including its skip rule (:284-286: e outside
 // [0,E) or |w| < 1e-8 contributes nothing) and output rule (:220-223: y is
 // zeroed when k_active > 0, untouched otherwise).  Only routed experts' codes
 // are ever read.
 //
-// Kernels (one stream, four launches per call):
-//  1. moe_gateup: workgroup = (pair, run of 16-group slices of H).  Builds the
-//     token's LUT_in slice in LDS, gathers gate row i and up row i for
-//     i = tid + 256*j in the same thread; partial sums go to the workspace
-//     and the last workgroup of the pair (ticket) reduces them in slice
-//     order and applies scales and SwiGLU -> inter[pair][I] (fp32).
-//  2. moe_down: workgroup = (pair, 16-group slice of I, row block of H).
-//     Builds LUT_down for the slice from inter, gathers, writes unscaled
-//     partials [pair][slice][H].
-//  3. moe_combine: y[t][h] = sum_j w_j * (sd_e[h] * sum_s partial[s]) in
-//     slot order -- a fixed order, so results are deterministic.
+// Four launches per call, no cross-workgroup synchronisation inside a kernel
+// (a "pair" is one routed (token, slot)):
+//  1. LUT_in of every token (the linear layer's LUT-build kernel).
+//  2. moe_gateup: workgroup = (pair, 32 intermediate rows) x 8 slice groups;
+//     thread (q, r) gathers gate row i and up row i for its slices, the slice
+//     partials are reduced in LDS in a fixed order, then SwiGLU gives 32
+//     intermediate values -- two 16-wide groups -- from which the same
+//     workgroup builds those groups' LUT_down rows (256 centroids each).
+//  3. moe_down: workgroup = (pair, 64 hidden rows) x 4 slice groups: gather
+//     from the pair's LUT_down, reduce, scale -> per-pair output [P][H].
+//  4. moe_combine: y[t][h] = sum_j w_j * out[t,j][h] in slot order -- a fixed
+//     order, so results are deterministic.
 //  Router: moe_route, one workgroup per token.
 #include <algorithm>
 #include <cstring>
@@ -35,18 +36,20 @@ namespace {
 constexpr int kNT = 256;
 constexpr int kGS = 16;
 constexpr int kCB = 256;
-constexpr int kMaxJ = 4;  // I <= 1024 (gate/up rows per thread)
+constexpr int kRowAlign = 256;
+constexpr int kRG = 32;   // intermediate rows per gate/up workgroup
+constexpr int kRD = 64;   // hidden rows per down workgroup
 }  // namespace
 
 struct MoE {
     int E = 0, H = 0, I = 0, top_k = 0, D = 0;
     int Gin = 0, Gi = 0, Sin = 0, Si = 0, Ip = 0, Hp = 0;
     DevBuf cb_in, cb_dn, gu, dn, gus, dns;
-    DevBuf part1, ctr, inter, part2, xstage, ystage, istage, wstage;
-    size_t ctr_n = 0;
+    DevBuf lut_in, lut_dn, dout, xstage, ystage, istage, wstage;
+    size_t lut_dn_pairs = 0;
     ~MoE() {
-        for (DevBuf *b : {&cb_in, &cb_dn, &gu, &dn, &gus, &dns, &part1, &ctr, &inter, &part2,
-                          &xstage, &ystage, &istage, &wstage})
+        for (DevBuf *b : {&cb_in, &cb_dn, &gu, &dn, &gus, &dns, &lut_in, &lut_dn, &dout, &xstage,
+                          &ystage, &istage, &wstage})
             b->release();
     }
 };
@@ -56,17 +59,14 @@ struct MoEParams {
     const uint8_t *dn;      // [E][Si][Hp][16]
     const float *gus;       // [E][2I]
     const float *dns;       // [E][H]
-    const float *cb_in;     // [256][D]
     const float *cb_dn;     // [256][D]
-    const void *x;          // [T][H]
+    const float *lut_in;    // [T][Sin*16][256]
+    float *lut_dn;          // [P][Si*16][256]
+    float *dout;            // [P][H]
     const int *idx;         // [T][k]
     const float *w;         // [T][k]
     void *y;                // [T][H]
-    float *part1;           // [P][n_split1][2][Ip]
-    unsigned *ctr;          // [P]
-    float *inter;           // [P][I]
-    float *part2;           // [P][Si][Hp]
-    int E, H, I, D, Sin, Si, Ip, Hp, T, k, spw1, n_split1, rpb2;
+    int E, H, I, D, Sin, Si, Ip, Hp, T, k;
 };
 
 __device__ __forceinline__ bool pair_active(const MoEParams &p, int pr, int *e_out) {
@@ -76,297 +76,254 @@ __device__ __forceinline__ bool pair_active(const MoEParams &p, int pr, int *e_o
     return e >= 0 && e < p.E && fabsf(w) >= 1e-8f;
 }
 
-// LUT[g][k = tid] for 16 groups from xs[16*D] (LDS) and centroid k in registers.
-template <int DMAX>
-__device__ __forceinline__ void build_slice(const float *xs, const float *cb, int D, float *lut) {
-    const int tid = threadIdx.x;
-#pragma unroll 4
-    for (int g = 0; g < kGS; ++g) {
-        const float *xg = xs + g * D;
-        float dot = 0.f;
-#pragma unroll
-        for (int d = 0; d < DMAX; ++d)
-            if (d < D) dot = fmaf(xg[d], cb[d], dot);
-        lut[g * kCB + tid] = dot;
-    }
+__device__ __forceinline__ uint4 ld_codes(const uint8_t *p) {
+    return *reinterpret_cast<const uint4 *>(p);
 }
 
-__device__ __forceinline__ float gather16(const float *lut, uint4 c) {
+// Sum of the 16 LUT entries selected by 16 codes from 16 consecutive LUT rows.
+__device__ __forceinline__ float gather16(const float *__restrict__ L, uint4 c) {
     const uint32_t w4[4] = {c.x, c.y, c.z, c.w};
+    float v[kGS];
+#pragma unroll
+    for (int g = 0; g < kGS; ++g) v[g] = L[g * kCB + ((w4[g >> 2] >> ((g & 3) * 8)) & 0xffu)];
     float a = 0.f;
 #pragma unroll
-    for (int g = 0; g < kGS; ++g) a += lut[g * kCB + ((w4[g >> 2] >> ((g & 3) * 8)) & 0xffu)];
+    for (int g = 0; g < kGS; ++g) a += v[g];
     return a;
 }
 
-template <int DT, typename T>
+template <int DT>
 __global__ __launch_bounds__(kNT) void moe_gateup_kernel(MoEParams p) {
-    constexpr int DMAX = DT > 0 ? DT : 32;
-    const int D = DT > 0 ? DT : p.D;
-    const int sc = kGS * D;
-    __shared__ float lut[kGS * kCB];
-    __shared__ float xs[kGS * 32];
-    __shared__ int s_last;
+    constexpr int QG = kNT / kRG;  // 8 slice groups
+    __shared__ float red[2][QG][kRG];
+    __shared__ float inter_s[kRG];
     const int tid = threadIdx.x;
-    const int pr = blockIdx.x / p.n_split1;
-    const int sp = blockIdx.x - pr * p.n_split1;
+    const int r = tid % kRG, q = tid / kRG;
+    const int nrb = (p.I + kRG - 1) / kRG;
+    const int pr = blockIdx.x / nrb;
+    const int rb = blockIdx.x - pr * nrb;
     int e;
     if (!pair_active(p, pr, &e)) return;
     const int t = pr / p.k;
-    const T *x = static_cast<const T *>(p.x);
-    const int nj = (p.I + kNT - 1) / kNT;
-
-    float cb[DMAX];
-#pragma unroll
-    for (int d = 0; d < DMAX; ++d) cb[d] = (d < D) ? p.cb_in[tid * D + d] : 0.f;
-    float ag[kMaxJ], au[kMaxJ];
-#pragma unroll
-    for (int j = 0; j < kMaxJ; ++j) ag[j] = au[j] = 0.f;
-
-    const int s0 = sp * p.spw1, s1 = min(p.Sin, s0 + p.spw1);
+    const int i = rb * kRG + r;                   // < Ip (multiple of 256)
     const uint8_t *eg = p.gu + (size_t)e * p.Sin * 2 * p.Ip * kGS;
-    for (int s = s0; s < s1; ++s) {
-        uint4 cg[kMaxJ], cu[kMaxJ];
-        const uint8_t *gs = eg + (size_t)s * 2 * p.Ip * kGS;
-#pragma unroll
-        for (int j = 0; j < kMaxJ; ++j)
-            if (j < nj) {
-                const int i = j * kNT + tid;
-                cg[j] = *reinterpret_cast<const uint4 *>(gs + (size_t)i * kGS);
-                cu[j] = *reinterpret_cast<const uint4 *>(gs + ((size_t)p.Ip + i) * kGS);
-            }
-        for (int i = tid; i < sc; i += kNT) {
-            const int col = s * sc + i;
-            xs[i] = col < p.H ? load_act(x, (size_t)t * p.H + col) : 0.f;
-        }
-        __syncthreads();
-        build_slice<DMAX>(xs, cb, D, lut);
-        __syncthreads();
-#pragma unroll
-        for (int j = 0; j < kMaxJ; ++j)
-            if (j < nj) {
-                ag[j] += gather16(lut, cg[j]);
-                au[j] += gather16(lut, cu[j]);
-            }
-        __syncthreads();
-    }
+    const float *L = p.lut_in + (size_t)t * p.Sin * kGS * kCB;
 
-    const float *gsc = p.gus + (size_t)e * 2 * p.I;
-    if (p.n_split1 == 1) {
-#pragma unroll
-        for (int j = 0; j < kMaxJ; ++j) {
-            const int i = j * kNT + tid;
-            if (j < nj && i < p.I) {
-                const float g = ag[j] * gsc[i], u = au[j] * gsc[p.I + i];
-                p.inter[(size_t)pr * p.I + i] = g / (1.f + expf(-g)) * u;
-            }
-        }
-        return;
+    float ag = 0.f, au = 0.f;
+    for (int s = q; s < p.Sin; s += QG) {  // one step when Sin <= 8 (H <= 2048 at D = 16)
+        const uint4 cg = ld_codes(eg + (((size_t)s * 2 + 0) * p.Ip + i) * kGS);
+        const uint4 cu = ld_codes(eg + (((size_t)s * 2 + 1) * p.Ip + i) * kGS);
+        ag += gather16(L + (size_t)s * kGS * kCB, cg);
+        au += gather16(L + (size_t)s * kGS * kCB, cu);
     }
-    float *pp = p.part1 + ((size_t)pr * p.n_split1 + sp) * 2 * p.Ip;
-#pragma unroll
-    for (int j = 0; j < kMaxJ; ++j)
-        if (j < nj) {
-            const int i = j * kNT + tid;
-            pp[i] = ag[j];
-            pp[p.Ip + i] = au[j];
-        }
-    __threadfence();
+    red[0][q][r] = ag;
+    red[1][q][r] = au;
     __syncthreads();
-    if (tid == 0) {
-        const unsigned old = atomicAdd(p.ctr + pr, 1u);
-        s_last = (old == (unsigned)(p.n_split1 - 1));
-        if (s_last) atomicExch(p.ctr + pr, 0u);
+    if (q == 0) {
+        float g = red[0][0][r], u = red[1][0][r];
+#pragma unroll
+        for (int k = 1; k < QG; ++k) {
+            g += red[0][k][r];
+            u += red[1][k][r];
+        }
+        float v = 0.f;
+        if (i < p.I) {
+            g *= p.gus[(size_t)e * 2 * p.I + i];
+            u *= p.gus[(size_t)e * 2 * p.I + p.I + i];
+            v = g / (1.f + expf(-g)) * u;
+        }
+        inter_s[r] = v;
     }
     __syncthreads();
-    if (!s_last) return;
-    __threadfence();
-    const float *pb = p.part1 + (size_t)pr * p.n_split1 * 2 * p.Ip;
+    // LUT_down rows of the kRG / D groups this workgroup produced.
+    constexpr int DMAX = DT > 0 ? DT : 32;
+    const int D = DT > 0 ? DT : p.D;
+    const int ng = kRG / D;
+    const int g0 = rb * ng;
+    float c[DMAX];
 #pragma unroll
-    for (int j = 0; j < kMaxJ; ++j) {
-        const int i = j * kNT + tid;
-        if (j < nj && i < p.I) {
-            float g = 0.f, u = 0.f;
-            for (int q = 0; q < p.n_split1; ++q) {
-                g += pb[(size_t)q * 2 * p.Ip + i];
-                u += pb[(size_t)q * 2 * p.Ip + p.Ip + i];
-            }
-            g *= gsc[i];
-            u *= gsc[p.I + i];
-            p.inter[(size_t)pr * p.I + i] = g / (1.f + expf(-g)) * u;
-        }
+    for (int d = 0; d < DMAX; ++d) c[d] = d < D ? p.cb_dn[tid * D + d] : 0.f;
+    float *Ld = p.lut_dn + (size_t)pr * p.Si * kGS * kCB;
+    for (int gl = 0; gl < ng; ++gl) {
+        const int g = g0 + gl;
+        if (g * D >= p.I) break;
+        float dot = 0.f;
+#pragma unroll
+        for (int d = 0; d < DMAX; ++d)
+            if (d < D) dot = fmaf(inter_s[gl * D + d], c[d], dot);
+        Ld[(size_t)g * kCB + tid] = dot;
     }
 }
 
-template <int DT>
 __global__ __launch_bounds__(kNT) void moe_down_kernel(MoEParams p) {
-    constexpr int DMAX = DT > 0 ? DT : 32;
-    const int D = DT > 0 ? DT : p.D;
-    const int sc = kGS * D;
-    __shared__ float lut[kGS * kCB];
-    __shared__ float xs[kGS * 32];
+    constexpr int QG = kNT / kRD;  // 4 slice groups
+    __shared__ float red[QG][kRD];
     const int tid = threadIdx.x;
-    const int n_rb = (p.H + kNT * p.rpb2 - 1) / (kNT * p.rpb2);
-    int b = blockIdx.x;
-    const int rb = b % n_rb;
-    b /= n_rb;
-    const int s = b % p.Si;
-    const int pr = b / p.Si;
+    const int r = tid % kRD, q = tid / kRD;
+    const int nrb = (p.H + kRD - 1) / kRD;
+    const int pr = blockIdx.x / nrb;
+    const int rb = blockIdx.x - pr * nrb;
     int e;
     if (!pair_active(p, pr, &e)) return;
-
-    float cb[DMAX];
+    const int h = rb * kRD + r;                   // < Hp
+    const uint8_t *ed = p.dn + (size_t)e * p.Si * p.Hp * kGS;
+    const float *L = p.lut_dn + (size_t)pr * p.Si * kGS * kCB;
+    float a = 0.f;
+    for (int s = q; s < p.Si; s += QG)  // one step when Si <= 4 (I <= 1024 at D = 16)
+        a += gather16(L + (size_t)s * kGS * kCB, ld_codes(ed + ((size_t)s * p.Hp + h) * kGS));
+    red[q][r] = a;
+    __syncthreads();
+    if (q != 0 || h >= p.H) return;
+    float s = red[0][r];
 #pragma unroll
-    for (int d = 0; d < DMAX; ++d) cb[d] = (d < D) ? p.cb_dn[tid * D + d] : 0.f;
-    for (int i = tid; i < sc; i += kNT) {
-        const int col = s * sc + i;
-        xs[i] = col < p.I ? p.inter[(size_t)pr * p.I + col] : 0.f;
-    }
-    const uint8_t *es = p.dn + ((size_t)e * p.Si + s) * p.Hp * kGS;
-    __syncthreads();
-    build_slice<DMAX>(xs, cb, D, lut);
-    __syncthreads();
-    float *out = p.part2 + ((size_t)pr * p.Si + s) * p.Hp;
-    for (int j = 0; j < p.rpb2; ++j) {
-        const int h = (rb * p.rpb2 + j) * kNT + tid;
-        if (h < p.Hp) out[h] = gather16(lut, *reinterpret_cast<const uint4 *>(es + (size_t)h * kGS));
-    }
+    for (int k = 1; k < QG; ++k) s += red[k][r];
+    p.dout[(size_t)pr * p.H + h] = s * p.dns[(size_t)e * p.H + h];
 }
 
 template <typename T>
 __global__ __launch_bounds__(kNT) void moe_combine_kernel(MoEParams p) {
+    // Slot weights (0 for skipped slots) and all per-pair outputs are loaded
+    // before the ordered sum, so the whole combine is one round trip.
+    constexpr int KB = 16;
     const int t = blockIdx.y;
-    const int h = blockIdx.x * kNT + threadIdx.x;
-    if (h >= p.H) return;
+    const int h = min((int)(blockIdx.x * kNT + threadIdx.x), p.H - 1);
     float y = 0.f;
-    for (int j = 0; j < p.k; ++j) {
-        const int pr = t * p.k + j;
-        int e;
-        if (!pair_active(p, pr, &e)) continue;
-        const float *pp = p.part2 + (size_t)pr * p.Si * p.Hp + h;
-        float s = 0.f;
-        for (int q = 0; q < p.Si; ++q) s += pp[(size_t)q * p.Hp];
-        y += (s * p.dns[(size_t)e * p.H + h]) * p.w[pr];
+    for (int j0 = 0; j0 < p.k; j0 += KB) {
+        float wj[KB], v[KB];
+#pragma unroll
+        for (int u = 0; u < KB; ++u) {
+            const int j = min(j0 + u, p.k - 1);
+            const int pr = t * p.k + j;
+            int e;
+            wj[u] = (j0 + u < p.k && pair_active(p, pr, &e)) ? p.w[pr] : 0.f;
+            v[u] = p.dout[(size_t)pr * p.H + h];
+        }
+#pragma unroll
+        for (int u = 0; u < KB; ++u)
+            if (wj[u] != 0.f) y += v[u] * wj[u];
     }
-    store_act(static_cast<T *>(p.y), (size_t)t * p.H + h, y);
+    if ((int)(blockIdx.x * kNT + threadIdx.x) < p.H) store_act(static_cast<T *>(p.y), (size_t)t * p.H + h, y);
 }
 
 // Router: top-k of the logits (descending, ties to the lower index) and the
-// softmax probability of each selected expert, optionally renormalised.
-__global__ __launch_bounds__(kNT) void moe_route_kernel(const float *logits, int E, int k,
+// softmax probability of each selected expert, optionally renormalised.  One
+// wave per token: lane l holds logits l + 64*i (E <= 1024); each of the k
+// rounds is a local argmax plus a 6-step shuffle reduction, no barriers.
+__global__ __launch_bounds__(kNT) void moe_route_kernel(const float *logits, int T, int E, int k,
                                                        int renorm, int *idx, float *w) {
-    __shared__ float lg[1024];
-    __shared__ unsigned char taken[1024];
-    __shared__ float rv[kNT];
-    __shared__ int ri[kNT];
-    __shared__ float s_max, s_sum;
-    __shared__ int sel[32];
-    const int t = blockIdx.x, tid = threadIdx.x;
+    constexpr int NV = 16;
+    __shared__ float selv[kNT / 64][32];
+    __shared__ int seli[kNT / 64][32];
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int t_raw = blockIdx.x * (kNT / 64) + wv;
+    const int t = min(t_raw, T - 1);
     const float *l = logits + (size_t)t * E;
-    for (int i = tid; i < E; i += kNT) {
-        lg[i] = l[i];
-        taken[i] = 0;
+    float v[NV];
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        const int e = lane + 64 * i;
+        const float x = l[min(e, E - 1)];
+        v[i] = e < E ? x : -INFINITY;
     }
-    __syncthreads();
+    uint32_t taken = 0;
     for (int j = 0; j < k; ++j) {
-        float bv = 0.f;
-        int bi = -1;
-        for (int i = tid; i < E; i += kNT)
-            if (!taken[i] && (bi < 0 || lg[i] > bv)) {
-                bv = lg[i];
-                bi = i;
+        float bv = -INFINITY;
+        int bi = 0x7fffffff;
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            const int e = lane + 64 * i;
+            if (e < E && !((taken >> i) & 1u) && (v[i] > bv || (v[i] == bv && e < bi))) {
+                bv = v[i];
+                bi = e;
             }
-        rv[tid] = bv;
-        ri[tid] = bi;
-        __syncthreads();
-        for (int st = kNT / 2; st > 0; st >>= 1) {
-            if (tid < st) {
-                const float ov = rv[tid + st];
-                const int oi = ri[tid + st];
-                const int mi = ri[tid];
-                if (oi >= 0 && (mi < 0 || ov > rv[tid] || (ov == rv[tid] && oi < mi))) {
-                    rv[tid] = ov;
-                    ri[tid] = oi;
-                }
+        }
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) {
+            const float ov = __shfl_xor(bv, off);
+            const int oi = __shfl_xor(bi, off);
+            if (ov > bv || (ov == bv && oi < bi)) {
+                bv = ov;
+                bi = oi;
             }
-            __syncthreads();
         }
-        if (tid == 0) {
-            sel[j] = ri[0];
-            taken[ri[0]] = 1;
+        if ((bi & 63) == lane) taken |= 1u << (bi >> 6);
+        if (lane == 0) {
+            selv[wv][j] = bv;
+            seli[wv][j] = bi;
         }
-        __syncthreads();
     }
-    // softmax statistics over all experts
+    // softmax statistics over all E logits
     float m = -INFINITY;
-    for (int i = tid; i < E; i += kNT) m = fmaxf(m, lg[i]);
-    rv[tid] = m;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) m = fmaxf(m, v[i]);
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+    float sum = 0.f;
+#pragma unroll
+    for (int i = 0; i < NV; ++i)
+        if (lane + 64 * i < E) sum += expf(v[i] - m);
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
     __syncthreads();
-    for (int st = kNT / 2; st > 0; st >>= 1) {
-        if (tid < st) rv[tid] = fmaxf(rv[tid], rv[tid + st]);
-        __syncthreads();
+    float wj = 0.f;
+    int ij = 0;
+    if (lane < k) {
+        ij = seli[wv][lane];
+        wj = expf(selv[wv][lane] - m) / sum;
     }
-    if (tid == 0) s_max = rv[0];
-    __syncthreads();
-    float s = 0.f;
-    for (int i = tid; i < E; i += kNT) s += expf(lg[i] - s_max);
-    rv[tid] = s;
-    __syncthreads();
-    for (int st = kNT / 2; st > 0; st >>= 1) {
-        if (tid < st) rv[tid] += rv[tid + st];
-        __syncthreads();
+    if (renorm) {
+        float tot = wj;
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) tot += __shfl_xor(tot, off);
+        wj = wj / tot;
     }
-    if (tid == 0) s_sum = rv[0];
-    __syncthreads();
-    if (tid == 0) {
-        float tot = 0.f;
-        float ww[32];
-        for (int j = 0; j < k; ++j) {
-            ww[j] = expf(lg[sel[j]] - s_max) / s_sum;
-            tot += ww[j];
-        }
-        for (int j = 0; j < k; ++j) {
-            idx[(size_t)t * k + j] = sel[j];
-            w[(size_t)t * k + j] = renorm ? ww[j] / tot : ww[j];
-        }
+    if (lane < k && t_raw < T) {
+        idx[(size_t)t * k + lane] = ij;
+        w[(size_t)t * k + lane] = wj;
     }
 }
 
 namespace {
 
-template <typename T>
-int moe_launch(MoE *m, const void *x, const int *idx, const float *w, void *y, int T_,
-               int k, hipStream_t st) {
-    const int P = T_ * k;
-    // Slices of the gate/up pass per workgroup: enough workgroups to fill the chip.
-    const int want = std::max(1, std::min(m->Sin, (512 + P - 1) / P));
-    const int spw1 = (m->Sin + want - 1) / want;
-    const int n_split1 = (m->Sin + spw1 - 1) / spw1;
-    int rc = m->inter.ensure((size_t)P * m->I * sizeof(float));
-    if (!rc) rc = m->part2.ensure((size_t)P * m->Si * m->Hp * sizeof(float));
-    if (!rc && n_split1 > 1) rc = m->part1.ensure((size_t)P * n_split1 * 2 * m->Ip * sizeof(float));
-    if (rc) return rc;
-    if ((size_t)P > m->ctr_n) {
-        rc = m->ctr.ensure((size_t)P * sizeof(unsigned));
-        if (rc) return rc;
-        OJX_HIP(hipMemset(m->ctr.ptr, 0, (size_t)P * sizeof(unsigned)));
-        m->ctr_n = P;
+int moe_forward(MoE *m, const void *x, const int *idx, const float *w, void *y, int T_, int k,
+                int dtype, hipStream_t st) {
+    if (k <= 0 || T_ <= 0) return OJASX_OK;
+    if (dtype != OJASX_DTYPE_F32 && dtype != OJASX_DTYPE_BF16) {
+        set_error("unsupported dtype %d", dtype);
+        return OJASX_ERR_INVALID;
     }
+    if (T_ > 65535) {
+        set_error("too many tokens in one call");
+        return OJASX_ERR_INVALID;
+    }
+    const size_t P = (size_t)T_ * k;
+    const int Gp_in = m->Sin * kGS;
+    int rc = m->lut_in.ensure((size_t)T_ * Gp_in * kCB * sizeof(float));
+    if (!rc) rc = m->dout.ensure(P * m->H * sizeof(float));
+    if (rc) return rc;
+    const size_t ldn = (size_t)m->Si * kGS * kCB * sizeof(float);
+    if (P > m->lut_dn_pairs) {
+        // LUT_down rows of padded groups (>= Gi) stay zero: written only here.
+        rc = m->lut_dn.ensure(P * ldn);
+        if (rc) return rc;
+        OJX_HIP(hipMemsetAsync(m->lut_dn.ptr, 0, P * ldn, st));
+        m->lut_dn_pairs = P;
+    }
+    rc = launch_lut_build(x, m->cb_in.as<float>(), T_, m->H, m->D, m->Gin, Gp_in,
+                          m->lut_in.as<float>(), dtype, st);
+    if (rc) return rc;
     MoEParams p{};
     p.gu = m->gu.as<uint8_t>();
     p.dn = m->dn.as<uint8_t>();
     p.gus = m->gus.as<float>();
     p.dns = m->dns.as<float>();
-    p.cb_in = m->cb_in.as<float>();
     p.cb_dn = m->cb_dn.as<float>();
-    p.x = x;
+    p.lut_in = m->lut_in.as<float>();
+    p.lut_dn = m->lut_dn.as<float>();
+    p.dout = m->dout.as<float>();
     p.idx = idx;
     p.w = w;
     p.y = y;
-    p.part1 = m->part1.as<float>();
-    p.ctr = m->ctr.as<unsigned>();
-    p.inter = m->inter.as<float>();
-    p.part2 = m->part2.as<float>();
     p.E = m->E;
     p.H = m->H;
     p.I = m->I;
@@ -377,38 +334,20 @@ int moe_launch(MoE *m, const void *x, const int *idx, const float *w, void *y, i
     p.Hp = m->Hp;
     p.T = T_;
     p.k = k;
-    p.spw1 = spw1;
-    p.n_split1 = n_split1;
-    // down pass: row blocks of 256*rpb2 rows, enough workgroups to fill the chip
-    const int per_pair = m->Si;
-    int rpb2 = std::max(1, m->Hp / kNT);
-    while (rpb2 > 1 && (size_t)P * per_pair * ((m->Hp / kNT + rpb2 - 1) / rpb2) < 512) rpb2 = (rpb2 + 1) / 2;
-    p.rpb2 = rpb2;
-    const int n_rb2 = (m->H + kNT * rpb2 - 1) / (kNT * rpb2);
-    if (m->D == 16) {
-        hipLaunchKernelGGL((moe_gateup_kernel<16, T>), dim3(P * n_split1), dim3(kNT), 0, st, p);
-        hipLaunchKernelGGL((moe_down_kernel<16>), dim3(P * m->Si * n_rb2), dim3(kNT), 0, st, p);
-    } else {
-        hipLaunchKernelGGL((moe_gateup_kernel<0, T>), dim3(P * n_split1), dim3(kNT), 0, st, p);
-        hipLaunchKernelGGL((moe_down_kernel<0>), dim3(P * m->Si * n_rb2), dim3(kNT), 0, st, p);
-    }
-    hipLaunchKernelGGL((moe_combine_kernel<T>), dim3((m->H + kNT - 1) / kNT, T_), dim3(kNT), 0,
-                       st, p);
+    const int nrb_g = (m->I + kRG - 1) / kRG;
+    const int nrb_d = (m->H + kRD - 1) / kRD;
+    if (m->D == 16)
+        hipLaunchKernelGGL(moe_gateup_kernel<16>, dim3(P * nrb_g), dim3(kNT), 0, st, p);
+    else
+        hipLaunchKernelGGL(moe_gateup_kernel<0>, dim3(P * nrb_g), dim3(kNT), 0, st, p);
+    hipLaunchKernelGGL(moe_down_kernel, dim3(P * nrb_d), dim3(kNT), 0, st, p);
+    dim3 gc((m->H + kNT - 1) / kNT, T_);
+    if (dtype == OJASX_DTYPE_F32)
+        hipLaunchKernelGGL(moe_combine_kernel<float>, gc, dim3(kNT), 0, st, p);
+    else
+        hipLaunchKernelGGL(moe_combine_kernel<__hip_bfloat16>, gc, dim3(kNT), 0, st, p);
     OJX_HIP(hipGetLastError());
     return OJASX_OK;
-}
-
-int moe_forward(MoE *m, const void *x, const int *idx, const float *w, void *y, int T_, int k,
-                int dtype, hipStream_t st) {
-    if (k <= 0 || T_ <= 0) return OJASX_OK;
-    if (T_ > 65535) {
-        set_error("too many tokens in one call");
-        return OJASX_ERR_INVALID;
-    }
-    if (dtype == OJASX_DTYPE_F32) return moe_launch<float>(m, x, idx, w, y, T_, k, st);
-    if (dtype == OJASX_DTYPE_BF16) return moe_launch<__hip_bfloat16>(m, x, idx, w, y, T_, k, st);
-    set_error("unsupported dtype %d", dtype);
-    return OJASX_ERR_INVALID;
 }
 
 }  // namespace
@@ -427,8 +366,8 @@ OJASX_API OjasxMoEHandle ojasx_create_moe(int num_experts, int hidden_dim, int i
     using namespace ojx;
     if (num_experts <= 0 || hidden_dim <= 0 || intermediate_dim <= 0 || block_dim <= 0 ||
         block_dim > 32 || hidden_dim % block_dim || intermediate_dim % block_dim ||
-        intermediate_dim > kMaxJ * kNT) {
-        set_error("invalid MoE shape E=%d H=%d I=%d block=%d", num_experts, hidden_dim,
+        kRG % block_dim) {
+        set_error("invalid MoE shape E=%d H=%d I=%d block=%d (block must divide 32)", num_experts, hidden_dim,
                   intermediate_dim, block_dim);
         return nullptr;
     }
@@ -443,8 +382,8 @@ OJASX_API OjasxMoEHandle ojasx_create_moe(int num_experts, int hidden_dim, int i
     m->Gi = intermediate_dim / block_dim;
     m->Sin = (m->Gin + kGS - 1) / kGS;
     m->Si = (m->Gi + kGS - 1) / kGS;
-    m->Ip = (int)round_up(intermediate_dim, kNT);
-    m->Hp = (int)round_up(hidden_dim, kNT);
+    m->Ip = (int)round_up(intermediate_dim, kRowAlign);
+    m->Hp = (int)round_up(hidden_dim, kRowAlign);
     const size_t E = num_experts, I = intermediate_dim, H = hidden_dim;
     // gate/up: [E][Sin][2][Ip][16], gate rows in half 0, up rows in half 1
     std::vector<uint8_t> gu(E * m->Sin * 2 * m->Ip * kGS, 0);
@@ -521,8 +460,9 @@ OJASX_API int ojasx_moe_route_device(const float *logits, int num_tokens, int nu
         set_error("router supports 1 <= k <= min(32, E), E <= 1024");
         return OJASX_ERR_INVALID;
     }
-    hipLaunchKernelGGL(moe_route_kernel, dim3(num_tokens), dim3(kNT), 0,
-                       static_cast<hipStream_t>(stream), logits, num_experts, k, renormalize, idx, w);
+    hipLaunchKernelGGL(moe_route_kernel, dim3((num_tokens + kNT / 64 - 1) / (kNT / 64)), dim3(kNT), 0,
+                       static_cast<hipStream_t>(stream), logits, num_tokens, num_experts, k,
+                       renormalize, idx, w);
     OJX_HIP(hipGetLastError());
     return OJASX_OK;
 }
