@@ -201,6 +201,21 @@ def test_kv_quantiser_closed_form():
         assert np.array_equal(codes, q.astype(np.uint8))
 
 
+def test_paged_int8_quantiser_known_answer():
+    """long_context.py:234-240: scale = amax/127 kept as float16, codes rounded
+    half to even (torch.round) and clamped to +-127."""
+    t = np.array([[127.0, 63.5, -63.5, 0.5, 1.5, -2.5, 2.5, 0.0],
+                  [1.0, -0.25, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0],
+                  [0.0] * 8], np.float32)
+    q, s = no.paged_quantize_int8(t)
+    assert q.dtype == np.int8 and s.dtype == np.float16
+    assert q[0].tolist() == [127, 64, -64, 0, 2, -2, 2, 0]   # half away would give 1, -3, 3
+    assert s[0, 0] == np.float16(1.0)
+    assert s[1, 0] == np.float16(np.float32(1.0) / np.float32(127.0))
+    assert q[1].tolist() == [127, -32, 0, 0, 0, 0, 0, 0]     # -31.75 -> -32
+    assert not q[2].any() and s[2, 0] == np.float16(np.float32(1e-8) / np.float32(127.0))
+
+
 def test_kv_golden_end_to_end():
     g = golden("kv_ref_head_t150")
     kc, ks, vc, vs = [], [], [], []
