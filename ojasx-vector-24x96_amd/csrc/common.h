@@ -57,6 +57,24 @@ __device__ __forceinline__ float load_act(const float *p, size_t i) { return p[i
 __device__ __forceinline__ float load_act(const __hip_bfloat16 *p, size_t i) {
     return __bfloat162float(p[i]);
 }
+// Four consecutive activations as fp32 (p + i must be 16-byte aligned for
+// fp32, 8-byte aligned for bf16).
+__device__ __forceinline__ float4 load4_act(const float *p, size_t i) {
+    return *reinterpret_cast<const float4 *>(p + i);
+}
+__device__ __forceinline__ float4 load4_act(const __hip_bfloat16 *p, size_t i) {
+    const uint2 u = *reinterpret_cast<const uint2 *>(p + i);
+    return make_float4(__uint_as_float(u.x << 16), __uint_as_float(u.x & 0xffff0000u),
+                       __uint_as_float(u.y << 16), __uint_as_float(u.y & 0xffff0000u));
+}
+
+// Sum over the 4 lanes of a quad (DPP quad permutes, no LDS traffic).
+__device__ __forceinline__ float quad_sum(float v) {
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false));
+    return v;
+}
+
 __device__ __forceinline__ void store_act(float *p, size_t i, float v) { p[i] = v; }
 __device__ __forceinline__ void store_act(__hip_bfloat16 *p, size_t i, float v) {
     p[i] = __float2bfloat16(v);

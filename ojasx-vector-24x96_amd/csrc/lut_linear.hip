@@ -8,10 +8,23 @@
 // added after the epilogue and not scaled) and of
 // split_manifold_lut_experiment/engine/split_manifold_engine.py:185-250.
 //
-// Two kernels per call and no cross-workgroup synchronisation.  At batch 1
-// both are latency-bound (1.1 MB of codes is ~0.14 us of HBM time against a
-// ~1.3 us kernel floor), so each issues every independent load first and
-// keeps the chain of dependent memory round trips to two:
+// block_dim 16 (the reference default and every configured shape): one
+// kernel, lut_dec_kernel.  At small batch a call is latency-bound (1.1 MB of
+// codes is ~0.14 us of HBM time against a ~1.3 us kernel floor and a ~1.6 us
+// gap between dependent launches), so the LUT entries a workgroup needs are
+// computed where they are used instead of in a second kernel:
+// LUT[g][code] = <x_g, C[code]>, with the codebook (16 KB) and x staged in
+// LDS.  Workgroup = 16*RPL output rows x all G groups; wave w owns the 16-group
+// slices w, w+NW, ... (NW = min(S, 16) waves); lane (r, j) owns row r (and
+// r+16 when RPL = 2) and the quarter j (4 floats) of every 16-float dot, so an
+// 8-lane LDS group reads two codebook rows.  The row's quarters and slices
+// are summed with DPP quad adds and an LDS reduction in a fixed order; the
+// row's CSR entries are split over its 4*NW lanes; the epilogue applies
+// (s_m * sum + bias) + outliers in the reference's order.  Round trip 1
+// issues the L2-resident staging loads before the HBM code loads so the LDS
+// writes do not wait for HBM.
+//
+// Other block sizes use two kernels and no cross-workgroup synchronisation:
 //  K1 lut_build: the LUT of every token, LUT[b][g][k] for all 256 centroids,
 //     into a workspace (workgroup = (1 group, 1 token), thread k owns
 //     centroid k): x and the codebook, then one store.
@@ -42,6 +55,8 @@ constexpr int kCB = 256;        // centroids in the (zero-padded) codebook
 constexpr int kRows = 32;       // rows per gather workgroup
 constexpr int kOB = 32;         // outlier entries loaded per batch
 constexpr size_t kXLdsBytes = 48 * 1024;  // x staged in LDS up to this size
+constexpr int kMaxDecWaves = 16;          // waves (slice owners) per decode workgroup
+constexpr size_t kMaxLds = 160 * 1024;    // LDS per workgroup on gfx950
 }  // namespace
 
 struct GatherParams {
@@ -220,6 +235,212 @@ __global__ __launch_bounds__(kNT) void lut_gather_kernel(GatherParams p) {
     }
 }
 
+struct DecParams {
+    const uint8_t *codes;   // [S][Mp][16]
+    const float *cb;        // [256][16]
+    const float *scales;    // [M]
+    const float *bias;      // [M] or null
+    const int *rowp;        // [M+1] (null: no outliers)
+    const int *col;         // [nnz]
+    const float *val;       // [nnz]
+    const void *x;          // [B][K], 16-byte aligned (fp32) / 8-byte (bf16)
+    void *y;                // [B][M]
+    int K, M, Mp, S, B, nnz, NW;
+};
+
+// Single-kernel forward for block_dim 16 (see the file comment).  x is staged
+// as [BT][S*256] with zeros past K, so groups past G contribute 0.
+template <typename T, int BT, int RPL>
+__global__ __launch_bounds__(1024) void lut_dec_kernel(DecParams p) {
+    constexpr int R = 16 * RPL;            // rows per workgroup
+    extern __shared__ float sm[];
+    float *cbs = sm;                       // [256][16]
+    float *xs = sm + kCB * 16;             // [BT][S*256]
+    __shared__ float part[2][16][R][BT];   // [manifold|outlier][wave][row][token]
+    const int tid = threadIdx.x, nthr = blockDim.x;
+    const int lane = tid & 63, w = tid >> 6;
+    const int r = lane >> 2, j = lane & 3;
+    const int NW = p.NW, S = p.S, KS = S * 256;
+    const int base = (int)blockIdx.x * R;  // base + R <= Mp: code loads need no clamp
+    const int t0 = (int)blockIdx.y * BT;
+    const int nt = min(BT, p.B - t0);
+    const bool outl = p.rowp != nullptr;
+    const T *__restrict__ x = static_cast<const T *>(p.x);
+
+    // ---- round trip 1: codebook and x (L2) first, then codes (HBM), row data
+    float4 cv4[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+        cv4[u] = reinterpret_cast<const float4 *>(p.cb)[min(tid + u * nthr, 1023)];
+    const int nx4 = KS / 4;
+    float4 xv4[BT][2];
+#pragma unroll
+    for (int t = 0; t < BT; ++t) {
+        const int tt = min(t, nt - 1);
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const int e = min(tid + u * nthr, nx4 - 1) * 4;
+            xv4[t][u] = load4_act(x, (size_t)(t0 + tt) * p.K + min(e, p.K - 4));
+            if (e >= p.K) xv4[t][u] = make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+    }
+    uint4 cw[RPL];
+#pragma unroll
+    for (int i = 0; i < RPL; ++i)
+        cw[i] = *reinterpret_cast<const uint4 *>(p.codes + ((size_t)w * p.Mp + base + r + 16 * i) * kGS);
+    float sc = 0.f, bs = 0.f;
+    if (tid < R) {
+        const int mm = min(base + tid, p.M - 1);
+        sc = p.scales[mm];
+        bs = p.bias ? p.bias[mm] : 0.f;
+    }
+    int j0[RPL], j1[RPL];
+#pragma unroll
+    for (int i = 0; i < RPL; ++i) j0[i] = j1[i] = 0;
+    if (outl) {
+#pragma unroll
+        for (int i = 0; i < RPL; ++i) {
+            const int mm = min(base + r + 16 * i, p.M - 1);
+            j0[i] = p.rowp[mm];
+            j1[i] = p.rowp[mm + 1];
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < 2; ++u) reinterpret_cast<float4 *>(cbs)[min(tid + u * nthr, 1023)] = cv4[u];
+    if (2 * nthr < 1024) {  // fewer than 512 threads: the rest of the codebook, 8 loads in flight
+        const float4 *c4 = reinterpret_cast<const float4 *>(p.cb);
+        for (int b = tid + 2 * nthr; b < 1024; b += 8 * nthr) {
+            float4 v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) v[u] = c4[min(b + u * nthr, 1023)];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) reinterpret_cast<float4 *>(cbs)[min(b + u * nthr, 1023)] = v[u];
+        }
+    }
+#pragma unroll
+    for (int t = 0; t < BT; ++t)
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+            reinterpret_cast<float4 *>(xs + t * KS)[min(tid + u * nthr, nx4 - 1)] = xv4[t][u];
+    if (2 * nthr < nx4) {  // more than two float4 of x per thread (K > 8192)
+        for (int t = 0; t < nt; ++t)
+            for (int i = tid + 2 * nthr; i < nx4; i += nthr) {
+                const int e = i * 4;
+                reinterpret_cast<float4 *>(xs + t * KS)[i] =
+                    e < p.K ? load4_act(x, (size_t)(t0 + t) * p.K + e) : make_float4(0.f, 0.f, 0.f, 0.f);
+            }
+    }
+    // ---- the lane's first CSR entry of each of its rows: j0 + lq (of 4*NW)
+    const int lq = w * 4 + j, LQ = NW * 4;
+    int oc[RPL];
+    float ov[RPL];
+    if (outl) {
+#pragma unroll
+        for (int i = 0; i < RPL; ++i) {
+            const int jj = min(j0[i] + lq, p.nnz - 1);
+            oc[i] = p.col[jj];
+            ov[i] = p.val[jj];
+        }
+    }
+    __syncthreads();
+
+    // ---- dots: lane (r, j) adds x_t[g][4j..4j+3] . C[code][4j..4j+3]
+    float acc[RPL][BT][2];
+#pragma unroll
+    for (int i = 0; i < RPL; ++i)
+#pragma unroll
+        for (int t = 0; t < BT; ++t) acc[i][t][0] = acc[i][t][1] = 0.f;
+    const float *cbj = cbs + 4 * j;
+    for (int s = w; s < S; s += NW) {
+        uint32_t wd[RPL][4];
+#pragma unroll
+        for (int i = 0; i < RPL; ++i) {
+            wd[i][0] = cw[i].x;
+            wd[i][1] = cw[i].y;
+            wd[i][2] = cw[i].z;
+            wd[i][3] = cw[i].w;
+        }
+        if (s + NW < S) {
+#pragma unroll
+            for (int i = 0; i < RPL; ++i)
+                cw[i] = *reinterpret_cast<const uint4 *>(
+                    p.codes + ((size_t)(s + NW) * p.Mp + base + r + 16 * i) * kGS);
+        }
+        const float *xsj = xs + s * 256 + 4 * j;
+#pragma unroll
+        for (int g = 0; g < kGS; ++g) {
+            float4 c[RPL];
+#pragma unroll
+            for (int i = 0; i < RPL; ++i) {
+                const int code = (wd[i][g >> 2] >> ((g & 3) * 8)) & 0xffu;
+                c[i] = *reinterpret_cast<const float4 *>(cbj + code * 16);
+            }
+#pragma unroll
+            for (int t = 0; t < BT; ++t) {
+                const float4 xv = *reinterpret_cast<const float4 *>(xsj + t * KS + g * 16);
+#pragma unroll
+                for (int i = 0; i < RPL; ++i) {
+                    float a = acc[i][t][g & 1];
+                    a = fmaf(xv.x, c[i].x, a);
+                    a = fmaf(xv.y, c[i].y, a);
+                    a = fmaf(xv.z, c[i].z, a);
+                    a = fmaf(xv.w, c[i].w, a);
+                    acc[i][t][g & 1] = a;
+                }
+            }
+        }
+    }
+    // ---- outliers of this lane; rows with more than 4*NW entries loop
+    float oa[RPL][BT];
+#pragma unroll
+    for (int i = 0; i < RPL; ++i)
+#pragma unroll
+        for (int t = 0; t < BT; ++t) oa[i][t] = 0.f;
+    if (outl) {
+#pragma unroll
+        for (int i = 0; i < RPL; ++i) {
+            const bool on = lq < j1[i] - j0[i];
+#pragma unroll
+            for (int t = 0; t < BT; ++t) oa[i][t] = on ? ov[i] * xs[min(t, nt - 1) * KS + oc[i]] : 0.f;
+            for (int jj = j0[i] + lq + LQ; jj < j1[i]; jj += LQ) {
+                const int c = p.col[jj];
+                const float v = p.val[jj];
+#pragma unroll
+                for (int t = 0; t < BT; ++t) oa[i][t] += v * xs[min(t, nt - 1) * KS + c];
+            }
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < RPL; ++i)
+#pragma unroll
+        for (int t = 0; t < BT; ++t) {
+            const float v = quad_sum(acc[i][t][0] + acc[i][t][1]);
+            const float o = quad_sum(oa[i][t]);
+            if (j == 0) {
+                part[0][w][r + 16 * i][t] = v;
+                part[1][w][r + 16 * i][t] = o;
+            }
+        }
+    __syncthreads();
+    if (tid >= R) return;
+    const int m = base + tid;
+    if (m >= p.M) return;
+    T *y = static_cast<T *>(p.y);
+#pragma unroll
+    for (int t = 0; t < BT; ++t) {
+        if (t >= nt) break;
+        float a = 0.f, o = 0.f;
+        for (int k = 0; k < NW; ++k) {
+            a += part[0][k][tid][t];
+            o += part[1][k][tid][t];
+        }
+        float v = a * sc;
+        if (p.bias) v += bs;
+        v += o;
+        store_act(y, (size_t)(t0 + t) * p.M + m, v);
+    }
+}
+
 // Standalone LUT build with a codebook of Kcb rows: one workgroup per
 // (group, token), thread k computes LUT[b][g][k].
 template <typename T>
@@ -262,6 +483,59 @@ int launch_gather(const GatherParams &gp, int M, dim3 grid_y, size_t lds, hipStr
     dim3 grid((M + R - 1) / R, grid_y.y);
     hipLaunchKernelGGL((lut_gather_kernel<R, BT, T>), grid, dim3(kNT), lds, st, gp);
     return OJASX_OK;
+}
+
+template <typename T, int BT, int RPL>
+int launch_dec(Linear *L, const void *x, void *y, int B, size_t lds, hipStream_t st) {
+    DecParams dp{};
+    dp.codes = L->codes.as<uint8_t>();
+    dp.cb = L->codebook.as<float>();
+    dp.scales = L->scales.as<float>();
+    dp.bias = L->has_bias ? L->bias.as<float>() : nullptr;
+    dp.rowp = L->nnz ? L->rowp.as<int>() : nullptr;
+    dp.col = L->col.as<int>();
+    dp.val = L->val.as<float>();
+    dp.x = x;
+    dp.y = y;
+    dp.K = L->K;
+    dp.M = L->M;
+    dp.Mp = L->Mp;
+    dp.S = L->S;
+    dp.B = B;
+    dp.nnz = (int)L->nnz;
+    dp.NW = std::min(L->S, kMaxDecWaves);
+    static size_t granted = 0;
+    const void *fn = reinterpret_cast<const void *>(&lut_dec_kernel<T, BT, RPL>);
+    int rc = ensure_dyn_lds(fn, lds, &granted);
+    if (rc) return rc;
+    dim3 grid((L->M + 16 * RPL - 1) / (16 * RPL), (B + BT - 1) / BT);
+    hipLaunchKernelGGL((lut_dec_kernel<T, BT, RPL>), grid, dim3(64 * dp.NW), lds, st, dp);
+    OJX_HIP(hipGetLastError());
+    return OJASX_OK;
+}
+
+// Single-kernel path when block_dim is 16, x is aligned for vector loads and
+// the staged x fits LDS; returns 1 when the two-kernel path must run instead.
+template <typename T>
+int try_dec(Linear *L, const void *x, void *y, int B, hipStream_t st) {
+    const size_t align = sizeof(T) == 4 ? 16 : 8;
+    if (L->D != 16 || (reinterpret_cast<uintptr_t>(x) % align)) return 1;
+    int bt = B >= 3 ? 4 : B;
+    const size_t xrow = (size_t)L->S * 256 * sizeof(float);
+    while (bt > 1 && kCB * 16 * sizeof(float) + bt * xrow > kMaxLds) bt /= 2;
+    const size_t lds = kCB * 16 * sizeof(float) + bt * xrow;
+    if (lds > kMaxLds) return 1;
+    // 32-row workgroups when that still gives about one workgroup per CU
+    const long wg32 = (long)((L->M + 31) / 32) * ((B + bt - 1) / bt);
+    const bool r2 = wg32 >= 192;
+    switch (bt * 2 + (r2 ? 1 : 0)) {
+        case 2: return launch_dec<T, 1, 1>(L, x, y, B, lds, st);
+        case 3: return launch_dec<T, 1, 2>(L, x, y, B, lds, st);
+        case 4: return launch_dec<T, 2, 1>(L, x, y, B, lds, st);
+        case 5: return launch_dec<T, 2, 2>(L, x, y, B, lds, st);
+        case 8: return launch_dec<T, 4, 1>(L, x, y, B, lds, st);
+        default: return launch_dec<T, 4, 2>(L, x, y, B, lds, st);
+    }
 }
 
 template <typename T>
@@ -320,8 +594,11 @@ int forward(Linear *L, const void *x, void *y, int B, int dtype, hipStream_t st)
         set_error("batch %d exceeds 65535", B);
         return OJASX_ERR_INVALID;
     }
+    int rc = dtype == OJASX_DTYPE_F32 ? try_dec<float>(L, x, y, B, st)
+                                      : try_dec<__hip_bfloat16>(L, x, y, B, st);
+    if (rc != 1) return rc;
     const int Gp = L->S * kGS;
-    int rc = L->lut.ensure((size_t)B * Gp * kCB * sizeof(float));
+    rc = L->lut.ensure((size_t)B * Gp * kCB * sizeof(float));
     if (rc) return rc;
     return dtype == OJASX_DTYPE_F32 ? launch<float>(L, x, y, B, st)
                                     : launch<__hip_bfloat16>(L, x, y, B, st);

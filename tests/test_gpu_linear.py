@@ -1,5 +1,6 @@
-"""GPU parity of the LUT linear path (K1 LUT build + K2 gather + K3 CSR)
-against the CPU oracle, through the HIP C-ABI.
+"""GPU parity of the LUT linear layer against the CPU oracle, through the HIP
+C-ABI: the single-kernel path (block_dim 16, aligned x) and the two-kernel
+LUT-build + gather path (other block sizes, unaligned x).
 
 Bars: bit-exact on integer-valued inputs (every partial sum exact in fp32,
 so any summation order gives the same bits) and on the reference's CSR known
@@ -73,7 +74,11 @@ def test_reference_t2(pkg):
 
 
 @pytest.mark.parametrize("M,K,B", [(97, 640, 2), (6912, 2560, 1), (6912, 2560, 3),
-                                   (2560, 2560, 8), (1000, 2560, 64)])
+                                   (2560, 2560, 8), (1000, 2560, 64),
+                                   (333, 2000, 5),    # 125 groups: partial last slice
+                                   (1000, 8192, 3),   # 32 slices: two per wave
+                                   (257, 5120, 2),    # 20 slices: one or two per wave
+                                   (64, 16, 7)])      # one group, one wave
 def test_integer_inputs_bit_exact(pkg, dev, M, K, B):
     import torch
     c = integer_case(M * 7 + B, M=M, K=K, B=B)
@@ -116,9 +121,39 @@ def test_odd_shapes(pkg, dev, M, K, D, Kcb, bias):
     assert rel_err(y, y_ref) < F32_TOL
 
 
+@pytest.mark.parametrize("M,K,B", [(130, 1024, 3), (70, 4096, 1)])
+def test_dense_outlier_rows(pkg, dev, M, K, B):
+    """Rows with more CSR entries than the lanes that share them (4 per wave)."""
+    import torch
+    d = gen.linear(M, K, B=B, seed=K + B, scales="u", bias=True, density=0.08)
+    assert np.diff(d["csr"][0]).max() > 4 * min(K // 256, 16)
+    nat = native_linear(pkg, d, M, K)
+    y = dev_forward(pkg, nat, torch.from_numpy(d["x"]).to(dev), 0, torch.float32).cpu().numpy()
+    y_ref = cpu.linear_forward(d["x"], d["codebook"], d["codes"], d["scales"], d["bias"], *d["csr"])
+    assert rel_err(y, y_ref) < F32_TOL
+
+
+@pytest.mark.parametrize("dtype_tag", [0, 1])
+def test_unaligned_activations(pkg, dev, dtype_tag):
+    """x that is not 16-byte aligned (fp32) / 8-byte aligned (bf16) takes the
+    two-kernel path; results stay within tolerance."""
+    import torch
+    M, K, B = 300, 512, 3
+    d = gen.linear(M, K, B=B, seed=31, scales="u")
+    nat = native_linear(pkg, d, M, K)
+    tdt = torch.float32 if dtype_tag == 0 else torch.bfloat16
+    buf = torch.empty(B * K + 1, device=dev, dtype=tdt)
+    xt = buf[1:].view(B, K)
+    xt.copy_(torch.from_numpy(d["x"]).to(dev).to(tdt))
+    y = dev_forward(pkg, nat, xt, dtype_tag, tdt).float().cpu().numpy()
+    x_used = xt.float().cpu().numpy()
+    y_ref = cpu.linear_forward(x_used, d["codebook"], d["codes"], d["scales"], None, *d["csr"])
+    assert rel_err(y, y_ref) < (F32_TOL if dtype_tag == 0 else BF16_TOL)
+
+
 def test_repeat_calls_deterministic_and_outlier_reset(pkg):
-    """The split-reduction tickets reset themselves: repeated calls give
-    identical bits; nnz = 0 clears the outliers."""
+    """Fixed reduction order: repeated calls give identical bits; nnz = 0
+    clears the outliers."""
     d = gen.linear(6912, 2560, B=2, seed=77, scales="u", bias=True)
     nat = native_linear(pkg, d, 6912, 2560)
     ys = [nat.forward(d["x"]) for _ in range(5)]
