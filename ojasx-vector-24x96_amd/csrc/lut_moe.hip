@@ -11,18 +11,20 @@
 // zeroed when k_active > 0, untouched otherwise).  Only routed experts' codes
 // are ever read.
 //
-// Four launches per call, no cross-workgroup synchronisation inside a kernel
-// (a "pair" is one routed (token, slot)):
-//  1. LUT_in of every token (the linear layer's LUT-build kernel).
-//  2. moe_gateup: workgroup = (pair, 32 intermediate rows) x 8 slice groups;
-//     thread (q, r) gathers gate row i and up row i for its slices, the slice
-//     partials are reduced in LDS in a fixed order, then SwiGLU gives 32
-//     intermediate values -- two 16-wide groups -- from which the same
-//     workgroup builds those groups' LUT_down rows (256 centroids each).
-//  3. moe_down: workgroup = (pair, 64 hidden rows) x 4 slice groups: gather
-//     from the pair's LUT_down, reduce, scale -> per-pair output [P][H].
-//  4. moe_combine: y[t][h] = sum_j w_j * out[t,j][h] in slot order -- a fixed
-//     order, so results are deterministic.
+// Three paths, none with cross-workgroup synchronisation inside a kernel (a
+// "pair" is one routed (token, slot)):
+//  * block_dim 16, fewer than kPartsMinTokens tokens (latency-bound): two
+//    launches that compute LUT entries where they are used, <v_g, C[code]>,
+//    from the codebook and the input vector staged in LDS -- moe_up_dec
+//    (gate/up + SwiGLU per (pair, 32 intermediate rows)) and moe_down_dec
+//    (down + combine per (token, hidden rows), slots summed in slot order).
+//  * block_dim 16, more tokens: the LUT path with each 16-group LUT slice in
+//    LDS, split over slices -- LUT_in build, moe_gu_part (pair, input slice),
+//    moe_dn_part (pair, intermediate slice: SwiGLU, LUT_down slice, gathers),
+//    moe_combine_parts.
+//  * other block sizes: LUT_in build, moe_gateup (gathers from the L2-resident
+//    LUT, SwiGLU, LUT_down rows), moe_down, moe_combine.
+// Every path sums slots in slot order, so results are deterministic.
 //  Router: moe_route, one workgroup per token.
 #include <algorithm>
 #include <cstring>
@@ -45,11 +47,11 @@ struct MoE {
     int E = 0, H = 0, I = 0, top_k = 0, D = 0;
     int Gin = 0, Gi = 0, Sin = 0, Si = 0, Ip = 0, Hp = 0;
     DevBuf cb_in, cb_dn, gu, dn, gus, dns;
-    DevBuf lut_in, lut_dn, dout, xstage, ystage, istage, wstage;
+    DevBuf lut_in, lut_dn, dout, inter, part_gu, part_dn, xstage, ystage, istage, wstage;
     size_t lut_dn_pairs = 0;
     ~MoE() {
-        for (DevBuf *b : {&cb_in, &cb_dn, &gu, &dn, &gus, &dns, &lut_in, &lut_dn, &dout, &xstage,
-                          &ystage, &istage, &wstage})
+        for (DevBuf *b : {&cb_in, &cb_dn, &gu, &dn, &gus, &dns, &lut_in, &lut_dn, &dout, &inter,
+                          &part_gu, &part_dn, &xstage, &ystage, &istage, &wstage})
             b->release();
     }
 };
@@ -180,6 +182,502 @@ __global__ __launch_bounds__(kNT) void moe_down_kernel(MoEParams p) {
     p.dout[(size_t)pr * p.H + h] = s * p.dns[(size_t)e * p.H + h];
 }
 
+// ---------------------------------------------------------------------------
+// block_dim 16: two launches.  LUT entries are computed where they are used,
+// <v_g, C[code]>, from the codebook and the input vector staged in LDS, with
+// lane (r, j) owning quarter j of every 16-float dot (as in lut_linear.hip).
+
+struct MoEDecParams {
+    const uint8_t *gu;      // [E][Sin][2][Ip][16]
+    const uint8_t *dn;      // [E][Si][Hp][16]
+    const float *gus;       // [E][2I]
+    const float *dns;       // [E][H]
+    const float *cb_in;     // [256][16]
+    const float *cb_dn;     // [256][16]
+    const void *x;          // [T][H]
+    float *inter;           // [P][I]
+    const int *idx;         // [T][k]
+    const float *w;         // [T][k]
+    void *y;                // [T][H]
+    int E, H, I, Sin, Si, Ip, Hp, T, k, NW;
+};
+
+__device__ __forceinline__ bool slot_active(const int *idx, const float *w, int pr, int E, int *e) {
+    *e = idx[pr];
+    return *e >= 0 && *e < E && fabsf(w[pr]) >= 1e-8f;
+}
+
+// Gate/up + SwiGLU.  Workgroup = (pair, 16*NI intermediate rows); wave w owns
+// input slices w, w+NW, ...; lane (r, j) owns gate and up rows i = base + r +
+// 16n (n < NI).  Writes inter[pair][i] = silu(s_g * gate_i) * (s_u * up_i).
+// Loads are issued codebook and x first (L2), then codes (HBM), so the LDS
+// stores wait only for the L2 loads.
+template <typename T, int NI>
+__global__ __launch_bounds__(1024) void moe_up_dec_kernel(MoEDecParams p) {
+    constexpr int R = 16 * NI;
+    extern __shared__ float sm[];
+    float *cbs = sm;                       // [256][16]
+    float *xs = sm + kCB * 16;             // [Sin*256], zero past H
+    __shared__ float part[2][16][R];
+    const int tid = threadIdx.x, nthr = blockDim.x;
+    const int lane = tid & 63, w = tid >> 6;
+    const int r = lane >> 2, j = lane & 3;
+    const int nib = (p.I + R - 1) / R;
+    const int pr = blockIdx.x / nib;
+    const int base = (blockIdx.x - pr * nib) * R;   // base + R <= Ip
+    int e;
+    if (!slot_active(p.idx, p.w, pr, p.E, &e)) return;
+    const int t = pr / p.k;
+    const int KS = p.Sin * 256, nx4 = KS / 4;
+    const T *__restrict__ x = static_cast<const T *>(p.x) + (size_t)t * p.H;
+
+    float4 cv4[2], xv4[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) cv4[u] = reinterpret_cast<const float4 *>(p.cb_in)[min(tid + u * nthr, 1023)];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        const int el = min(tid + u * nthr, nx4 - 1) * 4;
+        xv4[u] = load4_act(x, min(el, p.H - 4));
+        if (el >= p.H) xv4[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    const uint8_t *eg = p.gu + (size_t)e * p.Sin * 2 * p.Ip * kGS;
+    uint4 cw[NI][2];
+#pragma unroll
+    for (int n = 0; n < NI; ++n)
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+            cw[n][h] = ld_codes(eg + (((size_t)w * 2 + h) * p.Ip + base + r + 16 * n) * kGS);
+    float sg = 0.f, su = 0.f;
+    if (tid < R) {
+        const int i = min(base + tid, p.I - 1);
+        sg = p.gus[(size_t)e * 2 * p.I + i];
+        su = p.gus[(size_t)e * 2 * p.I + p.I + i];
+    }
+#pragma unroll
+    for (int u = 0; u < 2; ++u) reinterpret_cast<float4 *>(cbs)[min(tid + u * nthr, 1023)] = cv4[u];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) reinterpret_cast<float4 *>(xs)[min(tid + u * nthr, nx4 - 1)] = xv4[u];
+    for (int b = tid + 2 * nthr; b < 1024; b += nthr)     // fewer than 512 threads
+        reinterpret_cast<float4 *>(cbs)[b] = reinterpret_cast<const float4 *>(p.cb_in)[b];
+    for (int b = tid + 2 * nthr; b < nx4; b += nthr) {    // H > 8 * threads
+        const int el = b * 4;
+        reinterpret_cast<float4 *>(xs)[b] = el < p.H ? load4_act(x, el) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    __syncthreads();
+
+    float acc[NI][2][2];
+#pragma unroll
+    for (int n = 0; n < NI; ++n)
+        acc[n][0][0] = acc[n][0][1] = acc[n][1][0] = acc[n][1][1] = 0.f;
+    const float *cbj = cbs + 4 * j;
+    for (int s = w; s < p.Sin; s += p.NW) {
+        uint32_t wd[NI][2][4];
+#pragma unroll
+        for (int n = 0; n < NI; ++n)
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                wd[n][h][0] = cw[n][h].x;
+                wd[n][h][1] = cw[n][h].y;
+                wd[n][h][2] = cw[n][h].z;
+                wd[n][h][3] = cw[n][h].w;
+            }
+        if (s + p.NW < p.Sin) {
+#pragma unroll
+            for (int n = 0; n < NI; ++n)
+#pragma unroll
+                for (int h = 0; h < 2; ++h)
+                    cw[n][h] = ld_codes(eg + (((size_t)(s + p.NW) * 2 + h) * p.Ip + base + r + 16 * n) * kGS);
+        }
+        const float *xsj = xs + s * 256 + 4 * j;
+#pragma unroll
+        for (int g = 0; g < kGS; ++g) {
+            const float4 xv = *reinterpret_cast<const float4 *>(xsj + g * 16);
+#pragma unroll
+            for (int n = 0; n < NI; ++n)
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const int code = (wd[n][h][g >> 2] >> ((g & 3) * 8)) & 0xffu;
+                    const float4 c = *reinterpret_cast<const float4 *>(cbj + code * 16);
+                    float a = acc[n][h][g & 1];
+                    a = fmaf(xv.x, c.x, a);
+                    a = fmaf(xv.y, c.y, a);
+                    a = fmaf(xv.z, c.z, a);
+                    a = fmaf(xv.w, c.w, a);
+                    acc[n][h][g & 1] = a;
+                }
+        }
+    }
+#pragma unroll
+    for (int n = 0; n < NI; ++n)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const float v = quad_sum(acc[n][h][0] + acc[n][h][1]);
+            if (j == 0) part[h][w][r + 16 * n] = v;
+        }
+    __syncthreads();
+    if (tid >= R) return;
+    const int i = base + tid;
+    if (i >= p.I) return;
+    float g = 0.f, u = 0.f;
+    for (int k = 0; k < p.NW; ++k) {
+        g += part[0][k][tid];
+        u += part[1][k][tid];
+    }
+    g *= sg;
+    u *= su;
+    p.inter[(size_t)pr * p.I + i] = g / (1.f + expf(-g)) * u;
+}
+
+// Down projection + combine.  Workgroup = (token, 16*RPL hidden rows); wave w
+// owns slots w, w+NW, ...; lane (r, j) owns rows h = base + r + 16n.  The
+// token's k intermediate vectors and the down codebook are staged in LDS.
+// part[j][h] = s_dn[e_j][h] * dot_j(h), then y[t][h] = sum_j w_j * part[j][h]
+// over active slots in slot order (the reference's w * (s * sum) order).  A
+// wave's first slot, its codes (up to kDS slices) and its row scales are
+// loaded before the staging stores, so the kernel has one dependent round
+// trip (slot id -> codes) besides the staging.
+constexpr int kDS = 4;
+template <typename T, int RPL>
+__global__ __launch_bounds__(1024) void moe_down_dec_kernel(MoEDecParams p) {
+    constexpr int R = 16 * RPL;
+    extern __shared__ float sm[];
+    float *cbs = sm;                       // [256][16]
+    float *is = sm + kCB * 16;             // [k][Si*256], zero past I
+    __shared__ float part[32][R];
+    __shared__ float wsl[32];
+    __shared__ int onl[32];
+    const int tid = threadIdx.x, nthr = blockDim.x;
+    const int lane = tid & 63, w = tid >> 6;
+    const int r = lane >> 2, j = lane & 3;
+    const int t = blockIdx.y;
+    const int base = blockIdx.x * R;       // base + R <= Hp
+    const int IS = p.Si * 256, i4 = IS / 4, n4 = p.k * i4;
+
+    float4 cv4[2], iv4[4];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) cv4[u] = reinterpret_cast<const float4 *>(p.cb_dn)[min(tid + u * nthr, 1023)];
+    const float *it = p.inter + (size_t)t * p.k * p.I;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        // rows of inactive slots are stale and never used
+        const int b = min(tid + u * nthr, n4 - 1);
+        const int jj = b / i4, el = (b - jj * i4) * 4;
+        iv4[u] = *reinterpret_cast<const float4 *>(it + (size_t)jj * p.I + min(el, p.I - 4));
+        if (el >= p.I) iv4[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    int e0 = 0;
+    const bool on0 = w < p.k && slot_active(p.idx, p.w, t * p.k + min(w, p.k - 1), p.E, &e0);
+    uint4 cw[kDS][RPL];
+    float dsc[RPL];
+    {
+        const int ee = on0 ? e0 : 0;
+        const uint8_t *ed = p.dn + (size_t)ee * p.Si * p.Hp * kGS;
+#pragma unroll
+        for (int s = 0; s < kDS; ++s)
+#pragma unroll
+            for (int n = 0; n < RPL; ++n)
+                cw[s][n] = ld_codes(ed + ((size_t)min(s, p.Si - 1) * p.Hp + base + r + 16 * n) * kGS);
+#pragma unroll
+        for (int n = 0; n < RPL; ++n) dsc[n] = p.dns[(size_t)ee * p.H + min(base + r + 16 * n, p.H - 1)];
+    }
+    if (tid < p.k) {
+        int e;
+        onl[tid] = slot_active(p.idx, p.w, t * p.k + tid, p.E, &e) ? 1 : 0;
+        wsl[tid] = p.w[t * p.k + tid];
+    }
+#pragma unroll
+    for (int u = 0; u < 2; ++u) reinterpret_cast<float4 *>(cbs)[min(tid + u * nthr, 1023)] = cv4[u];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) reinterpret_cast<float4 *>(is)[min(tid + u * nthr, n4 - 1)] = iv4[u];
+    for (int b = tid + 2 * nthr; b < 1024; b += nthr)      // fewer than 512 threads
+        reinterpret_cast<float4 *>(cbs)[b] = reinterpret_cast<const float4 *>(p.cb_dn)[b];
+    for (int b = tid + 4 * nthr; b < n4; b += nthr) {      // k*I > 16 * threads
+        const int jj = b / i4, el = (b - jj * i4) * 4;
+        reinterpret_cast<float4 *>(is)[b] = el < p.I
+            ? *reinterpret_cast<const float4 *>(it + (size_t)jj * p.I + el) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    __syncthreads();
+    const float *cbj = cbs + 4 * j;
+    for (int js = w; js < p.k; js += p.NW) {
+        int e = e0;
+        bool on = on0;
+        if (js != w) {                             // later slots of this wave (k > NW)
+            on = slot_active(p.idx, p.w, t * p.k + js, p.E, &e);
+            const int ee = on ? e : 0;
+            const uint8_t *ed = p.dn + (size_t)ee * p.Si * p.Hp * kGS;
+#pragma unroll
+            for (int s = 0; s < kDS; ++s)
+#pragma unroll
+                for (int n = 0; n < RPL; ++n)
+                    cw[s][n] = ld_codes(ed + ((size_t)min(s, p.Si - 1) * p.Hp + base + r + 16 * n) * kGS);
+#pragma unroll
+            for (int n = 0; n < RPL; ++n) dsc[n] = p.dns[(size_t)ee * p.H + min(base + r + 16 * n, p.H - 1)];
+        }
+        if (!on) continue;                         // wave-uniform
+        const uint8_t *ed = p.dn + (size_t)e * p.Si * p.Hp * kGS;
+        float acc[RPL][2];
+#pragma unroll
+        for (int n = 0; n < RPL; ++n) acc[n][0] = acc[n][1] = 0.f;
+        for (int s = 0; s < p.Si; ++s) {
+            uint4 cs[RPL];
+#pragma unroll
+            for (int n = 0; n < RPL; ++n) {
+                cs[n] = cw[0][n];
+#pragma unroll
+                for (int q = 1; q < kDS; ++q)
+                    if (s == q) cs[n] = cw[q][n];
+                if (s >= kDS) cs[n] = ld_codes(ed + ((size_t)s * p.Hp + base + r + 16 * n) * kGS);
+            }
+            const float *ij = is + js * IS + s * 256 + 4 * j;
+#pragma unroll
+            for (int g = 0; g < kGS; ++g) {
+                const float4 iv = *reinterpret_cast<const float4 *>(ij + g * 16);
+#pragma unroll
+                for (int n = 0; n < RPL; ++n) {
+                    const uint32_t wd = g < 4 ? cs[n].x : g < 8 ? cs[n].y : g < 12 ? cs[n].z : cs[n].w;
+                    const int code = (wd >> ((g & 3) * 8)) & 0xffu;
+                    const float4 c = *reinterpret_cast<const float4 *>(cbj + code * 16);
+                    float a = acc[n][g & 1];
+                    a = fmaf(iv.x, c.x, a);
+                    a = fmaf(iv.y, c.y, a);
+                    a = fmaf(iv.z, c.z, a);
+                    a = fmaf(iv.w, c.w, a);
+                    acc[n][g & 1] = a;
+                }
+            }
+        }
+#pragma unroll
+        for (int n = 0; n < RPL; ++n) {
+            const float v = quad_sum(acc[n][0] + acc[n][1]);
+            if (j == 0) part[js][r + 16 * n] = dsc[n] * v;
+        }
+    }
+    __syncthreads();
+    if (tid >= R) return;
+    const int h = base + tid;
+    if (h >= p.H) return;
+    float y = 0.f;
+    for (int js = 0; js < p.k; ++js)
+        if (onl[js]) y += wsl[js] * part[js][tid];
+    store_act(static_cast<T *>(p.y), (size_t)t * p.H + h, y);
+}
+
+// ---------------------------------------------------------------------------
+// Many tokens (block_dim 16): LUT path with the LUT slice in LDS, split over
+// slices.  A "pair" is one routed (token, slot).
+//  A. LUT_in[t][g][k] of every token (lut_build_kernel).
+//  B. moe_gu_part: workgroup = (pair, input slice s): stage LUT_in[t][s]
+//     (16 groups x 256, 16 KB) in LDS, gather the slice's 16 codes of all 2I
+//     gate/up rows of the pair's expert -> part_gu[pair][s][2*Ip].
+//  D. moe_dn_part: workgroup = (pair, intermediate slice sd): sum part_gu over
+//     the input slices in order, scale, SwiGLU for the slice's 256
+//     intermediate values, build their LUT_down rows in LDS, gather the slice's
+//     codes of all H down rows -> part_dn[pair][sd][H].
+//  E. moe_combine_parts: y[t][h] = sum_j w_j * (s_dn[e_j][h] * sum_sd part_dn)
+//     over active slots in slot order.
+struct MoEPartParams {
+    const uint8_t *gu;      // [E][Sin][2][Ip][16]
+    const uint8_t *dn;      // [E][Si][Hp][16]
+    const float *gus;       // [E][2I]
+    const float *dns;       // [E][H]
+    const float *cb_dn;     // [256][16]
+    const float *lut_in;    // [T][Sin*16][256]
+    float *part_gu;         // [P][Sin][2*Ip]
+    float *part_dn;         // [P][Si][H]
+    const int *idx;         // [T][k]
+    const float *w;         // [T][k]
+    void *y;                // [T][H]
+    int E, H, I, Sin, Si, Ip, Hp, T, k;
+};
+
+constexpr int kRowsPT = 8;   // code rows per thread per batch in the gather kernels
+
+__device__ __forceinline__ float gather16_lds(const float *L, uint4 c) {
+    const uint32_t w4[4] = {c.x, c.y, c.z, c.w};
+    float v[kGS];
+#pragma unroll
+    for (int g = 0; g < kGS; ++g) v[g] = L[g * kCB + ((w4[g >> 2] >> ((g & 3) * 8)) & 0xffu)];
+    float a = 0.f;
+#pragma unroll
+    for (int g = 0; g < kGS; ++g) a += v[g];
+    return a;
+}
+
+__global__ __launch_bounds__(kNT) void moe_gu_part_kernel(MoEPartParams p) {
+    __shared__ float4 lut4[kGS * kCB / 4];          // LUT_in[t][s*16 .. s*16+15][256]
+    const float *lut = reinterpret_cast<const float *>(lut4);
+    const int tid = threadIdx.x;
+    const int pr = blockIdx.x / p.Sin;
+    const int s = blockIdx.x - pr * p.Sin;
+    int e;
+    if (!slot_active(p.idx, p.w, pr, p.E, &e)) return;
+    const int t = pr / p.k;
+    const int nrow = 2 * p.Ip;
+    const float4 *src = reinterpret_cast<const float4 *>(p.lut_in + ((size_t)t * p.Sin + s) * kGS * kCB);
+    float4 v[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) v[u] = src[tid + u * kNT];
+    const uint8_t *codes = p.gu + ((size_t)e * p.Sin + s) * nrow * kGS;
+    uint4 cw[kRowsPT];
+#pragma unroll
+    for (int u = 0; u < kRowsPT; ++u) cw[u] = ld_codes(codes + (size_t)min(tid + u * kNT, nrow - 1) * kGS);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) lut4[tid + u * kNT] = v[u];
+    __syncthreads();
+    float *out = p.part_gu + ((size_t)pr * p.Sin + s) * nrow;
+    for (int r0 = 0; r0 < nrow; r0 += kRowsPT * kNT) {
+        uint4 nx[kRowsPT];
+        const bool more = r0 + kRowsPT * kNT < nrow;
+        if (more) {
+#pragma unroll
+            for (int u = 0; u < kRowsPT; ++u)
+                nx[u] = ld_codes(codes + (size_t)min(r0 + kRowsPT * kNT + tid + u * kNT, nrow - 1) * kGS);
+        }
+#pragma unroll
+        for (int u = 0; u < kRowsPT; ++u) {
+            const int row = r0 + tid + u * kNT;
+            const float a = gather16_lds(lut, cw[u]);
+            if (row < nrow) out[row] = a;
+        }
+        if (more) {
+#pragma unroll
+            for (int u = 0; u < kRowsPT; ++u) cw[u] = nx[u];
+        }
+    }
+}
+
+__global__ __launch_bounds__(kNT) void moe_dn_part_kernel(MoEPartParams p) {
+    __shared__ float inter_s[kCB];                  // the slice's 256 intermediate values
+    __shared__ float lut[kGS * kCB];                // LUT_down rows of the slice's 16 groups
+    const int tid = threadIdx.x;
+    const int pr = blockIdx.x / p.Si;
+    const int sd = blockIdx.x - pr * p.Si;
+    int e;
+    if (!slot_active(p.idx, p.w, pr, p.E, &e)) return;
+    const int nrow = 2 * p.Ip;
+    // ---- loads: gate/up partials of intermediate index i, codebook row tid,
+    // down codes of the first rows
+    const int i = sd * kCB + tid;                   // < Ip (Ip is a multiple of 256)
+    const float *pg = p.part_gu + (size_t)pr * p.Sin * nrow;
+    float gv[16], uv[16];
+#pragma unroll
+    for (int s = 0; s < 16; ++s) {
+        const int ss = min(s, p.Sin - 1);
+        gv[s] = pg[(size_t)ss * nrow + i];
+        uv[s] = pg[(size_t)ss * nrow + p.Ip + i];
+    }
+    const int ic = min(i, p.I - 1);
+    const float sg = p.gus[(size_t)e * 2 * p.I + ic];
+    const float su = p.gus[(size_t)e * 2 * p.I + p.I + ic];
+    float c[kGS];
+    {
+        const float4 *c4 = reinterpret_cast<const float4 *>(p.cb_dn + tid * kGS);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const float4 f = c4[q];
+            c[4 * q] = f.x;
+            c[4 * q + 1] = f.y;
+            c[4 * q + 2] = f.z;
+            c[4 * q + 3] = f.w;
+        }
+    }
+    const uint8_t *codes = p.dn + ((size_t)e * p.Si + sd) * p.Hp * kGS;
+    uint4 cw[kRowsPT];
+#pragma unroll
+    for (int u = 0; u < kRowsPT; ++u) cw[u] = ld_codes(codes + (size_t)min(tid + u * kNT, p.Hp - 1) * kGS);
+    // ---- SwiGLU of intermediate value i (partials summed in slice order)
+    {
+        float g = 0.f, u = 0.f;
+#pragma unroll
+        for (int s = 0; s < 16; ++s) {
+            if (s < p.Sin) {
+                g += gv[s];
+                u += uv[s];
+            }
+        }
+        for (int s = 16; s < p.Sin; ++s) {       // more than 16 input slices (H > 4096)
+            g += pg[(size_t)s * nrow + i];
+            u += pg[(size_t)s * nrow + p.Ip + i];
+        }
+        g *= sg;
+        u *= su;
+        inter_s[tid] = i < p.I ? g / (1.f + expf(-g)) * u : 0.f;
+    }
+    __syncthreads();
+    // ---- LUT_down[g][tid] for the slice's 16 groups
+#pragma unroll
+    for (int g = 0; g < kGS; ++g) {
+        float dot = 0.f;
+#pragma unroll
+        for (int d = 0; d < kGS; ++d) dot = fmaf(inter_s[g * kGS + d], c[d], dot);
+        lut[g * kCB + tid] = dot;
+    }
+    __syncthreads();
+    float *out = p.part_dn + ((size_t)pr * p.Si + sd) * p.H;
+    for (int r0 = 0; r0 < p.H; r0 += kRowsPT * kNT) {
+        uint4 nx[kRowsPT];
+        const bool more = r0 + kRowsPT * kNT < p.H;
+        if (more) {
+#pragma unroll
+            for (int u = 0; u < kRowsPT; ++u)
+                nx[u] = ld_codes(codes + (size_t)min(r0 + kRowsPT * kNT + tid + u * kNT, p.Hp - 1) * kGS);
+        }
+#pragma unroll
+        for (int u = 0; u < kRowsPT; ++u) {
+            const int h = r0 + tid + u * kNT;
+            const float a = gather16_lds(lut, cw[u]);
+            if (h < p.H) out[h] = a;
+        }
+        if (more) {
+#pragma unroll
+            for (int u = 0; u < kRowsPT; ++u) cw[u] = nx[u];
+        }
+    }
+}
+
+// Slots are taken KB at a time with all their loads (slot ids, weights, down
+// partials of up to kCS slices, scales) in flight together: two round trips
+// per batch instead of two per slot.
+template <typename T>
+__global__ __launch_bounds__(kNT) void moe_combine_parts_kernel(MoEPartParams p) {
+    constexpr int KB = 16, kCS = 4;
+    const int t = blockIdx.y;
+    const int h = min((int)(blockIdx.x * kNT + threadIdx.x), p.H - 1);
+    float y = 0.f;
+    for (int j0 = 0; j0 < p.k; j0 += KB) {
+        int ev[KB];
+        float wv[KB];
+        bool on[KB];
+#pragma unroll
+        for (int u = 0; u < KB; ++u) {
+            const int pr = t * p.k + min(j0 + u, p.k - 1);
+            on[u] = slot_active(p.idx, p.w, pr, p.E, &ev[u]) && j0 + u < p.k;
+            wv[u] = p.w[pr];
+        }
+        float a[KB], sc[KB];
+#pragma unroll
+        for (int u = 0; u < KB; ++u) {
+            const int pr = t * p.k + min(j0 + u, p.k - 1);
+            const int e = on[u] ? ev[u] : 0;
+            const float *pd = p.part_dn + (size_t)pr * p.Si * p.H + h;
+            float v[kCS];
+#pragma unroll
+            for (int s = 0; s < kCS; ++s) v[s] = pd[(size_t)min(s, p.Si - 1) * p.H];
+            float acc = 0.f;
+#pragma unroll
+            for (int s = 0; s < kCS; ++s)
+                if (s < p.Si) acc += v[s];
+            for (int s = kCS; s < p.Si; ++s) acc += pd[(size_t)s * p.H];   // I > 1024
+            a[u] = acc;
+            sc[u] = p.dns[(size_t)e * p.H + h];
+        }
+#pragma unroll
+        for (int u = 0; u < KB; ++u)
+            if (on[u]) y += wv[u] * (sc[u] * a[u]);
+    }
+    if ((int)(blockIdx.x * kNT + threadIdx.x) < p.H) store_act(static_cast<T *>(p.y), (size_t)t * p.H + h, y);
+}
+
 template <typename T>
 __global__ __launch_bounds__(kNT) void moe_combine_kernel(MoEParams p) {
     // Slot weights (0 for skipped slots) and all per-pair outputs are loaded
@@ -285,6 +783,112 @@ __global__ __launch_bounds__(kNT) void moe_route_kernel(const float *logits, int
 
 namespace {
 
+constexpr size_t kMaxLds = 160 * 1024;
+// From this many tokens the LUT path (LUT in LDS, split over slices) beats
+// computing LUT entries in place: measured 24.3 vs 23.7 us at 4 tokens and
+// 26.5 vs 40.5 us at 8 on the 512-expert H 2048 / I 768 top-10 layer.
+constexpr int kPartsMinTokens = 5;
+
+template <typename T>
+int moe_forward_dec(MoE *m, const void *x, const int *idx, const float *w, void *y, int T_, int k,
+                    hipStream_t st) {
+    const size_t P = (size_t)T_ * k;
+    int rc = m->inter.ensure(P * m->I * sizeof(float));
+    if (rc) return rc;
+    MoEDecParams p{};
+    p.gu = m->gu.as<uint8_t>();
+    p.dn = m->dn.as<uint8_t>();
+    p.gus = m->gus.as<float>();
+    p.dns = m->dns.as<float>();
+    p.cb_in = m->cb_in.as<float>();
+    p.cb_dn = m->cb_dn.as<float>();
+    p.x = x;
+    p.inter = m->inter.as<float>();
+    p.idx = idx;
+    p.w = w;
+    p.y = y;
+    p.E = m->E;
+    p.H = m->H;
+    p.I = m->I;
+    p.Sin = m->Sin;
+    p.Si = m->Si;
+    p.Ip = m->Ip;
+    p.Hp = m->Hp;
+    p.T = T_;
+    p.k = k;
+    // gate/up + SwiGLU: 32 intermediate rows per workgroup
+    {
+        constexpr int NI = 2;
+        p.NW = std::min(m->Sin, 16);
+        const size_t lds = (size_t)(kCB * 16 + m->Sin * 256) * sizeof(float);
+        static size_t granted = 0;
+        const void *fn = reinterpret_cast<const void *>(&moe_up_dec_kernel<T, NI>);
+        rc = ensure_dyn_lds(fn, lds, &granted);
+        if (rc) return rc;
+        const int nib = (m->I + 16 * NI - 1) / (16 * NI);
+        hipLaunchKernelGGL((moe_up_dec_kernel<T, NI>), dim3(P * nib), dim3(64 * p.NW), lds, st, p);
+    }
+    // down + combine: 16 or 32 hidden rows per workgroup
+    {
+        p.NW = std::min(k, 16);
+        const size_t lds = (size_t)(kCB * 16 + (size_t)k * m->Si * 256) * sizeof(float);
+        const bool r2 = (long)T_ * ((m->H + 31) / 32) >= 192;
+        const void *fn = r2 ? reinterpret_cast<const void *>(&moe_down_dec_kernel<T, 2>)
+                            : reinterpret_cast<const void *>(&moe_down_dec_kernel<T, 1>);
+        static size_t granted1 = 0, granted2 = 0;
+        rc = ensure_dyn_lds(fn, lds, r2 ? &granted2 : &granted1);
+        if (rc) return rc;
+        if (r2)
+            hipLaunchKernelGGL((moe_down_dec_kernel<T, 2>), dim3((m->H + 31) / 32, T_), dim3(64 * p.NW),
+                               lds, st, p);
+        else
+            hipLaunchKernelGGL((moe_down_dec_kernel<T, 1>), dim3((m->H + 15) / 16, T_), dim3(64 * p.NW),
+                               lds, st, p);
+    }
+    OJX_HIP(hipGetLastError());
+    return OJASX_OK;
+}
+
+template <typename T>
+int moe_forward_parts(MoE *m, const void *x, const int *idx, const float *w, void *y, int T_, int k,
+                      int dtype, hipStream_t st) {
+    const size_t P = (size_t)T_ * k;
+    const int Gp_in = m->Sin * kGS;
+    int rc = m->lut_in.ensure((size_t)T_ * Gp_in * kCB * sizeof(float));
+    if (!rc) rc = m->part_gu.ensure(P * m->Sin * 2 * m->Ip * sizeof(float));
+    if (!rc) rc = m->part_dn.ensure(P * m->Si * m->H * sizeof(float));
+    if (rc) return rc;
+    rc = launch_lut_build(x, m->cb_in.as<float>(), T_, m->H, m->D, m->Gin, Gp_in,
+                          m->lut_in.as<float>(), dtype, st);
+    if (rc) return rc;
+    MoEPartParams p{};
+    p.gu = m->gu.as<uint8_t>();
+    p.dn = m->dn.as<uint8_t>();
+    p.gus = m->gus.as<float>();
+    p.dns = m->dns.as<float>();
+    p.cb_dn = m->cb_dn.as<float>();
+    p.lut_in = m->lut_in.as<float>();
+    p.part_gu = m->part_gu.as<float>();
+    p.part_dn = m->part_dn.as<float>();
+    p.idx = idx;
+    p.w = w;
+    p.y = y;
+    p.E = m->E;
+    p.H = m->H;
+    p.I = m->I;
+    p.Sin = m->Sin;
+    p.Si = m->Si;
+    p.Ip = m->Ip;
+    p.Hp = m->Hp;
+    p.T = T_;
+    p.k = k;
+    hipLaunchKernelGGL(moe_gu_part_kernel, dim3(P * m->Sin), dim3(kNT), 0, st, p);
+    hipLaunchKernelGGL(moe_dn_part_kernel, dim3(P * m->Si), dim3(kNT), 0, st, p);
+    hipLaunchKernelGGL((moe_combine_parts_kernel<T>), dim3((m->H + kNT - 1) / kNT, T_), dim3(kNT), 0, st, p);
+    OJX_HIP(hipGetLastError());
+    return OJASX_OK;
+}
+
 int moe_forward(MoE *m, const void *x, const int *idx, const float *w, void *y, int T_, int k,
                 int dtype, hipStream_t st) {
     if (k <= 0 || T_ <= 0) return OJASX_OK;
@@ -295,6 +899,21 @@ int moe_forward(MoE *m, const void *x, const int *idx, const float *w, void *y, 
     if (T_ > 65535) {
         set_error("too many tokens in one call");
         return OJASX_ERR_INVALID;
+    }
+    {
+        // single-kernel-per-stage path: block_dim 16, aligned activations,
+        // the staged vectors fit LDS
+        const size_t align = dtype == OJASX_DTYPE_F32 ? 16 : 8;
+        const bool ok = m->D == 16 && k <= 32 && m->H % 4 == 0 && m->I % 4 == 0 &&
+                        reinterpret_cast<uintptr_t>(x) % align == 0 &&
+                        (size_t)(kCB * 16 + (size_t)k * m->Si * 256) * 4 <= kMaxLds &&
+                        (size_t)(kCB * 16 + m->Sin * 256) * 4 <= kMaxLds;
+        if (m->D == 16 && T_ >= kPartsMinTokens)
+            return dtype == OJASX_DTYPE_F32 ? moe_forward_parts<float>(m, x, idx, w, y, T_, k, dtype, st)
+                                            : moe_forward_parts<__hip_bfloat16>(m, x, idx, w, y, T_, k, dtype, st);
+        if (ok)
+            return dtype == OJASX_DTYPE_F32 ? moe_forward_dec<float>(m, x, idx, w, y, T_, k, st)
+                                            : moe_forward_dec<__hip_bfloat16>(m, x, idx, w, y, T_, k, st);
     }
     const size_t P = (size_t)T_ * k;
     const int Gp_in = m->Sin * kGS;

@@ -144,3 +144,55 @@ def test_repeat_deterministic_and_skips(pkg, dev, baseline_moe):
                            m["dn_codes"], m["dn_scales"], idx[0], w[0])
     assert rel_err(ys[0][0], want) < 1e-5
     assert all(np.array_equal(ys[0], yy) for yy in ys[1:])
+
+
+def device_moe(pkg, dev, nat, x_t, idx, w, k, dtype_tag=0):
+    import torch
+    T, H = x_t.shape
+    y = torch.empty(T, H, device=dev, dtype=x_t.dtype)
+    it = torch.from_numpy(np.ascontiguousarray(idx, np.int32)).to(dev)
+    wt = torch.from_numpy(np.ascontiguousarray(w, np.float32)).to(dev)
+    rc = pkg.lib().ojasx_moe_forward_device(nat.handle, vp(x_t), vp(it), vp(wt), vp(y), T, k,
+                                            dtype_tag, None)
+    assert rc == 0, pkg.lib().ojasx_get_last_error()
+    torch.cuda.synchronize()
+    return y.float().cpu().numpy()
+
+
+@pytest.mark.parametrize("T", [3, 6])   # below / from the token count that selects the LUT path
+@pytest.mark.parametrize("E,H,I,k,D", [
+    (40, 480, 208, 20, 16),    # partial input/intermediate slices; 20 slots > 16 waves
+    (64, 512, 256, 32, 16),    # the largest k of the single-kernel stages
+    (48, 256, 96, 6, 8),       # block_dim 8: LUT-build + gather path
+    (24, 4352, 1152, 4, 16),   # 17 input slices, 5 intermediate slices
+])
+def test_moe_shapes(pkg, dev, E, H, I, k, D, T):
+    import torch
+    m = gen.moe(E=E, H=H, I=I, T=T, D=D, seed=E + k, scales="u")
+    nat = make_native(pkg, m, E, H, I, k)
+    idx, w = cpu.router_topk(m["logits"], k, renorm=True)
+    idx[0, 1] = idx[0, 0]                           # a repeated expert within a token
+    y = device_moe(pkg, dev, nat, torch.from_numpy(m["x"]).to(dev), idx, w, k)
+    for t in range(T):
+        want = cpu.moe_forward(m["x"][t], m["cb_in"], m["cb_down"], m["gu_codes"], m["gu_scales"],
+                               m["dn_codes"], m["dn_scales"], idx[t], w[t])
+        assert rel_err(y[t], want) < 1e-5, t
+
+
+@pytest.mark.parametrize("dtype_tag", [0, 1])
+def test_moe_unaligned_activations(pkg, dev, baseline_moe, dtype_tag):
+    """x not aligned for vector loads takes the LUT-build path."""
+    import torch
+    m, nat = baseline_moe
+    T = 2
+    tdt = torch.float32 if dtype_tag == 0 else torch.bfloat16
+    buf = torch.empty(T * 2048 + 1, device=dev, dtype=tdt)
+    xt = buf[1:].view(T, 2048)
+    xt.copy_(torch.from_numpy(m["x"][:T]).to(dev).to(tdt))
+    idx, w = cpu.router_topk(m["logits"][:T], 10)
+    y = device_moe(pkg, dev, nat, xt, idx, w, 10, dtype_tag)
+    xr = xt.float().cpu().numpy()
+    for t in range(T):
+        want = cpu.moe_forward(xr[t], m["cb_in"], m["cb_down"], m["gu_codes"], m["gu_scales"],
+                               m["dn_codes"], m["dn_scales"], idx[t], w[t])
+        assert rel_err(y[t], want) < (1e-5 if dtype_tag == 0 else 1e-2)
