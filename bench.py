@@ -10,16 +10,24 @@ exceeds the 256 MB Infinity Cache and the codes really stream from HBM.
 
 Printed: one JSON line.  ``value`` is microseconds per call (lower is
 better), measured with HIP events on the launch stream over the K timed
-steps.  ``roofline`` relates the algorithmic code bytes of one call to that
-per-call time; ``cpu_baseline`` times the reference's own C++ engine
-(compiled from its sources into oracle/_ref when present, else the repo's C
-restatement) on the host, one thread, on the same inputs.  Extra fields give
-the MoE and KV-decode figures of the same run.
+back-to-back steps (it includes the GPU's gap between dependent launches).
+``roofline`` relates the algorithmic code bytes of one launch to the
+kernel's own average duration, measured live over another K steps with the
+library's start/stop events (hipExtLaunchKernelGGL, the kernel's begin and
+end on the launch stream); ``traffic`` is the HBM bytes per launch from the
+rocprofv3 FETCH_SIZE/WRITE_SIZE summary under profiles/ when present.
+``cpu_baseline`` times the reference's own C++ engine (compiled from its
+sources into oracle/_ref when present, else the repo's C restatement) on the
+host, one thread, on the same inputs.  Extra fields give the MoE and
+KV-decode figures of the same run.  Before the timed region one 64 MiB
+device-to-device copy runs: a kernel of known traffic that calibrates the
+PMC byte counters of a profiled run of this script.
 """
 import argparse
 import ctypes
 import json
 import os
+import re
 import sys
 import time
 
@@ -30,6 +38,32 @@ import numpy as np  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0
 M_GU, K_GU = 6912, 2560
+CAL_COPY_BYTES = 64 << 20
+TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "lut_dec_kernel_2560x6912_b1_hbm_traffic.md")
+
+
+def measured_traffic():
+    """HBM bytes per launch of the benchmarked kernel, from the committed
+    rocprofv3 PMC summary (None when absent)."""
+    try:
+        with open(TRAFFIC_SUMMARY) as f:
+            m = re.search(r"traffic_bytes_per_launch:\s*(\d+)", f.read())
+        return int(m.group(1)) if m else None
+    except OSError:
+        return None
+
+
+def timed_kernels(pkg, run):
+    """Run `run()` with the library's per-kernel start/stop events on and
+    return {kernel: {"calls", "avg_us"}}."""
+    pkg._lib.kernel_timing_enable(True)
+    try:
+        run()
+        rep = pkg._lib.kernel_timing_report()
+    finally:
+        pkg._lib.kernel_timing_enable(False)
+    rep.pop("_dropped", None)
+    return rep
 
 
 def parse():
@@ -118,10 +152,12 @@ def bench_moe(pkg, torch, steps, warmup, cpu_seconds, do_cpu):
         torch.cuda.synchronize()
         us = e0.elapsed_time(e1) * 1e3 / nsteps
         code_bytes = float(distinct.mean()) * per_expert
+        kern = timed_kernels(pkg, lambda: [fwd(i) for i in range(min(nsteps, 200))])
         res[f"T{T}"] = {"us_per_call": round(us, 3), "distinct_experts_mean": float(distinct.mean()),
                         "code_bytes_per_call": int(code_bytes),
                         "achieved_GBs": round(code_bytes / (us * 1e-6) / 1e9, 2),
-                        "frac_of_8TBs": round(code_bytes / (us * 1e-6) / 8e12, 5)}
+                        "frac_of_8TBs": round(code_bytes / (us * 1e-6) / 8e12, 5),
+                        "kernels_avg_us": {k: v["avg_us"] for k, v in kern.items()}}
     if do_cpu and ref.available():
         m = banks[0][1]
         R = ref.RefMoE(m["cb_in"], m["cb_down"], m["gu_codes"], m["gu_scales"], m["dn_codes"],
@@ -173,9 +209,11 @@ def bench_kv(pkg, torch, steps):
         us = e0.elapsed_time(e1) * 1e3 / n
         code_bytes = 2 * T * 8 * 8
         all_bytes = code_bytes + 2 * T * 8 * 4
+        kern = timed_kernels(pkg, lambda: [call() for _ in range(200)])
         res[f"T{T}"] = {"us_per_call": round(us, 3), "code_bytes": code_bytes,
                         "achieved_code_GBs": round(code_bytes / (us * 1e-6) / 1e9, 2),
-                        "achieved_all_GBs": round(all_bytes / (us * 1e-6) / 1e9, 2)}
+                        "achieved_all_GBs": round(all_bytes / (us * 1e-6) / 1e9, 2),
+                        "kernels_avg_us": {k: v["avg_us"] for k, v in kern.items()}}
     return res
 
 
@@ -224,6 +262,13 @@ def main():
                                *base["csr"])
     rel = float(np.abs(y.cpu().numpy() - y_ref).max() / np.abs(y_ref).max())
 
+    # PMC calibration: one device-to-device copy of known size (read and write)
+    cal_src = torch.ones(CAL_COPY_BYTES // 4, device=dev)
+    cal_dst = torch.empty_like(cal_src)
+    cal_dst.copy_(cal_src)
+    torch.cuda.synchronize()
+    del cal_src, cal_dst
+
     n = len(handles)
     for i in range(args.warmup):
         fwd(handles[i % n], xp, yp, 1, 0, sp)
@@ -240,8 +285,13 @@ def main():
     us_call = ms * 1e3 / args.steps
 
     code_bytes = M_GU * (K_GU // 16)
-    achieved = code_bytes / (us_call * 1e-6) / 1e9
     all_bytes = wbytes + K_GU * 4 + M_GU * 4
+    # the kernel's own duration, same calls, library start/stop events
+    kern = timed_kernels(pkg, lambda: [fwd(handles[i % n], xp, yp, 1, 0, sp)
+                                       for i in range(args.steps)])
+    kname = max(kern, key=lambda k: kern[k]["calls"] * kern[k]["avg_us"])
+    kernel_us = kern[kname]["avg_us"]
+    achieved = code_bytes / (kernel_us * 1e-6) / 1e9
 
     out = {
         "metric": "LUT-GEMV 2560->6912 us/call (HBM GB/s on code bytes alongside)",
@@ -261,10 +311,15 @@ def main():
                    "out_features": M_GU, "weight_instances": n,
                    "working_set_MB": round(n * wbytes / 2**20, 1)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 5), "traffic": None,
-                     "algorithmic_bytes_per_call": code_bytes,
-                     "all_compulsory_bytes_per_call": all_bytes,
-                     "achieved_all_bytes_GBs": round(all_bytes / (us_call * 1e-6) / 1e9, 2)},
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 5),
+                     "traffic": measured_traffic(),
+                     "kernel": kname, "kernel_avg_us": round(kernel_us, 4),
+                     "kernel_launches_timed": kern[kname]["calls"],
+                     "algorithmic_bytes_per_launch": code_bytes,
+                     "all_compulsory_bytes_per_launch": all_bytes,
+                     "achieved_all_bytes_GBs": round(all_bytes / (kernel_us * 1e-6) / 1e9, 2),
+                     "call_period_GBs": round(code_bytes / (us_call * 1e-6) / 1e9, 2)},
+        "pmc_calibration_copy_bytes": CAL_COPY_BYTES,
         "parity_rel_err": rel,
         "wall_s_timed": round(t_wall, 3),
     }

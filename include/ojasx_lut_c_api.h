@@ -57,6 +57,15 @@ OJASX_API const char *ojasx_get_version(void);
 OJASX_API const char *ojasx_get_backend_name(void);
 /* No reference counterpart: message of the last failing call (thread-local). */
 OJASX_API const char *ojasx_get_last_error(void);
+/* No reference counterpart (measurement): while enabled, every kernel the
+ * library launches records events at its own start and end; the report
+ * synchronises the device, writes {"kernel": {"calls": n, "avg_us": t}, ...,
+ * "_dropped": d} (at most 65536 launches are kept) into buf, clears the
+ * records and returns the length needed including the terminating NUL.
+ * Not thread-safe; timing changes launch overhead, so time throughput with
+ * it disabled. */
+OJASX_API int ojasx_kernel_timing_enable(int enable);
+OJASX_API int ojasx_kernel_timing_report(char *buf, size_t buf_size);
 
 /* ---- linear (ref.h:46-91) --------------------------------------------- */
 /* ref.h:46-55.  codes_data is [out_features][in_features/block_dim] uint8,

@@ -21,6 +21,8 @@ SIGNATURES = {
     "ojasx_get_version": (ctypes.c_char_p, []),
     "ojasx_get_backend_name": (ctypes.c_char_p, []),
     "ojasx_get_last_error": (ctypes.c_char_p, []),
+    "ojasx_kernel_timing_enable": (ci, [ci]),
+    "ojasx_kernel_timing_report": (ci, [ctypes.c_char_p, ctypes.c_size_t]),
     "ojasx_create_linear": (vp, [ci, ci, ci, ci, vp, vp, vp, vp]),
     "ojasx_set_linear_outliers": (ci, [vp, ci, vp, vp, vp]),
     "ojasx_linear_forward": (ci, [vp, vp, vp, ci, ci]),
@@ -92,3 +94,21 @@ def check(rc, what):
         msg = lib().ojasx_get_last_error().decode(errors="replace")
         raise OjasxError(f"{what} failed with code {rc}: {msg}")
     return rc
+
+
+def kernel_timing_enable(on=True):
+    """Start (or stop) recording per-kernel start/stop events in the library;
+    starting clears earlier records."""
+    check(lib().ojasx_kernel_timing_enable(1 if on else 0), "ojasx_kernel_timing_enable")
+
+
+def kernel_timing_report():
+    """Synchronise the device and return {kernel: {"calls": n, "avg_us": t}}
+    for the launches recorded since timing was enabled (records are cleared)."""
+    import json
+    buf = ctypes.create_string_buffer(1 << 20)
+    n = lib().ojasx_kernel_timing_report(buf, len(buf))
+    if n <= 0:
+        raise OjasxError("ojasx_kernel_timing_report failed: "
+                         + lib().ojasx_get_last_error().decode(errors="replace"))
+    return json.loads(buf.value.decode())

@@ -3,6 +3,7 @@
 
 #include <hip/hip_runtime.h>
 #include <hip/hip_bf16.h>
+#include <hip/hip_ext.h>
 
 #include <cstddef>
 #include <cstdint>
@@ -35,6 +36,23 @@ struct DevBuf {
 };
 
 int upload(DevBuf &buf, const void *host, size_t n);  // ensure + memcpy
+
+// Optional per-kernel timing (ojasx_kernel_timing_*): when enabled, launches
+// record start/stop events at the kernel's own begin and end
+// (hipExtLaunchKernelGGL), kept per kernel name until the report.
+bool timing_on();
+void timing_events(const char *name, hipEvent_t *start, hipEvent_t *stop);
+
+#define OJX_LAUNCH(kernel, grid, block, lds, st, ...)                                      \
+    do {                                                                                    \
+        if (::ojx::timing_on()) {                                                           \
+            hipEvent_t _a = nullptr, _b = nullptr;                                          \
+            ::ojx::timing_events(#kernel, &_a, &_b);                                        \
+            hipExtLaunchKernelGGL(kernel, grid, block, lds, st, _a, _b, 0, __VA_ARGS__);     \
+        } else {                                                                            \
+            hipLaunchKernelGGL(kernel, grid, block, lds, st, __VA_ARGS__);                  \
+        }                                                                                   \
+    } while (0)
 
 // LUT[b][g][k] = <x_b[gD:(g+1)D], C[k]> for g < Gp (0 for g >= G) and all 256
 // centroids of the zero-padded codebook cb [256][D]; x [B][K] in dtype.
@@ -119,18 +137,6 @@ __device__ __forceinline__ void stage_to_lds(float *dst, const __hip_bfloat16 *s
 #pragma unroll
         for (int u = 0; u < U; ++u) dst[min(b + u * NT, n - 1)] = v[u];
     }
-}
-
-// Exclusive prefix sum over the 64 lanes of a wave of a value < 256.
-__device__ __forceinline__ int wave_excl_scan_u8(int v) {
-    const uint64_t lt = (uint64_t(1) << (threadIdx.x & 63)) - 1;
-    int r = 0;
-#pragma unroll
-    for (int b = 0; b < 8; ++b) {
-        const uint64_t m = __ballot(v & (1 << b));
-        r += __popcll(m & lt) << b;
-    }
-    return r;
 }
 
 }  // namespace ojx

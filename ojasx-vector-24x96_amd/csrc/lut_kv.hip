@@ -474,11 +474,11 @@ int kv_decode(const float *q, const uint8_t *kc, const float *ks, const uint8_t 
     if (fast && ntt == 1) {
         rc = ensure_dyn_lds(reinterpret_cast<const void *>(&kv_decode_chunk_kernel<8, 16, 4, 1>), lds, &g1);
         if (rc) return rc;
-        hipLaunchKernelGGL((kv_decode_chunk_kernel<8, 16, 4, 1>), grid, dim3(kNT), lds, st, p);
+        OJX_LAUNCH((kv_decode_chunk_kernel<8, 16, 4, 1>), grid, dim3(kNT), lds, st, p);
     } else if (fast) {
         rc = ensure_dyn_lds(reinterpret_cast<const void *>(&kv_decode_chunk_kernel<8, 16, 4, 4>), lds, &g4);
         if (rc) return rc;
-        hipLaunchKernelGGL((kv_decode_chunk_kernel<8, 16, 4, 4>), grid, dim3(kNT), lds, st, p);
+        OJX_LAUNCH((kv_decode_chunk_kernel<8, 16, 4, 4>), grid, dim3(kNT), lds, st, p);
     } else {
         // runtime-shape fallback: one token per thread
         p.Tc = kNT;
@@ -493,11 +493,11 @@ int kv_decode(const float *q, const uint8_t *kc, const float *ks, const uint8_t 
         grid.x = p.n_chunks;
         rc = ensure_dyn_lds(reinterpret_cast<const void *>(&kv_decode_chunk_kernel<0, 0, 8, 1>), lds, &g0);
         if (rc) return rc;
-        hipLaunchKernelGGL((kv_decode_chunk_kernel<0, 0, 8, 1>), grid, dim3(kNT), lds, st, p);
+        OJX_LAUNCH((kv_decode_chunk_kernel<0, 0, 8, 1>), grid, dim3(kNT), lds, st, p);
     }
     const int nch = p.n_chunks;
     if (nch > 1)
-        hipLaunchKernelGGL(kv_merge_kernel, dim3(Hq), dim3(kNT), (size_t)nch * 4, st,
+        OJX_LAUNCH(kv_merge_kernel, dim3(Hq), dim3(kNT), (size_t)nch * 4, st,
                            wk.o.as<float>(), wk.ml.as<float>(), nch, hd, out);
     OJX_HIP(hipGetLastError());
     return OJASX_OK;
@@ -610,7 +610,7 @@ OJASX_API int ojasx_kv_cache_append(OjasxKVHandle handle, int head_idx, const fl
     }
     OJX_HIP(hipMemcpy(c->kstage.ptr, k, (size_t)c->hd * 4, hipMemcpyHostToDevice));
     OJX_HIP(hipMemcpy(c->vstage.ptr, v, (size_t)c->hd * 4, hipMemcpyHostToDevice));
-    hipLaunchKernelGGL(kv_append_kernel, dim3(1), dim3(128), 0, nullptr, c->kstage.as<float>(),
+    OJX_LAUNCH(kv_append_kernel, dim3(1), dim3(128), 0, nullptr, c->kstage.as<float>(),
                        c->vstage.as<float>(), c->hd, c->D, hh.kc.as<uint8_t>() + (size_t)hh.len * c->G,
                        hh.vc.as<uint8_t>() + (size_t)hh.len * c->G, hh.ks.as<float>() + hh.len,
                        hh.vs.as<float>() + hh.len);

@@ -481,7 +481,7 @@ int launch_gather(const GatherParams &gp, int M, dim3 grid_y, size_t lds, hipStr
     int rc = ensure_dyn_lds(fn, lds, &granted);
     if (rc) return rc;
     dim3 grid((M + R - 1) / R, grid_y.y);
-    hipLaunchKernelGGL((lut_gather_kernel<R, BT, T>), grid, dim3(kNT), lds, st, gp);
+    OJX_LAUNCH((lut_gather_kernel<R, BT, T>), grid, dim3(kNT), lds, st, gp);
     return OJASX_OK;
 }
 
@@ -509,7 +509,7 @@ int launch_dec(Linear *L, const void *x, void *y, int B, size_t lds, hipStream_t
     int rc = ensure_dyn_lds(fn, lds, &granted);
     if (rc) return rc;
     dim3 grid((L->M + 16 * RPL - 1) / (16 * RPL), (B + BT - 1) / BT);
-    hipLaunchKernelGGL((lut_dec_kernel<T, BT, RPL>), grid, dim3(64 * dp.NW), lds, st, dp);
+    OJX_LAUNCH((lut_dec_kernel<T, BT, RPL>), grid, dim3(64 * dp.NW), lds, st, dp);
     OJX_HIP(hipGetLastError());
     return OJASX_OK;
 }
@@ -543,11 +543,11 @@ int launch(Linear *L, const void *x, void *y, int B, hipStream_t st) {
     const int Gp = L->S * kGS;
     dim3 g1(Gp, B);
     if (L->D == 16)
-        hipLaunchKernelGGL((lut_build_kernel<16, T>), g1, dim3(kCB), 0, st,
+        OJX_LAUNCH((lut_build_kernel<16, T>), g1, dim3(kCB), 0, st,
                            static_cast<const T *>(x), L->codebook.as<float>(), L->K, L->D, L->G,
                            Gp, L->lut.as<float>());
     else
-        hipLaunchKernelGGL((lut_build_kernel<0, T>), g1, dim3(kCB), 0, st,
+        OJX_LAUNCH((lut_build_kernel<0, T>), g1, dim3(kCB), 0, st,
                            static_cast<const T *>(x), L->codebook.as<float>(), L->K, L->D, L->G,
                            Gp, L->lut.as<float>());
 
@@ -616,12 +616,12 @@ int launch_lut_build(const void *x, const float *cb, int B, int K, int D, int G,
     const bool d16 = D == 16;
     if (dtype == OJASX_DTYPE_F32) {
         const float *xf = static_cast<const float *>(x);
-        if (d16) hipLaunchKernelGGL((lut_build_kernel<16, float>), g, dim3(kCB), 0, st, xf, cb, K, D, G, Gp, lut);
-        else hipLaunchKernelGGL((lut_build_kernel<0, float>), g, dim3(kCB), 0, st, xf, cb, K, D, G, Gp, lut);
+        if (d16) OJX_LAUNCH((lut_build_kernel<16, float>), g, dim3(kCB), 0, st, xf, cb, K, D, G, Gp, lut);
+        else OJX_LAUNCH((lut_build_kernel<0, float>), g, dim3(kCB), 0, st, xf, cb, K, D, G, Gp, lut);
     } else {
         const __hip_bfloat16 *xb = static_cast<const __hip_bfloat16 *>(x);
-        if (d16) hipLaunchKernelGGL((lut_build_kernel<16, __hip_bfloat16>), g, dim3(kCB), 0, st, xb, cb, K, D, G, Gp, lut);
-        else hipLaunchKernelGGL((lut_build_kernel<0, __hip_bfloat16>), g, dim3(kCB), 0, st, xb, cb, K, D, G, Gp, lut);
+        if (d16) OJX_LAUNCH((lut_build_kernel<16, __hip_bfloat16>), g, dim3(kCB), 0, st, xb, cb, K, D, G, Gp, lut);
+        else OJX_LAUNCH((lut_build_kernel<0, __hip_bfloat16>), g, dim3(kCB), 0, st, xb, cb, K, D, G, Gp, lut);
     }
     OJX_HIP(hipGetLastError());
     return OJASX_OK;
@@ -737,11 +737,11 @@ OJASX_API int ojasx_build_lut_device(const void *x, const float *codebook, int b
     hipStream_t st = static_cast<hipStream_t>(stream);
     dim3 grid(groups, batch_size);
     if (dtype == OJASX_DTYPE_F32)
-        hipLaunchKernelGGL(build_lut_kernel<float>, grid, dim3(kCB), 0, st,
+        OJX_LAUNCH(build_lut_kernel<float>, grid, dim3(kCB), 0, st,
                            static_cast<const float *>(x), codebook, groups, block_dim,
                            codebook_size, lut);
     else if (dtype == OJASX_DTYPE_BF16)
-        hipLaunchKernelGGL(build_lut_kernel<__hip_bfloat16>, grid, dim3(kCB), 0, st,
+        OJX_LAUNCH(build_lut_kernel<__hip_bfloat16>, grid, dim3(kCB), 0, st,
                            static_cast<const __hip_bfloat16 *>(x), codebook, groups, block_dim,
                            codebook_size, lut);
     else {

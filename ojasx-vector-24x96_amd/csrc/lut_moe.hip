@@ -826,7 +826,7 @@ int moe_forward_dec(MoE *m, const void *x, const int *idx, const float *w, void 
         rc = ensure_dyn_lds(fn, lds, &granted);
         if (rc) return rc;
         const int nib = (m->I + 16 * NI - 1) / (16 * NI);
-        hipLaunchKernelGGL((moe_up_dec_kernel<T, NI>), dim3(P * nib), dim3(64 * p.NW), lds, st, p);
+        OJX_LAUNCH((moe_up_dec_kernel<T, NI>), dim3(P * nib), dim3(64 * p.NW), lds, st, p);
     }
     // down + combine: 16 or 32 hidden rows per workgroup
     {
@@ -839,10 +839,10 @@ int moe_forward_dec(MoE *m, const void *x, const int *idx, const float *w, void 
         rc = ensure_dyn_lds(fn, lds, r2 ? &granted2 : &granted1);
         if (rc) return rc;
         if (r2)
-            hipLaunchKernelGGL((moe_down_dec_kernel<T, 2>), dim3((m->H + 31) / 32, T_), dim3(64 * p.NW),
+            OJX_LAUNCH((moe_down_dec_kernel<T, 2>), dim3((m->H + 31) / 32, T_), dim3(64 * p.NW),
                                lds, st, p);
         else
-            hipLaunchKernelGGL((moe_down_dec_kernel<T, 1>), dim3((m->H + 15) / 16, T_), dim3(64 * p.NW),
+            OJX_LAUNCH((moe_down_dec_kernel<T, 1>), dim3((m->H + 15) / 16, T_), dim3(64 * p.NW),
                                lds, st, p);
     }
     OJX_HIP(hipGetLastError());
@@ -882,9 +882,9 @@ int moe_forward_parts(MoE *m, const void *x, const int *idx, const float *w, voi
     p.Hp = m->Hp;
     p.T = T_;
     p.k = k;
-    hipLaunchKernelGGL(moe_gu_part_kernel, dim3(P * m->Sin), dim3(kNT), 0, st, p);
-    hipLaunchKernelGGL(moe_dn_part_kernel, dim3(P * m->Si), dim3(kNT), 0, st, p);
-    hipLaunchKernelGGL((moe_combine_parts_kernel<T>), dim3((m->H + kNT - 1) / kNT, T_), dim3(kNT), 0, st, p);
+    OJX_LAUNCH(moe_gu_part_kernel, dim3(P * m->Sin), dim3(kNT), 0, st, p);
+    OJX_LAUNCH(moe_dn_part_kernel, dim3(P * m->Si), dim3(kNT), 0, st, p);
+    OJX_LAUNCH((moe_combine_parts_kernel<T>), dim3((m->H + kNT - 1) / kNT, T_), dim3(kNT), 0, st, p);
     OJX_HIP(hipGetLastError());
     return OJASX_OK;
 }
@@ -956,15 +956,15 @@ int moe_forward(MoE *m, const void *x, const int *idx, const float *w, void *y, 
     const int nrb_g = (m->I + kRG - 1) / kRG;
     const int nrb_d = (m->H + kRD - 1) / kRD;
     if (m->D == 16)
-        hipLaunchKernelGGL(moe_gateup_kernel<16>, dim3(P * nrb_g), dim3(kNT), 0, st, p);
+        OJX_LAUNCH(moe_gateup_kernel<16>, dim3(P * nrb_g), dim3(kNT), 0, st, p);
     else
-        hipLaunchKernelGGL(moe_gateup_kernel<0>, dim3(P * nrb_g), dim3(kNT), 0, st, p);
-    hipLaunchKernelGGL(moe_down_kernel, dim3(P * nrb_d), dim3(kNT), 0, st, p);
+        OJX_LAUNCH(moe_gateup_kernel<0>, dim3(P * nrb_g), dim3(kNT), 0, st, p);
+    OJX_LAUNCH(moe_down_kernel, dim3(P * nrb_d), dim3(kNT), 0, st, p);
     dim3 gc((m->H + kNT - 1) / kNT, T_);
     if (dtype == OJASX_DTYPE_F32)
-        hipLaunchKernelGGL(moe_combine_kernel<float>, gc, dim3(kNT), 0, st, p);
+        OJX_LAUNCH(moe_combine_kernel<float>, gc, dim3(kNT), 0, st, p);
     else
-        hipLaunchKernelGGL(moe_combine_kernel<__hip_bfloat16>, gc, dim3(kNT), 0, st, p);
+        OJX_LAUNCH(moe_combine_kernel<__hip_bfloat16>, gc, dim3(kNT), 0, st, p);
     OJX_HIP(hipGetLastError());
     return OJASX_OK;
 }
@@ -1079,7 +1079,7 @@ OJASX_API int ojasx_moe_route_device(const float *logits, int num_tokens, int nu
         set_error("router supports 1 <= k <= min(32, E), E <= 1024");
         return OJASX_ERR_INVALID;
     }
-    hipLaunchKernelGGL(moe_route_kernel, dim3((num_tokens + kNT / 64 - 1) / (kNT / 64)), dim3(kNT), 0,
+    OJX_LAUNCH(moe_route_kernel, dim3((num_tokens + kNT / 64 - 1) / (kNT / 64)), dim3(kNT), 0,
                        static_cast<hipStream_t>(stream), logits, num_tokens, num_experts, k,
                        renormalize, idx, w);
     OJX_HIP(hipGetLastError());

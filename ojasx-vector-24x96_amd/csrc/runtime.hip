@@ -4,6 +4,10 @@
 // ojasx_lut_c_api.cpp:17-31 (version and backend strings); the strings name
 // this engine instead of the reference's CPU backends.
 #include <cstdarg>
+#include <cstring>
+#include <map>
+#include <string>
+#include <vector>
 
 #include "common.h"
 
@@ -49,9 +53,87 @@ int upload(DevBuf &buf, const void *host, size_t n) {
     return OJASX_OK;
 }
 
+// ---- kernel timing -------------------------------------------------------
+namespace {
+struct TimingRecord {
+    std::string name;
+    hipEvent_t start, stop;
+};
+constexpr size_t kMaxTimed = 1 << 16;  // event pairs kept between reports
+bool g_timing = false;
+std::vector<TimingRecord> g_records;   // used entries
+std::vector<std::pair<hipEvent_t, hipEvent_t>> g_pool;
+size_t g_dropped = 0;
+}  // namespace
+
+bool timing_on() { return g_timing; }
+
+void timing_events(const char *name, hipEvent_t *start, hipEvent_t *stop) {
+    *start = *stop = nullptr;
+    if (g_records.size() >= kMaxTimed) {
+        ++g_dropped;
+        return;
+    }
+    if (g_pool.size() <= g_records.size()) {
+        hipEvent_t a, b;
+        if (hipEventCreate(&a) != hipSuccess) return;
+        if (hipEventCreate(&b) != hipSuccess) {
+            (void)hipEventDestroy(a);
+            return;
+        }
+        g_pool.emplace_back(a, b);
+    }
+    auto &pr = g_pool[g_records.size()];
+    // "(ns::kernel<...>)" -> "kernel<...>"
+    std::string n(name);
+    if (!n.empty() && n.front() == '(') n = n.substr(1, n.size() - 2);
+    g_records.push_back({n, pr.first, pr.second});
+    *start = pr.first;
+    *stop = pr.second;
+}
+
 }  // namespace ojx
 
 extern "C" {
+
+OJASX_API int ojasx_kernel_timing_enable(int enable) {
+    ojx::g_timing = enable != 0;
+    ojx::g_records.clear();
+    ojx::g_dropped = 0;
+    return OJASX_OK;
+}
+
+OJASX_API int ojasx_kernel_timing_report(char *buf, size_t buf_size) {
+    using namespace ojx;
+    OJX_HIP(hipDeviceSynchronize());
+    std::map<std::string, std::pair<double, long>> agg;   // name -> (total ms, count)
+    for (const auto &r : g_records) {
+        float ms = 0.f;
+        if (hipEventElapsedTime(&ms, r.start, r.stop) != hipSuccess) continue;
+        auto &a = agg[r.name];
+        a.first += ms;
+        a.second += 1;
+    }
+    std::string out = "{";
+    bool first = true;
+    for (const auto &kv : agg) {
+        char item[512];
+        snprintf(item, sizeof(item), "%s\"%s\": {\"calls\": %ld, \"avg_us\": %.4f}", first ? "" : ", ",
+                 kv.first.c_str(), kv.second.second, 1e3 * kv.second.first / kv.second.second);
+        out += item;
+        first = false;
+    }
+    char tail[64];
+    snprintf(tail, sizeof(tail), "%s\"_dropped\": %zu}", first ? "" : ", ", g_dropped);
+    out += tail;
+    if (buf && buf_size) {
+        strncpy(buf, out.c_str(), buf_size - 1);
+        buf[buf_size - 1] = '\0';
+    }
+    g_records.clear();
+    g_dropped = 0;
+    return (int)out.size() + 1;
+}
 
 OJASX_API const char *ojasx_get_version(void) { return "OjasX-LUT-Engine-v1.0.0-MI355X-HIP"; }
 
