@@ -705,13 +705,52 @@ __global__ __launch_bounds__(kNT) void moe_combine_kernel(MoEParams p) {
 
 // Router: top-k of the logits (descending, ties to the lower index) and the
 // softmax probability of each selected expert, optionally renormalised.  One
-// wave per token: lane l holds logits l + 64*i (E <= 1024); each of the k
-// rounds is a local argmax plus a 6-step shuffle reduction, no barriers.
+// wave per token: lane l holds logits l + 64*i (E <= 1024).  Each of the k
+// rounds is a local argmax over the lane's 16 values, a DPP max over the wave
+// (quad permutes and row mirrors inside each 16-lane row, then the 4 row
+// leaders read into scalars), and a DPP min over the expert ids of the lanes
+// that hold that maximum -- no LDS round trips, no barriers.
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) {
+    return __builtin_amdgcn_update_dpp(v, v, CTRL, 0xF, 0xF, false);
+}
+__device__ __forceinline__ float wave_max_f(float v) {
+    v = fmaxf(v, __int_as_float(dpp_i<0xB1>(__float_as_int(v))));   // quad_perm [1,0,3,2]
+    v = fmaxf(v, __int_as_float(dpp_i<0x4E>(__float_as_int(v))));   // quad_perm [2,3,0,1]
+    v = fmaxf(v, __int_as_float(dpp_i<0x141>(__float_as_int(v))));  // row_half_mirror
+    v = fmaxf(v, __int_as_float(dpp_i<0x140>(__float_as_int(v))));  // row_mirror
+    const int iv = __float_as_int(v);
+    const float a = __int_as_float(__builtin_amdgcn_readlane(iv, 0));
+    const float b = __int_as_float(__builtin_amdgcn_readlane(iv, 16));
+    const float c = __int_as_float(__builtin_amdgcn_readlane(iv, 32));
+    const float d = __int_as_float(__builtin_amdgcn_readlane(iv, 48));
+    return fmaxf(fmaxf(a, b), fmaxf(c, d));
+}
+__device__ __forceinline__ int wave_min_i(int v) {
+    v = min(v, dpp_i<0xB1>(v));
+    v = min(v, dpp_i<0x4E>(v));
+    v = min(v, dpp_i<0x141>(v));
+    v = min(v, dpp_i<0x140>(v));
+    const int a = __builtin_amdgcn_readlane(v, 0), b = __builtin_amdgcn_readlane(v, 16);
+    const int c = __builtin_amdgcn_readlane(v, 32), d = __builtin_amdgcn_readlane(v, 48);
+    return min(min(a, b), min(c, d));
+}
+__device__ __forceinline__ float wave_sum_f(float v) {
+    v += __int_as_float(dpp_i<0xB1>(__float_as_int(v)));
+    v += __int_as_float(dpp_i<0x4E>(__float_as_int(v)));
+    v += __int_as_float(dpp_i<0x141>(__float_as_int(v)));
+    v += __int_as_float(dpp_i<0x140>(__float_as_int(v)));
+    const int iv = __float_as_int(v);
+    const float a = __int_as_float(__builtin_amdgcn_readlane(iv, 0));
+    const float b = __int_as_float(__builtin_amdgcn_readlane(iv, 16));
+    const float c = __int_as_float(__builtin_amdgcn_readlane(iv, 32));
+    const float d = __int_as_float(__builtin_amdgcn_readlane(iv, 48));
+    return (a + b) + (c + d);
+}
+
 __global__ __launch_bounds__(kNT) void moe_route_kernel(const float *logits, int T, int E, int k,
                                                        int renorm, int *idx, float *w) {
     constexpr int NV = 16;
-    __shared__ float selv[kNT / 64][32];
-    __shared__ int seli[kNT / 64][32];
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int t_raw = blockIdx.x * (kNT / 64) + wv;
     const int t = min(t_raw, T - 1);
@@ -724,59 +763,41 @@ __global__ __launch_bounds__(kNT) void moe_route_kernel(const float *logits, int
         v[i] = e < E ? x : -INFINITY;
     }
     uint32_t taken = 0;
+    float myv = 0.f;   // lane j < k keeps the j-th selection
+    int myi = 0;
     for (int j = 0; j < k; ++j) {
         float bv = -INFINITY;
         int bi = 0x7fffffff;
 #pragma unroll
         for (int i = 0; i < NV; ++i) {
             const int e = lane + 64 * i;
-            if (e < E && !((taken >> i) & 1u) && (v[i] > bv || (v[i] == bv && e < bi))) {
+            if (e < E && !((taken >> i) & 1u) && (v[i] > bv || bi == 0x7fffffff)) {
                 bv = v[i];
                 bi = e;
             }
         }
-#pragma unroll
-        for (int off = 32; off > 0; off >>= 1) {
-            const float ov = __shfl_xor(bv, off);
-            const int oi = __shfl_xor(bi, off);
-            if (ov > bv || (ov == bv && oi < bi)) {
-                bv = ov;
-                bi = oi;
-            }
-        }
-        if ((bi & 63) == lane) taken |= 1u << (bi >> 6);
-        if (lane == 0) {
-            selv[wv][j] = bv;
-            seli[wv][j] = bi;
+        const float m = wave_max_f(bv);
+        const int wi = wave_min_i(bi != 0x7fffffff && bv == m ? bi : 0x7fffffff);
+        if ((wi & 63) == lane) taken |= 1u << (wi >> 6);
+        if (lane == j) {
+            myv = m;
+            myi = wi;
         }
     }
     // softmax statistics over all E logits
-    float m = -INFINITY;
+    float mx = -INFINITY;
 #pragma unroll
-    for (int i = 0; i < NV; ++i) m = fmaxf(m, v[i]);
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+    for (int i = 0; i < NV; ++i) mx = fmaxf(mx, v[i]);
+    mx = wave_max_f(mx);
     float sum = 0.f;
 #pragma unroll
     for (int i = 0; i < NV; ++i)
-        if (lane + 64 * i < E) sum += expf(v[i] - m);
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
-    __syncthreads();
-    float wj = 0.f;
-    int ij = 0;
-    if (lane < k) {
-        ij = seli[wv][lane];
-        wj = expf(selv[wv][lane] - m) / sum;
-    }
-    if (renorm) {
-        float tot = wj;
-#pragma unroll
-        for (int off = 32; off > 0; off >>= 1) tot += __shfl_xor(tot, off);
-        wj = wj / tot;
-    }
+        if (lane + 64 * i < E) sum += expf(v[i] - mx);
+    sum = wave_sum_f(sum);
+    float wj = lane < k ? expf(myv - mx) / sum : 0.f;
+    if (renorm) wj = wj / wave_sum_f(wj);
     if (lane < k && t_raw < T) {
-        idx[(size_t)t * k + lane] = ij;
+        idx[(size_t)t * k + lane] = myi;
         w[(size_t)t * k + lane] = wj;
     }
 }
