@@ -176,6 +176,28 @@ OJASX_API int ojasx_moe_forward_device(OjasxMoEHandle handle, const void *x, con
 OJASX_API int ojasx_moe_route_device(const float *logits, int num_tokens, int num_experts, int k,
                                      int renormalize, int *idx, float *w, void *stream);
 
+/* ---- math engine (ojasx_24x96/math_engine.py, codec.py) ------------------ */
+/* math_engine.py:136-208 subspace_lut_rvq_gemm, device pointers on `stream`:
+ * y[b][m] = row_scales[m] * sum_{s,g} <x[b][g*block .. +block), C_s[code_s(m,g)]>
+ * (+ bias[m]), x zero-padded to G = ceil(columns/block) blocks.  packed_codes
+ * holds `stages` little-endian bit streams (codec.py:176-195) of
+ * rows * G codes of `bits` in {1,2,4,8} bits, stage s at packed_codes +
+ * s * stage_stride_bytes (no alignment required); codebooks fp32
+ * [stages][2^bits][block]; row_scales fp32 [rows]; bias fp32 [rows] or NULL.
+ * x and y are fp32 or bf16 per dtype (y in x's dtype).  block <= 64. */
+OJASX_API int ojasx_subspace_lut_gemm_device(const void *x, int batch, int columns, int rows,
+                                             const uint8_t *packed_codes, size_t stage_stride_bytes,
+                                             int stages, int bits, int block_size,
+                                             const float *codebooks, const float *row_scales,
+                                             const float *bias, void *y, int dtype, void *stream);
+/* codec.py:176-195 pack_codes: count codes (uint8, < 2^bits) -> ceil(count*bits/8)
+ * packed bytes, little-endian within each byte. */
+OJASX_API int ojasx_pack_codes_device(const uint8_t *codes, long count, int bits, uint8_t *packed,
+                                      void *stream);
+/* codec.py:198-214 unpack_codes: inverse of pack_codes for `count` codes. */
+OJASX_API int ojasx_unpack_codes_device(const uint8_t *packed, long count, int bits, uint8_t *codes,
+                                        void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -10,16 +10,18 @@ Faces, each mirroring a reference interface:
 * ``native``: ``NativeSplitManifoldLinear``, ``NativeKVCache``,
   ``NativeSplitManifoldMoE``, ``get_engine_info`` (reference ctypes binding)
 * ``engine``: ``SplitManifoldLUTLinear`` (reference PyTorch module)
+* ``math_engine``: ``QuantizedWeight``, ``pack_codes``, ``unpack_codes``,
+  ``subspace_lut_rvq_gemm`` (reference codec container and math engine)
 """
 from . import _lib
 from ._lib import OjasxError, lib
 
-__all__ = ["OjasxError", "lib", "native", "engine"]
+__all__ = ["OjasxError", "lib", "native", "engine", "math_engine"]
 
 
 def __getattr__(name):
     # Lazy submodules: ``engine`` imports torch, ``native`` only numpy.
     import importlib
-    if name in ("native", "engine", "moe", "kv", "math_engine"):
+    if name in ("native", "engine", "math_engine"):
         return importlib.import_module(f"{__name__}.{name}")
     raise AttributeError(name)

@@ -49,6 +49,9 @@ SIGNATURES = {
     "ojasx_destroy_moe": (None, [vp]),
     "ojasx_moe_forward_device": (ci, [vp, vp, vp, vp, vp, ci, ci, ci, vp]),
     "ojasx_moe_route_device": (ci, [vp, ci, ci, ci, ci, vp, vp, vp]),
+    "ojasx_subspace_lut_gemm_device": (ci, [vp, ci, ci, ci, vp, cz, ci, ci, ci, vp, vp, vp, vp, ci, vp]),
+    "ojasx_pack_codes_device": (ci, [vp, ctypes.c_long, ci, vp, vp]),
+    "ojasx_unpack_codes_device": (ci, [vp, ctypes.c_long, ci, vp, vp]),
 }
 
 DTYPE_F32 = 0
