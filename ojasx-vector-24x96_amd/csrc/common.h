@@ -93,6 +93,47 @@ __device__ __forceinline__ float quad_sum(float v) {
     return v;
 }
 
+// Wave64 reductions with DPP inside each 16-lane row (quad permutes, half
+// mirror, mirror) and the 4 row leaders read into scalars; the result is
+// uniform across the wave.  No LDS traffic.
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) {
+    return __builtin_amdgcn_update_dpp(v, v, CTRL, 0xF, 0xF, false);
+}
+__device__ __forceinline__ float wave_max_f(float v) {
+    v = fmaxf(v, __int_as_float(dpp_i<0xB1>(__float_as_int(v))));   // quad_perm [1,0,3,2]
+    v = fmaxf(v, __int_as_float(dpp_i<0x4E>(__float_as_int(v))));   // quad_perm [2,3,0,1]
+    v = fmaxf(v, __int_as_float(dpp_i<0x141>(__float_as_int(v))));  // row_half_mirror
+    v = fmaxf(v, __int_as_float(dpp_i<0x140>(__float_as_int(v))));  // row_mirror
+    const int iv = __float_as_int(v);
+    const float a = __int_as_float(__builtin_amdgcn_readlane(iv, 0));
+    const float b = __int_as_float(__builtin_amdgcn_readlane(iv, 16));
+    const float c = __int_as_float(__builtin_amdgcn_readlane(iv, 32));
+    const float d = __int_as_float(__builtin_amdgcn_readlane(iv, 48));
+    return fmaxf(fmaxf(a, b), fmaxf(c, d));
+}
+__device__ __forceinline__ int wave_min_i(int v) {
+    v = min(v, dpp_i<0xB1>(v));
+    v = min(v, dpp_i<0x4E>(v));
+    v = min(v, dpp_i<0x141>(v));
+    v = min(v, dpp_i<0x140>(v));
+    const int a = __builtin_amdgcn_readlane(v, 0), b = __builtin_amdgcn_readlane(v, 16);
+    const int c = __builtin_amdgcn_readlane(v, 32), d = __builtin_amdgcn_readlane(v, 48);
+    return min(min(a, b), min(c, d));
+}
+__device__ __forceinline__ float wave_sum_f(float v) {
+    v += __int_as_float(dpp_i<0xB1>(__float_as_int(v)));
+    v += __int_as_float(dpp_i<0x4E>(__float_as_int(v)));
+    v += __int_as_float(dpp_i<0x141>(__float_as_int(v)));
+    v += __int_as_float(dpp_i<0x140>(__float_as_int(v)));
+    const int iv = __float_as_int(v);
+    const float a = __int_as_float(__builtin_amdgcn_readlane(iv, 0));
+    const float b = __int_as_float(__builtin_amdgcn_readlane(iv, 16));
+    const float c = __int_as_float(__builtin_amdgcn_readlane(iv, 32));
+    const float d = __int_as_float(__builtin_amdgcn_readlane(iv, 48));
+    return (a + b) + (c + d);
+}
+
 __device__ __forceinline__ void store_act(float *p, size_t i, float v) { p[i] = v; }
 __device__ __forceinline__ void store_act(__hip_bfloat16 *p, size_t i, float v) {
     p[i] = __float2bfloat16(v);

@@ -105,3 +105,52 @@ def test_reference_codebook_special_case(pkg, dev):
         kc, ks, vc, vs = gen.kv_logical(d, j)
         want = cpu.kv_attention_ref(d["q"][j], kc, ks, vc, vs, 0.02)
         assert rel_err(out[j], want) < 1e-5
+
+
+def check_all_heads(d, out, T, Hq, Hkv):
+    R = Hq // Hkv
+    for j in range(Hq):
+        h = j // R
+        kc, ks, vc, vs = gen.kv_logical(d, h)
+        Kd = d["k_cb"][h][kc.astype(np.int64)].reshape(T, -1) * ks[:, None].astype(np.float64)
+        Vd = d["v_cb"][h][vc.astype(np.int64)].reshape(T, -1) * vs[:, None].astype(np.float64)
+        exact = no.full_softmax_attention(d["q"][j], Kd, Vd)
+        assert rel_err(out[j], exact) < 1e-5, j
+
+
+@pytest.mark.parametrize("T,Hq,Hkv", [(3000, 16, 2),    # GQA 8: two workgroups of 4 heads (short path)
+                                      (9000, 16, 2),    # GQA 8, long-context path
+                                      (5000, 4, 4),     # no GQA, long-context path
+                                      (64, 3, 1)])      # 3 query heads, one full chunk
+def test_paged_decode_gqa_ratios(pkg, dev, T, Hq, Hkv):
+    d = gen.kv(H_kv=Hkv, H_q=Hq, T=T, seed=T + Hq, shuffle_pages=True)
+    out = decode(pkg, d, T, Hq, Hkv)
+    check_all_heads(d, out, T, Hq, Hkv)
+
+
+def test_paged_decode_runtime_shape(pkg, dev):
+    """head_dim 64 with block 8 (8 groups): the runtime-shape kernel."""
+    T, Hq, Hkv = 700, 4, 2
+    d = gen.kv(H_kv=Hkv, H_q=Hq, T=T, head_dim=64, D=8, seed=21, shuffle_pages=True)
+    out = decode(pkg, d, T, Hq, Hkv, hd=64, D=8)
+    check_all_heads(d, out, T, Hq, Hkv)
+
+
+def test_paged_decode_unaligned_query(pkg, dev):
+    """q not 16-byte aligned takes the runtime-shape kernel."""
+    import torch
+    T, Hq, Hkv = 1500, 8, 2
+    d = gen.kv(H_kv=Hkv, H_q=Hq, T=T, seed=22, shuffle_pages=True)
+    t = {k: torch.from_numpy(np.ascontiguousarray(d[k])).to(dev)
+         for k in ("k_codes", "k_scales", "v_codes", "v_scales", "k_cb", "v_cb", "block_table")}
+    qbuf = torch.empty(Hq * 128 + 1, device=dev)
+    qt = qbuf[1:].view(Hq, 128)
+    qt.copy_(torch.from_numpy(d["q"]).to(dev))
+    out = torch.empty(Hq, 128, device=dev)
+    rc = pkg.lib().ojasx_kv_decode_paged_device(
+        vp(qt), vp(t["k_codes"]), vp(t["k_scales"]), vp(t["v_codes"]), vp(t["v_scales"]),
+        vp(t["k_cb"]), vp(t["v_cb"]), vp(t["block_table"]), T, d["page"], Hq, Hkv, 128, 16, -1.0,
+        vp(out), None)
+    assert rc == 0, pkg.lib().ojasx_get_last_error()
+    torch.cuda.synchronize()
+    check_all_heads(d, out.cpu().numpy(), T, Hq, Hkv)
