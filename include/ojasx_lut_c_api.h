@@ -50,7 +50,7 @@ enum {
 };
 
 /* Activation / output element types of the device entry points. */
-enum { OJASX_DTYPE_F32 = 0, OJASX_DTYPE_BF16 = 1 };
+enum { OJASX_DTYPE_F32 = 0, OJASX_DTYPE_BF16 = 1, OJASX_DTYPE_F16 = 2 };
 
 /* ---- metadata (ref.h:40-41) ------------------------------------------- */
 OJASX_API const char *ojasx_get_version(void);
@@ -147,6 +147,44 @@ OJASX_API int ojasx_kv_decode_paged_device(const float *q, const uint8_t *k_code
                                            int seq_len, int page_size, int num_q_heads,
                                            int num_kv_heads, int head_dim, int block_dim,
                                            float scale_factor, float *out, void *stream);
+
+/* Device append into the paged code layout above; replaces
+ * HeadKVCache::append_token (ojasx_lut_kv_cache.cpp:16-65, ref.h:103-108) for
+ * num_tokens tokens and all kv heads in one call.
+ *   k, v [num_tokens][num_kv_heads][head_dim] fp32
+ *   s = max(1e-8, max_d |k_d|) / 127 per token and head, x = k / s;
+ *   with codebooks ([num_kv_heads][256][block_dim] fp32): code[g] = the
+ *     centroid nearest x[g*block_dim ..) in squared distance (fmaf in d order,
+ *     ties to the lower index);
+ *   with both codebooks NULL: the reference quantiser,
+ *     clamp(round_half_away(x[g*block_dim]), -128, 127) + 128.
+ *   slot_mapping [num_tokens] int32: page * page_size + offset of each token
+ *     (negative or >= num_pages * page_size: token skipped).
+ * head_dim / block_dim <= 64, head_dim <= 16384. */
+OJASX_API int ojasx_kv_encode_append_device(const float *k, const float *v, int num_tokens,
+                                            int num_kv_heads, int head_dim, int block_dim,
+                                            const float *k_codebook, const float *v_codebook,
+                                            const int *slot_mapping, int page_size,
+                                            int num_pages, uint8_t *k_codes, float *k_scales,
+                                            uint8_t *v_codes, float *v_scales, void *stream);
+
+/* PagedCompressedKVCache._quantize_int8 (ojasx_24x96/long_context.py:234-240)
+ * on device: rows of dim elements of x (dtype F32, BF16 or F16), row r of
+ * group g at x + g*x_group_stride + r*dim (elements), int8 codes to
+ * q + g*q_group_stride + r*dim and the fp16 scale to scale + g*scale_group_stride + r.
+ * Arithmetic as torch on a tensor of x's dtype: s = T(max(max|x|, T(1e-8)) / 127),
+ * q = clamp(round_half_even(T(x / s)), -127, 127). */
+OJASX_API int ojasx_quantize_int8_device(const void *x, long groups, int rows, int dim,
+                                         long x_group_stride, int dtype, int8_t *q,
+                                         long q_group_stride, void *scale_f16,
+                                         long scale_group_stride, void *stream);
+/* long_context.py:242-244 _dequantize_int8: out[g][r][d] = dtype(float(q) * float(s))
+ * into a contiguous [groups][rows][dim] out (F32, BF16 or F16); q and scale
+ * addressed as in ojasx_quantize_int8_device. */
+OJASX_API int ojasx_dequantize_int8_device(const int8_t *q, const void *scale_f16, long groups,
+                                           int rows, int dim, long q_group_stride,
+                                           long scale_group_stride, void *out, int dtype,
+                                           void *stream);
 
 /* ---- MoE (ref.h:125-150) ---------------------------------------------- */
 OJASX_API OjasxMoEHandle ojasx_create_moe(int num_experts, int hidden_dim,

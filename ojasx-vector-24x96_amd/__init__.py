@@ -12,16 +12,19 @@ Faces, each mirroring a reference interface:
 * ``engine``: ``SplitManifoldLUTLinear`` (reference PyTorch module)
 * ``math_engine``: ``QuantizedWeight``, ``pack_codes``, ``unpack_codes``,
   ``subspace_lut_rvq_gemm`` (reference codec container and math engine)
+* ``long_context``: ``PagedCompressedKVCache`` (reference int8 paged KV cache)
+  and ``PagedCodeKVCache`` (paged codebook-code KV cache with device append
+  and decode)
 """
 from . import _lib
 from ._lib import OjasxError, lib
 
-__all__ = ["OjasxError", "lib", "native", "engine", "math_engine"]
+__all__ = ["OjasxError", "lib", "native", "engine", "math_engine", "long_context"]
 
 
 def __getattr__(name):
     # Lazy submodules: ``engine`` imports torch, ``native`` only numpy.
     import importlib
-    if name in ("native", "engine", "math_engine"):
+    if name in ("native", "engine", "math_engine", "long_context"):
         return importlib.import_module(f"{__name__}.{name}")
     raise AttributeError(name)

@@ -15,6 +15,7 @@ LIB_PATH = os.path.join(HERE, "libojasx_lut_hip.so")
 _lib = None
 
 vp, ci, cf, cz = ctypes.c_void_p, ctypes.c_int, ctypes.c_float, ctypes.c_size_t
+cl = ctypes.c_long
 
 # name -> (restype, argtypes); the set of symbols declared in include/ojasx_lut_c_api.h
 SIGNATURES = {
@@ -52,6 +53,10 @@ SIGNATURES = {
     "ojasx_subspace_lut_gemm_device": (ci, [vp, ci, ci, ci, vp, cz, ci, ci, ci, vp, vp, vp, vp, ci, vp]),
     "ojasx_pack_codes_device": (ci, [vp, ctypes.c_long, ci, vp, vp]),
     "ojasx_unpack_codes_device": (ci, [vp, ctypes.c_long, ci, vp, vp]),
+    "ojasx_quantize_int8_device": (ci, [vp, cl, ci, ci, cl, ci, vp, cl, vp, cl, vp]),
+    "ojasx_dequantize_int8_device": (ci, [vp, vp, cl, ci, ci, cl, cl, vp, ci, vp]),
+    "ojasx_kv_encode_append_device": (ci, [vp, vp, ci, ci, ci, ci, vp, vp, vp, ci, ci, vp, vp, vp,
+                                           vp, vp]),
 }
 
 DTYPE_F32 = 0

@@ -4,6 +4,7 @@
 #include <hip/hip_runtime.h>
 #include <hip/hip_bf16.h>
 #include <hip/hip_ext.h>
+#include <hip/hip_fp16.h>
 
 #include <cstddef>
 #include <cstdint>
@@ -75,6 +76,17 @@ __device__ __forceinline__ float load_act(const float *p, size_t i) { return p[i
 __device__ __forceinline__ float load_act(const __hip_bfloat16 *p, size_t i) {
     return __bfloat162float(p[i]);
 }
+__device__ __forceinline__ float load_act(const __half *p, size_t i) { return __half2float(p[i]); }
+
+// v rounded (to nearest even) to the element type of p and back to fp32:
+// the result of a torch elementwise op on tensors of that type.
+__device__ __forceinline__ float round_as(const float *, float v) { return v; }
+__device__ __forceinline__ float round_as(const __hip_bfloat16 *, float v) {
+    return __bfloat162float(__float2bfloat16(v));
+}
+__device__ __forceinline__ float round_as(const __half *, float v) {
+    return __half2float(__float2half_rn(v));
+}
 // Four consecutive activations as fp32 (p + i must be 16-byte aligned for
 // fp32, 8-byte aligned for bf16).
 __device__ __forceinline__ float4 load4_act(const float *p, size_t i) {
@@ -112,6 +124,18 @@ __device__ __forceinline__ float wave_max_f(float v) {
     const float d = __int_as_float(__builtin_amdgcn_readlane(iv, 48));
     return fmaxf(fmaxf(a, b), fmaxf(c, d));
 }
+__device__ __forceinline__ float wave_min_f(float v) {
+    v = fminf(v, __int_as_float(dpp_i<0xB1>(__float_as_int(v))));
+    v = fminf(v, __int_as_float(dpp_i<0x4E>(__float_as_int(v))));
+    v = fminf(v, __int_as_float(dpp_i<0x141>(__float_as_int(v))));
+    v = fminf(v, __int_as_float(dpp_i<0x140>(__float_as_int(v))));
+    const int iv = __float_as_int(v);
+    const float a = __int_as_float(__builtin_amdgcn_readlane(iv, 0));
+    const float b = __int_as_float(__builtin_amdgcn_readlane(iv, 16));
+    const float c = __int_as_float(__builtin_amdgcn_readlane(iv, 32));
+    const float d = __int_as_float(__builtin_amdgcn_readlane(iv, 48));
+    return fminf(fminf(a, b), fminf(c, d));
+}
 __device__ __forceinline__ int wave_min_i(int v) {
     v = min(v, dpp_i<0xB1>(v));
     v = min(v, dpp_i<0x4E>(v));
@@ -138,6 +162,7 @@ __device__ __forceinline__ void store_act(float *p, size_t i, float v) { p[i] = 
 __device__ __forceinline__ void store_act(__hip_bfloat16 *p, size_t i, float v) {
     p[i] = __float2bfloat16(v);
 }
+__device__ __forceinline__ void store_act(__half *p, size_t i, float v) { p[i] = __float2half_rn(v); }
 
 // Copy n activations (converted to fp32) from global memory to LDS with all
 // of a thread's loads in flight before the first LDS store: loads and stores

@@ -101,6 +101,17 @@ def kv_quantize_token(k, block_dim=16):
     return codes, s[0]
 
 
+def kv_encode_token(k, codebook, block_dim=16):
+    """Nearest-centroid codebook KV encoder for one token of one head (see
+    lut_oracle.c orc_kv_encode_token)."""
+    k = _f32(k).reshape(-1)
+    cb = _f32(codebook)
+    codes = np.empty(k.size // block_dim, np.uint8)
+    s = np.zeros(1, np.float32)
+    lib().orc_kv_encode_token(_p(k), k.size, block_dim, _p(cb), _p(codes), _p(s))
+    return codes, s[0]
+
+
 def kv_attention_ref(q, k_codes, k_scales, v_codes, v_scales, scale_factor=-1.0,
                      block_dim=16):
     """Reference scalar-codebook decode attention for one head (logits, two-pass

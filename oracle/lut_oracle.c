@@ -163,6 +163,41 @@ ORC_API void orc_kv_quantize_token(const float *k, int head_dim, int D,
     }
 }
 
+/* Codebook KV encoder for one token of one head (defined by this build; the
+ * step before the general-codebook decode).  Scale as orc_kv_quantize_token
+ * (NAT/src/ojasx_lut_kv_cache.cpp:29-34); x_d = k_d / s;
+ * code[g] = argmin_c sum_{d<D} (x[gD+d] - cb[c][d])^2 over the 256 rows of
+ * cb [256][D], the sum accumulated with fmaf in d order from 0, ties to the
+ * lower c.  With cb[c] = (c - 128) e_0 and other coordinates zero this is the
+ * reference quantiser away from half-way ties. */
+ORC_API void orc_kv_encode_token(const float *k, int head_dim, int D, const float *cb,
+                                 uint8_t *codes, float *scale) {
+    float mx = 1e-8f;
+    for (int d = 0; d < head_dim; ++d) {
+        float a = fabsf(k[d]);
+        mx = mx > a ? mx : a;
+    }
+    const float s = mx / 127.0f;
+    *scale = s;
+    const int G = head_dim / D;
+    for (int g = 0; g < G; ++g) {
+        float best = 0.0f;
+        int bi = 0;
+        for (int c = 0; c < 256; ++c) {
+            float dist = 0.0f;
+            for (int d = 0; d < D; ++d) {
+                const float df = k[g * D + d] / s - cb[c * D + d];
+                dist = fmaf(df, df, dist);
+            }
+            if (c == 0 || dist < best) {
+                best = dist;
+                bi = c;
+            }
+        }
+        codes[g] = (uint8_t)bi;
+    }
+}
+
 /* Reference decode attention for one head over T tokens.
  * logits: NAT/src/ojasx_lut_kv_cache.cpp:67-108 (LUT_q[g][c] = q[g*D]*(c-128),
  * sum over g ascending, times s_t times sf; sf <= 0 means 1/sqrt(head_dim)).

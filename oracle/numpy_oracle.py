@@ -153,15 +153,44 @@ def full_softmax_attention(q, K, V, scale=None):
     return p @ np.asarray(V, np.float64)
 
 
-def paged_quantize_int8(t):
-    """PagedCompressedKVCache._quantize_int8 (long_context.py:234-240):
-    s = max(|t|_D, 1e-8) / 127 stored as float16; q = clamp(round_half_even(t / s),
-    -127, 127) int8 (division by the fp32 scale before the fp16 cast)."""
-    t = np.asarray(t, np.float32)
-    amax = np.maximum(np.abs(t).max(axis=-1, keepdims=True), np.float32(1e-8))
-    s = (amax / np.float32(127.0)).astype(np.float32)
-    q = np.clip(np.rint(t / s), -127, 127).astype(np.int8)
+def round_to(a, kind):
+    """fp32 values rounded to nearest even in ``kind`` ("float32", "bfloat16",
+    "float16") and returned as fp32: the result of a torch elementwise op on
+    tensors of that type (finite inputs)."""
+    a = np.asarray(a, np.float32)
+    if kind == "float32":
+        return a
+    if kind == "float16":
+        return a.astype(np.float16).astype(np.float32)
+    if kind == "bfloat16":
+        u = a.view(np.uint32).astype(np.uint64)
+        u = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16) << 16
+        return u.astype(np.uint32).view(np.float32)
+    raise ValueError(kind)
+
+
+def paged_quantize_int8(t, kind="float32"):
+    """PagedCompressedKVCache._quantize_int8 (long_context.py:234-240) on a
+    tensor of element type ``kind`` (t holds values of that type):
+    a = max(|t|_D, T(1e-8)), s = T(a / 127), q = clamp(round_half_even(T(t / s)),
+    -127, 127) int8 with every elementwise result T() rounded to the type as
+    torch does; s returned as float16.  An all-zero float16 row gives s = 0
+    and 0/0 in the reference; q is 0 there."""
+    t = round_to(t, kind)
+    amax = np.maximum(np.abs(t).max(axis=-1, keepdims=True), round_to(np.float32(1e-8), kind))
+    s = round_to(amax / np.float32(127.0), kind)
+    with np.errstate(invalid="ignore", divide="ignore"):
+        v = np.rint(round_to(t / s, kind))
+    v = np.where(np.isnan(v), 0, v)
+    q = np.clip(v, -127, 127).astype(np.int8)
     return q, s.astype(np.float16)
+
+
+def paged_dequantize_int8(q, s, kind="float32"):
+    """PagedCompressedKVCache._dequantize_int8 (long_context.py:242-244):
+    float(q) * float(s) in fp32, then rounded to ``kind``."""
+    v = np.asarray(q, np.float32) * np.asarray(s, np.float16).astype(np.float32)
+    return round_to(v, kind)
 
 
 def code_domain_kv_decode(q_heads, kv_group, k_cb, v_cb, k_codes, k_scales, v_codes, v_scales,
