@@ -18,8 +18,8 @@ end on the launch stream); ``traffic`` is the HBM bytes per launch from the
 rocprofv3 FETCH_SIZE/WRITE_SIZE summary under profiles/ when present.
 ``cpu_baseline`` times the reference's own C++ engine (compiled from its
 sources into oracle/_ref when present, else the repo's C restatement) on the
-host, one thread, on the same inputs.  Extra fields give the MoE and
-KV-decode figures of the same run.  Before the timed region one 64 MiB
+host, one thread, on the same inputs.  Extra fields give the MoE,
+KV-decode and KV-append figures of the same run.  Before the timed region one 64 MiB
 device-to-device copy runs: a kernel of known traffic that calibrates the
 PMC byte counters of a profiled run of this script.
 """
@@ -177,7 +177,7 @@ def bench_moe(pkg, torch, steps, warmup, cpu_seconds, do_cpu):
     return res
 
 
-def bench_kv(pkg, torch, steps):
+def bench_kv(pkg, torch, steps, do_cpu=True):
     """Paged code-domain decode: 8 kv / 32 q heads, head_dim 128, page 16."""
     from oracle import gen
     L = pkg.lib()
@@ -214,6 +214,68 @@ def bench_kv(pkg, torch, steps):
                         "achieved_code_GBs": round(code_bytes / (us * 1e-6) / 1e9, 2),
                         "achieved_all_GBs": round(all_bytes / (us * 1e-6) / 1e9, 2),
                         "kernels_avg_us": {k: v["avg_us"] for k, v in kern.items()}}
+    res["append"] = bench_kv_append(pkg, torch, steps, do_cpu)
+    return res
+
+
+def bench_kv_append(pkg, torch, steps, do_cpu, cpu_seconds=2.0):
+    """Device KV append (encode + paged write) for 8 kv heads x 128, per call
+    of 1 or 16 tokens, with the 256 x 16 codebooks (nearest centroid) and with
+    the reference's scalar quantiser; each call writes fresh slots of a
+    4096-page pool.  Beside it the reference engine's ojasx_kv_cache_append
+    on the host, 8 heads per token."""
+    from oracle import ref
+    L = pkg.lib()
+    vp = ctypes.c_void_p
+    dev = torch.device("cuda:0")
+    st = torch.cuda.current_stream()
+    Hkv, hd, D, P, pages = 8, 128, 16, 16, 4096
+    r = np.random.default_rng(17)
+    kc = torch.zeros(pages, Hkv, P, hd // D, dtype=torch.uint8, device=dev)
+    vc = torch.zeros_like(kc)
+    ks = torch.zeros(pages, Hkv, P, device=dev)
+    vs = torch.zeros_like(ks)
+    cb = torch.from_numpy(r.normal(0, 30, size=(2, Hkv, 256, D)).astype(np.float32)).to(dev)
+    res = {}
+    n = max(50, steps // 4)
+    for tokens in (1, 16):
+        kv = torch.from_numpy(r.normal(size=(2, n, tokens, Hkv, hd)).astype(np.float32)).to(dev)
+        slots = torch.arange(n * tokens, dtype=torch.int32, device=dev).view(n, tokens)
+        for mode in ("codebook", "scalar"):
+            cbk = vp(cb[0].data_ptr()) if mode == "codebook" else None
+            cbv = vp(cb[1].data_ptr()) if mode == "codebook" else None
+            call = lambda i: L.ojasx_kv_encode_append_device(
+                vp(kv[0, i].data_ptr()), vp(kv[1, i].data_ptr()), tokens, Hkv, hd, D, cbk, cbv,
+                vp(slots[i].data_ptr()), P, pages, vp(kc.data_ptr()), vp(ks.data_ptr()),
+                vp(vc.data_ptr()), vp(vs.data_ptr()), vp(st.cuda_stream))
+            for i in range(min(n, 20)):
+                call(i)
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(st)
+            for i in range(n):
+                call(i)
+            e1.record(st)
+            torch.cuda.synchronize()
+            us = e0.elapsed_time(e1) * 1e3 / n
+            kern = timed_kernels(pkg, lambda: [call(i) for i in range(n)])
+            res[f"{mode}_{tokens}tok"] = {
+                "us_per_call": round(us, 3), "us_per_token": round(us / tokens, 3),
+                "kernels_avg_us": {k: v["avg_us"] for k, v in kern.items()}}
+    if do_cpu and ref.available():
+        R = ref.lib()
+        h = R.ojasx_create_kv_cache(Hkv, hd, 1 << 17, D)
+        k = r.normal(size=(Hkv, hd)).astype(np.float32)
+        p = lambda a: a.ctypes.data_as(vp)
+        count, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < cpu_seconds and count < 100000:
+            for head in range(Hkv):
+                R.ojasx_kv_cache_append(h, head, p(k[head]), p(k[head]))
+            count += 1
+        res["cpu_reference_us_per_token"] = round((time.perf_counter() - t0) / count * 1e6, 3)
+        res["cpu_reference_sample"] = (f"{count} tokens x {Hkv} heads of ojasx_kv_cache_append, "
+                                       "1 thread (reference engine, scalar quantiser)")
+        R.ojasx_destroy_kv_cache(h)
     return res
 
 
@@ -330,7 +392,7 @@ def main():
     if not args.no_extra:
         out["moe_512x_top10"] = bench_moe(pkg, torch, min(args.steps, 400), args.warmup,
                                           args.cpu_seconds / 2, not args.no_cpu)
-        out["kv_decode_gqa4"] = bench_kv(pkg, torch, args.steps)
+        out["kv_decode_gqa4"] = bench_kv(pkg, torch, args.steps, not args.no_cpu)
     print(json.dumps(out))
 
 
