@@ -78,9 +78,11 @@ def parse():
     return ap.parse_args()
 
 
-def time_cpu_linear(d, seconds):
+def time_cpu_linear(d, seconds, y_gpu):
     """Reference C++ engine (or the C restatement) on the host, 1 thread,
-    ojasx_run.cpp's method: 50 warm-up calls, then timed calls."""
+    ojasx_run.cpp's method: 50 warm-up calls, then timed calls.  Its output on
+    the benchmarked instance is also the parity check of the GPU result
+    (``parity_rel_err``, max |GPU - CPU| / max |CPU|)."""
     from oracle import ref, cpu
     x = d["x"]
     if ref.available():
@@ -90,6 +92,8 @@ def time_cpu_linear(d, seconds):
     else:
         call = lambda: cpu.linear_forward(x, d["codebook"], d["codes"], d["scales"], None, *d["csr"])
         kind = "port"
+    y_cpu = np.asarray(call(), np.float64).reshape(-1)
+    rel = float(np.abs(np.asarray(y_gpu, np.float64).reshape(-1) - y_cpu).max() / np.abs(y_cpu).max())
     for _ in range(50):
         call()
     n, t0 = 0, time.perf_counter()
@@ -101,14 +105,15 @@ def time_cpu_linear(d, seconds):
             break
     return dict(value=el / n * 1e6, unit="us/call", cores=1, kind=kind,
                 sample=f"{n} calls of LUT-GEMV 2560->6912 B=1 fp32 with CSR, 1 thread, "
-                       f"after 50 warm-up calls")
+                       f"after 50 warm-up calls", parity_rel_err=rel)
 
 
 def bench_moe(pkg, torch, steps, warmup, cpu_seconds, do_cpu):
     """512-expert top-10 MoE layer (H 2048, I 768), T = 1 and 16 tokens.  Two
     expert banks (2 x 151 MB, above the 256 MB Infinity Cache) alternate and
     every step has its own routing, so routed experts' codes come from HBM."""
-    from oracle import gen, ref
+    from oracle import ref
+    gen = pkg.synthetic
     L = pkg.lib()
     vp = ctypes.c_void_p
     p = lambda a: a.ctypes.data_as(vp)
@@ -179,7 +184,7 @@ def bench_moe(pkg, torch, steps, warmup, cpu_seconds, do_cpu):
 
 def bench_kv(pkg, torch, steps, do_cpu=True):
     """Paged code-domain decode: 8 kv / 32 q heads, head_dim 128, page 16."""
-    from oracle import gen
+    gen = pkg.synthetic
     L = pkg.lib()
     vp = ctypes.c_void_p
     dev = torch.device("cuda:0")
@@ -288,9 +293,9 @@ def main():
         sys.exit(2)
     import torch
     import __graft_entry__
-    from oracle import gen, cpu
 
     pkg = __graft_entry__.load_package()
+    gen = pkg.synthetic
     L = pkg.lib()
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
@@ -317,12 +322,9 @@ def main():
     xp, yp = ctypes.c_void_p(x.data_ptr()), ctypes.c_void_p(y.data_ptr())
     fwd = L.ojasx_linear_forward_device
 
-    # parity of the benchmarked configuration (instance 0) against the oracle
     assert fwd(handles[0], xp, yp, 1, 0, sp) == 0
     torch.cuda.synchronize()
-    y_ref = cpu.linear_forward(base["x"], base["codebook"], base["codes"], base["scales"], None,
-                               *base["csr"])
-    rel = float(np.abs(y.cpu().numpy() - y_ref).max() / np.abs(y_ref).max())
+    y_bench = y.cpu().numpy()
 
     # PMC calibration: one device-to-device copy of known size (read and write)
     cal_src = torch.ones(CAL_COPY_BYTES // 4, device=dev)
@@ -382,11 +384,10 @@ def main():
                      "achieved_all_bytes_GBs": round(all_bytes / (kernel_us * 1e-6) / 1e9, 2),
                      "call_period_GBs": round(code_bytes / (us_call * 1e-6) / 1e9, 2)},
         "pmc_calibration_copy_bytes": CAL_COPY_BYTES,
-        "parity_rel_err": rel,
         "wall_s_timed": round(t_wall, 3),
     }
     if not args.no_cpu:
-        out["cpu_baseline"] = time_cpu_linear(base, args.cpu_seconds)
+        out["cpu_baseline"] = time_cpu_linear(base, args.cpu_seconds, y_bench)
     for h in handles:
         L.ojasx_destroy_linear(h)
     if not args.no_extra:

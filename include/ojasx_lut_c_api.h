@@ -39,6 +39,7 @@ extern "C" {
 typedef void *OjasxLinearHandle; /* ref.h:35 */
 typedef void *OjasxKVHandle;     /* ref.h:36 */
 typedef void *OjasxMoEHandle;    /* ref.h:37 */
+typedef void *OjasxDecoderHandle; /* no reference counterpart (the decoder below) */
 
 enum {
     OJASX_OK = 0,
@@ -235,6 +236,64 @@ OJASX_API int ojasx_pack_codes_device(const uint8_t *codes, long count, int bits
 /* codec.py:198-214 unpack_codes: inverse of pack_codes for `count` codes. */
 OJASX_API int ojasx_unpack_codes_device(const uint8_t *packed, long count, int bits, uint8_t *codes,
                                         void *stream);
+
+/* ---- decoder (no reference counterpart) ---------------------------------- */
+/* A decoder stack whose linears are LUT linears and whose KV cache is the paged
+ * code cache, greedy batch-1 decode: the reference's 4B-shaped configuration
+ * (hidden 2560, 36 layers, 32 q / 8 kv heads, MLP 9728).  Each layer:
+ *   qkv = Wqkv RMSNorm(x; input_norm); q, k per-head RMSNorm (q_norm, k_norm)
+ *   and RoPE (theta); k, v encoded into the layer's KV cache (256 x 16
+ *   codebooks per kv head); attention over the cache; x += Wo attn;
+ *   x += Wdown (silu(gate) * up) with [gate; up] = Wgate_up RMSNorm(x; post_norm).
+ * Head: logits = Wlm RMSNorm(x; final_norm); next token = first argmax.
+ * head_dim must be 128; every linear block_dim 16. */
+OJASX_API OjasxDecoderHandle ojasx_create_decoder(int hidden, int layers, int q_heads,
+                                                  int kv_heads, int head_dim, int intermediate,
+                                                  int vocab, int max_context, int page_size,
+                                                  int max_steps, float rms_eps, float rope_theta);
+OJASX_API void ojasx_destroy_decoder(OjasxDecoderHandle handle);
+/* Linear handles (ojasx_create_linear) are referenced, not copied, and must
+ * outlive the decoder: qkv hidden -> (q_heads + 2 kv_heads) * 128 (q rows,
+ * then k, then v), o q_heads*128 -> hidden, gate_up hidden -> 2*intermediate
+ * (gate rows, then up rows), down intermediate -> hidden.  The other arrays
+ * are device pointers, copied: norms [hidden] / [128], codebooks
+ * [kv_heads][256][16] fp32. */
+OJASX_API int ojasx_decoder_set_layer(OjasxDecoderHandle handle, int layer,
+                                      OjasxLinearHandle qkv, OjasxLinearHandle o,
+                                      OjasxLinearHandle gate_up, OjasxLinearHandle down,
+                                      const float *input_norm, const float *post_norm,
+                                      const float *q_norm, const float *k_norm,
+                                      const float *k_codebook, const float *v_codebook);
+/* lm_head hidden -> vocab (referenced); final_norm [hidden] and embedding
+ * [vocab][hidden] fp32 device pointers, copied. */
+OJASX_API int ojasx_decoder_set_head(OjasxDecoderHandle handle, OjasxLinearHandle lm_head,
+                                     const float *final_norm, const float *embedding);
+/* Prefilled context of one layer, device pointers in the paged layout of
+ * ojasx_kv_decode_paged_device with the identity block table. */
+OJASX_API int ojasx_decoder_set_context(OjasxDecoderHandle handle, int layer,
+                                        const uint8_t *k_codes, const float *k_scales,
+                                        const uint8_t *v_codes, const float *v_scales,
+                                        int num_tokens);
+/* Position of the next token (= context length). */
+OJASX_API int ojasx_decoder_reset(OjasxDecoderHandle handle, int position);
+/* Greedy decode of num_tokens tokens starting from first_token at the current
+ * position: tokens_out [num_tokens] (host), last_logits [vocab] (host, or
+ * NULL) = logits of the last step.  use_graph != 0 replays one captured HIP
+ * graph per token (captured on the first such call).  Synchronous. */
+OJASX_API int ojasx_decoder_generate(OjasxDecoderHandle handle, int first_token, int num_tokens,
+                                     int use_graph, int *tokens_out, float *last_logits);
+/* Host copy of one layer's KV cache rows for tokens [first_token,
+ * first_token + num_tokens), first_token a multiple of page_size: codes
+ * [pages][kv_heads][page_size][8], scales [pages][kv_heads][page_size]. */
+OJASX_API int ojasx_decoder_read_kv(OjasxDecoderHandle handle, int layer, int first_token,
+                                    int num_tokens, uint8_t *k_codes, float *k_scales,
+                                    uint8_t *v_codes, float *v_scales);
+/* Fused fp32 batch-1 LUT linear of the decoder: prologue 0 = none, 1 =
+ * RMSNorm(x; norm_weight, eps), 2 = silu(x[:K]) * x[K:] from a 2K row; y =
+ * residual + (...) when residual != NULL (residual may equal y). */
+OJASX_API int ojasx_linear_forward_fused_device(OjasxLinearHandle handle, const float *x,
+                                                float *y, int prologue, const float *norm_weight,
+                                                float eps, const float *residual, void *stream);
 
 #ifdef __cplusplus
 }

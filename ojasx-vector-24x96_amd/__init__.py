@@ -15,16 +15,20 @@ Faces, each mirroring a reference interface:
 * ``long_context``: ``PagedCompressedKVCache`` (reference int8 paged KV cache)
   and ``PagedCodeKVCache`` (paged codebook-code KV cache with device append
   and decode)
+* ``decoder``: ``LUTDecoder`` / ``synthetic_decoder``, the 4B-shaped greedy
+  decoder over LUT linears and the code KV cache (HIP graph per token)
+* ``synthetic``: seeded synthetic inputs of the benchmark configurations
 """
 from . import _lib
 from ._lib import OjasxError, lib
 
-__all__ = ["OjasxError", "lib", "native", "engine", "math_engine", "long_context"]
+__all__ = ["OjasxError", "lib", "native", "engine", "math_engine", "long_context", "decoder",
+           "synthetic"]
 
 
 def __getattr__(name):
     # Lazy submodules: ``engine`` imports torch, ``native`` only numpy.
     import importlib
-    if name in ("native", "engine", "math_engine", "long_context"):
+    if name in ("native", "engine", "math_engine", "long_context", "decoder", "synthetic"):
         return importlib.import_module(f"{__name__}.{name}")
     raise AttributeError(name)

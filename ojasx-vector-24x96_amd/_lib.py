@@ -57,6 +57,15 @@ SIGNATURES = {
     "ojasx_dequantize_int8_device": (ci, [vp, vp, cl, ci, ci, cl, cl, vp, ci, vp]),
     "ojasx_kv_encode_append_device": (ci, [vp, vp, ci, ci, ci, ci, vp, vp, vp, ci, ci, vp, vp, vp,
                                            vp, vp]),
+    "ojasx_create_decoder": (vp, [ci, ci, ci, ci, ci, ci, ci, ci, ci, ci, cf, cf]),
+    "ojasx_destroy_decoder": (None, [vp]),
+    "ojasx_decoder_set_layer": (ci, [vp, ci, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp]),
+    "ojasx_decoder_set_head": (ci, [vp, vp, vp, vp]),
+    "ojasx_decoder_set_context": (ci, [vp, ci, vp, vp, vp, vp, ci]),
+    "ojasx_decoder_reset": (ci, [vp, ci]),
+    "ojasx_decoder_generate": (ci, [vp, ci, ci, ci, vp, vp]),
+    "ojasx_decoder_read_kv": (ci, [vp, ci, ci, ci, vp, vp, vp, vp]),
+    "ojasx_linear_forward_fused_device": (ci, [vp, vp, vp, ci, vp, cf, vp, vp]),
 }
 
 DTYPE_F32 = 0

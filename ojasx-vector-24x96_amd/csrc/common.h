@@ -55,6 +55,20 @@ void timing_events(const char *name, hipEvent_t *start, hipEvent_t *stop);
         }                                                                                   \
     } while (0)
 
+// Linear handles (lut_linear.hip): shape, and the fused fp32 batch-1 forward
+// with a prologue (0 none, 1 RMSNorm with weight w, 2 SwiGLU from a [2K] row)
+// and an optional residual added to the output (may alias y).
+int linear_shape(const void *h, int *K, int *M, int *D);
+int linear_forward_fused(void *h, const float *x, float *y, int pro, const float *w, float eps,
+                         const float *res, hipStream_t st);
+
+// Paged code-domain decode (lut_kv.hip) with the context length read on the
+// device, *len_dev + len_add <= T_max; head dim 128, block dim 16.
+int kv_decode_device_len(const float *q, const uint8_t *kc, const float *ks, const uint8_t *vc,
+                         const float *vs, const float *kcb, const float *vcb, const int *bt,
+                         const int *len_dev, int len_add, int T_max, int P, int Hq, int Hkv,
+                         float sf, float *part_o, float *part_ml, float *out, hipStream_t st);
+
 // LUT[b][g][k] = <x_b[gD:(g+1)D], C[k]> for g < Gp (0 for g >= G) and all 256
 // centroids of the zero-padded codebook cb [256][D]; x [B][K] in dtype.
 int launch_lut_build(const void *x, const float *cb, int B, int K, int D, int G, int Gp,

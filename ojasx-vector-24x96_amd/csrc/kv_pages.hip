@@ -31,13 +31,13 @@
 #include <cmath>
 
 #include "common.h"
+#include "kv_encode.h"
 
 namespace ojx {
 
 namespace {
-constexpr int kNT = 256;
+constexpr int kNT = kEncNT;
 constexpr int kNW = kNT / 64;
-constexpr int kMaxEncGroups = 64;
 }  // namespace
 
 struct QuantParams {
@@ -95,116 +95,21 @@ struct EncodeParams {
     int Hkv, hd, D, G, P, num_pages;
 };
 
-// Distance of x (LDS, D floats) to centroid row c; DT > 0: the row is in
-// registers, DT == 0: read from memory.
-template <int DT>
-__device__ __forceinline__ float centroid_dist(const float *x, const float *creg, const float *cmem,
-                                               int D) {
-    float dist = 0.f;
-    if constexpr (DT > 0) {
-#pragma unroll
-        for (int d = 0; d < DT; ++d) {
-            const float df = x[d] - creg[d];
-            dist = fmaf(df, df, dist);
-        }
-    } else {
-        for (int d = 0; d < D; ++d) {
-            const float df = x[d] - cmem[d];
-            dist = fmaf(df, df, dist);
-        }
-    }
-    return dist;
-}
-
 template <int DT>
 __global__ __launch_bounds__(kNT) void kv_encode_append_kernel(EncodeParams p) {
     extern __shared__ float xs[];                // [2][hd]: k / s_k, v / s_v
-    __shared__ float red[2][kNW];
-    __shared__ float wd[2][kMaxEncGroups][kNW];  // per-wave minimum distance
-    __shared__ int wi[2][kMaxEncGroups][kNW];    // and its lowest centroid
-    const int i = blockIdx.x, h = blockIdx.y, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int i = blockIdx.x, h = blockIdx.y;
+    float kreg[DT > 0 ? DT : 1], vreg[DT > 0 ? DT : 1];
+    const float *kcb = p.kcb ? p.kcb + (size_t)h * 256 * p.D : nullptr;
+    const float *vcb = p.vcb ? p.vcb + (size_t)h * 256 * p.D : nullptr;
+    if (kcb) enc_load_centroids<DT>(kcb, vcb, kreg, vreg);
     const int slot = p.slots[i];
     if (slot < 0 || slot / p.P >= p.num_pages) return;   // skipped slot; workgroup-uniform
-    const float *kr = p.k + ((size_t)i * p.Hkv + h) * p.hd;
-    const float *vr = p.v + ((size_t)i * p.Hkv + h) * p.hd;
-    float mk = 0.f, mv = 0.f;
-    for (int d = tid; d < p.hd; d += kNT) {
-        mk = fmaxf(mk, fabsf(kr[d]));
-        mv = fmaxf(mv, fabsf(vr[d]));
-    }
-    mk = wave_max_f(mk);
-    mv = wave_max_f(mv);
-    if (lane == 0) {
-        red[0][w] = mk;
-        red[1][w] = mv;
-    }
-    __syncthreads();
-    mk = fmaxf(fmaxf(red[0][0], red[0][1]), fmaxf(red[0][2], red[0][3]));
-    mv = fmaxf(fmaxf(red[1][0], red[1][1]), fmaxf(red[1][2], red[1][3]));
-    const float sk = fmaxf(1e-8f, mk) / 127.0f;
-    const float sv = fmaxf(1e-8f, mv) / 127.0f;
-    for (int d = tid; d < p.hd; d += kNT) {
-        xs[d] = kr[d] / sk;
-        xs[p.hd + d] = vr[d] / sv;
-    }
     const int page = slot / p.P;
     const size_t row = ((size_t)page * p.Hkv + h) * p.P + (slot - page * p.P);
-    uint8_t *kc = p.kc + row * p.G;
-    uint8_t *vc = p.vc + row * p.G;
-    if (tid == 0) {
-        p.ks[row] = sk;
-        p.vs[row] = sv;
-    }
-    if (p.kcb == nullptr) {
-        __syncthreads();
-        for (int e = tid; e < 2 * p.G; e += kNT) {
-            const int kv = e >= p.G, g = e - kv * p.G;
-            int q = (int)roundf(xs[kv * p.hd + g * p.D]);
-            q = max(-128, min(127, q));
-            (kv ? vc : kc)[g] = (uint8_t)(q + 128);
-        }
-        return;
-    }
-    const int c = tid;
-    const float *kcr = p.kcb + ((size_t)h * 256 + c) * p.D;
-    const float *vcr = p.vcb + ((size_t)h * 256 + c) * p.D;
-    float kreg[DT > 0 ? DT : 1], vreg[DT > 0 ? DT : 1];
-    if constexpr (DT > 0) {
-#pragma unroll
-        for (int d = 0; d < DT; d += 4) {
-            const float4 a = *reinterpret_cast<const float4 *>(kcr + d);
-            const float4 b = *reinterpret_cast<const float4 *>(vcr + d);
-            kreg[d] = a.x, kreg[d + 1] = a.y, kreg[d + 2] = a.z, kreg[d + 3] = a.w;
-            vreg[d] = b.x, vreg[d + 1] = b.y, vreg[d + 2] = b.z, vreg[d + 3] = b.w;
-        }
-    }
-    __syncthreads();                             // xs complete
-    for (int g = 0; g < p.G; ++g) {
-        const float dk = centroid_dist<DT>(xs + g * p.D, kreg, kcr, p.D);
-        const float dv = centroid_dist<DT>(xs + p.hd + g * p.D, vreg, vcr, p.D);
-        const float mk2 = wave_min_f(dk), mv2 = wave_min_f(dv);
-        const int ik = wave_min_i(dk == mk2 ? c : 0x7fffffff);
-        const int iv = wave_min_i(dv == mv2 ? c : 0x7fffffff);
-        if (lane == 0) {
-            wd[0][g][w] = mk2;
-            wi[0][g][w] = ik;
-            wd[1][g][w] = mv2;
-            wi[1][g][w] = iv;
-        }
-    }
-    __syncthreads();
-    for (int e = tid; e < 2 * p.G; e += kNT) {
-        const int kv = e >= p.G, g = e - kv * p.G;
-        float bm = wd[kv][g][0];
-        int bi = wi[kv][g][0];
-#pragma unroll
-        for (int q = 1; q < kNW; ++q)
-            if (wd[kv][g][q] < bm) {   // strictly smaller: earlier waves hold lower indices
-                bm = wd[kv][g][q];
-                bi = wi[kv][g][q];
-            }
-        (kv ? vc : kc)[g] = (uint8_t)bi;
-    }
+    encode_kv_token<DT>(p.k + ((size_t)i * p.Hkv + h) * p.hd, p.v + ((size_t)i * p.Hkv + h) * p.hd,
+                        kcb, vcb, kreg, vreg, p.hd, p.D, p.G, p.kc + row * p.G, p.vc + row * p.G,
+                        p.ks + row, p.vs + row, xs);
 }
 
 }  // namespace ojx

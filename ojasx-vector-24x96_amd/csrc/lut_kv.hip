@@ -98,6 +98,11 @@ struct KVParams {
     float *out;      // [Hq][hd] (written directly when n_chunks == 1)
     int T, P, Hq, Hkv, hd, D, G, Tc, RS, n_chunks;
     float sf;
+    // Context length read on the device, *len_dev + len_add, when len_dev is
+    // set (kv_decode_small_kernel only): n_chunks then covers the longest
+    // context and chunks past the current one exit at once.
+    const int *len_dev;
+    int len_add;
 };
 
 // One workgroup = (chunk of 256 tokens, kv head, group of RS query heads);
@@ -481,9 +486,11 @@ __global__ __launch_bounds__(kNT) void kv_decode_small_kernel(KVParams p) {
     const int j0 = h * R + blockIdx.z * 4;
     const int nj = min(4, R - (int)blockIdx.z * 4);
     const int c = blockIdx.x;
+    const int T = p.len_dev ? *p.len_dev + p.len_add : p.T;
+    if (c * kSmallC >= T) return;        // whole workgroup: a chunk past the context
     const int t = c * kSmallC + lane;
-    const bool live = t < p.T;
-    const int tc = min(t, p.T - 1);
+    const bool live = t < T;
+    const int tc = min(t, T - 1);
 
     // ---- round trip 1: codebooks, q, block table (one entry per token)
     const float4 *gk = reinterpret_cast<const float4 *>(p.kcb + (size_t)h * 256 * 16);
@@ -587,12 +594,17 @@ __global__ __launch_bounds__(kNT) void kv_decode_small_kernel(KVParams p) {
 // Log-sum-exp merge of the chunks of one query head, chunks in order:
 // (max, sum) pairs staged in LDS, max and normaliser by wave shuffles, then
 // each thread sums one output coordinate over the chunks.
+// With len_dev set, only the first ceil((*len_dev + len_add) / chunk) of the
+// n_chunks (the partials' stride) are merged.
 __global__ __launch_bounds__(kNT) void kv_merge_kernel(const float *part_o, const float *part_ml,
-                                                      int n_chunks, int hd, float *out) {
+                                                      int stride_chunks, int hd, float *out,
+                                                      const int *len_dev, int len_add, int chunk) {
     extern __shared__ float wsm[];   // [n_chunks] chunk weights
     __shared__ float red[kNT / 64];
     const int j = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    const float *ml = part_ml + (size_t)j * n_chunks * 2;
+    const int n_chunks =
+        len_dev ? min(stride_chunks, (*len_dev + len_add + chunk - 1) / chunk) : stride_chunks;
+    const float *ml = part_ml + (size_t)j * stride_chunks * 2;
     float m = -INFINITY;
     for (int c = tid; c < n_chunks; c += kNT) m = fmaxf(m, ml[2 * c]);
 #pragma unroll
@@ -619,7 +631,7 @@ __global__ __launch_bounds__(kNT) void kv_merge_kernel(const float *part_o, cons
     for (int q = 1; q < kNT / 64; ++q) l += red[q];
     const float inv = 1.f / l;
     for (int d = tid; d < hd; d += kNT) {
-        const float *po = part_o + (size_t)j * n_chunks * hd + d;
+        const float *po = part_o + (size_t)j * stride_chunks * hd + d;
         float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
         int c = 0;
         for (; c + 8 <= n_chunks; c += 8) {
@@ -644,6 +656,32 @@ struct KVWork {
     }
 };
 static thread_local KVWork t_work;
+
+// Decode with the context length read on the device (*len_dev + len_add, at
+// most T_max): the short-context kernel over ceil(T_max / 64) chunks, the
+// chunks past the current length exiting at once, then the merge of the live
+// chunks.  Head dim 128, block dim 16; partials part_o [Hq][n][128] and
+// part_ml [Hq][n][2] with n = ceil(T_max / 64).  Launches a fixed grid, so a
+// captured graph can replay it as the context grows.
+int kv_decode_device_len(const float *q, const uint8_t *kc, const float *ks, const uint8_t *vc,
+                         const float *vs, const float *kcb, const float *vcb, const int *bt,
+                         const int *len_dev, int len_add, int T_max, int P, int Hq, int Hkv,
+                         float sf, float *part_o, float *part_ml, float *out, hipStream_t st) {
+    if (Hkv <= 0 || Hq <= 0 || Hq % Hkv || P <= 0 || T_max <= 0) {
+        set_error("invalid KV decode shape Hq=%d Hkv=%d page=%d T_max=%d", Hq, Hkv, P, T_max);
+        return OJASX_ERR_INVALID;
+    }
+    const int n_chunks = (T_max + kSmallC - 1) / kSmallC;
+    const int nz = (Hq / Hkv + 3) / 4;
+    KVParams p{q, kc, vc, ks, vs, kcb, vcb, bt, part_o, part_ml, out, T_max, P,
+               Hq, Hkv, 128, 16, 8, kSmallC, 4, n_chunks, sf, len_dev, len_add};
+    OJX_LAUNCH(kv_decode_small_kernel, dim3(n_chunks, Hkv, nz), dim3(kNT), 0, st, p);
+    if (n_chunks > 1)
+        OJX_LAUNCH(kv_merge_kernel, dim3(Hq), dim3(kNT), (size_t)n_chunks * 4, st, part_o, part_ml,
+                   n_chunks, 128, out, len_dev, len_add, kSmallC);
+    OJX_HIP(hipGetLastError());
+    return OJASX_OK;
+}
 
 int kv_decode(const float *q, const uint8_t *kc, const float *ks, const uint8_t *vc,
               const float *vs, const float *kcb, const float *vcb, const int *bt, int T, int P,
@@ -678,7 +716,7 @@ int kv_decode(const float *q, const uint8_t *kc, const float *ks, const uint8_t 
             OJX_LAUNCH(kv_decode_small_kernel, dim3(n_chunks, Hkv, nz), dim3(kNT), 0, st, p);
             if (n_chunks > 1)
                 OJX_LAUNCH(kv_merge_kernel, dim3(Hq), dim3(kNT), (size_t)n_chunks * 4, st,
-                           wk.o.as<float>(), wk.ml.as<float>(), n_chunks, hd, out);
+                           wk.o.as<float>(), wk.ml.as<float>(), n_chunks, hd, out, nullptr, 0, 1);
             OJX_HIP(hipGetLastError());
             return OJASX_OK;
         }
@@ -705,7 +743,7 @@ int kv_decode(const float *q, const uint8_t *kc, const float *ks, const uint8_t 
         OJX_LAUNCH(kv_decode_wide_kernel, dim3(n_chunks, Hkv, nz), dim3(kWideNT), lds, st, p);
         if (n_chunks > 1)
             OJX_LAUNCH(kv_merge_kernel, dim3(Hq), dim3(kNT), (size_t)n_chunks * 4, st,
-                       wk.o.as<float>(), wk.ml.as<float>(), n_chunks, hd, out);
+                       wk.o.as<float>(), wk.ml.as<float>(), n_chunks, hd, out, nullptr, 0, 1);
         OJX_HIP(hipGetLastError());
         return OJASX_OK;
     }
@@ -731,7 +769,7 @@ int kv_decode(const float *q, const uint8_t *kc, const float *ks, const uint8_t 
     const int nch = p.n_chunks;
     if (nch > 1)
         OJX_LAUNCH(kv_merge_kernel, dim3(Hq), dim3(kNT), (size_t)nch * 4, st,
-                           wk.o.as<float>(), wk.ml.as<float>(), nch, hd, out);
+                           wk.o.as<float>(), wk.ml.as<float>(), nch, hd, out, nullptr, 0, 1);
     OJX_HIP(hipGetLastError());
     return OJASX_OK;
 }

@@ -40,6 +40,7 @@
 //     a fixed order and the epilogue applies (s_m * sum + bias) + outliers in
 //     the reference's order: deterministic results.
 #include <algorithm>
+#include <type_traits>
 #include <cstring>
 #include <vector>
 
@@ -243,20 +244,46 @@ struct DecParams {
     const int *rowp;        // [M+1] (null: no outliers)
     const int *col;         // [nnz]
     const float *val;       // [nnz]
-    const void *x;          // [B][K], 16-byte aligned (fp32) / 8-byte (bf16)
+    const void *x;          // [B][xrow], 16-byte aligned (fp32) / 8-byte (bf16)
     void *y;                // [B][M]
+    const float *pro_w;     // RMSNorm weight [K] (prologue 1)
+    const float *res;       // residual [B][M] added to y (may alias y)
+    float eps;              // RMSNorm epsilon
     int K, M, Mp, S, B, nnz, NW;
+    int xrow;               // elements per token row of x: K, or 2K for SwiGLU
 };
 
+// Prologues of the fused decoder variants, applied as x is staged in LDS:
+//   kProNone    x as given;
+//   kProRms     RMSNorm: the row is staged as x * w and r = 1/sqrt(mean(x^2) + eps)
+//               multiplies the manifold and outlier sums in the epilogue (r is a
+//               per-token scalar, so it factors out of the linear map);
+//   kProSwiglu  x[i] = silu(a[i]) * a[K + i] from a row a of 2K elements
+//               (gate half, then up half), silu(v) = v / (1 + exp(-v)).
+enum { kProNone = 0, kProRms = 1, kProSwiglu = 2 };
+
+__device__ __forceinline__ float silu_f(float v) { return v / (1.0f + expf(-v)); }
+__device__ __forceinline__ float4 swiglu4(float4 g, float4 u) {
+    return make_float4(silu_f(g.x) * u.x, silu_f(g.y) * u.y, silu_f(g.z) * u.z, silu_f(g.w) * u.w);
+}
+__device__ __forceinline__ float4 mul4(float4 a, float4 b) {
+    return make_float4(a.x * b.x, a.y * b.y, a.z * b.z, a.w * b.w);
+}
+__device__ __forceinline__ float sumsq4(float4 a) {
+    return fmaf(a.w, a.w, fmaf(a.z, a.z, fmaf(a.y, a.y, a.x * a.x)));
+}
+
 // Single-kernel forward for block_dim 16 (see the file comment).  x is staged
-// as [BT][S*256] with zeros past K, so groups past G contribute 0.
-template <typename T, int BT, int RPL>
+// as [BT][S*256] with zeros past K, so groups past G contribute 0.  PRO selects
+// a prologue (kPro*), RES adds p.res to the output.
+template <typename T, int BT, int RPL, int PRO = kProNone, bool RES = false>
 __global__ __launch_bounds__(1024) void lut_dec_kernel(DecParams p) {
     constexpr int R = 16 * RPL;            // rows per workgroup
     extern __shared__ float sm[];
     float *cbs = sm;                       // [256][16]
     float *xs = sm + kCB * 16;             // [BT][S*256]
     __shared__ float part[2][16][R][BT];   // [manifold|outlier][wave][row][token]
+    __shared__ float ssq_part[16][BT];     // per-wave sums of x^2 (RMSNorm prologue)
     const int tid = threadIdx.x, nthr = blockDim.x;
     const int lane = tid & 63, w = tid >> 6;
     const int r = lane >> 2, j = lane & 3;
@@ -274,13 +301,19 @@ __global__ __launch_bounds__(1024) void lut_dec_kernel(DecParams p) {
         cv4[u] = reinterpret_cast<const float4 *>(p.cb)[min(tid + u * nthr, 1023)];
     const int nx4 = KS / 4;
     float4 xv4[BT][2];
+    float4 av4[PRO == kProNone ? 1 : BT][2];   // RMSNorm weight or SwiGLU up half
 #pragma unroll
     for (int t = 0; t < BT; ++t) {
         const int tt = min(t, nt - 1);
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
             const int e = min(tid + u * nthr, nx4 - 1) * 4;
-            xv4[t][u] = load4_act(x, (size_t)(t0 + tt) * p.K + min(e, p.K - 4));
+            const int ec = min(e, p.K - 4);
+            xv4[t][u] = load4_act(x, (size_t)(t0 + tt) * p.xrow + ec);
+            if constexpr (PRO == kProRms)
+                av4[t][u] = *reinterpret_cast<const float4 *>(p.pro_w + ec);
+            if constexpr (PRO == kProSwiglu)
+                av4[t][u] = load4_act(x, (size_t)(t0 + tt) * p.xrow + p.K + ec);
             if (e >= p.K) xv4[t][u] = make_float4(0.f, 0.f, 0.f, 0.f);
         }
     }
@@ -317,18 +350,47 @@ __global__ __launch_bounds__(1024) void lut_dec_kernel(DecParams p) {
             for (int u = 0; u < 8; ++u) reinterpret_cast<float4 *>(cbs)[min(b + u * nthr, 1023)] = v[u];
         }
     }
+    float ssq[BT];
 #pragma unroll
-    for (int t = 0; t < BT; ++t)
+    for (int t = 0; t < BT; ++t) {
+        ssq[t] = 0.f;
 #pragma unroll
-        for (int u = 0; u < 2; ++u)
-            reinterpret_cast<float4 *>(xs + t * KS)[min(tid + u * nthr, nx4 - 1)] = xv4[t][u];
+        for (int u = 0; u < 2; ++u) {
+            float4 v = xv4[t][u];
+            if constexpr (PRO == kProRms) {
+                // x^2 once per element: the clamped duplicate indices past nx4 count 0
+                if (tid + u * nthr < nx4) ssq[t] += sumsq4(v);
+                v = mul4(v, av4[t][u]);
+            }
+            if constexpr (PRO == kProSwiglu) v = swiglu4(v, av4[t][u]);
+            if constexpr (PRO == kProSwiglu)
+                if (min(tid + u * nthr, nx4 - 1) * 4 >= p.K) v = make_float4(0.f, 0.f, 0.f, 0.f);
+            reinterpret_cast<float4 *>(xs + t * KS)[min(tid + u * nthr, nx4 - 1)] = v;
+        }
+    }
     if (2 * nthr < nx4) {  // more than two float4 of x per thread (K > 8192)
         for (int t = 0; t < nt; ++t)
             for (int i = tid + 2 * nthr; i < nx4; i += nthr) {
                 const int e = i * 4;
-                reinterpret_cast<float4 *>(xs + t * KS)[i] =
-                    e < p.K ? load4_act(x, (size_t)(t0 + t) * p.K + e) : make_float4(0.f, 0.f, 0.f, 0.f);
+                float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+                if (e < p.K) {
+                    v = load4_act(x, (size_t)(t0 + t) * p.xrow + e);
+                    if constexpr (PRO == kProRms) {
+                        ssq[t] += sumsq4(v);
+                        v = mul4(v, *reinterpret_cast<const float4 *>(p.pro_w + e));
+                    }
+                    if constexpr (PRO == kProSwiglu)
+                        v = swiglu4(v, load4_act(x, (size_t)(t0 + t) * p.xrow + p.K + e));
+                }
+                reinterpret_cast<float4 *>(xs + t * KS)[i] = v;
             }
+    }
+    if constexpr (PRO == kProRms) {
+#pragma unroll
+        for (int t = 0; t < BT; ++t) {
+            const float v = wave_sum_f(ssq[t]);
+            if (lane == 0) ssq_part[w][t] = v;
+        }
     }
     // ---- the lane's first CSR entry of each of its rows: j0 + lq (of 4*NW)
     const int lq = w * 4 + j, LQ = NW * 4;
@@ -434,10 +496,19 @@ __global__ __launch_bounds__(1024) void lut_dec_kernel(DecParams p) {
             a += part[0][k][tid][t];
             o += part[1][k][tid][t];
         }
+        if constexpr (PRO == kProRms) {
+            float q = 0.f;
+            for (int k = 0; k < NW; ++k) q += ssq_part[k][t];
+            const float rn = 1.0f / sqrtf(q / (float)p.K + p.eps);
+            a *= rn;
+            o *= rn;
+        }
         float v = a * sc;
         if (p.bias) v += bs;
         v += o;
-        store_act(y, (size_t)(t0 + t) * p.M + m, v);
+        const size_t yi = (size_t)(t0 + t) * p.M + m;
+        if constexpr (RES) v = p.res[yi] + v;
+        store_act(y, yi, v);
     }
 }
 
@@ -485,8 +556,30 @@ int launch_gather(const GatherParams &gp, int M, dim3 grid_y, size_t lds, hipStr
     return OJASX_OK;
 }
 
+// Fused prologue / epilogue of a decoder call (kPro*, residual); none for
+// the reference-facing entry points.
+struct Fuse {
+    int pro = kProNone;
+    const float *w = nullptr;
+    float eps = 0.f;
+    const float *res = nullptr;
+};
+
+template <typename T, int BT, int RPL, int PRO, bool RES>
+int launch_dec_v(const DecParams &dp, int M, int B, size_t lds, hipStream_t st) {
+    static size_t granted = 0;
+    const void *fn = reinterpret_cast<const void *>(&lut_dec_kernel<T, BT, RPL, PRO, RES>);
+    int rc = ensure_dyn_lds(fn, lds, &granted);
+    if (rc) return rc;
+    dim3 grid((M + 16 * RPL - 1) / (16 * RPL), (B + BT - 1) / BT);
+    OJX_LAUNCH((lut_dec_kernel<T, BT, RPL, PRO, RES>), grid, dim3(64 * dp.NW), lds, st, dp);
+    OJX_HIP(hipGetLastError());
+    return OJASX_OK;
+}
+
 template <typename T, int BT, int RPL>
-int launch_dec(Linear *L, const void *x, void *y, int B, size_t lds, hipStream_t st) {
+int launch_dec(Linear *L, const void *x, void *y, int B, size_t lds, hipStream_t st,
+               const Fuse &f) {
     DecParams dp{};
     dp.codes = L->codes.as<uint8_t>();
     dp.cb = L->codebook.as<float>();
@@ -504,20 +597,34 @@ int launch_dec(Linear *L, const void *x, void *y, int B, size_t lds, hipStream_t
     dp.B = B;
     dp.nnz = (int)L->nnz;
     dp.NW = std::min(L->S, kMaxDecWaves);
-    static size_t granted = 0;
-    const void *fn = reinterpret_cast<const void *>(&lut_dec_kernel<T, BT, RPL>);
-    int rc = ensure_dyn_lds(fn, lds, &granted);
-    if (rc) return rc;
-    dim3 grid((L->M + 16 * RPL - 1) / (16 * RPL), (B + BT - 1) / BT);
-    OJX_LAUNCH((lut_dec_kernel<T, BT, RPL>), grid, dim3(64 * dp.NW), lds, st, dp);
-    OJX_HIP(hipGetLastError());
-    return OJASX_OK;
+    dp.xrow = f.pro == kProSwiglu ? 2 * L->K : L->K;
+    dp.pro_w = f.w;
+    dp.eps = f.eps;
+    dp.res = f.res;
+    const bool fused = f.pro != kProNone || f.res;
+    if constexpr (std::is_same<T, float>::value && BT == 1) {
+        if (fused) {
+            const bool r = f.res != nullptr;
+            if (f.pro == kProRms)
+                return r ? launch_dec_v<T, 1, RPL, kProRms, true>(dp, L->M, B, lds, st)
+                         : launch_dec_v<T, 1, RPL, kProRms, false>(dp, L->M, B, lds, st);
+            if (f.pro == kProSwiglu)
+                return r ? launch_dec_v<T, 1, RPL, kProSwiglu, true>(dp, L->M, B, lds, st)
+                         : launch_dec_v<T, 1, RPL, kProSwiglu, false>(dp, L->M, B, lds, st);
+            return launch_dec_v<T, 1, RPL, kProNone, true>(dp, L->M, B, lds, st);
+        }
+    }
+    if (fused) {
+        set_error("fused prologue / residual: fp32 and batch 1 only");
+        return OJASX_ERR_INVALID;
+    }
+    return launch_dec_v<T, BT, RPL, kProNone, false>(dp, L->M, B, lds, st);
 }
 
 // Single-kernel path when block_dim is 16, x is aligned for vector loads and
 // the staged x fits LDS; returns 1 when the two-kernel path must run instead.
 template <typename T>
-int try_dec(Linear *L, const void *x, void *y, int B, hipStream_t st) {
+int try_dec(Linear *L, const void *x, void *y, int B, hipStream_t st, const Fuse &f = Fuse{}) {
     const size_t align = sizeof(T) == 4 ? 16 : 8;
     if (L->D != 16 || (reinterpret_cast<uintptr_t>(x) % align)) return 1;
     int bt = B >= 3 ? 4 : B;
@@ -529,12 +636,12 @@ int try_dec(Linear *L, const void *x, void *y, int B, hipStream_t st) {
     const long wg32 = (long)((L->M + 31) / 32) * ((B + bt - 1) / bt);
     const bool r2 = wg32 >= 192;
     switch (bt * 2 + (r2 ? 1 : 0)) {
-        case 2: return launch_dec<T, 1, 1>(L, x, y, B, lds, st);
-        case 3: return launch_dec<T, 1, 2>(L, x, y, B, lds, st);
-        case 4: return launch_dec<T, 2, 1>(L, x, y, B, lds, st);
-        case 5: return launch_dec<T, 2, 2>(L, x, y, B, lds, st);
-        case 8: return launch_dec<T, 4, 1>(L, x, y, B, lds, st);
-        default: return launch_dec<T, 4, 2>(L, x, y, B, lds, st);
+        case 2: return launch_dec<T, 1, 1>(L, x, y, B, lds, st, f);
+        case 3: return launch_dec<T, 1, 2>(L, x, y, B, lds, st, f);
+        case 4: return launch_dec<T, 2, 1>(L, x, y, B, lds, st, f);
+        case 5: return launch_dec<T, 2, 2>(L, x, y, B, lds, st, f);
+        case 8: return launch_dec<T, 4, 1>(L, x, y, B, lds, st, f);
+        default: return launch_dec<T, 4, 2>(L, x, y, B, lds, st, f);
     }
 }
 
@@ -608,6 +715,39 @@ int forward(Linear *L, const void *x, void *y, int B, int dtype, hipStream_t st)
 
 int linear_forward(void *h, const void *x, void *y, int B, int dtype, hipStream_t st) {
     return forward(static_cast<Linear *>(h), x, y, B, dtype, st);
+}
+
+int linear_shape(const void *h, int *K, int *M, int *D) {
+    const Linear *L = static_cast<const Linear *>(h);
+    *K = L->K;
+    *M = L->M;
+    *D = L->D;
+    return OJASX_OK;
+}
+
+int linear_forward_fused(void *h, const float *x, float *y, int pro, const float *w, float eps,
+                         const float *res, hipStream_t st) {
+    Linear *L = static_cast<Linear *>(h);
+    if (pro < kProNone || pro > kProSwiglu) {
+        set_error("unknown prologue %d", pro);
+        return OJASX_ERR_INVALID;
+    }
+    if (pro == kProRms && !w) return OJASX_ERR_NULL;
+    if (L->K % 4 || (pro == kProRms && (reinterpret_cast<uintptr_t>(w) & 15))) {
+        set_error("fused linear: in_features %% 4 == 0 and a 16-byte aligned norm weight needed");
+        return OJASX_ERR_INVALID;
+    }
+    Fuse f;
+    f.pro = pro;
+    f.w = w;
+    f.eps = eps;
+    f.res = res;
+    const int rc = try_dec<float>(L, x, y, 1, st, f);
+    if (rc == 1) {
+        set_error("fused linear: block_dim 16 and a 16-byte aligned x needed");
+        return OJASX_ERR_INVALID;
+    }
+    return rc;
 }
 
 int launch_lut_build(const void *x, const float *cb, int B, int K, int D, int G, int Gp,
@@ -721,6 +861,14 @@ OJASX_API int ojasx_linear_forward_device(OjasxLinearHandle handle, const void *
                                           int batch_size, int dtype, void *stream) {
     if (!handle || !x || !y) return OJASX_ERR_NULL;
     return ojx::linear_forward(handle, x, y, batch_size, dtype, static_cast<hipStream_t>(stream));
+}
+
+OJASX_API int ojasx_linear_forward_fused_device(OjasxLinearHandle handle, const float *x,
+                                                float *y, int prologue, const float *norm_weight,
+                                                float eps, const float *residual, void *stream) {
+    if (!handle || !x || !y) return OJASX_ERR_NULL;
+    return ojx::linear_forward_fused(handle, x, y, prologue, norm_weight, eps, residual,
+                                     static_cast<hipStream_t>(stream));
 }
 
 OJASX_API int ojasx_build_lut_device(const void *x, const float *codebook, int batch_size,

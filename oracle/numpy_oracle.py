@@ -262,3 +262,91 @@ def subspace_lut_rvq_gemm(x, codebooks, packed_codes, bits, rows, cols, block, r
     if bias is not None:
         y = y + np.asarray(bias, dtype)[None, :]
     return y.reshape(*shp[:-1], rows)
+
+
+# --- the LUT decoder (ojasx-vector-24x96_amd/csrc/decoder.hip) ------------------
+# Not a reference function: the reference runs its 4B-shaped configuration only
+# as a benchmark description.  Each piece below is textbook arithmetic
+# (RMSNorm, RoPE by rotate-half, softmax attention, SwiGLU) composed with the
+# pinned pieces of this oracle: the dequantised LUT linear (engine_forward /
+# linear_fp64) and the code-domain KV dequantisation K_t = s_t * C[code_t].
+
+def rmsnorm(x, w, eps):
+    x = np.asarray(x, np.float64)
+    return x / np.sqrt(np.mean(x * x, axis=-1, keepdims=True) + eps) * np.asarray(w, np.float64)
+
+
+def rope_tables(max_pos, head_dim, theta):
+    """cos / sin [max_pos][head_dim/2]: angle = fp32(pos) * fp32(1 / theta^(2i/hd)),
+    cos and sin of that fp32 angle rounded to fp32."""
+    half = head_dim // 2
+    inv = (1.0 / np.power(np.float64(theta), np.arange(half, dtype=np.float64) * 2 / head_dim))
+    inv = inv.astype(np.float32)
+    ang = np.arange(max_pos, dtype=np.float32)[:, None] * inv[None, :]
+    return np.cos(ang.astype(np.float64)).astype(np.float32), np.sin(ang.astype(np.float64)).astype(np.float32)
+
+
+def rope(x, cos, sin):
+    """Rotate-half RoPE of one head vector x [hd] with the position's cos/sin [hd/2]."""
+    x = np.asarray(x, np.float64)
+    half = x.shape[-1] // 2
+    c, s = np.asarray(cos, np.float64), np.asarray(sin, np.float64)
+    lo, hi = x[:half], x[half:]
+    return np.concatenate([lo * c - hi * s, hi * c + lo * s])
+
+
+def lut_dense(w):
+    """Dense fp64 matrix of a LUT linear {codebook, codes, csr} with unit scales."""
+    return dequantize(w["codebook"], w["codes"], np.ones(w["codes"].shape[0]), csr=w["csr"])
+
+
+def decoder_step(x, weights, cfg, pos, caches, dense=None):
+    """One greedy step of the LUT decoder in fp64 from the residual x (the
+    token's embedding row) at position `pos`.  caches[l] = (kc, ks, vc, vs)
+    holds every layer's code cache for tokens 0..pos in the paged layout with
+    the identity block table, including the new token's codes (written by the
+    step under test).  Returns (logits, new_kv) with new_kv[l] = (k_rot, v) of
+    the new token per kv head, for checking its codes."""
+    hd, Hq, Hkv = cfg.head_dim, cfg.q_heads, cfg.kv_heads
+    R = Hq // Hkv
+    cos, sin = rope_tables(pos + 1, hd, cfg.rope_theta)
+    dense = dense if dense is not None else {}
+    x = np.asarray(x, np.float64)
+    new_kv = []
+    T = pos + 1
+    for l, w in enumerate(weights["layers"]):
+        W = {k: dense.get((l, k)) for k in ("qkv", "o", "gate_up", "down")}
+        for k in W:
+            if W[k] is None:
+                W[k] = dense[(l, k)] = lut_dense(w[k])
+        h = rmsnorm(x, w["input_norm"], cfg.rms_eps)
+        qkv = W["qkv"] @ h
+        q = qkv[:Hq * hd].reshape(Hq, hd)
+        k = qkv[Hq * hd:(Hq + Hkv) * hd].reshape(Hkv, hd)
+        v = qkv[(Hq + Hkv) * hd:].reshape(Hkv, hd)
+        q = np.stack([rope(rmsnorm(q[j], w["q_norm"], cfg.rms_eps), cos[pos], sin[pos])
+                      for j in range(Hq)])
+        k = np.stack([rope(rmsnorm(k[j], w["k_norm"], cfg.rms_eps), cos[pos], sin[pos])
+                      for j in range(Hkv)])
+        new_kv.append((k, v))
+        kc, ks, vc, vs = caches[l]
+        attn = np.zeros((Hq, hd))
+        for h_ in range(Hkv):
+            kcl = kc[:, h_].reshape(-1, kc.shape[-1])[:T].astype(np.int64)
+            vcl = vc[:, h_].reshape(-1, vc.shape[-1])[:T].astype(np.int64)
+            Kd = w["k_codebook"][h_][kcl].reshape(T, hd) * ks[:, h_].reshape(-1)[:T, None].astype(np.float64)
+            Vd = w["v_codebook"][h_][vcl].reshape(T, hd) * vs[:, h_].reshape(-1)[:T, None].astype(np.float64)
+            for j in range(h_ * R, (h_ + 1) * R):
+                attn[j] = full_softmax_attention(q[j], Kd, Vd, 1.0 / math.sqrt(hd))
+        x = x + W["o"] @ attn.reshape(-1)
+        h2 = rmsnorm(x, w["post_norm"], cfg.rms_eps)
+        gu = W["gate_up"] @ h2
+        I = gu.shape[0] // 2
+        a = silu(gu[:I]) * gu[I:]
+        x = x + W["down"] @ a
+    Wl = dense.get("lm")
+    if Wl is None:
+        Wl = dense["lm"] = lut_dense(weights["lm_head"])
+    logits = Wl @ rmsnorm(x, weights["final_norm"], cfg.rms_eps)
+    return logits, new_kv
+
