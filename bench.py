@@ -18,10 +18,10 @@ end on the launch stream); ``traffic`` is the HBM bytes per launch from the
 rocprofv3 FETCH_SIZE/WRITE_SIZE summary under profiles/ when present.
 ``cpu_baseline`` times the reference's own C++ engine (compiled from its
 sources into oracle/_ref when present, else the repo's C restatement) on the
-host, one thread, on the same inputs.  Extra fields give the MoE,
-KV-decode and KV-append figures of the same run.  Before the timed region one 64 MiB
-device-to-device copy runs: a kernel of known traffic that calibrates the
-PMC byte counters of a profiled run of this script.
+host, one thread, on the same inputs.  Extra fields give the MoE, KV-decode,
+KV-append and 4B-shaped decoder figures of the same run.  Before the timed
+region one 64 MiB device-to-device copy runs: a kernel of known traffic that
+calibrates the PMC byte counters of a profiled run of this script.
 """
 import argparse
 import ctypes
@@ -74,7 +74,8 @@ def parse():
     ap.add_argument("--instances", type=int, default=160)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--no-extra", action="store_true", help="skip the MoE and KV figures")
+    ap.add_argument("--no-extra", action="store_true",
+                    help="skip the MoE, KV and decoder figures")
     return ap.parse_args()
 
 
@@ -284,6 +285,45 @@ def bench_kv_append(pkg, torch, steps, do_cpu, cpu_seconds=2.0):
     return res
 
 
+def bench_decoder(pkg, torch, n_tokens=128, context=4096):
+    """The 4B-shaped LUT decoder (hidden 2560, 36 layers, 32 q / 8 kv heads,
+    MLP 9728, LUT LM head over 151936 tokens): greedy decode of n_tokens at a
+    4096-token code KV context, one HIP graph per token and eager launches.
+    Seeded random weights and context (synthetic_decoder)."""
+    decm = pkg.decoder
+    cfg = decm.DecoderConfig(max_steps=n_tokens, max_context=context + n_tokens)
+    t0 = time.perf_counter()
+    d, _ = decm.synthetic_decoder(cfg, context=context, seed=3, device="cuda:0")
+    t_build = time.perf_counter() - t0
+    res = {"config": "hidden 2560, 36 layers, 32 q / 8 kv heads, head_dim 128, MLP 9728, "
+                     f"vocab {cfg.vocab}, all linears LUT d=16/256 + 0.38% CSR, "
+                     f"{context}-token 8-bit code KV context, page 16",
+           "tokens": n_tokens, "build_s": round(t_build, 1)}
+    runs = {}
+    for mode, graph in (("graph", True), ("eager", False)):
+        d.reset(context)
+        d.generate(1, 4, use_graph=graph)          # warm-up (captures the graph)
+        d.reset(context)
+        t0 = time.perf_counter()
+        toks = d.generate(1, n_tokens, use_graph=graph)
+        el = time.perf_counter() - t0
+        runs[mode] = toks
+        res[mode] = {"tokens_per_s": round(n_tokens / el, 2),
+                     "ms_per_token": round(el / n_tokens * 1e3, 4)}
+    res["graph_equals_eager"] = bool(np.array_equal(runs["graph"], runs["eager"]))
+    d.reset(context)
+    kern = timed_kernels(pkg, lambda: d.generate(1, 8, use_graph=False))
+    res["kernels_per_token_us"] = {k: round(v["avg_us"] * v["calls"] / 8, 2)
+                                   for k, v in sorted(kern.items(), key=lambda kv: -kv[1]["avg_us"] * kv[1]["calls"])}
+    per_layer_codes = (6144 * 160 + 2560 * 256 + 19456 * 160 + 2560 * 608)
+    code_bytes = 36 * per_layer_codes + cfg.vocab * 160
+    ms = res["graph"]["ms_per_token"]
+    res["code_bytes_per_token"] = code_bytes
+    res["achieved_code_GBs"] = round(code_bytes / (ms * 1e-3) / 1e9, 2)
+    d.close()
+    return res
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -394,6 +434,7 @@ def main():
         out["moe_512x_top10"] = bench_moe(pkg, torch, min(args.steps, 400), args.warmup,
                                           args.cpu_seconds / 2, not args.no_cpu)
         out["kv_decode_gqa4"] = bench_kv(pkg, torch, args.steps, not args.no_cpu)
+        out["decoder_4b_shaped"] = bench_decoder(pkg, torch)
     print(json.dumps(out))
 
 

@@ -107,9 +107,29 @@ __global__ __launch_bounds__(kArgNT) void argmax_embed_kernel(const float *logit
     __shared__ int wi[kArgNT / 64];
     __shared__ int pick;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    // each thread visits its indices in increasing order, 8 float4 loads in
+    // flight per batch; strict > keeps the first maximum
     float best = -INFINITY;
     int bi = 0x7fffffff;
-    for (int i = tid; i < V; i += kArgNT) {
+    const int n4 = V / 4;
+    const float4 *l4 = reinterpret_cast<const float4 *>(logits);
+    for (int b = tid; b < n4; b += kArgNT * 8) {
+        float4 v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int i4 = b + u * kArgNT;
+            v[u] = i4 < n4 ? l4[i4] : make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int i = (b + u * kArgNT) * 4;
+            if (v[u].x > best) { best = v[u].x; bi = i; }
+            if (v[u].y > best) { best = v[u].y; bi = i + 1; }
+            if (v[u].z > best) { best = v[u].z; bi = i + 2; }
+            if (v[u].w > best) { best = v[u].w; bi = i + 3; }
+        }
+    }
+    for (int i = n4 * 4 + tid; i < V; i += kArgNT) {
         const float v = logits[i];
         if (v > best) {
             best = v;

@@ -630,6 +630,30 @@ __global__ __launch_bounds__(kNT) void kv_merge_kernel(const float *part_o, cons
 #pragma unroll
     for (int q = 1; q < kNT / 64; ++q) l += red[q];
     const float inv = 1.f / l;
+    if (2 * hd <= kNT) {
+        // two threads per coordinate, even and odd chunks, 16 loads in flight each
+        __shared__ float half_sum[kNT / 2];
+        const int hf = tid / hd, d = tid - hf * hd;
+        float acc = 0.f;
+        if (hf < 2) {
+            const float *po = part_o + (size_t)j * stride_chunks * hd + d;
+            float o[4] = {0.f, 0.f, 0.f, 0.f};
+            int c = hf;
+            for (; c + 30 < n_chunks; c += 32) {
+                float v[16];
+#pragma unroll
+                for (int u = 0; u < 16; ++u) v[u] = po[(size_t)(c + 2 * u) * hd];
+#pragma unroll
+                for (int u = 0; u < 16; ++u) o[u & 3] = fmaf(v[u], wsm[c + 2 * u], o[u & 3]);
+            }
+            for (; c < n_chunks; c += 2) o[0] = fmaf(po[(size_t)c * hd], wsm[c], o[0]);
+            acc = (o[0] + o[1]) + (o[2] + o[3]);
+            if (hf == 1) half_sum[d] = acc;
+        }
+        __syncthreads();
+        if (hf == 0) out[(size_t)j * hd + d] = (acc + half_sum[d]) * inv;
+        return;
+    }
     for (int d = tid; d < hd; d += kNT) {
         const float *po = part_o + (size_t)j * stride_chunks * hd + d;
         float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};

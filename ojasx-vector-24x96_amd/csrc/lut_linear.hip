@@ -275,9 +275,13 @@ __device__ __forceinline__ float sumsq4(float4 a) {
 
 // Single-kernel forward for block_dim 16 (see the file comment).  x is staged
 // as [BT][S*256] with zeros past K, so groups past G contribute 0.  PRO selects
-// a prologue (kPro*), RES adds p.res to the output.
-template <typename T, int BT, int RPL, int PRO = kProNone, bool RES = false>
-__global__ __launch_bounds__(1024) void lut_dec_kernel(DecParams p) {
+// a prologue (kPro*), RES adds p.res to the output.  HO (high occupancy) caps
+// the kernel at 64 VGPRs, so three workgroups of up to 10 waves share a CU:
+// for grids with more workgroups than fit twice per CU, where the 76-VGPR
+// build would run a second round (gate/up 2560 -> 19456: 13.1 -> ~10 us);
+// smaller grids keep the faster per-workgroup build.
+template <typename T, int BT, int RPL, int PRO = kProNone, bool RES = false, bool HO = false>
+__global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(HO ? 8 : 1))) void lut_dec_kernel(DecParams p) {
     constexpr int R = 16 * RPL;            // rows per workgroup
     extern __shared__ float sm[];
     float *cbs = sm;                       // [256][16]
@@ -565,16 +569,29 @@ struct Fuse {
     const float *res = nullptr;
 };
 
-template <typename T, int BT, int RPL, int PRO, bool RES>
-int launch_dec_v(const DecParams &dp, int M, int B, size_t lds, hipStream_t st) {
+template <typename T, int BT, int RPL, int PRO, bool RES, bool HO>
+int launch_dec_g(const DecParams &dp, dim3 grid, size_t lds, hipStream_t st) {
     static size_t granted = 0;
-    const void *fn = reinterpret_cast<const void *>(&lut_dec_kernel<T, BT, RPL, PRO, RES>);
+    const void *fn = reinterpret_cast<const void *>(&lut_dec_kernel<T, BT, RPL, PRO, RES, HO>);
     int rc = ensure_dyn_lds(fn, lds, &granted);
     if (rc) return rc;
-    dim3 grid((M + 16 * RPL - 1) / (16 * RPL), (B + BT - 1) / BT);
-    OJX_LAUNCH((lut_dec_kernel<T, BT, RPL, PRO, RES>), grid, dim3(64 * dp.NW), lds, st, dp);
+    OJX_LAUNCH((lut_dec_kernel<T, BT, RPL, PRO, RES, HO>), grid, dim3(64 * dp.NW), lds, st, dp);
     OJX_HIP(hipGetLastError());
     return OJASX_OK;
+}
+
+// Workgroups above which a batch-1 launch takes the 64-VGPR build: twice the
+// CUs of an MI355X (256).
+constexpr long kHighOccWorkgroups = 512;
+
+template <typename T, int BT, int RPL, int PRO, bool RES>
+int launch_dec_v(const DecParams &dp, int M, int B, size_t lds, hipStream_t st) {
+    dim3 grid((M + 16 * RPL - 1) / (16 * RPL), (B + BT - 1) / BT);
+    if constexpr (BT == 1) {
+        if ((long)grid.x * grid.y > kHighOccWorkgroups)
+            return launch_dec_g<T, BT, RPL, PRO, RES, true>(dp, grid, lds, st);
+    }
+    return launch_dec_g<T, BT, RPL, PRO, RES, false>(dp, grid, lds, st);
 }
 
 template <typename T, int BT, int RPL>

@@ -236,3 +236,17 @@ def test_cpu_tensor_fails_loudly(pkg):
     layer = pkg.engine.SplitManifoldLUTLinear(32, 8)
     with pytest.raises(RuntimeError, match="GPU only"):
         layer(torch.zeros(1, 32))
+
+
+@pytest.mark.parametrize("B", [1, 2, 5])
+def test_large_m_tile_loop(pkg, dev, B):
+    """60000 output rows: more row tiles than resident workgroups, so each
+    workgroup walks several tiles with the codebook and x staged once."""
+    import torch
+    M, K = 60000, 2560
+    d = gen.linear(M, K, B=B, seed=60 + B, scales="u", bias=True)
+    nat = native_linear(pkg, d, M, K)
+    x_t = torch.from_numpy(d["x"]).to(dev)
+    y = dev_forward(pkg, nat, x_t, 0, torch.float32).cpu().numpy()
+    want = cpu.linear_forward(d["x"], d["codebook"], d["codes"], d["scales"], d["bias"], *d["csr"])
+    assert rel_err(y, want) < F32_TOL
