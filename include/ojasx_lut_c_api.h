@@ -187,6 +187,22 @@ OJASX_API int ojasx_dequantize_int8_device(const int8_t *q, const void *scale_f1
                                            long scale_group_stride, void *out, int dtype,
                                            void *stream);
 
+/* ojasx_kv_decode_paged_device with the context length read on the device
+ * (*seq_len_dev, clamped to max_seq_len; 0 leaves out untouched), so a captured
+ * HIP graph can replay the call as the context grows: the launch covers
+ * max_seq_len.  head_dim 128, block_dim 16, 16-byte aligned q and codebooks.
+ * Chunks of 64 * tokens_per_lane tokens (1, 2 or 4; 0 picks by max_seq_len).
+ * Workspace as ojasx_kv_decode_paged_device: call once outside a capture with
+ * the same max_seq_len before capturing. */
+OJASX_API int ojasx_kv_decode_paged_device_len(const float *q, const uint8_t *k_codes,
+                                               const float *k_scales, const uint8_t *v_codes,
+                                               const float *v_scales, const float *k_cb,
+                                               const float *v_cb, const int *block_table,
+                                               const int *seq_len_dev, int max_seq_len,
+                                               int page_size, int num_q_heads, int num_kv_heads,
+                                               int head_dim, int block_dim, float scale_factor,
+                                               int tokens_per_lane, float *out, void *stream);
+
 /* ---- MoE (ref.h:125-150) ---------------------------------------------- */
 OJASX_API OjasxMoEHandle ojasx_create_moe(int num_experts, int hidden_dim,
                                           int intermediate_dim, int top_k, int block_dim,

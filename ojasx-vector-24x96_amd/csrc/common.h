@@ -63,11 +63,19 @@ int linear_forward_fused(void *h, const float *x, float *y, int pro, const float
                          const float *res, hipStream_t st);
 
 // Paged code-domain decode (lut_kv.hip) with the context length read on the
-// device, *len_dev + len_add <= T_max; head dim 128, block dim 16.
+// device, *len_dev + len_add <= T_max; head dim 128, block dim 16; chunks of
+// 64 * tpl tokens (tpl 1, 2 or 4; 0 picks by T_max); partials part_o
+// [Hq][n][128] / part_ml [Hq][n][2], n = kv_device_len_chunks(T_max, tpl).
+int kv_device_len_tpl(int T_max);
+inline int kv_device_len_chunks(int T_max, int tpl) {
+    if (tpl == 0) tpl = kv_device_len_tpl(T_max);
+    return (T_max + 64 * tpl - 1) / (64 * tpl);
+}
 int kv_decode_device_len(const float *q, const uint8_t *kc, const float *ks, const uint8_t *vc,
                          const float *vs, const float *kcb, const float *vcb, const int *bt,
                          const int *len_dev, int len_add, int T_max, int P, int Hq, int Hkv,
-                         float sf, float *part_o, float *part_ml, float *out, hipStream_t st);
+                         float sf, float *part_o, float *part_ml, float *out, hipStream_t st,
+                         int tpl = 0);
 
 // LUT[b][g][k] = <x_b[gD:(g+1)D], C[k]> for g < Gp (0 for g >= G) and all 256
 // centroids of the zero-padded codebook cb [256][D]; x [B][K] in dtype.

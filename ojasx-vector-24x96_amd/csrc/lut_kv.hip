@@ -464,35 +464,37 @@ __global__ __launch_bounds__(kWideNT) void kv_decode_wide_kernel(KVParams p) {
 }
 
 // Short-context fast path (G = 8, D = 16, up to 4 query heads per kv head):
-// chunks of 64 tokens, 256 threads, wave j = query head j, lane = token.
-// A 64-token chunk costs 4x fewer FMAs computing scores directly,
-// <q_j,g, Ck[code]> from the K codebook in LDS, than building LUT_q; the
-// chunk's softmax statistics are in-wave DPP reductions; lane l then owns
-// output dims 2l, 2l+1 and adds p_t * vs_t * Cv[code][..] over the 64 tokens.
+// chunks of 64 * TPL tokens, 256 threads, wave j = query head j, lane l =
+// tokens l, l + 64, ... (TPL per lane).  A short chunk costs 4x fewer FMAs
+// computing scores directly, <q_j,g, Ck[code]> from the K codebook in LDS,
+// than building LUT_q; the chunk's softmax statistics are in-wave DPP
+// reductions; lane l then owns output dims 2l, 2l+1 and adds
+// p_t * vs_t * Cv[code][..] over the chunk's tokens.  Wave u < TPL loads the
+// codes and scales of tokens 64u .. 64u + 63.
 constexpr int kSmallC = 64;
-// Longest context for the small-chunk kernel: measured 13.9 vs 14.7 us (wide)
+// Longest context for the 64-token chunks: measured 13.9 vs 14.7 us (wide)
 // at 4096 tokens and 22.1 vs 15.0 us at 8192 (8 kv / 32 q heads).
 constexpr int kSmallMaxT = 4096;
 
+template <int TPL>
 __global__ __launch_bounds__(kNT) void kv_decode_small_kernel(KVParams p) {
+    constexpr int C = kSmallC * TPL;     // tokens per chunk
     __shared__ float4 ck4[256 * 4];      // K codebook [256][16]
     __shared__ float4 cv4[256 * 4];      // V codebook [256][16]
     __shared__ float4 q4s[4 * 32];       // q [4][128]
-    __shared__ uint2 kcw[kSmallC], vcw[kSmallC];
-    __shared__ float wsc[4][kSmallC];    // p_jt * vs_t
+    __shared__ uint2 kcw[C], vcw[C];
+    __shared__ float wsc[4][C];          // K scale * sf and V scale, then p_jt * vs_t
     const int tid = threadIdx.x, lane = tid & 63, j = tid >> 6;
     const int R = p.Hq / p.Hkv;
     const int h = blockIdx.y;
     const int j0 = h * R + blockIdx.z * 4;
     const int nj = min(4, R - (int)blockIdx.z * 4);
     const int c = blockIdx.x;
-    const int T = p.len_dev ? *p.len_dev + p.len_add : p.T;
-    if (c * kSmallC >= T) return;        // whole workgroup: a chunk past the context
-    const int t = c * kSmallC + lane;
-    const bool live = t < T;
-    const int tc = min(t, T - 1);
+    // device length clamped to the launch's longest context p.T
+    const int T = p.len_dev ? min(*p.len_dev + p.len_add, p.T) : p.T;
+    if (c * C >= T) return;              // whole workgroup: a chunk past the context
 
-    // ---- round trip 1: codebooks, q, block table (one entry per token)
+    // ---- round trip 1: codebooks, q, block table entry of wave j's tokens
     const float4 *gk = reinterpret_cast<const float4 *>(p.kcb + (size_t)h * 256 * 16);
     const float4 *gv = reinterpret_cast<const float4 *>(p.vcb + (size_t)h * 256 * 16);
     float4 a[4], b[4];
@@ -503,12 +505,15 @@ __global__ __launch_bounds__(kNT) void kv_decode_small_kernel(KVParams p) {
     }
     float4 qv = make_float4(0.f, 0.f, 0.f, 0.f);
     if (tid < nj * 32) qv = reinterpret_cast<const float4 *>(p.q + (size_t)j0 * 128)[tid];
-    const int pg = p.bt[tc / p.P];
-    // ---- round trip 2: token codes and scales (wave 0 loads for the chunk)
+    const int tw = c * C + j * kSmallC + lane;   // the token wave j loads (j < TPL)
+    const bool wlive = j < TPL && tw < T;
+    const int twc = min(tw, T - 1);
+    const int pg = p.bt[twc / p.P];
+    // ---- round trip 2: token codes and scales
     uint2 kw = make_uint2(0, 0), vw = make_uint2(0, 0);
     float ksv = 0.f, vsv = 0.f;
-    if (j == 0) {
-        const size_t slot = ((size_t)pg * p.Hkv + h) * p.P + (tc % p.P);
+    if (j < TPL) {
+        const size_t slot = ((size_t)pg * p.Hkv + h) * p.P + (twc % p.P);
         kw = *reinterpret_cast<const uint2 *>(p.kc + slot * 8);
         vw = *reinterpret_cast<const uint2 *>(p.vc + slot * 8);
         ksv = p.ks[slot];
@@ -520,44 +525,63 @@ __global__ __launch_bounds__(kNT) void kv_decode_small_kernel(KVParams p) {
         cv4[tid + u * kNT] = b[u];
     }
     if (tid < 128) q4s[tid] = qv;
-    if (j == 0) {
-        kcw[lane] = kw;
-        vcw[lane] = vw;
-        wsc[0][lane] = live ? ksv * p.sf : 0.f;   // K scale * sf, then V scale below
-        wsc[1][lane] = live ? vsv : 0.f;
+    if (j < TPL) {
+        const int tl = j * kSmallC + lane;
+        kcw[tl] = kw;
+        vcw[tl] = vw;
+        wsc[0][tl] = wlive ? ksv * p.sf : 0.f;
+        wsc[1][tl] = wlive ? vsv : 0.f;
     }
     __syncthreads();
-    const float kf = wsc[0][lane], vf = wsc[1][lane];
-    const uint2 kwl = kcw[lane];
+    float kf[TPL], vf[TPL];
+    uint2 kwl[TPL];
+#pragma unroll
+    for (int u = 0; u < TPL; ++u) {
+        kf[u] = wsc[0][u * kSmallC + lane];
+        vf[u] = wsc[1][u * kSmallC + lane];
+        kwl[u] = kcw[u * kSmallC + lane];
+    }
     __syncthreads();   // wsc is rewritten with the weights below
 
-    // ---- score of token `lane` for head j: sum_g <q_j,g, Ck[code_g]> * ks * sf
-    float s = -INFINITY;
-    if (j < nj) {
-        const uint32_t kd[2] = {kwl.x, kwl.y};
-        float acc = 0.f;
+    // ---- scores of tokens lane + 64u for head j: sum_g <q_j,g, Ck[code_g]> * ks * sf
+    float sc[TPL];
 #pragma unroll
-        for (int g = 0; g < 8; ++g) {
-            const uint32_t code = (kd[g >> 2] >> ((g & 3) * 8)) & 0xffu;
-            const float4 *cr = ck4 + code * 4;
-            const float4 *qr = q4s + j * 32 + g * 4;
-            float dot = 0.f;
+    for (int u = 0; u < TPL; ++u) {
+        sc[u] = -INFINITY;
+        if (j < nj) {
+            const uint32_t kd[2] = {kwl[u].x, kwl[u].y};
+            float acc = 0.f;
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const float4 cq = cr[u], qq = qr[u];
-                dot = fmaf(qq.x, cq.x, dot);
-                dot = fmaf(qq.y, cq.y, dot);
-                dot = fmaf(qq.z, cq.z, dot);
-                dot = fmaf(qq.w, cq.w, dot);
+            for (int g = 0; g < 8; ++g) {
+                const uint32_t code = (kd[g >> 2] >> ((g & 3) * 8)) & 0xffu;
+                const float4 *cr = ck4 + code * 4;
+                const float4 *qr = q4s + j * 32 + g * 4;
+                float dot = 0.f;
+#pragma unroll
+                for (int w = 0; w < 4; ++w) {
+                    const float4 cq = cr[w], qq = qr[w];
+                    dot = fmaf(qq.x, cq.x, dot);
+                    dot = fmaf(qq.y, cq.y, dot);
+                    dot = fmaf(qq.z, cq.z, dot);
+                    dot = fmaf(qq.w, cq.w, dot);
+                }
+                acc += dot;
             }
-            acc += dot;
+            if (c * C + u * kSmallC + lane < T) sc[u] = acc * kf[u];
         }
-        if (live) s = acc * kf;
     }
-    const float m = wave_max_f(s);
-    const float e = (s == -INFINITY) ? 0.f : expf(s - m);
-    const float l = wave_sum_f(e);
-    wsc[j][lane] = e * vf;
+    float smax = sc[0];
+#pragma unroll
+    for (int u = 1; u < TPL; ++u) smax = fmaxf(smax, sc[u]);
+    const float m = wave_max_f(smax);
+    float esum = 0.f;
+#pragma unroll
+    for (int u = 0; u < TPL; ++u) {
+        const float e = (sc[u] == -INFINITY) ? 0.f : expf(sc[u] - m);
+        esum += e;
+        wsc[j][u * kSmallC + lane] = e * vf[u];
+    }
+    const float l = wave_sum_f(esum);
     __syncthreads();
 
     // ---- V: lane owns dims 2*lane, 2*lane+1 (group g = lane / 8)
@@ -566,7 +590,7 @@ __global__ __launch_bounds__(kNT) void kv_decode_small_kernel(KVParams p) {
         const float *cvf = reinterpret_cast<const float *>(cv4);
         float o0 = 0.f, o1 = 0.f;
 #pragma unroll 8
-        for (int tl = 0; tl < kSmallC; ++tl) {
+        for (int tl = 0; tl < C; ++tl) {
             const uint2 cw = vcw[tl];
             const uint32_t code = ((g < 4 ? cw.x : cw.y) >> ((g & 3) * 8)) & 0xffu;
             const float2 cvv = *reinterpret_cast<const float2 *>(cvf + code * 16 + d0);
@@ -604,6 +628,7 @@ __global__ __launch_bounds__(kNT) void kv_merge_kernel(const float *part_o, cons
     const int j = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int n_chunks =
         len_dev ? min(stride_chunks, (*len_dev + len_add + chunk - 1) / chunk) : stride_chunks;
+    if (n_chunks <= 0) return;                      // empty context: out untouched
     const float *ml = part_ml + (size_t)j * stride_chunks * 2;
     float m = -INFINITY;
     for (int c = tid; c < n_chunks; c += kNT) m = fmaxf(m, ml[2 * c]);
@@ -687,22 +712,41 @@ static thread_local KVWork t_work;
 // chunks.  Head dim 128, block dim 16; partials part_o [Hq][n][128] and
 // part_ml [Hq][n][2] with n = ceil(T_max / 64).  Launches a fixed grid, so a
 // captured graph can replay it as the context grows.
+// Tokens per lane of the short-context kernel for a device-length decode of
+// up to T_max tokens (chunks of 64 * TPL).  64-token chunks measured fastest
+// in the decoder at 4224 tokens: 12.5 us per call against 15.6 us with 128
+// (the merge shrinks less than the per-workgroup work grows).
+int kv_device_len_tpl(int T_max) {
+    (void)T_max;
+    return 1;
+}
+
 int kv_decode_device_len(const float *q, const uint8_t *kc, const float *ks, const uint8_t *vc,
                          const float *vs, const float *kcb, const float *vcb, const int *bt,
                          const int *len_dev, int len_add, int T_max, int P, int Hq, int Hkv,
-                         float sf, float *part_o, float *part_ml, float *out, hipStream_t st) {
+                         float sf, float *part_o, float *part_ml, float *out, hipStream_t st,
+                         int tpl) {
     if (Hkv <= 0 || Hq <= 0 || Hq % Hkv || P <= 0 || T_max <= 0) {
         set_error("invalid KV decode shape Hq=%d Hkv=%d page=%d T_max=%d", Hq, Hkv, P, T_max);
         return OJASX_ERR_INVALID;
     }
-    const int n_chunks = (T_max + kSmallC - 1) / kSmallC;
+    if (tpl == 0) tpl = kv_device_len_tpl(T_max);
+    if (tpl != 1 && tpl != 2 && tpl != 4) {
+        set_error("tokens per lane must be 0, 1, 2 or 4 (got %d)", tpl);
+        return OJASX_ERR_INVALID;
+    }
+    const int C = kSmallC * tpl;
+    const int n_chunks = (T_max + C - 1) / C;
     const int nz = (Hq / Hkv + 3) / 4;
     KVParams p{q, kc, vc, ks, vs, kcb, vcb, bt, part_o, part_ml, out, T_max, P,
-               Hq, Hkv, 128, 16, 8, kSmallC, 4, n_chunks, sf, len_dev, len_add};
-    OJX_LAUNCH(kv_decode_small_kernel, dim3(n_chunks, Hkv, nz), dim3(kNT), 0, st, p);
+               Hq, Hkv, 128, 16, 8, C, 4, n_chunks, sf, len_dev, len_add};
+    const dim3 grid(n_chunks, Hkv, nz);
+    if (tpl == 1) OJX_LAUNCH(kv_decode_small_kernel<1>, grid, dim3(kNT), 0, st, p);
+    else if (tpl == 2) OJX_LAUNCH(kv_decode_small_kernel<2>, grid, dim3(kNT), 0, st, p);
+    else OJX_LAUNCH(kv_decode_small_kernel<4>, grid, dim3(kNT), 0, st, p);
     if (n_chunks > 1)
         OJX_LAUNCH(kv_merge_kernel, dim3(Hq), dim3(kNT), (size_t)n_chunks * 4, st, part_o, part_ml,
-                   n_chunks, 128, out, len_dev, len_add, kSmallC);
+                   n_chunks, 128, out, len_dev, len_add, C);
     OJX_HIP(hipGetLastError());
     return OJASX_OK;
 }
@@ -737,7 +781,7 @@ int kv_decode(const float *q, const uint8_t *kc, const float *ks, const uint8_t 
             }
             KVParams p{q, kc, vc, ks, vs, kcb, vcb, bt, wk.o.as<float>(), wk.ml.as<float>(), out, T, P,
                        Hq, Hkv, hd, D, G, kSmallC, 4, n_chunks, sf};
-            OJX_LAUNCH(kv_decode_small_kernel, dim3(n_chunks, Hkv, nz), dim3(kNT), 0, st, p);
+            OJX_LAUNCH(kv_decode_small_kernel<1>, dim3(n_chunks, Hkv, nz), dim3(kNT), 0, st, p);
             if (n_chunks > 1)
                 OJX_LAUNCH(kv_merge_kernel, dim3(Hq), dim3(kNT), (size_t)n_chunks * 4, st,
                            wk.o.as<float>(), wk.ml.as<float>(), n_chunks, hd, out, nullptr, 0, 1);
@@ -972,6 +1016,42 @@ OJASX_API int ojasx_kv_decode_paged_device(const float *q, const uint8_t *k_code
     return kv_decode(q, k_codes, k_scales, v_codes, v_scales, k_cb, v_cb, block_table, seq_len,
                      page_size, num_q_heads, num_kv_heads, head_dim, block_dim, scale_factor, out,
                      static_cast<hipStream_t>(stream), t_work);
+}
+
+OJASX_API int ojasx_kv_decode_paged_device_len(const float *q, const uint8_t *k_codes,
+                                               const float *k_scales, const uint8_t *v_codes,
+                                               const float *v_scales, const float *k_cb,
+                                               const float *v_cb, const int *block_table,
+                                               const int *seq_len_dev, int max_seq_len,
+                                               int page_size, int num_q_heads, int num_kv_heads,
+                                               int head_dim, int block_dim, float scale_factor,
+                                               int tokens_per_lane, float *out, void *stream) {
+    using namespace ojx;
+    if (!q || !k_codes || !k_scales || !v_codes || !v_scales || !k_cb || !v_cb || !block_table ||
+        !seq_len_dev || !out)
+        return OJASX_ERR_NULL;
+    auto aligned = [](const void *ptr, uintptr_t a) { return (reinterpret_cast<uintptr_t>(ptr) % a) == 0; };
+    if (head_dim != 128 || block_dim != 16 || num_kv_heads <= 0 || num_q_heads <= 0 ||
+        num_q_heads % num_kv_heads || max_seq_len <= 0 || page_size <= 0 || !aligned(q, 16) ||
+        !aligned(k_cb, 16) || !aligned(v_cb, 16) || !aligned(k_codes, 8) || !aligned(v_codes, 8)) {
+        set_error("device-length decode: head_dim 128, block_dim 16, 16-byte aligned q and "
+                  "codebooks, 8-byte aligned codes");
+        return OJASX_ERR_INVALID;
+    }
+    if (tokens_per_lane != 0 && tokens_per_lane != 1 && tokens_per_lane != 2 &&
+        tokens_per_lane != 4) {
+        set_error("tokens_per_lane must be 0, 1, 2 or 4 (got %d)", tokens_per_lane);
+        return OJASX_ERR_INVALID;
+    }
+    const int n = kv_device_len_chunks(max_seq_len, tokens_per_lane);
+    int rc = t_work.o.ensure((size_t)num_q_heads * n * 128 * 4);
+    if (!rc) rc = t_work.ml.ensure((size_t)num_q_heads * n * 2 * 4);
+    if (rc) return rc;
+    if (scale_factor <= 0.f) scale_factor = 1.0f / sqrtf(128.f);
+    return kv_decode_device_len(q, k_codes, k_scales, v_codes, v_scales, k_cb, v_cb, block_table,
+                                seq_len_dev, 0, max_seq_len, page_size, num_q_heads, num_kv_heads,
+                                scale_factor, t_work.o.as<float>(), t_work.ml.as<float>(), out,
+                                static_cast<hipStream_t>(stream), tokens_per_lane);
 }
 
 }  // extern "C"

@@ -154,3 +154,97 @@ def test_paged_decode_unaligned_query(pkg, dev):
     assert rc == 0, pkg.lib().ojasx_get_last_error()
     torch.cuda.synchronize()
     check_all_heads(d, out.cpu().numpy(), T, Hq, Hkv)
+
+
+def decode_device_len(pkg, t, d, seq_dev, Tmax, Hq, Hkv, tpl, out, stream=None):
+    rc = pkg.lib().ojasx_kv_decode_paged_device_len(
+        vp(t["q"]), vp(t["k_codes"]), vp(t["k_scales"]), vp(t["v_codes"]), vp(t["v_scales"]),
+        vp(t["k_cb"]), vp(t["v_cb"]), vp(t["block_table"]), vp(seq_dev), Tmax, d["page"], Hq, Hkv,
+        128, 16, -1.0, tpl, vp(out), stream)
+    assert rc == 0, pkg.lib().ojasx_get_last_error()
+
+
+def device_tensors(d, dev):
+    import torch
+    return {k: torch.from_numpy(np.ascontiguousarray(d[k])).to(dev)
+            for k in ("q", "k_codes", "k_scales", "v_codes", "v_scales", "k_cb", "v_cb",
+                      "block_table")}
+
+
+def check_prefix(d, out, T, Hq=32, Hkv=8):
+    """rel <= 1e-5 against the exact fp64 attention over the first T tokens,
+    and against the oracle within 1e-5 plus the oracle's own fp32 error."""
+    R = Hq // Hkv
+    for j in range(Hq):
+        h = j // R
+        kc, ks, vc, vs = (a[:T] for a in gen.kv_logical(d, h))
+        want = cpu.kv_attention_cb(d["q"][j], d["k_cb"][h], d["v_cb"][h], kc, ks, vc, vs)
+        Kd = d["k_cb"][h][kc.astype(np.int64)].reshape(T, -1) * ks[:, None].astype(np.float64)
+        Vd = d["v_cb"][h][vc.astype(np.int64)].reshape(T, -1) * vs[:, None].astype(np.float64)
+        exact = no.full_softmax_attention(d["q"][j], Kd, Vd)
+        assert rel_err(out[j], exact) < 1e-5, (T, j)
+        assert rel_err(out[j], want) < 1e-5 + rel_err(want, exact), (T, j)
+
+
+@pytest.mark.parametrize("T,Tmax,tpl", [(2048, 2048, 1), (3000, 4224, 2), (4100, 4224, 4),
+                                        (1, 300, 2), (130, 4224, 0), (64, 64, 1), (4224, 4224, 0)])
+def test_paged_decode_device_length(pkg, dev, T, Tmax, tpl):
+    """Context length read on the device: chunks of 64, 128 or 256 tokens,
+    the launch sized for Tmax and the chunks past T idle; equal to the oracle
+    over the first T tokens."""
+    import torch
+    d = gen.kv(H_kv=8, H_q=32, T=Tmax, seed=T + Tmax, shuffle_pages=True)
+    t = device_tensors(d, dev)
+    seq = torch.tensor([T], dtype=torch.int32, device=dev)
+    out = torch.empty(32, 128, device=dev)
+    decode_device_len(pkg, t, d, seq, Tmax, 32, 8, tpl, out)
+    torch.cuda.synchronize()
+    check_prefix(d, out.cpu().numpy(), T)
+
+
+def test_paged_decode_device_length_empty_and_errors(pkg, dev):
+    import torch
+    d = gen.kv(H_kv=8, H_q=32, T=300, seed=2)
+    t = device_tensors(d, dev)
+    out = torch.full((32, 128), 7.0, device=dev)
+    seq = torch.zeros(1, dtype=torch.int32, device=dev)
+    decode_device_len(pkg, t, d, seq, 300, 32, 8, 1, out)
+    torch.cuda.synchronize()
+    assert torch.all(out == 7.0)
+    L = pkg.lib()
+    rc = L.ojasx_kv_decode_paged_device_len(
+        vp(t["q"]), vp(t["k_codes"]), vp(t["k_scales"]), vp(t["v_codes"]), vp(t["v_scales"]),
+        vp(t["k_cb"]), vp(t["v_cb"]), vp(t["block_table"]), vp(seq), 300, 16, 32, 8, 128, 16,
+        -1.0, 3, vp(out), None)
+    assert rc == -3
+
+
+def test_paged_decode_device_length_graph_replay(pkg, dev):
+    """One captured HIP graph replayed as the device-side length grows: each
+    replay equals the eager call at that length, bit for bit, and the oracle."""
+    import torch
+    Tmax = 4224
+    d = gen.kv(H_kv=8, H_q=32, T=Tmax, seed=77, shuffle_pages=True)
+    t = device_tensors(d, dev)
+    seq = torch.tensor([100], dtype=torch.int32, device=dev)
+    out = torch.empty(32, 128, device=dev)
+    eager = torch.empty(32, 128, device=dev)
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        decode_device_len(pkg, t, d, seq, Tmax, 32, 8, 0, eager,
+                          ctypes.c_void_p(s.cuda_stream))       # workspace before capture
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        decode_device_len(pkg, t, d, seq, Tmax, 32, 8, 0, out,
+                          ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    for T in (100, 1000, 2500, 4224, 64):
+        seq.fill_(T)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        with torch.cuda.stream(s):
+            decode_device_len(pkg, t, d, seq, Tmax, 32, 8, 0, eager, ctypes.c_void_p(s.cuda_stream))
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), T
+        check_prefix(d, out.cpu().numpy(), T)
