@@ -17,18 +17,21 @@ Faces, each mirroring a reference interface:
   and decode)
 * ``decoder``: ``LUTDecoder`` / ``synthetic_decoder``, the 4B-shaped greedy
   decoder over LUT linears and the code KV cache (HIP graph per token)
+* ``oqpack``: the reference's oqpack.v1 container (verify, mmap, write) and
+  the loader of its residual-VQ linears as GPU LUT layers
 * ``synthetic``: seeded synthetic inputs of the benchmark configurations
 """
 from . import _lib
 from ._lib import OjasxError, lib
 
 __all__ = ["OjasxError", "lib", "native", "engine", "math_engine", "long_context", "decoder",
-           "synthetic"]
+           "oqpack", "synthetic"]
 
 
 def __getattr__(name):
     # Lazy submodules: ``engine`` imports torch, ``native`` only numpy.
     import importlib
-    if name in ("native", "engine", "math_engine", "long_context", "decoder", "synthetic"):
+    if name in ("native", "engine", "math_engine", "long_context", "decoder", "oqpack",
+                "synthetic"):
         return importlib.import_module(f"{__name__}.{name}")
     raise AttributeError(name)
