@@ -18,10 +18,12 @@ end on the launch stream); ``traffic`` is the HBM bytes per launch from the
 rocprofv3 FETCH_SIZE/WRITE_SIZE summary under profiles/ when present.
 ``cpu_baseline`` times the reference's own C++ engine (compiled from its
 sources into oracle/_ref when present, else the repo's C restatement) on the
-host, one thread, on the same inputs.  Extra fields give the MoE, KV-decode,
-KV-append and 4B-shaped decoder figures of the same run.  Before the timed
-region one 64 MiB device-to-device copy runs: a kernel of known traffic that
-calibrates the PMC byte counters of a profiled run of this script.
+host, one thread, on the same inputs.  ``sustained`` runs the same call on
+all N instances in one grouped launch (the sustained rate).  Extra fields
+give the MoE, KV-decode, KV-append and 4B-shaped decoder figures of the same
+run.  Before the timed region one 64 MiB device-to-device copy runs: a
+kernel of known traffic that calibrates the PMC byte counters of a profiled
+run of this script.
 """
 import argparse
 import ctypes
@@ -40,13 +42,15 @@ HBM_PEAK_GBS = 8000.0
 M_GU, K_GU = 6912, 2560
 CAL_COPY_BYTES = 64 << 20
 TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "lut_dec_kernel_2560x6912_b1_hbm_traffic.md")
+GROUP_TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles",
+                                     "lut_group_kernel_160x2560x6912_hbm_traffic.md")
 
 
-def measured_traffic():
+def measured_traffic(path=TRAFFIC_SUMMARY):
     """HBM bytes per launch of the benchmarked kernel, from the committed
     rocprofv3 PMC summary (None when absent)."""
     try:
-        with open(TRAFFIC_SUMMARY) as f:
+        with open(path) as f:
             m = re.search(r"traffic_bytes_per_launch:\s*(\d+)", f.read())
         return int(m.group(1)) if m else None
     except OSError:
@@ -107,6 +111,47 @@ def time_cpu_linear(d, seconds, y_gpu):
     return dict(value=el / n * 1e6, unit="us/call", cores=1, kind=kind,
                 sample=f"{n} calls of LUT-GEMV 2560->6912 B=1 fp32 with CSR, 1 thread, "
                        f"after 50 warm-up calls", parity_rel_err=rel)
+
+
+def bench_sustained(pkg, torch, handles, x, code_bytes, all_bytes, steps):
+    """The same LUT-GEMV on all N weight instances in one grouped launch
+    (ojasx_linear_forward_grouped_device: MFMA-built LUT slices, gathered
+    per row): the sustained rate over a working set above the Infinity
+    Cache, the persistent-launch form of the sustained-GB/s measurement."""
+    L = pkg.lib()
+    vp = ctypes.c_void_p
+    n = len(handles)
+    dev = x.device
+    st = torch.cuda.current_stream()
+    sp = vp(st.cuda_stream)
+    ys = torch.empty(n, M_GU, device=dev)
+    H = (vp * n)(*handles)
+    X = (vp * n)(*([x.data_ptr()] * n))
+    Y = (vp * n)(*[ys[i].data_ptr() for i in range(n)])
+    call = lambda: L.ojasx_linear_forward_grouped_device(H, n, X, Y, sp)
+    for _ in range(5):
+        assert call() == 0, L.ojasx_get_last_error()
+    torch.cuda.synchronize()
+    reps = max(20, steps // 50)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(st)
+    for _ in range(reps):
+        call()
+    e1.record(st)
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / reps
+    kern = timed_kernels(pkg, lambda: [call() for _ in range(reps)])
+    kus = kern["lut_group_kernel"]["avg_us"]
+    ach = n * code_bytes / (kus * 1e-6) / 1e9
+    ach_all = n * all_bytes / (kus * 1e-6) / 1e9
+    return {"kernel": "lut_group_kernel", "instances": n, "launches": reps,
+            "us_per_launch": round(us, 3), "kernel_avg_us": round(kus, 3),
+            "us_per_linear": round(kus / n, 4),
+            "achieved_code_GBs": round(ach, 1), "frac_code": round(ach / HBM_PEAK_GBS, 4),
+            "achieved_all_bytes_GBs": round(ach_all, 1),
+            "frac_all_bytes": round(ach_all / HBM_PEAK_GBS, 4),
+            "algorithmic_bytes_per_launch": n * code_bytes,
+            "traffic": measured_traffic(GROUP_TRAFFIC_SUMMARY) if n == 160 else None}
 
 
 def bench_moe(pkg, torch, steps, warmup, cpu_seconds, do_cpu):
@@ -426,6 +471,7 @@ def main():
         "pmc_calibration_copy_bytes": CAL_COPY_BYTES,
         "wall_s_timed": round(t_wall, 3),
     }
+    out["sustained"] = bench_sustained(pkg, torch, handles, x, code_bytes, all_bytes, args.steps)
     if not args.no_cpu:
         out["cpu_baseline"] = time_cpu_linear(base, args.cpu_seconds, y_bench)
     for h in handles:

@@ -102,6 +102,14 @@ OJASX_API void ojasx_destroy_linear(OjasxLinearHandle handle);
  * stream (a hipStream_t; NULL = default stream). */
 OJASX_API int ojasx_linear_forward_device(OjasxLinearHandle handle, const void *x, void *y,
                                           int batch_size, int dtype, void *stream);
+/* Many independent linears in one launch (no reference counterpart; the
+ * sustained-throughput form of ref.h:72-78): y_i = handles[i](x_i) for i <
+ * count, batch 1, fp32 device pointers (x_i 16-byte aligned), block_dim 16.
+ * Each 16-group LUT slice is built with MFMA and gathered per row.  Calls from
+ * one host thread share a staging buffer: order them on one stream. */
+OJASX_API int ojasx_linear_forward_grouped_device(const OjasxLinearHandle *handles, int count,
+                                                  const float *const *xs, float *const *ys,
+                                                  void *stream);
 /* LUT[b][g][k] = <x_b[g*D:(g+1)*D], C[k]> for k < codebook_size (fp32 out,
  * [batch][groups][codebook_size]); the standalone LUT build of
  * split_manifold_engine.py:185-200 / ojasx_lut_cpu.cpp:18-102 (no reference

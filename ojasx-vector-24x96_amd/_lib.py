@@ -59,6 +59,7 @@ SIGNATURES = {
     "ojasx_dequantize_int8_device": (ci, [vp, vp, cl, ci, ci, cl, cl, vp, ci, vp]),
     "ojasx_kv_encode_append_device": (ci, [vp, vp, ci, ci, ci, ci, vp, vp, vp, ci, ci, vp, vp, vp,
                                            vp, vp]),
+    "ojasx_linear_forward_grouped_device": (ci, [vp, ci, vp, vp, vp]),
     "ojasx_create_decoder": (vp, [ci, ci, ci, ci, ci, ci, ci, ci, ci, ci, cf, cf]),
     "ojasx_destroy_decoder": (None, [vp]),
     "ojasx_decoder_set_layer": (ci, [vp, ci, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp]),

@@ -59,6 +59,20 @@ void timing_events(const char *name, hipEvent_t *start, hipEvent_t *stop);
 // with a prologue (0 none, 1 RMSNorm with weight w, 2 SwiGLU from a [2K] row)
 // and an optional residual added to the output (may alias y).
 int linear_shape(const void *h, int *K, int *M, int *D);
+// One linear of a grouped launch (lut_group.hip).
+struct GroupItem {
+    const uint8_t *codes;     // [S][Mp][16]
+    const float *cb;          // [256][16]
+    const float *scales;      // [M]
+    const float *bias;        // [M] or null
+    const int *rowp;          // [M+1] or null
+    const int *col;
+    const float *val;
+    const float *x;           // [K], 16-byte aligned
+    float *y;                 // [M]
+    int K, M, Mp, S;
+};
+int linear_items(const void *h, GroupItem *it);
 int linear_forward_fused(void *h, const float *x, float *y, int pro, const float *w, float eps,
                          const float *res, hipStream_t st);
 

@@ -1,0 +1,217 @@
+// lut_group.hip -- many independent LUT linears (block_dim 16, batch 1, fp32)
+// in one launch: the sustained-throughput path.
+//
+// y_i[m] = (s_m * sum_g LUT_i[g, codes_i[m, g]] + bias_i[m]) + sum_j val_j x_i[col_j]
+// for every instance i, with LUT_i[g, k] = <x_i[16g..16g+16), C_i[k]> (the
+// formula and epilogue order of ojasx_lut_cpu.cpp:18-206).
+//
+// A single batch-1 call is latency-bound and runs lut_dec_kernel, which dots
+// x with codebook rows read from LDS: 64 bytes of LDS per code byte, which
+// caps it near 1.2 TB/s of code bytes on a full chip.  Here a workgroup owns
+// 512 rows of one instance and builds each 16-group slice's LUT (16 x 256 =
+// X_slice[16 x 16] . C^T[16 x 256]) with 64 fp32 MFMAs (v_mfma_f32_16x16x4f32,
+// 16 per wave), then gathers 16 LUT entries per row: 4 bytes of LDS per code
+// byte.  Codes come from the handles' slice-major tiles [S][Mp][16]: one
+// 16-byte load per row and slice, kPF slices in flight (a register ring
+// shifted each slice), so a slice's gathers do not wait for HBM.  One LUT
+// buffer (26 KB of LDS per workgroup with x) keeps five workgroups per CU.
+#include <algorithm>
+#include <vector>
+
+#include "common.h"
+
+namespace ojx {
+
+namespace {
+constexpr int kGNT = 256;               // threads per workgroup
+constexpr int kGRows = 512;             // rows per workgroup (2 per thread)
+constexpr int kLutStride = 260;         // floats per LUT row (pads the MFMA stores' banks)
+constexpr int kPF = 4;                  // slices of codes in flight
+typedef float v4f __attribute__((ext_vector_type(4)));
+}  // namespace
+
+__global__ __launch_bounds__(kGNT) void lut_group_kernel(const GroupItem *__restrict__ items) {
+    __shared__ float L[16 * kLutStride];
+    extern __shared__ float xs[];                     // [S * 256], zero past K
+    const GroupItem it = items[blockIdx.y];
+    const int base = (int)blockIdx.x * kGRows;
+    if (base >= it.M) return;                         // whole workgroup
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int S = it.S, KS = S * 256;
+    const bool outl = it.rowp != nullptr;
+
+    // ---- round trip 1, L2-resident data first (vmcnt counts in order, so the
+    //      x stores into LDS then do not wait for the HBM code loads): x, the
+    //      codebook operands (wave w: centroid tiles 4w..4w+3), row bounds
+    const int nx4 = KS / 4;
+    float4 xv[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        const int e = min(tid + u * kGNT, nx4 - 1) * 4;
+        xv[u] = *reinterpret_cast<const float4 *>(it.x + min(e, it.K - 4));
+        if (e >= it.K) xv[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    float bop[4][4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks)
+            bop[t][ks] = it.cb[(16 * (4 * w + t) + (lane & 15)) * 16 + 4 * ks + (lane >> 4)];
+    int j0[2] = {0, 0}, j1[2] = {0, 0};               // the rows' CSR ranges
+    if (outl) {
+#pragma unroll
+        for (int r2 = 0; r2 < 2; ++r2) {
+            const int m = min(base + tid + kGNT * r2, it.M - 1);
+            j0[r2] = it.rowp[m];
+            j1[r2] = it.rowp[m + 1];
+        }
+    }
+    // ---- then HBM: codes of slices 0..kPF-1 (past S: repeats, never used)
+    uint4 ring[kPF][2];
+#pragma unroll
+    for (int q = 0; q < kPF; ++q)
+#pragma unroll
+        for (int r2 = 0; r2 < 2; ++r2)   // base + 511 < Mp: Mp is a multiple of 1024
+            ring[q][r2] = *reinterpret_cast<const uint4 *>(
+                it.codes + ((size_t)min(q, S - 1) * it.Mp + base + tid + kGNT * r2) * 16);
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+        if (tid + u * kGNT < nx4) reinterpret_cast<float4 *>(xs)[tid + u * kGNT] = xv[u];
+    for (int i = tid + 4 * kGNT; i < nx4; i += kGNT) {   // K > 4096: the rest of x
+        const int e = i * 4;
+        reinterpret_cast<float4 *>(xs)[i] =
+            e < it.K ? *reinterpret_cast<const float4 *>(it.x + e) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    __syncthreads();
+
+    float acc[2] = {0.f, 0.f};
+    for (int s = 0; s < S; ++s) {
+        // ---- LUT_s[g][k] = sum_d x[16(16s + g) + d] C[k][d]: A = X_s (16 x 16), B = C^T;
+        //      the four tiles' MFMA chains interleaved
+        float a[4];
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) a[ks] = xs[s * 256 + (lane & 15) * 16 + 4 * ks + (lane >> 4)];
+        v4f c[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) c[t] = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+                c[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[ks], bop[t][ks], c[t], 0, 0, 0);
+        // D[g = 4 (lane / 16) + v][k = 16 (4w + t) + lane % 16]
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+            for (int v = 0; v < 4; ++v)
+                L[(4 * (lane >> 4) + v) * kLutStride + 16 * (4 * w + t) + (lane & 15)] = c[t][v];
+        __syncthreads();
+        uint4 cw[2] = {ring[0][0], ring[0][1]};
+#pragma unroll
+        for (int q = 0; q + 1 < kPF; ++q) {
+            ring[q][0] = ring[q + 1][0];
+            ring[q][1] = ring[q + 1][1];
+        }
+        if (s + kPF < S) {
+#pragma unroll
+            for (int r2 = 0; r2 < 2; ++r2)
+                ring[kPF - 1][r2] = *reinterpret_cast<const uint4 *>(
+                    it.codes + ((size_t)(s + kPF) * it.Mp + base + tid + kGNT * r2) * 16);
+        }
+#pragma unroll
+        for (int r2 = 0; r2 < 2; ++r2) {
+            const uint32_t wd[4] = {cw[r2].x, cw[r2].y, cw[r2].z, cw[r2].w};
+            float pg[16];
+#pragma unroll
+            for (int g = 0; g < 16; ++g) pg[g] = L[g * kLutStride + ((wd[g >> 2] >> ((g & 3) * 8)) & 0xffu)];
+            acc[r2] += (((pg[0] + pg[1]) + (pg[2] + pg[3])) + ((pg[4] + pg[5]) + (pg[6] + pg[7]))) +
+                       (((pg[8] + pg[9]) + (pg[10] + pg[11])) + ((pg[12] + pg[13]) + (pg[14] + pg[15])));
+        }
+        __syncthreads();   // the gathers of slice s before the build of s + 1
+    }
+
+    // ---- epilogue: (s_m * sum + bias) + the row's CSR outliers (4 loads in
+    //      flight; batching both rows' entries measured slower)
+#pragma unroll
+    for (int r2 = 0; r2 < 2; ++r2) {
+        const int m = base + tid + kGNT * r2;
+        if (m >= it.M) continue;
+        float o = 0.f;
+        if (outl) {
+            int j = j0[r2];
+            for (; j + 4 <= j1[r2]; j += 4) {
+                int c[4];
+                float v[4];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    c[u] = it.col[j + u];
+                    v[u] = it.val[j + u];
+                }
+#pragma unroll
+                for (int u = 0; u < 4; ++u) o += v[u] * xs[c[u]];
+            }
+            for (; j < j1[r2]; ++j) o += it.val[j] * xs[it.col[j]];
+        }
+        float y = acc[r2] * it.scales[m];
+        if (it.bias) y += it.bias[m];
+        it.y[m] = y + o;
+    }
+}
+
+// Per host thread: the staged item array.
+struct GroupWork {
+    DevBuf items;
+    std::vector<GroupItem> host;
+    ~GroupWork() { items.release(); }
+};
+static thread_local GroupWork t_group;
+
+}  // namespace ojx
+
+extern "C" {
+
+OJASX_API int ojasx_linear_forward_grouped_device(const OjasxLinearHandle *handles, int count,
+                                                  const float *const *xs, float *const *ys,
+                                                  void *stream) {
+    using namespace ojx;
+    if (!handles || !xs || !ys) return OJASX_ERR_NULL;
+    if (count <= 0) return OJASX_OK;
+    if (count > 65535) {
+        set_error("at most 65535 linears per grouped call (got %d)", count);
+        return OJASX_ERR_INVALID;
+    }
+    GroupWork &gw = t_group;
+    gw.host.resize(count);
+    int max_blocks = 0;
+    size_t lds = 0;
+    for (int i = 0; i < count; ++i) {
+        if (!handles[i] || !xs[i] || !ys[i]) return OJASX_ERR_NULL;
+        GroupItem &it = gw.host[i];
+        int rc = linear_items(handles[i], &it);
+        if (rc) return rc;
+        if (reinterpret_cast<uintptr_t>(xs[i]) & 15) {
+            set_error("grouped linear %d: x must be 16-byte aligned", i);
+            return OJASX_ERR_INVALID;
+        }
+        it.x = xs[i];
+        it.y = ys[i];
+        max_blocks = std::max(max_blocks, (it.M + kGRows - 1) / kGRows);
+        lds = std::max(lds, (size_t)it.S * 256 * sizeof(float));
+    }
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    int rc = gw.items.ensure(sizeof(GroupItem) * count);
+    if (rc) return rc;
+    OJX_HIP(hipMemcpyAsync(gw.items.ptr, gw.host.data(), sizeof(GroupItem) * count,
+                           hipMemcpyHostToDevice, st));
+    // the limit covers the static LUT buffers too (their sum passes 64 KB for K > 7000)
+    static size_t granted = 0;
+    rc = ensure_dyn_lds(reinterpret_cast<const void *>(&lut_group_kernel),
+                        lds + 16 * kLutStride * sizeof(float), &granted);
+    if (rc) return rc;
+    OJX_LAUNCH(lut_group_kernel, dim3(max_blocks, count), dim3(kGNT), lds, st,
+               gw.items.as<GroupItem>());
+    OJX_HIP(hipGetLastError());
+    return OJASX_OK;
+}
+
+}  // extern "C"

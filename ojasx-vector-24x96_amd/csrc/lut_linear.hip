@@ -734,6 +734,29 @@ int linear_forward(void *h, const void *x, void *y, int B, int dtype, hipStream_
     return forward(static_cast<Linear *>(h), x, y, B, dtype, st);
 }
 
+// The device arrays of a block_dim-16 handle for the grouped kernel
+// (lut_group.hip); x and y are filled by the caller.
+int linear_items(const void *h, GroupItem *it) {
+    const Linear *L = static_cast<const Linear *>(h);
+    if (L->D != 16 || L->K % 4) {
+        set_error("grouped linear: block_dim 16 and in_features %% 4 == 0 needed (got %d, %d)",
+                  L->D, L->K);
+        return OJASX_ERR_INVALID;
+    }
+    it->codes = L->codes.as<uint8_t>();
+    it->cb = L->codebook.as<float>();
+    it->scales = L->scales.as<float>();
+    it->bias = L->has_bias ? L->bias.as<float>() : nullptr;
+    it->rowp = L->nnz ? L->rowp.as<int>() : nullptr;
+    it->col = L->col.as<int>();
+    it->val = L->val.as<float>();
+    it->K = L->K;
+    it->M = L->M;
+    it->Mp = L->Mp;
+    it->S = L->S;
+    return OJASX_OK;
+}
+
 int linear_shape(const void *h, int *K, int *M, int *D) {
     const Linear *L = static_cast<const Linear *>(h);
     *K = L->K;

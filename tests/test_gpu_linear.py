@@ -250,3 +250,31 @@ def test_large_m_tile_loop(pkg, dev, B):
     y = dev_forward(pkg, nat, x_t, 0, torch.float32).cpu().numpy()
     want = cpu.linear_forward(d["x"], d["codebook"], d["codes"], d["scales"], d["bias"], *d["csr"])
     assert rel_err(y, want) < F32_TOL
+
+
+def test_grouped_linears(pkg, dev):
+    """Many linears of different shapes in one launch (MFMA-built LUT slices)
+    against the oracle, each rel <= 1e-5: partial row blocks, one-slice and
+    38-slice inputs, with and without outliers and bias."""
+    import torch
+    shapes = [(6912, 2560, True, False), (700, 256, False, True), (513, 9728, True, True),
+              (40, 64, True, False), (1025, 4096, False, False)]
+    nats, xs, ys, ds = [], [], [], []
+    for i, (M, K, outl, bias) in enumerate(shapes):
+        d = gen.linear(M, K, B=1, seed=90 + i, scales="u", bias=bias, outliers=outl)
+        nats.append(native_linear(pkg, d, M, K))
+        xs.append(torch.from_numpy(d["x"][0]).to(dev))
+        ys.append(torch.full((M,), 7.0, device=dev))
+        ds.append(d)
+    n = len(shapes)
+    H = (ctypes.c_void_p * n)(*[nat.handle for nat in nats])
+    X = (ctypes.c_void_p * n)(*[x.data_ptr() for x in xs])
+    Y = (ctypes.c_void_p * n)(*[y.data_ptr() for y in ys])
+    rc = pkg.lib().ojasx_linear_forward_grouped_device(H, n, X, Y, None)
+    assert rc == 0, pkg.lib().ojasx_get_last_error()
+    torch.cuda.synchronize()
+    for (M, K, outl, bias), d, y in zip(shapes, ds, ys):
+        csr = d["csr"] if outl else (np.zeros(M + 1, np.int32), np.zeros(0, np.int32),
+                                     np.zeros(0, np.float32))
+        want = cpu.linear_forward(d["x"], d["codebook"], d["codes"], d["scales"], d["bias"], *csr)
+        assert rel_err(y.cpu().numpy()[None], want) < F32_TOL, (M, K)
