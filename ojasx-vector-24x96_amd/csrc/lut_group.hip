@@ -8,13 +8,17 @@
 // A single batch-1 call is latency-bound and runs lut_dec_kernel, which dots
 // x with codebook rows read from LDS: 64 bytes of LDS per code byte, which
 // caps it near 1.2 TB/s of code bytes on a full chip.  Here a workgroup owns
-// 512 rows of one instance and builds each 16-group slice's LUT (16 x 256 =
+// 1024 rows of one instance and builds each 16-group slice's LUT (16 x 256 =
 // X_slice[16 x 16] . C^T[16 x 256]) with 64 fp32 MFMAs (v_mfma_f32_16x16x4f32,
 // 16 per wave), then gathers 16 LUT entries per row: 4 bytes of LDS per code
 // byte.  Codes come from the handles' slice-major tiles [S][Mp][16]: one
 // 16-byte load per row and slice, kPF slices in flight (a register ring
 // shifted each slice), so a slice's gathers do not wait for HBM.  One LUT
-// buffer (26 KB of LDS per workgroup with x) keeps five workgroups per CU.
+// buffer (26 KB of LDS per workgroup with x).  The MFMA build is a fixed
+// 65,536 MACs per slice, so 1024 rows per workgroup (4 per thread) amortise
+// it over twice the codes of 512 (measured per slice, uncontended: build
+// 0.55 us, gather 0.38 us for 2 rows per thread; 160 x 2560->6912 in one
+// launch: 79.6 us at 4 rows per thread, 86-90 us at 2 or 8).
 #include <algorithm>
 #include <vector>
 
@@ -24,9 +28,10 @@ namespace ojx {
 
 namespace {
 constexpr int kGNT = 256;               // threads per workgroup
-constexpr int kGRows = 512;             // rows per workgroup (2 per thread)
+constexpr int kRPT = 4;                 // rows per thread
+constexpr int kGRows = kGNT * kRPT;     // rows per workgroup
 constexpr int kLutStride = 260;         // floats per LUT row (pads the MFMA stores' banks)
-constexpr int kPF = 4;                  // slices of codes in flight
+constexpr int kPF = 2;                  // slices of codes in flight
 typedef float v4f __attribute__((ext_vector_type(4)));
 }  // namespace
 
@@ -57,23 +62,23 @@ __global__ __launch_bounds__(kGNT) void lut_group_kernel(const GroupItem *__rest
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks)
             bop[t][ks] = it.cb[(16 * (4 * w + t) + (lane & 15)) * 16 + 4 * ks + (lane >> 4)];
-    int j0[2] = {0, 0}, j1[2] = {0, 0};               // the rows' CSR ranges
+    int j0[kRPT] = {}, j1[kRPT] = {};               // the rows' CSR ranges
     if (outl) {
 #pragma unroll
-        for (int r2 = 0; r2 < 2; ++r2) {
+        for (int r2 = 0; r2 < kRPT; ++r2) {
             const int m = min(base + tid + kGNT * r2, it.M - 1);
             j0[r2] = it.rowp[m];
             j1[r2] = it.rowp[m + 1];
         }
     }
     // ---- then HBM: codes of slices 0..kPF-1 (past S: repeats, never used)
-    uint4 ring[kPF][2];
+    uint4 ring[kPF][kRPT];
 #pragma unroll
     for (int q = 0; q < kPF; ++q)
 #pragma unroll
-        for (int r2 = 0; r2 < 2; ++r2)   // base + 511 < Mp: Mp is a multiple of 1024
+        for (int r2 = 0; r2 < kRPT; ++r2)   // rows past Mp clamp: loaded, never stored
             ring[q][r2] = *reinterpret_cast<const uint4 *>(
-                it.codes + ((size_t)min(q, S - 1) * it.Mp + base + tid + kGNT * r2) * 16);
+                it.codes + ((size_t)min(q, S - 1) * it.Mp + min(base + tid + kGNT * r2, it.Mp - 1)) * 16);
 #pragma unroll
     for (int u = 0; u < 4; ++u)
         if (tid + u * kGNT < nx4) reinterpret_cast<float4 *>(xs)[tid + u * kGNT] = xv[u];
@@ -84,7 +89,7 @@ __global__ __launch_bounds__(kGNT) void lut_group_kernel(const GroupItem *__rest
     }
     __syncthreads();
 
-    float acc[2] = {0.f, 0.f};
+    float acc[kRPT] = {};
     for (int s = 0; s < S; ++s) {
         // ---- LUT_s[g][k] = sum_d x[16(16s + g) + d] C[k][d]: A = X_s (16 x 16), B = C^T;
         //      the four tiles' MFMA chains interleaved
@@ -106,20 +111,21 @@ __global__ __launch_bounds__(kGNT) void lut_group_kernel(const GroupItem *__rest
             for (int v = 0; v < 4; ++v)
                 L[(4 * (lane >> 4) + v) * kLutStride + 16 * (4 * w + t) + (lane & 15)] = c[t][v];
         __syncthreads();
-        uint4 cw[2] = {ring[0][0], ring[0][1]};
+        uint4 cw[kRPT];
 #pragma unroll
-        for (int q = 0; q + 1 < kPF; ++q) {
-            ring[q][0] = ring[q + 1][0];
-            ring[q][1] = ring[q + 1][1];
-        }
+        for (int r2 = 0; r2 < kRPT; ++r2) cw[r2] = ring[0][r2];
+#pragma unroll
+        for (int q = 0; q + 1 < kPF; ++q)
+#pragma unroll
+            for (int r2 = 0; r2 < kRPT; ++r2) ring[q][r2] = ring[q + 1][r2];
         if (s + kPF < S) {
 #pragma unroll
-            for (int r2 = 0; r2 < 2; ++r2)
+            for (int r2 = 0; r2 < kRPT; ++r2)
                 ring[kPF - 1][r2] = *reinterpret_cast<const uint4 *>(
-                    it.codes + ((size_t)(s + kPF) * it.Mp + base + tid + kGNT * r2) * 16);
+                    it.codes + ((size_t)(s + kPF) * it.Mp + min(base + tid + kGNT * r2, it.Mp - 1)) * 16);
         }
 #pragma unroll
-        for (int r2 = 0; r2 < 2; ++r2) {
+        for (int r2 = 0; r2 < kRPT; ++r2) {
             const uint32_t wd[4] = {cw[r2].x, cw[r2].y, cw[r2].z, cw[r2].w};
             float pg[16];
 #pragma unroll
@@ -133,7 +139,7 @@ __global__ __launch_bounds__(kGNT) void lut_group_kernel(const GroupItem *__rest
     // ---- epilogue: (s_m * sum + bias) + the row's CSR outliers (4 loads in
     //      flight; batching both rows' entries measured slower)
 #pragma unroll
-    for (int r2 = 0; r2 < 2; ++r2) {
+    for (int r2 = 0; r2 < kRPT; ++r2) {
         const int m = base + tid + kGNT * r2;
         if (m >= it.M) continue;
         float o = 0.f;
