@@ -8,35 +8,30 @@
 // A single batch-1 call is latency-bound and runs lut_dec_kernel, which dots
 // x with codebook rows read from LDS: 64 bytes of LDS per code byte, which
 // caps it near 1.2 TB/s of code bytes on a full chip.  Here a workgroup owns
-// 1024 rows of one instance and builds each 16-group slice's LUT (16 x 256 =
-// X_slice[16 x 16] . C^T[16 x 256]) with 64 fp32 MFMAs (v_mfma_f32_16x16x4f32,
-// 16 per wave), then gathers 16 LUT entries per row: 4 bytes of LDS per code
-// byte.  Codes come from the handles' slice-major tiles [S][Mp][16]: one
-// 16-byte load per row and slice, kPF slices in flight (a register ring
-// shifted each slice), so a slice's gathers do not wait for HBM.  One LUT
-// buffer (26 KB of LDS per workgroup with x).  The MFMA build is a fixed
-// 65,536 MACs per slice, so 1024 rows per workgroup (4 per thread) amortise
-// it over twice the codes of 512 (measured per slice, uncontended: build
-// 0.55 us, gather 0.38 us for 2 rows per thread; 160 x 2560->6912 in one
-// launch: 79.6 us at 4 rows per thread, 86-90 us at 2 or 8).
+// 1024 rows of one instance and runs the MFMA-built LUT slice loop of
+// lut_slices.h over the handles' slice-major code tiles: 4 bytes of LDS per
+// code byte.  The MFMA build is a fixed 65,536 MACs per slice, so 1024 rows
+// per workgroup (4 per thread) amortise it over twice the codes of 512
+// (measured per slice, uncontended: build 0.55 us, gather 0.38 us for 2 rows
+// per thread; 160 x 2560->6912 in one launch: 79.6 us at 4 rows per thread,
+// 86-90 us at 2 or 8).
 #include <algorithm>
 #include <vector>
 
 #include "common.h"
+#include "lut_slices.h"
 
 namespace ojx {
 
 namespace {
-constexpr int kGNT = 256;               // threads per workgroup
+constexpr int kPF = 2;                  // slices of codes in flight
+constexpr int kGNT = 256;               // threads per workgroup (4 waves)
 constexpr int kRPT = 4;                 // rows per thread
 constexpr int kGRows = kGNT * kRPT;     // rows per workgroup
-constexpr int kLutStride = 260;         // floats per LUT row (pads the MFMA stores' banks)
-constexpr int kPF = 2;                  // slices of codes in flight
-typedef float v4f __attribute__((ext_vector_type(4)));
 }  // namespace
 
 __global__ __launch_bounds__(kGNT) void lut_group_kernel(const GroupItem *__restrict__ items) {
-    __shared__ float L[16 * kLutStride];
+    __shared__ float L[slices::kLutFloats];
     extern __shared__ float xs[];                     // [S * 256], zero past K
     const GroupItem it = items[blockIdx.y];
     const int base = (int)blockIdx.x * kGRows;
@@ -57,11 +52,7 @@ __global__ __launch_bounds__(kGNT) void lut_group_kernel(const GroupItem *__rest
         if (e >= it.K) xv[u] = make_float4(0.f, 0.f, 0.f, 0.f);
     }
     float bop[4][4];
-#pragma unroll
-    for (int t = 0; t < 4; ++t)
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks)
-            bop[t][ks] = it.cb[(16 * (4 * w + t) + (lane & 15)) * 16 + 4 * ks + (lane >> 4)];
+    slices::load_cb_operands<4>(it.cb, w, lane, bop);
     int j0[kRPT] = {}, j1[kRPT] = {};               // the rows' CSR ranges
     if (outl) {
 #pragma unroll
@@ -71,14 +62,12 @@ __global__ __launch_bounds__(kGNT) void lut_group_kernel(const GroupItem *__rest
             j1[r2] = it.rowp[m + 1];
         }
     }
-    // ---- then HBM: codes of slices 0..kPF-1 (past S: repeats, never used)
+    // ---- then HBM: codes of slices 0..kPF-1 (rows past Mp clamp: loaded, never stored)
+    int row[kRPT];
+#pragma unroll
+    for (int r2 = 0; r2 < kRPT; ++r2) row[r2] = min(base + tid + kGNT * r2, it.Mp - 1);
     uint4 ring[kPF][kRPT];
-#pragma unroll
-    for (int q = 0; q < kPF; ++q)
-#pragma unroll
-        for (int r2 = 0; r2 < kRPT; ++r2)   // rows past Mp clamp: loaded, never stored
-            ring[q][r2] = *reinterpret_cast<const uint4 *>(
-                it.codes + ((size_t)min(q, S - 1) * it.Mp + min(base + tid + kGNT * r2, it.Mp - 1)) * 16);
+    slices::ring_start(it.codes, row, it.Mp, 0, S, ring);
 #pragma unroll
     for (int u = 0; u < 4; ++u)
         if (tid + u * kGNT < nx4) reinterpret_cast<float4 *>(xs)[tid + u * kGNT] = xv[u];
@@ -90,51 +79,7 @@ __global__ __launch_bounds__(kGNT) void lut_group_kernel(const GroupItem *__rest
     __syncthreads();
 
     float acc[kRPT] = {};
-    for (int s = 0; s < S; ++s) {
-        // ---- LUT_s[g][k] = sum_d x[16(16s + g) + d] C[k][d]: A = X_s (16 x 16), B = C^T;
-        //      the four tiles' MFMA chains interleaved
-        float a[4];
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks) a[ks] = xs[s * 256 + (lane & 15) * 16 + 4 * ks + (lane >> 4)];
-        v4f c[4];
-#pragma unroll
-        for (int t = 0; t < 4; ++t) c[t] = v4f{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks)
-#pragma unroll
-            for (int t = 0; t < 4; ++t)
-                c[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[ks], bop[t][ks], c[t], 0, 0, 0);
-        // D[g = 4 (lane / 16) + v][k = 16 (4w + t) + lane % 16]
-#pragma unroll
-        for (int t = 0; t < 4; ++t)
-#pragma unroll
-            for (int v = 0; v < 4; ++v)
-                L[(4 * (lane >> 4) + v) * kLutStride + 16 * (4 * w + t) + (lane & 15)] = c[t][v];
-        __syncthreads();
-        uint4 cw[kRPT];
-#pragma unroll
-        for (int r2 = 0; r2 < kRPT; ++r2) cw[r2] = ring[0][r2];
-#pragma unroll
-        for (int q = 0; q + 1 < kPF; ++q)
-#pragma unroll
-            for (int r2 = 0; r2 < kRPT; ++r2) ring[q][r2] = ring[q + 1][r2];
-        if (s + kPF < S) {
-#pragma unroll
-            for (int r2 = 0; r2 < kRPT; ++r2)
-                ring[kPF - 1][r2] = *reinterpret_cast<const uint4 *>(
-                    it.codes + ((size_t)(s + kPF) * it.Mp + min(base + tid + kGNT * r2, it.Mp - 1)) * 16);
-        }
-#pragma unroll
-        for (int r2 = 0; r2 < kRPT; ++r2) {
-            const uint32_t wd[4] = {cw[r2].x, cw[r2].y, cw[r2].z, cw[r2].w};
-            float pg[16];
-#pragma unroll
-            for (int g = 0; g < 16; ++g) pg[g] = L[g * kLutStride + ((wd[g >> 2] >> ((g & 3) * 8)) & 0xffu)];
-            acc[r2] += (((pg[0] + pg[1]) + (pg[2] + pg[3])) + ((pg[4] + pg[5]) + (pg[6] + pg[7]))) +
-                       (((pg[8] + pg[9]) + (pg[10] + pg[11])) + ((pg[12] + pg[13]) + (pg[14] + pg[15])));
-        }
-        __syncthreads();   // the gathers of slice s before the build of s + 1
-    }
+    slices::slice_loop<4, kRPT, false, kPF>(xs, L, bop, it.codes, row, it.Mp, 0, S, w, lane, ring, acc);
 
     // ---- epilogue: (s_m * sum + bias) + the row's CSR outliers (4 loads in
     //      flight; batching both rows' entries measured slower)
@@ -212,7 +157,7 @@ OJASX_API int ojasx_linear_forward_grouped_device(const OjasxLinearHandle *handl
     // the limit covers the static LUT buffers too (their sum passes 64 KB for K > 7000)
     static size_t granted = 0;
     rc = ensure_dyn_lds(reinterpret_cast<const void *>(&lut_group_kernel),
-                        lds + 16 * kLutStride * sizeof(float), &granted);
+                        lds + slices::lut_bytes(false), &granted);
     if (rc) return rc;
     OJX_LAUNCH(lut_group_kernel, dim3(max_blocks, count), dim3(kGNT), lds, st,
                gw.items.as<GroupItem>());

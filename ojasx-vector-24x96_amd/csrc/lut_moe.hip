@@ -13,15 +13,14 @@
 //
 // Three paths, none with cross-workgroup synchronisation inside a kernel (a
 // "pair" is one routed (token, slot)):
-//  * block_dim 16, fewer than kPartsMinTokens tokens (latency-bound): two
+//  * block_dim 16, fewer than kGroupMinTokens tokens (latency-bound): two
 //    launches that compute LUT entries where they are used, <v_g, C[code]>,
 //    from the codebook and the input vector staged in LDS -- moe_up_dec
 //    (gate/up + SwiGLU per (pair, 32 intermediate rows)) and moe_down_dec
 //    (down + combine per (token, hidden rows), slots summed in slot order).
-//  * block_dim 16, more tokens: the LUT path with each 16-group LUT slice in
-//    LDS, split over slices -- LUT_in build, moe_gu_part (pair, input slice),
-//    moe_dn_part (pair, intermediate slice: SwiGLU, LUT_down slice, gathers),
-//    moe_combine_parts.
+//  * block_dim 16, more tokens: the pairs as grouped LUT GEMVs, each
+//    workgroup building its 16-group LUT slices with MFMA -- moe_gu_group
+//    (gate/up + SwiGLU), moe_dn_group (down, scaled), moe_combine.
 //  * other block sizes: LUT_in build, moe_gateup (gathers from the L2-resident
 //    LUT, SwiGLU, LUT_down rows), moe_down, moe_combine.
 // Every path sums slots in slot order, so results are deterministic.
@@ -31,6 +30,7 @@
 #include <vector>
 
 #include "common.h"
+#include "lut_slices.h"
 
 namespace ojx {
 
@@ -47,11 +47,11 @@ struct MoE {
     int E = 0, H = 0, I = 0, top_k = 0, D = 0;
     int Gin = 0, Gi = 0, Sin = 0, Si = 0, Ip = 0, Hp = 0;
     DevBuf cb_in, cb_dn, gu, dn, gus, dns;
-    DevBuf lut_in, lut_dn, dout, inter, part_gu, part_dn, xstage, ystage, istage, wstage;
+    DevBuf lut_in, lut_dn, dout, inter, gu_part, xstage, ystage, istage, wstage;
     size_t lut_dn_pairs = 0;
     ~MoE() {
         for (DevBuf *b : {&cb_in, &cb_dn, &gu, &dn, &gus, &dns, &lut_in, &lut_dn, &dout, &inter,
-                          &part_gu, &part_dn, &xstage, &ystage, &istage, &wstage})
+                          &gu_part, &xstage, &ystage, &istage, &wstage})
             b->release();
     }
 };
@@ -463,219 +463,206 @@ __global__ __launch_bounds__(1024) void moe_down_dec_kernel(MoEDecParams p) {
 }
 
 // ---------------------------------------------------------------------------
-// Many tokens (block_dim 16): LUT path with the LUT slice in LDS, split over
-// slices.  A "pair" is one routed (token, slot).
-//  A. LUT_in[t][g][k] of every token (lut_build_kernel).
-//  B. moe_gu_part: workgroup = (pair, input slice s): stage LUT_in[t][s]
-//     (16 groups x 256, 16 KB) in LDS, gather the slice's 16 codes of all 2I
-//     gate/up rows of the pair's expert -> part_gu[pair][s][2*Ip].
-//  D. moe_dn_part: workgroup = (pair, intermediate slice sd): sum part_gu over
-//     the input slices in order, scale, SwiGLU for the slice's 256
-//     intermediate values, build their LUT_down rows in LDS, gather the slice's
-//     codes of all H down rows -> part_dn[pair][sd][H].
-//  E. moe_combine_parts: y[t][h] = sum_j w_j * (s_dn[e_j][h] * sum_sd part_dn)
-//     over active slots in slot order.
-struct MoEPartParams {
+// Many tokens (block_dim 16): the routed pairs as grouped LUT GEMVs.  Each
+// workgroup builds the LUT slices it gathers from with MFMA (lut_slices.h),
+// so no LUT goes through memory.  A "pair" is one routed (token, slot).
+//  moe_gu_group: workgroup = (256 IPT intermediate indices, pair, slice part):
+//    x_t staged in LDS, each thread holds the gate row i and the up row Ip + i
+//    of IPT indices i of the pair's expert (one [Sin][2 Ip][16] code tile).
+//    With the input slices in one part it writes inter[pair][i] =
+//    silu(s_g * gate_i) * (s_u * up_i); with NS parts, part ps of slices
+//    [ps Sin / NS, (ps + 1) Sin / NS) writes its raw sums to
+//    gu_part[pair][ps][2 Ip] and moe_dn_group sums the parts in order.
+//  moe_dn_group: workgroup = (256 R hidden rows, pair): inter[pair] staged in
+//    LDS -> dout[pair][h] = s_dn[e][h] * down_h.
+//  moe_combine: y[t][h] = sum_j w_j dout[pair (t, j)][h], active slots in
+//    slot order.
+// Inactive pairs (expert outside [0, E) or |w| < 1e-8) exit at once: their
+// codes are never read.
+struct MoEGroupParams {
     const uint8_t *gu;      // [E][Sin][2][Ip][16]
     const uint8_t *dn;      // [E][Si][Hp][16]
     const float *gus;       // [E][2I]
     const float *dns;       // [E][H]
+    const float *cb_in;     // [256][16]
     const float *cb_dn;     // [256][16]
-    const float *lut_in;    // [T][Sin*16][256]
-    float *part_gu;         // [P][Sin][2*Ip]
-    float *part_dn;         // [P][Si][H]
+    const void *x;          // [T][H]
+    float *inter;           // [P][Ip]
+    float *gu_part;         // [P][NS][2 Ip]
+    float *dout;            // [P][H]
     const int *idx;         // [T][k]
     const float *w;         // [T][k]
-    void *y;                // [T][H]
-    int E, H, I, Sin, Si, Ip, Hp, T, k;
+    int E, H, I, Sin, Si, Ip, Hp, k, NS;
 };
 
-constexpr int kRowsPT = 8;   // code rows per thread per batch in the gather kernels
+// Staging of an input vector into xs[0 .. S*256) (zeros past n): XR values per
+// thread are loaded into registers by stage_load before the caller issues
+// its code loads, and stored by stage_store with the rest.
+template <int NT>
+constexpr int stage_regs() { return NT >= 2048 ? 1 : 2048 / NT; }
 
-__device__ __forceinline__ float gather16_lds(const float *L, uint4 c) {
-    const uint32_t w4[4] = {c.x, c.y, c.z, c.w};
-    float v[kGS];
+template <int NT, typename T>
+__device__ __forceinline__ void stage_load(const T *v, int n, float (&r)[stage_regs<NT>()]) {
 #pragma unroll
-    for (int g = 0; g < kGS; ++g) v[g] = L[g * kCB + ((w4[g >> 2] >> ((g & 3) * 8)) & 0xffu)];
-    float a = 0.f;
-#pragma unroll
-    for (int g = 0; g < kGS; ++g) a += v[g];
-    return a;
+    for (int u = 0; u < stage_regs<NT>(); ++u) {
+        const int i = threadIdx.x + u * NT;
+        r[u] = load_act(v, min(i, n - 1));
+        if (i >= n) r[u] = 0.f;
+    }
 }
 
-__global__ __launch_bounds__(kNT) void moe_gu_part_kernel(MoEPartParams p) {
-    __shared__ float4 lut4[kGS * kCB / 4];          // LUT_in[t][s*16 .. s*16+15][256]
-    const float *lut = reinterpret_cast<const float *>(lut4);
-    const int tid = threadIdx.x;
-    const int pr = blockIdx.x / p.Sin;
-    const int s = blockIdx.x - pr * p.Sin;
-    int e;
-    if (!slot_active(p.idx, p.w, pr, p.E, &e)) return;
-    const int t = pr / p.k;
-    const int nrow = 2 * p.Ip;
-    const float4 *src = reinterpret_cast<const float4 *>(p.lut_in + ((size_t)t * p.Sin + s) * kGS * kCB);
-    float4 v[4];
+template <int NT, typename T>
+__device__ __forceinline__ void stage_store(const T *v, int n, int S, const float (&r)[stage_regs<NT>()],
+                                            float *xs) {
 #pragma unroll
-    for (int u = 0; u < 4; ++u) v[u] = src[tid + u * kNT];
-    const uint8_t *codes = p.gu + ((size_t)e * p.Sin + s) * nrow * kGS;
-    uint4 cw[kRowsPT];
+    for (int u = 0; u < stage_regs<NT>(); ++u) {
+        const int i = threadIdx.x + u * NT;
+        if (i < S * 256) xs[i] = r[u];
+    }
+    for (int i = threadIdx.x + stage_regs<NT>() * NT; i < S * 256; i += NT)
+        xs[i] = i < n ? load_act(v, i) : 0.f;
+}
+
+__device__ __forceinline__ float swiglu_scaled(float g, float u, float sg, float su) {
+    g *= sg;
+    u *= su;
+    return g / (1.f + expf(-g)) * u;
+}
+
+template <typename T, int NW, int IPT, bool DB, int PF>
+__global__ __launch_bounds__(64 * NW) void moe_gu_group_kernel(MoEGroupParams p) {
+    constexpr int NT = 64 * NW;
+    __shared__ float L[DB ? 2 * slices::kLutFloats : slices::kLutFloats];
+    extern __shared__ float xs[];                   // [Sin * 256]
+    const int pr = blockIdx.y;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int ps = blockIdx.z;
+    const int s0 = ps * p.Sin / p.NS, s1 = (ps + 1) * p.Sin / p.NS;
+    // the slot, x of its token and the codebook operands (none depends on the
+    // expert id), then the expert's codes and scales
+    const int e = p.idx[pr];
+    const float wgt = p.w[pr];
+    const T *xr = static_cast<const T *>(p.x) + (size_t)(pr / p.k) * p.H;
+    float xv[stage_regs<NT>()];
+    stage_load<NT>(xr, p.H, xv);
+    float bop[16 / NW][4];
+    slices::load_cb_operands<NW>(p.cb_in, w, lane, bop);
+    if (!(e >= 0 && e < p.E && fabsf(wgt) >= 1e-8f)) return;   // whole workgroup
+    // rows 2r, 2r + 1: gate and up of index i_r (clamped: loaded, never stored)
+    const int i0 = (int)blockIdx.x * (NT * IPT) + tid;
+    int row[2 * IPT];
 #pragma unroll
-    for (int u = 0; u < kRowsPT; ++u) cw[u] = ld_codes(codes + (size_t)min(tid + u * kNT, nrow - 1) * kGS);
+    for (int r = 0; r < IPT; ++r) {
+        const int i = min(i0 + NT * r, p.I - 1);
+        row[2 * r] = i;
+        row[2 * r + 1] = p.Ip + i;
+    }
+    const uint8_t *codes = p.gu + (size_t)e * p.Sin * 2 * p.Ip * kGS;
+    uint4 ring[PF][2 * IPT];
+    slices::ring_start(codes, row, 2 * p.Ip, s0, s1, ring);
+    float sg[IPT], su[IPT];
+    if (p.NS == 1) {
+        const float *sc = p.gus + (size_t)e * 2 * p.I;
 #pragma unroll
-    for (int u = 0; u < 4; ++u) lut4[tid + u * kNT] = v[u];
+        for (int r = 0; r < IPT; ++r) {
+            sg[r] = sc[row[2 * r]];
+            su[r] = sc[p.I + row[2 * r]];
+        }
+    }
+    stage_store<NT>(xr, p.H, p.Sin, xv, xs);
     __syncthreads();
-    float *out = p.part_gu + ((size_t)pr * p.Sin + s) * nrow;
-    for (int r0 = 0; r0 < nrow; r0 += kRowsPT * kNT) {
-        uint4 nx[kRowsPT];
-        const bool more = r0 + kRowsPT * kNT < nrow;
-        if (more) {
+    float acc[2 * IPT] = {};
+    slices::slice_loop<NW, 2 * IPT, DB, PF>(xs, L, bop, codes, row, 2 * p.Ip, s0, s1, w, lane, ring, acc);
 #pragma unroll
-            for (int u = 0; u < kRowsPT; ++u)
-                nx[u] = ld_codes(codes + (size_t)min(r0 + kRowsPT * kNT + tid + u * kNT, nrow - 1) * kGS);
-        }
-#pragma unroll
-        for (int u = 0; u < kRowsPT; ++u) {
-            const int row = r0 + tid + u * kNT;
-            const float a = gather16_lds(lut, cw[u]);
-            if (row < nrow) out[row] = a;
-        }
-        if (more) {
-#pragma unroll
-            for (int u = 0; u < kRowsPT; ++u) cw[u] = nx[u];
+    for (int r = 0; r < IPT; ++r) {
+        const int i = i0 + NT * r;
+        if (i >= p.I) continue;
+        if (p.NS == 1) {
+            p.inter[(size_t)pr * p.Ip + i] = swiglu_scaled(acc[2 * r], acc[2 * r + 1], sg[r], su[r]);
+        } else {
+            float *o = p.gu_part + ((size_t)pr * p.NS + ps) * 2 * p.Ip;
+            o[i] = acc[2 * r];
+            o[p.Ip + i] = acc[2 * r + 1];
         }
     }
 }
 
-__global__ __launch_bounds__(kNT) void moe_dn_part_kernel(MoEPartParams p) {
-    __shared__ float inter_s[kCB];                  // the slice's 256 intermediate values
-    __shared__ float lut[kGS * kCB];                // LUT_down rows of the slice's 16 groups
-    const int tid = threadIdx.x;
-    const int pr = blockIdx.x / p.Si;
-    const int sd = blockIdx.x - pr * p.Si;
-    int e;
-    if (!slot_active(p.idx, p.w, pr, p.E, &e)) return;
-    const int nrow = 2 * p.Ip;
-    // ---- loads: gate/up partials of intermediate index i, codebook row tid,
-    // down codes of the first rows
-    const int i = sd * kCB + tid;                   // < Ip (Ip is a multiple of 256)
-    const float *pg = p.part_gu + (size_t)pr * p.Sin * nrow;
-    float gv[16], uv[16];
+// NS: gate/up parts to sum (1: the intermediate vector is ready in inter).
+template <int NW, int R, bool DB, int PF, int NS>
+__global__ __launch_bounds__(64 * NW) void moe_dn_group_kernel(MoEGroupParams p) {
+    constexpr int NT = 64 * NW, XR = stage_regs<NT>();
+    __shared__ float L[DB ? 2 * slices::kLutFloats : slices::kLutFloats];
+    extern __shared__ float xs[];                   // [Si * 256]
+    const int pr = blockIdx.y;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int e = p.idx[pr];
+    const float wgt = p.w[pr];
+    // the pair's intermediate vector (or its gate/up part sums, in part
+    // order) and the codebook operands, then the expert's codes and scales
+    float gv[XR], uv[XR];
+    if constexpr (NS == 1) {
+        stage_load<NT>(p.inter + (size_t)pr * p.Ip, p.I, gv);
+    } else {
+        const float *gp = p.gu_part + (size_t)pr * NS * 2 * p.Ip;
 #pragma unroll
-    for (int s = 0; s < 16; ++s) {
-        const int ss = min(s, p.Sin - 1);
-        gv[s] = pg[(size_t)ss * nrow + i];
-        uv[s] = pg[(size_t)ss * nrow + p.Ip + i];
-    }
-    const int ic = min(i, p.I - 1);
-    const float sg = p.gus[(size_t)e * 2 * p.I + ic];
-    const float su = p.gus[(size_t)e * 2 * p.I + p.I + ic];
-    float c[kGS];
-    {
-        const float4 *c4 = reinterpret_cast<const float4 *>(p.cb_dn + tid * kGS);
+        for (int u = 0; u < XR; ++u) {
+            const int i = min(tid + u * NT, p.I - 1);
+            float g = 0.f, v = 0.f;
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const float4 f = c4[q];
-            c[4 * q] = f.x;
-            c[4 * q + 1] = f.y;
-            c[4 * q + 2] = f.z;
-            c[4 * q + 3] = f.w;
-        }
-    }
-    const uint8_t *codes = p.dn + ((size_t)e * p.Si + sd) * p.Hp * kGS;
-    uint4 cw[kRowsPT];
-#pragma unroll
-    for (int u = 0; u < kRowsPT; ++u) cw[u] = ld_codes(codes + (size_t)min(tid + u * kNT, p.Hp - 1) * kGS);
-    // ---- SwiGLU of intermediate value i (partials summed in slice order)
-    {
-        float g = 0.f, u = 0.f;
-#pragma unroll
-        for (int s = 0; s < 16; ++s) {
-            if (s < p.Sin) {
-                g += gv[s];
-                u += uv[s];
+            for (int q = 0; q < NS; ++q) {
+                g += gp[(size_t)q * 2 * p.Ip + i];
+                v += gp[(size_t)q * 2 * p.Ip + p.Ip + i];
             }
+            gv[u] = g;
+            uv[u] = v;
         }
-        for (int s = 16; s < p.Sin; ++s) {       // more than 16 input slices (H > 4096)
-            g += pg[(size_t)s * nrow + i];
-            u += pg[(size_t)s * nrow + p.Ip + i];
+    }
+    float bop[16 / NW][4];
+    slices::load_cb_operands<NW>(p.cb_dn, w, lane, bop);
+    if (!(e >= 0 && e < p.E && fabsf(wgt) >= 1e-8f)) return;
+    const int h0 = (int)blockIdx.x * (NT * R) + tid;
+    int row[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) row[r] = min(h0 + NT * r, p.H - 1);
+    const uint8_t *codes = p.dn + (size_t)e * p.Si * p.Hp * kGS;
+    uint4 ring[PF][R];
+    slices::ring_start(codes, row, p.Hp, 0, p.Si, ring);
+    float scl[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) scl[r] = p.dns[(size_t)e * p.H + row[r]];
+    if constexpr (NS == 1) {
+        stage_store<NT>(p.inter + (size_t)pr * p.Ip, p.I, p.Si, gv, xs);
+    } else {
+        const float *sc = p.gus + (size_t)e * 2 * p.I;
+        const float *gp = p.gu_part + (size_t)pr * NS * 2 * p.Ip;
+#pragma unroll
+        for (int u = 0; u < XR; ++u) {
+            const int i = tid + u * NT;
+            const int ic = min(i, p.I - 1);
+            const float v = swiglu_scaled(gv[u], uv[u], sc[ic], sc[p.I + ic]);
+            if (i < p.Si * 256) xs[i] = i < p.I ? v : 0.f;
         }
-        g *= sg;
-        u *= su;
-        inter_s[tid] = i < p.I ? g / (1.f + expf(-g)) * u : 0.f;
+        for (int i = tid + XR * NT; i < p.Si * 256; i += NT) {   // I > 256 XR
+            float v = 0.f;
+            if (i < p.I) {
+                float g = 0.f, u = 0.f;
+                for (int q = 0; q < NS; ++q) {
+                    g += gp[(size_t)q * 2 * p.Ip + i];
+                    u += gp[(size_t)q * 2 * p.Ip + p.Ip + i];
+                }
+                v = swiglu_scaled(g, u, sc[i], sc[p.I + i]);
+            }
+            xs[i] = v;
+        }
     }
     __syncthreads();
-    // ---- LUT_down[g][tid] for the slice's 16 groups
+    float acc[R] = {};
+    slices::slice_loop<NW, R, DB, PF>(xs, L, bop, codes, row, p.Hp, 0, p.Si, w, lane, ring, acc);
 #pragma unroll
-    for (int g = 0; g < kGS; ++g) {
-        float dot = 0.f;
-#pragma unroll
-        for (int d = 0; d < kGS; ++d) dot = fmaf(inter_s[g * kGS + d], c[d], dot);
-        lut[g * kCB + tid] = dot;
+    for (int r = 0; r < R; ++r) {
+        const int h = h0 + NT * r;
+        if (h < p.H) p.dout[(size_t)pr * p.H + h] = scl[r] * acc[r];
     }
-    __syncthreads();
-    float *out = p.part_dn + ((size_t)pr * p.Si + sd) * p.H;
-    for (int r0 = 0; r0 < p.H; r0 += kRowsPT * kNT) {
-        uint4 nx[kRowsPT];
-        const bool more = r0 + kRowsPT * kNT < p.H;
-        if (more) {
-#pragma unroll
-            for (int u = 0; u < kRowsPT; ++u)
-                nx[u] = ld_codes(codes + (size_t)min(r0 + kRowsPT * kNT + tid + u * kNT, p.Hp - 1) * kGS);
-        }
-#pragma unroll
-        for (int u = 0; u < kRowsPT; ++u) {
-            const int h = r0 + tid + u * kNT;
-            const float a = gather16_lds(lut, cw[u]);
-            if (h < p.H) out[h] = a;
-        }
-        if (more) {
-#pragma unroll
-            for (int u = 0; u < kRowsPT; ++u) cw[u] = nx[u];
-        }
-    }
-}
-
-// Slots are taken KB at a time with all their loads (slot ids, weights, down
-// partials of up to kCS slices, scales) in flight together: two round trips
-// per batch instead of two per slot.
-template <typename T>
-__global__ __launch_bounds__(kNT) void moe_combine_parts_kernel(MoEPartParams p) {
-    constexpr int KB = 16, kCS = 4;
-    const int t = blockIdx.y;
-    const int h = min((int)(blockIdx.x * kNT + threadIdx.x), p.H - 1);
-    float y = 0.f;
-    for (int j0 = 0; j0 < p.k; j0 += KB) {
-        int ev[KB];
-        float wv[KB];
-        bool on[KB];
-#pragma unroll
-        for (int u = 0; u < KB; ++u) {
-            const int pr = t * p.k + min(j0 + u, p.k - 1);
-            on[u] = slot_active(p.idx, p.w, pr, p.E, &ev[u]) && j0 + u < p.k;
-            wv[u] = p.w[pr];
-        }
-        float a[KB], sc[KB];
-#pragma unroll
-        for (int u = 0; u < KB; ++u) {
-            const int pr = t * p.k + min(j0 + u, p.k - 1);
-            const int e = on[u] ? ev[u] : 0;
-            const float *pd = p.part_dn + (size_t)pr * p.Si * p.H + h;
-            float v[kCS];
-#pragma unroll
-            for (int s = 0; s < kCS; ++s) v[s] = pd[(size_t)min(s, p.Si - 1) * p.H];
-            float acc = 0.f;
-#pragma unroll
-            for (int s = 0; s < kCS; ++s)
-                if (s < p.Si) acc += v[s];
-            for (int s = kCS; s < p.Si; ++s) acc += pd[(size_t)s * p.H];   // I > 1024
-            a[u] = acc;
-            sc[u] = p.dns[(size_t)e * p.H + h];
-        }
-#pragma unroll
-        for (int u = 0; u < KB; ++u)
-            if (on[u]) y += wv[u] * (sc[u] * a[u]);
-    }
-    if ((int)(blockIdx.x * kNT + threadIdx.x) < p.H) store_act(static_cast<T *>(p.y), (size_t)t * p.H + h, y);
 }
 
 template <typename T>
@@ -767,10 +754,10 @@ __global__ __launch_bounds__(kNT) void moe_route_kernel(const float *logits, int
 namespace {
 
 constexpr size_t kMaxLds = 160 * 1024;
-// From this many tokens the LUT path (LUT in LDS, split over slices) beats
-// computing LUT entries in place: measured 24.3 vs 23.7 us at 4 tokens and
-// 26.5 vs 40.5 us at 8 on the 512-expert H 2048 / I 768 top-10 layer.
-constexpr int kPartsMinTokens = 5;
+// From this many tokens the grouped path beats computing LUT entries in place:
+// measured 18.4 vs 21.6 us at 3 tokens, 16.9 vs 18.2 us at 2 (the 512-expert
+// H 2048 / I 768 top-10 layer).
+constexpr int kGroupMinTokens = 3;
 
 template <typename T>
 int moe_forward_dec(MoE *m, const void *x, const int *idx, const float *w, void *y, int T_, int k,
@@ -832,30 +819,55 @@ int moe_forward_dec(MoE *m, const void *x, const int *idx, const float *w, void 
     return OJASX_OK;
 }
 
+// Launch shapes of the grouped path (the 512-expert H 2048 / I 768 top-10
+// layer, 3-16 tokens): gate/up workgroups of 4 waves with one intermediate
+// index per thread, down workgroups of 8 waves with one hidden row per
+// thread, both with two LUT buffers and two slices of codes in flight; the
+// gate/up input slices split in two parts below 128 routed slots, where
+// there are too few workgroups to fill the CUs.
+constexpr int kGuWaves = 4, kGuIdx = 1, kDnWaves = 8, kDnRows = 1, kGroupPF = 2;
+constexpr bool kGroupDB = true;
+constexpr size_t kGroupSplitBelow = 128;
+
+template <int NS>
+int launch_dn(const MoEGroupParams &p, size_t P, size_t lds, hipStream_t st) {
+    const void *fn = reinterpret_cast<const void *>(
+        &moe_dn_group_kernel<kDnWaves, kDnRows, kGroupDB, kGroupPF, NS>);
+    static size_t granted = 0;
+    int rc = ensure_dyn_lds(fn, lds + slices::lut_bytes(kGroupDB), &granted);
+    if (rc) return rc;
+    const int nb = (p.H + 64 * kDnWaves * kDnRows - 1) / (64 * kDnWaves * kDnRows);
+    OJX_LAUNCH((moe_dn_group_kernel<kDnWaves, kDnRows, kGroupDB, kGroupPF, NS>), dim3(nb, P),
+               dim3(64 * kDnWaves), lds, st, p);
+    return OJASX_OK;
+}
+
 template <typename T>
-int moe_forward_parts(MoE *m, const void *x, const int *idx, const float *w, void *y, int T_, int k,
-                      int dtype, hipStream_t st) {
+int moe_forward_group(MoE *m, const void *x, const int *idx, const float *w, void *y, int T_, int k,
+                      hipStream_t st) {
     const size_t P = (size_t)T_ * k;
-    const int Gp_in = m->Sin * kGS;
-    int rc = m->lut_in.ensure((size_t)T_ * Gp_in * kCB * sizeof(float));
-    if (!rc) rc = m->part_gu.ensure(P * m->Sin * 2 * m->Ip * sizeof(float));
-    if (!rc) rc = m->part_dn.ensure(P * m->Si * m->H * sizeof(float));
+    if (P > 65535) {
+        set_error("at most 65535 routed slots per call (got %zu)", P);
+        return OJASX_ERR_INVALID;
+    }
+    const int ns = P < kGroupSplitBelow && m->Sin >= 2 ? 2 : 1;
+    int rc = m->inter.ensure(P * m->Ip * sizeof(float));
+    if (!rc) rc = m->dout.ensure(P * m->H * sizeof(float));
+    if (!rc && ns > 1) rc = m->gu_part.ensure(P * ns * 2 * m->Ip * sizeof(float));
     if (rc) return rc;
-    rc = launch_lut_build(x, m->cb_in.as<float>(), T_, m->H, m->D, m->Gin, Gp_in,
-                          m->lut_in.as<float>(), dtype, st);
-    if (rc) return rc;
-    MoEPartParams p{};
+    MoEGroupParams p{};
     p.gu = m->gu.as<uint8_t>();
     p.dn = m->dn.as<uint8_t>();
     p.gus = m->gus.as<float>();
     p.dns = m->dns.as<float>();
+    p.cb_in = m->cb_in.as<float>();
     p.cb_dn = m->cb_dn.as<float>();
-    p.lut_in = m->lut_in.as<float>();
-    p.part_gu = m->part_gu.as<float>();
-    p.part_dn = m->part_dn.as<float>();
+    p.x = x;
+    p.inter = m->inter.as<float>();
+    p.gu_part = m->gu_part.as<float>();
+    p.dout = m->dout.as<float>();
     p.idx = idx;
     p.w = w;
-    p.y = y;
     p.E = m->E;
     p.H = m->H;
     p.I = m->I;
@@ -863,11 +875,32 @@ int moe_forward_parts(MoE *m, const void *x, const int *idx, const float *w, voi
     p.Si = m->Si;
     p.Ip = m->Ip;
     p.Hp = m->Hp;
-    p.T = T_;
     p.k = k;
-    OJX_LAUNCH(moe_gu_part_kernel, dim3(P * m->Sin), dim3(kNT), 0, st, p);
-    OJX_LAUNCH(moe_dn_part_kernel, dim3(P * m->Si), dim3(kNT), 0, st, p);
-    OJX_LAUNCH((moe_combine_parts_kernel<T>), dim3((m->H + kNT - 1) / kNT, T_), dim3(kNT), 0, st, p);
+    p.NS = ns;
+    {
+        const void *fn = reinterpret_cast<const void *>(
+            &moe_gu_group_kernel<T, kGuWaves, kGuIdx, kGroupDB, kGroupPF>);
+        const size_t lds = (size_t)m->Sin * 256 * sizeof(float);
+        static size_t granted = 0;
+        rc = ensure_dyn_lds(fn, lds + slices::lut_bytes(kGroupDB), &granted);
+        if (rc) return rc;
+        const int nb = (m->I + 64 * kGuWaves * kGuIdx - 1) / (64 * kGuWaves * kGuIdx);
+        OJX_LAUNCH((moe_gu_group_kernel<T, kGuWaves, kGuIdx, kGroupDB, kGroupPF>), dim3(nb, P, ns),
+                   dim3(64 * kGuWaves), lds, st, p);
+    }
+    rc = ns == 1 ? launch_dn<1>(p, P, (size_t)m->Si * 256 * sizeof(float), st)
+                 : launch_dn<2>(p, P, (size_t)m->Si * 256 * sizeof(float), st);
+    if (rc) return rc;
+    MoEParams cp{};
+    cp.dout = m->dout.as<float>();
+    cp.idx = idx;
+    cp.w = w;
+    cp.y = y;
+    cp.E = m->E;
+    cp.H = m->H;
+    cp.T = T_;
+    cp.k = k;
+    OJX_LAUNCH((moe_combine_kernel<T>), dim3((m->H + kNT - 1) / kNT, T_), dim3(kNT), 0, st, cp);
     OJX_HIP(hipGetLastError());
     return OJASX_OK;
 }
@@ -891,9 +924,9 @@ int moe_forward(MoE *m, const void *x, const int *idx, const float *w, void *y, 
                         reinterpret_cast<uintptr_t>(x) % align == 0 &&
                         (size_t)(kCB * 16 + (size_t)k * m->Si * 256) * 4 <= kMaxLds &&
                         (size_t)(kCB * 16 + m->Sin * 256) * 4 <= kMaxLds;
-        if (m->D == 16 && T_ >= kPartsMinTokens)
-            return dtype == OJASX_DTYPE_F32 ? moe_forward_parts<float>(m, x, idx, w, y, T_, k, dtype, st)
-                                            : moe_forward_parts<__hip_bfloat16>(m, x, idx, w, y, T_, k, dtype, st);
+        if (m->D == 16 && T_ >= kGroupMinTokens)
+            return dtype == OJASX_DTYPE_F32 ? moe_forward_group<float>(m, x, idx, w, y, T_, k, st)
+                                            : moe_forward_group<__hip_bfloat16>(m, x, idx, w, y, T_, k, st);
         if (ok)
             return dtype == OJASX_DTYPE_F32 ? moe_forward_dec<float>(m, x, idx, w, y, T_, k, st)
                                             : moe_forward_dec<__hip_bfloat16>(m, x, idx, w, y, T_, k, st);

@@ -159,7 +159,7 @@ def device_moe(pkg, dev, nat, x_t, idx, w, k, dtype_tag=0):
     return y.float().cpu().numpy()
 
 
-@pytest.mark.parametrize("T", [3, 6])   # below / from the token count that selects the LUT path
+@pytest.mark.parametrize("T", [2, 6])   # below / from the token count that selects the grouped path
 @pytest.mark.parametrize("E,H,I,k,D", [
     (40, 480, 208, 20, 16),    # partial input/intermediate slices; 20 slots > 16 waves
     (64, 512, 256, 32, 16),    # the largest k of the single-kernel stages
