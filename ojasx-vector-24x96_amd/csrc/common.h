@@ -108,6 +108,28 @@ inline int ensure_dyn_lds(const void *fn, size_t bytes, size_t *granted) {
 }
 
 // ---- device helpers ------------------------------------------------------
+// Load through a global-address-space pointer.  Pointers read from device
+// memory (not kernel arguments) are otherwise generic, their loads become
+// flat loads, and a flat load counts against the LDS counter too: every wait
+// for an LDS result would then also wait for the loads still in flight.
+template <typename T>
+__device__ __forceinline__ T gld(const T *p) {
+    typedef __attribute__((address_space(1))) const T global_t;
+    return *reinterpret_cast<global_t *>(reinterpret_cast<uintptr_t>(p));
+}
+// 16-byte vectors: loaded as the compiler's own vector types (HIP's vector
+// structs have no copy from the global address space).
+__device__ __forceinline__ uint4 gld(const uint4 *p) {
+    typedef unsigned int v4u __attribute__((ext_vector_type(4)));
+    const v4u v = gld(reinterpret_cast<const v4u *>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ float4 gld(const float4 *p) {
+    typedef float v4f_t __attribute__((ext_vector_type(4)));
+    const v4f_t v = gld(reinterpret_cast<const v4f_t *>(p));
+    return make_float4(v.x, v.y, v.z, v.w);
+}
+
 __device__ __forceinline__ float load_act(const float *p, size_t i) { return p[i]; }
 __device__ __forceinline__ float load_act(const __hip_bfloat16 *p, size_t i) {
     return __bfloat162float(p[i]);

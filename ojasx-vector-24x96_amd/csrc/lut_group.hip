@@ -30,7 +30,7 @@ constexpr int kRPT = 4;                 // rows per thread
 constexpr int kGRows = kGNT * kRPT;     // rows per workgroup
 }  // namespace
 
-__global__ __launch_bounds__(kGNT) void lut_group_kernel(const GroupItem *__restrict__ items) {
+__global__ __launch_bounds__(kGNT) __attribute__((amdgpu_waves_per_eu(4))) void lut_group_kernel(const GroupItem *__restrict__ items) {
     __shared__ float L[slices::kLutFloats];
     extern __shared__ float xs[];                     // [S * 256], zero past K
     const GroupItem it = items[blockIdx.y];
@@ -48,7 +48,7 @@ __global__ __launch_bounds__(kGNT) void lut_group_kernel(const GroupItem *__rest
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
         const int e = min(tid + u * kGNT, nx4 - 1) * 4;
-        xv[u] = *reinterpret_cast<const float4 *>(it.x + min(e, it.K - 4));
+        xv[u] = gld(reinterpret_cast<const float4 *>(it.x + min(e, it.K - 4)));
         if (e >= it.K) xv[u] = make_float4(0.f, 0.f, 0.f, 0.f);
     }
     float bop[4][4];
@@ -58,8 +58,8 @@ __global__ __launch_bounds__(kGNT) void lut_group_kernel(const GroupItem *__rest
 #pragma unroll
         for (int r2 = 0; r2 < kRPT; ++r2) {
             const int m = min(base + tid + kGNT * r2, it.M - 1);
-            j0[r2] = it.rowp[m];
-            j1[r2] = it.rowp[m + 1];
+            j0[r2] = gld(it.rowp + m);
+            j1[r2] = gld(it.rowp + m + 1);
         }
     }
     // ---- then HBM: codes of slices 0..kPF-1 (rows past Mp clamp: loaded, never stored)
@@ -74,7 +74,7 @@ __global__ __launch_bounds__(kGNT) void lut_group_kernel(const GroupItem *__rest
     for (int i = tid + 4 * kGNT; i < nx4; i += kGNT) {   // K > 4096: the rest of x
         const int e = i * 4;
         reinterpret_cast<float4 *>(xs)[i] =
-            e < it.K ? *reinterpret_cast<const float4 *>(it.x + e) : make_float4(0.f, 0.f, 0.f, 0.f);
+            e < it.K ? gld(reinterpret_cast<const float4 *>(it.x + e)) : make_float4(0.f, 0.f, 0.f, 0.f);
     }
     __syncthreads();
 
@@ -95,16 +95,16 @@ __global__ __launch_bounds__(kGNT) void lut_group_kernel(const GroupItem *__rest
                 float v[4];
 #pragma unroll
                 for (int u = 0; u < 4; ++u) {
-                    c[u] = it.col[j + u];
-                    v[u] = it.val[j + u];
+                    c[u] = gld(it.col + j + u);
+                    v[u] = gld(it.val + j + u);
                 }
 #pragma unroll
                 for (int u = 0; u < 4; ++u) o += v[u] * xs[c[u]];
             }
-            for (; j < j1[r2]; ++j) o += it.val[j] * xs[it.col[j]];
+            for (; j < j1[r2]; ++j) o += gld(it.val + j) * xs[gld(it.col + j)];
         }
-        float y = acc[r2] * it.scales[m];
-        if (it.bias) y += it.bias[m];
+        float y = acc[r2] * gld(it.scales + m);
+        if (it.bias) y += gld(it.bias + m);
         it.y[m] = y + o;
     }
 }

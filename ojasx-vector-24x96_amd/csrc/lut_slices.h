@@ -8,8 +8,7 @@
 // (16 / NW) w), then each thread gathers the 16 entries its rows' codes
 // select: 4 bytes of LDS per code byte.  Codes are slice-major tiles
 // [S][Mp][16]: one 16-byte load per row and slice, PF slices in flight in a
-// register ring (slice s + PF is loaded into the slot slice s frees), so a
-// slice's gathers do not wait for HBM.
+// register ring, so a slice's gathers do not wait for HBM.
 // With DB (two LUT buffers) the MFMAs of slice s + 1 are issued before the
 // gathers of slice s and their results stored after them: one barrier per
 // slice and the build off the critical path, for workgroups that are few per
@@ -43,11 +42,11 @@ __device__ __forceinline__ void load_cb_operands(const float *__restrict__ cb, i
     for (int t = 0; t < TPW; ++t)
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks)
-            bop[t][ks] = cb[(16 * (TPW * w + t) + (lane & 15)) * 16 + 4 * ks + (lane >> 4)];
+            bop[t][ks] = gld(cb + (16 * (TPW * w + t) + (lane & 15)) * 16 + 4 * ks + (lane >> 4));
 }
 
 __device__ __forceinline__ uint4 ld_code_row(const uint8_t *codes, int s, int Mp, int row) {
-    return *reinterpret_cast<const uint4 *>(codes + ((size_t)s * Mp + row) * 16);
+    return gld(reinterpret_cast<const uint4 *>(codes + ((size_t)s * Mp + row) * 16));
 }
 
 // Codes of slices s0 .. s0 + PF - 1 (slices from s1 on repeat s1 - 1 and go
@@ -116,36 +115,34 @@ __device__ __forceinline__ void slice_loop(const float *xs, float *L, const floa
         build_store<NW>(L, w, lane, c);
         __syncthreads();
     }
-    // the ring slot of slice s is (s - s0) % PF, a constant in the unrolled body
+    // Slice s uses ring slot (s - s0) % PF, a constant in the unrolled body, so
+    // the ring never moves registers (a move of a register whose load is in
+    // flight would wait for that load); the slot is refilled with slice s + PF
+    // once its gathers are issued, unconditionally (past the last slice it
+    // reloads that slice: a conditional load would need a second copy of the
+    // slot).
     for (int sb = s0; sb < s1; sb += PF) {
 #pragma unroll
         for (int q = 0; q < PF; ++q) {
             const int s = sb + q;
             if (s >= s1) break;
-            uint4 cw[R];
+            __builtin_amdgcn_sched_barrier(0);   // each slice scheduled on its own
             if constexpr (DB) {
                 const bool nb = s + 1 < s1;
                 if (nb) build_issue<NW>(xs, s + 1, lane, bop, c);
+                gather(L + ((s - s0) & 1) * kLutFloats, ring[q], acc);
 #pragma unroll
-                for (int r = 0; r < R; ++r) cw[r] = ring[q][r];
-                if (s + PF < s1) {
-#pragma unroll
-                    for (int r = 0; r < R; ++r) ring[q][r] = ld_code_row(codes, s + PF, Mp, row[r]);
-                }
-                gather(L + ((s - s0) & 1) * kLutFloats, cw, acc);
+                for (int r = 0; r < R; ++r) ring[q][r] = ld_code_row(codes, min(s + PF, s1 - 1), Mp, row[r]);
                 if (nb) build_store<NW>(L + ((s + 1 - s0) & 1) * kLutFloats, w, lane, c);
                 __syncthreads();   // slice s + 1's LUT written, slice s's gathers done
             } else {
                 build_issue<NW>(xs, s, lane, bop, c);
                 build_store<NW>(L, w, lane, c);
                 __syncthreads();
+                __builtin_amdgcn_sched_barrier(0);
+                gather(L, ring[q], acc);
 #pragma unroll
-                for (int r = 0; r < R; ++r) cw[r] = ring[q][r];
-                if (s + PF < s1) {
-#pragma unroll
-                    for (int r = 0; r < R; ++r) ring[q][r] = ld_code_row(codes, s + PF, Mp, row[r]);
-                }
-                gather(L, cw, acc);
+                for (int r = 0; r < R; ++r) ring[q][r] = ld_code_row(codes, min(s + PF, s1 - 1), Mp, row[r]);
                 __syncthreads();   // the gathers of slice s before the build of s + 1
             }
         }
