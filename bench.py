@@ -80,6 +80,8 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true",
                     help="skip the MoE, KV and decoder figures")
+    ap.add_argument("--extra", default="moe,kv,decoder",
+                    help="comma-separated extra figures to run (moe, kv, decoder)")
     return ap.parse_args()
 
 
@@ -476,10 +478,13 @@ def main():
         out["cpu_baseline"] = time_cpu_linear(base, args.cpu_seconds, y_bench)
     for h in handles:
         L.ojasx_destroy_linear(h)
-    if not args.no_extra:
+    extra = set() if args.no_extra else set(args.extra.split(","))
+    if "moe" in extra:
         out["moe_512x_top10"] = bench_moe(pkg, torch, min(args.steps, 400), args.warmup,
                                           args.cpu_seconds / 2, not args.no_cpu)
+    if "kv" in extra:
         out["kv_decode_gqa4"] = bench_kv(pkg, torch, args.steps, not args.no_cpu)
+    if "decoder" in extra:
         out["decoder_4b_shaped"] = bench_decoder(pkg, torch)
     print(json.dumps(out))
 

@@ -278,3 +278,44 @@ def test_grouped_linears(pkg, dev):
                                      np.zeros(0, np.float32))
         want = cpu.linear_forward(d["x"], d["codebook"], d["codes"], d["scales"], d["bias"], *csr)
         assert rel_err(y.cpu().numpy()[None], want) < F32_TOL, (M, K)
+
+
+def test_grouped_linears_repeat_and_errors(pkg, dev):
+    """Two grouped calls in a row (the second with fewer linears reuses the
+    staged item buffer), an empty call, and the argument checks."""
+    import torch
+    L = pkg.lib()
+    shapes = [(300, 512), (1100, 1024), (64, 160)]
+    nats, xs, ds = [], [], []
+    for i, (M, K) in enumerate(shapes):
+        d = gen.linear(M, K, B=1, seed=130 + i, scales="u", bias=True, outliers=True)
+        nats.append(native_linear(pkg, d, M, K))
+        xs.append(torch.from_numpy(d["x"][0]).to(dev))
+        ds.append(d)
+
+    def run(sel):
+        ys = [torch.full((shapes[i][0],), -1.0, device=dev) for i in sel]
+        n = len(sel)
+        H = (ctypes.c_void_p * n)(*[nats[i].handle for i in sel])
+        X = (ctypes.c_void_p * n)(*[xs[i].data_ptr() for i in sel])
+        Y = (ctypes.c_void_p * n)(*[y.data_ptr() for y in ys])
+        assert L.ojasx_linear_forward_grouped_device(H, n, X, Y, None) == 0, L.ojasx_get_last_error()
+        torch.cuda.synchronize()
+        for i, y in zip(sel, ys):
+            d = ds[i]
+            want = cpu.linear_forward(d["x"], d["codebook"], d["codes"], d["scales"], d["bias"],
+                                      *d["csr"])
+            assert rel_err(y.cpu().numpy()[None], want) < F32_TOL, shapes[i]
+
+    run([0, 1, 2])
+    run([2, 0])
+    one = (ctypes.c_void_p * 1)(nats[0].handle)
+    xp = (ctypes.c_void_p * 1)(xs[0].data_ptr())
+    y = torch.empty(shapes[0][0], device=dev)
+    yp = (ctypes.c_void_p * 1)(y.data_ptr())
+    assert L.ojasx_linear_forward_grouped_device(one, 0, xp, yp, None) == 0
+    assert L.ojasx_linear_forward_grouped_device(None, 1, xp, yp, None) != 0
+    bad = (ctypes.c_void_p * 1)(xs[0].data_ptr() + 4)
+    assert L.ojasx_linear_forward_grouped_device(one, 1, bad, yp, None) != 0
+    assert b"aligned" in L.ojasx_get_last_error()
+

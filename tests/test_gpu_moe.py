@@ -124,25 +124,29 @@ def test_baseline_moe_bf16(pkg, dev, baseline_moe):
         assert rel_err(y[t].float().cpu().numpy(), want) < 1e-2
 
 
-def test_repeat_deterministic_and_skips(pkg, dev, baseline_moe):
+@pytest.mark.parametrize("T", [1, 4])   # the in-place path and the grouped path
+def test_repeat_deterministic_and_skips(pkg, dev, baseline_moe, T):
     """Skipped slots (id out of range, |w| < 1e-8) and repeated experts within a
     token; repeated calls return identical bits."""
     import torch
     m, nat = baseline_moe
-    idx = np.array([[5, 600, 5, 9, -3, 11, 12, 13, 14, 15]], np.int32)
-    w = np.array([[0.2, 0.3, 0.1, 1e-9, 0.1, 0.05, 0.05, 0.05, 0.1, 0.05]], np.float32)
+    row_i = np.array([5, 600, 5, 9, -3, 11, 12, 13, 14, 15], np.int32)
+    row_w = np.array([0.2, 0.3, 0.1, 1e-9, 0.1, 0.05, 0.05, 0.05, 0.1, 0.05], np.float32)
+    idx = np.stack([np.roll(row_i, t) for t in range(T)])
+    w = np.stack([np.roll(row_w, t) for t in range(T)])
     it, wt = torch.from_numpy(idx).to(dev), torch.from_numpy(w).to(dev)
-    x = torch.from_numpy(m["x"][:1]).to(dev)
+    x = torch.from_numpy(m["x"][:T]).to(dev)
     ys = []
     for _ in range(3):
-        y = torch.empty(1, 2048, device=dev)
-        assert pkg.lib().ojasx_moe_forward_device(nat.handle, vp(x), vp(it), vp(wt), vp(y), 1, 10,
+        y = torch.empty(T, 2048, device=dev)
+        assert pkg.lib().ojasx_moe_forward_device(nat.handle, vp(x), vp(it), vp(wt), vp(y), T, 10,
                                                   0, None) == 0
         torch.cuda.synchronize()
         ys.append(y.cpu().numpy())
-    want = cpu.moe_forward(m["x"][0], m["cb_in"], m["cb_down"], m["gu_codes"], m["gu_scales"],
-                           m["dn_codes"], m["dn_scales"], idx[0], w[0])
-    assert rel_err(ys[0][0], want) < 1e-5
+    for t in range(T):
+        want = cpu.moe_forward(m["x"][t], m["cb_in"], m["cb_down"], m["gu_codes"], m["gu_scales"],
+                               m["dn_codes"], m["dn_scales"], idx[t], w[t])
+        assert rel_err(ys[0][t], want) < 1e-5, t
     assert all(np.array_equal(ys[0], yy) for yy in ys[1:])
 
 
