@@ -80,8 +80,8 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true",
                     help="skip the MoE, KV and decoder figures")
-    ap.add_argument("--extra", default="moe,kv,decoder",
-                    help="comma-separated extra figures to run (moe, kv, decoder)")
+    ap.add_argument("--extra", default="batched,moe,kv,decoder",
+                    help="comma-separated extra figures to run (batched, moe, kv, decoder)")
     return ap.parse_args()
 
 
@@ -227,6 +227,64 @@ def bench_moe(pkg, torch, steps, warmup, cpu_seconds, do_cpu):
         res["cpu_reference_sample"] = f"{n} single-token calls, 1 thread (reference engine)"
     for h, _ in banks:
         L.ojasx_destroy_moe(h)
+    return res
+
+
+def bench_batched(pkg, torch, steps, warmup):
+    """LUT-GEMV 2560->6912 at batch 8, 16, 32 and 64,
+    fp32 and bf16 activations, on 32 distinct weight instances in round robin
+    (35 MB).  From 32 tokens the call runs as x . W^T on fp32 MFMA
+    (lut_mm_kernel), below that the in-place LUT kernel (lut_dec_kernel).
+    Per-token code bytes are the codes of one call (1,105,920 B)."""
+    gen = pkg.synthetic
+    L = pkg.lib()
+    vp = ctypes.c_void_p
+    p = lambda a: a.ctypes.data_as(vp)
+    base = gen.linear(M_GU, K_GU, B=64, seed=2027)
+    r = np.random.default_rng(8)
+    hs = []
+    for i in range(32):
+        codes = base["codes"] if i == 0 else r.integers(0, 256, size=base["codes"].shape,
+                                                        dtype=np.uint8)
+        h = L.ojasx_create_linear(K_GU, M_GU, 16, 256, p(base["codebook"]), p(codes),
+                                  p(base["scales"]), None)
+        assert h, L.ojasx_get_last_error()
+        rp, cl, vl = base["csr"]
+        assert L.ojasx_set_linear_outliers(h, vl.size, p(rp), p(cl), p(vl)) == 0
+        hs.append(h)
+    dev = torch.device("cuda:0")
+    st = torch.cuda.current_stream()
+    sp = vp(st.cuda_stream)
+    code_bytes = M_GU * (K_GU // 16)
+    res = {}
+    n = max(50, min(steps, 400))
+    for dt, tag in ((0, "fp32"), (1, "bf16")):
+        for B in (8, 16, 32, 64):
+            x = torch.from_numpy(base["x"][:B]).to(dev)
+            if dt:
+                x = x.to(torch.bfloat16)
+            y = torch.empty(B, M_GU, device=dev, dtype=x.dtype)
+            call = lambda i: L.ojasx_linear_forward_device(hs[i % 32], vp(x.data_ptr()),
+                                                           vp(y.data_ptr()), B, dt, sp)
+            for i in range(min(warmup, 50)):
+                assert call(i) == 0, L.ojasx_get_last_error()
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(st)
+            for i in range(n):
+                call(i)
+            e1.record(st)
+            torch.cuda.synchronize()
+            us = e0.elapsed_time(e1) * 1e3 / n
+            kern = timed_kernels(pkg, lambda: [call(i) for i in range(min(n, 200))])
+            name, kv = next(iter(kern.items()))
+            mfma = 2.0 * M_GU * K_GU * B / (kv["avg_us"] * 1e-6) / 1e12
+            res[f"{tag}_B{B}"] = {"us_per_call": round(us, 3), "us_per_token": round(us / B, 3),
+                                  "kernel": name, "kernel_avg_us": kv["avg_us"],
+                                  "code_GBs": round(code_bytes / (kv["avg_us"] * 1e-6) / 1e9, 1),
+                                  "useful_TFLOPs": round(mfma, 2)}
+    for h in hs:
+        L.ojasx_destroy_linear(h)
     return res
 
 
@@ -479,6 +537,8 @@ def main():
     for h in handles:
         L.ojasx_destroy_linear(h)
     extra = set() if args.no_extra else set(args.extra.split(","))
+    if "batched" in extra:
+        out["lut_gemv_batched"] = bench_batched(pkg, torch, args.steps, args.warmup)
     if "moe" in extra:
         out["moe_512x_top10"] = bench_moe(pkg, torch, min(args.steps, 400), args.warmup,
                                           args.cpu_seconds / 2, not args.no_cpu)

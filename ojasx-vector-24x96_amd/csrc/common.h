@@ -73,6 +73,22 @@ struct GroupItem {
     int K, M, Mp, S;
 };
 int linear_items(const void *h, GroupItem *it);
+
+// The block_dim-16 linear for many tokens on MFMA (lut_mm.hip): x [B][K] in
+// dtype (fp32 16-byte aligned, or bf16), y [B][M] in dtype.
+struct MmParams {
+    const uint8_t *codes;   // [S][Mp][16]
+    const float *cb;        // [256][16]
+    const float *scales;    // [M]
+    const float *bias;      // [M] or null
+    const int *rowp;        // [M + 1] or null
+    const int *col;
+    const float *val;
+    const void *x;
+    void *y;
+    int K, M, Mp, S, B;
+};
+int launch_mm(const MmParams &p, int dtype, hipStream_t st);
 int linear_forward_fused(void *h, const float *x, float *y, int pro, const float *w, float eps,
                          const float *res, hipStream_t st);
 

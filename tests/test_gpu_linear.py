@@ -78,7 +78,9 @@ def test_reference_t2(pkg):
                                    (333, 2000, 5),    # 125 groups: partial last slice
                                    (1000, 8192, 3),   # 32 slices: two per wave
                                    (257, 5120, 2),    # 20 slices: one or two per wave
-                                   (64, 16, 7)])      # one group, one wave
+                                   (64, 16, 7),       # one group, one wave
+                                   (333, 2000, 35),   # MFMA path: ragged rows, tokens, slices
+                                   (70, 464, 33)])
 def test_integer_inputs_bit_exact(pkg, dev, M, K, B):
     import torch
     c = integer_case(M * 7 + B, M=M, K=K, B=B)
@@ -96,6 +98,35 @@ def test_baseline_configs_fp32(pkg, dev, M, K, B):
     y = dev_forward(pkg, nat, torch.from_numpy(d["x"]).to(dev), 0, torch.float32).cpu().numpy()
     y_ref = cpu.linear_forward(d["x"], d["codebook"], d["codes"], d["scales"], None, *d["csr"])
     assert rel_err(y, y_ref) < F32_TOL
+
+
+@pytest.mark.parametrize("M,K,B,dt,density", [
+    (700, 2000, 32, 0, 0.02),      # dense outliers: more than the LDS stage holds
+    (129, 4096, 40, 0, 0.02),
+    (6912, 2560, 36, 1, 0.0038),   # outliers staged in LDS, added slice by slice
+    (300, 256, 48, 1, 0.02),
+    (1000, 2560, 33, 0, 0.0038)])
+def test_mfma_batched_shapes(pkg, dev, M, K, B, dt, density):
+    """Many tokens (x . W^T on MFMA): ragged rows, tokens and slices, bias,
+    outliers given with each row's columns shuffled (the handle sorts them),
+    fp32 (rel 1e-5) and bf16 activations (rel 1e-2)."""
+    import torch
+    d = gen.linear(M, K, B=B, seed=M + K + B, scales="u", bias=True, density=density)
+    rp, cl, vl = d["csr"]
+    r = np.random.default_rng(M)
+    cl, vl = cl.copy(), vl.copy()
+    for m in range(M):
+        perm = r.permutation(rp[m + 1] - rp[m]) + rp[m]
+        cl[rp[m]:rp[m + 1]], vl[rp[m]:rp[m + 1]] = cl[perm], vl[perm]
+    d["csr"] = (rp, cl, vl)
+    nat = native_linear(pkg, d, M, K)
+    x = torch.from_numpy(d["x"]).to(dev)
+    if dt:
+        x = x.to(torch.bfloat16)
+    y = dev_forward(pkg, nat, x, dt, x.dtype).float().cpu().numpy()
+    y_ref = cpu.linear_forward(x.float().cpu().numpy(), d["codebook"], d["codes"], d["scales"],
+                               d["bias"], *d["csr"])
+    assert rel_err(y, y_ref) < (BF16_TOL if dt else F32_TOL)
 
 
 @pytest.mark.parametrize("B", [1, 8, 64])
