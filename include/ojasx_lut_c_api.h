@@ -80,7 +80,8 @@ OJASX_API OjasxLinearHandle ojasx_create_linear(int in_features, int out_feature
                                                 const float *bias_data);
 /* ref.h:60-66.  CSR over [out_features][in_features]; replaces any previous
  * outliers; nnz == 0 clears them.  Validated: row_ptrs monotone from 0 to
- * nnz, columns in range (-3 otherwise). */
+ * nnz, columns in range (-3 otherwise).  Each row's entries are stored sorted
+ * by column (stable), so a row's outlier sum is formed in column order. */
 OJASX_API int ojasx_set_linear_outliers(OjasxLinearHandle handle, int nnz,
                                         const int *row_ptrs, const int *col_indices,
                                         const float *values);
@@ -99,7 +100,9 @@ OJASX_API void ojasx_destroy_linear(OjasxLinearHandle handle);
 
 /* Device variant of ref.h:72-78 (no reference counterpart): x [batch][in],
  * y [batch][out] in HBM, dtype OJASX_DTYPE_F32 or _BF16 for both, enqueued on
- * stream (a hipStream_t; NULL = default stream). */
+ * stream (a hipStream_t; NULL = default stream).  block_dim 16: below 32
+ * tokens one in-place LUT kernel; from 32 tokens (in_features <= 65535, fp32
+ * x 16-byte aligned) x . W^T on fp32 MFMA with W decoded from the codes. */
 OJASX_API int ojasx_linear_forward_device(OjasxLinearHandle handle, const void *x, void *y,
                                           int batch_size, int dtype, void *stream);
 /* Many independent linears in one launch (no reference counterpart; the
@@ -198,7 +201,7 @@ OJASX_API int ojasx_dequantize_int8_device(const int8_t *q, const void *scale_f1
 /* ojasx_kv_decode_paged_device with the context length read on the device
  * (*seq_len_dev, clamped to max_seq_len; 0 leaves out untouched), so a captured
  * HIP graph can replay the call as the context grows: the launch covers
- * max_seq_len.  head_dim 128, block_dim 16, 16-byte aligned q and codebooks.
+ * max_seq_len (block_table holds ceil(max_seq_len / page_size) entries).  head_dim 128, block_dim 16, 16-byte aligned q and codebooks.
  * Chunks of 64 * tokens_per_lane tokens (1, 2 or 4; 0 picks by max_seq_len).
  * Workspace as ojasx_kv_decode_paged_device: call once outside a capture with
  * the same max_seq_len before capturing. */
