@@ -73,6 +73,7 @@ __global__ __launch_bounds__(kEncNT) void attn_prep_kernel(AttnPrepParams p) {
     constexpr int half = kHd / 2;
     const float c = tid < kHd ? p.cos_t[(size_t)pos * half + (tid % half)] : 0.f;
     const float s = tid < kHd ? p.sin_t[(size_t)pos * half + (tid % half)] : 0.f;
+    const int page = is_q ? 0 : p.bt[pos / p.P];   // with the row loads, not after the rotation
     const float ss = wave_sum_f(v * v);
     if (lane == 0) red[w] = ss;
     __syncthreads();
@@ -89,7 +90,6 @@ __global__ __launch_bounds__(kEncNT) void attn_prep_kernel(AttnPrepParams p) {
     }
     if (tid < kHd) kr[tid] = out;
     __syncthreads();
-    const int page = p.bt[pos / p.P];
     const size_t row = ((size_t)page * p.Hkv + h) * p.P + (pos % p.P);
     const float *vr = p.qkv + (size_t)(p.Hq + p.Hkv + h) * kHd;
     encode_kv_token<kBd>(kr, vr, kcb, vcb, kreg, vreg, kHd, kBd, kG, p.kc + row * kG,

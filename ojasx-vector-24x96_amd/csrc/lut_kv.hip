@@ -490,11 +490,10 @@ __global__ __launch_bounds__(kNT) void kv_decode_small_kernel(KVParams p) {
     const int j0 = h * R + blockIdx.z * 4;
     const int nj = min(4, R - (int)blockIdx.z * 4);
     const int c = blockIdx.x;
-    // device length clamped to the launch's longest context p.T
-    const int T = p.len_dev ? min(*p.len_dev + p.len_add, p.T) : p.T;
-    if (c * C >= T) return;              // whole workgroup: a chunk past the context
-
-    // ---- round trip 1: codebooks, q, block table entry of wave j's tokens
+    // ---- round trip 1, none of it waiting for the device length: the length,
+    // codebooks, q, and the block-table entry of wave j's token (the table
+    // covers the launch's longest context p.T)
+    const int len = p.len_dev ? *p.len_dev : 0;
     const float4 *gk = reinterpret_cast<const float4 *>(p.kcb + (size_t)h * 256 * 16);
     const float4 *gv = reinterpret_cast<const float4 *>(p.vcb + (size_t)h * 256 * 16);
     float4 a[4], b[4];
@@ -506,14 +505,16 @@ __global__ __launch_bounds__(kNT) void kv_decode_small_kernel(KVParams p) {
     float4 qv = make_float4(0.f, 0.f, 0.f, 0.f);
     if (tid < nj * 32) qv = reinterpret_cast<const float4 *>(p.q + (size_t)j0 * 128)[tid];
     const int tw = c * C + j * kSmallC + lane;   // the token wave j loads (j < TPL)
+    const int pg = j < TPL ? p.bt[min(tw, p.T - 1) / p.P] : 0;
+    // device length clamped to the launch's longest context p.T
+    const int T = p.len_dev ? min(len + p.len_add, p.T) : p.T;
+    if (c * C >= T) return;              // whole workgroup: a chunk past the context
     const bool wlive = j < TPL && tw < T;
-    const int twc = min(tw, T - 1);
-    const int pg = p.bt[twc / p.P];
-    // ---- round trip 2: token codes and scales
+    // ---- round trip 2: codes and scales of the live tokens
     uint2 kw = make_uint2(0, 0), vw = make_uint2(0, 0);
     float ksv = 0.f, vsv = 0.f;
-    if (j < TPL) {
-        const size_t slot = ((size_t)pg * p.Hkv + h) * p.P + (twc % p.P);
+    if (wlive) {
+        const size_t slot = ((size_t)pg * p.Hkv + h) * p.P + (tw % p.P);
         kw = *reinterpret_cast<const uint2 *>(p.kc + slot * 8);
         vw = *reinterpret_cast<const uint2 *>(p.vc + slot * 8);
         ksv = p.ks[slot];
