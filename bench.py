@@ -110,9 +110,30 @@ def time_cpu_linear(d, seconds, y_gpu):
         el = time.perf_counter() - t0
         if el > seconds or n >= 1000:
             break
-    return dict(value=el / n * 1e6, unit="us/call", cores=1, kind=kind,
-                sample=f"{n} calls of LUT-GEMV 2560->6912 B=1 fp32 with CSR, 1 thread, "
-                       f"after 50 warm-up calls", parity_rel_err=rel)
+    out = dict(value=el / n * 1e6, unit="us/call", cores=1, kind=kind,
+               sample=f"{n} calls of LUT-GEMV 2560->6912 B=1 fp32 with CSR, 1 thread, "
+                      f"after 50 warm-up calls", parity_rel_err=rel)
+    if kind == "reference":
+        # the reference's other builds and thread counts: scalar (its Makefile
+        # flags) and -march=x86-64-v3 (its AVX2 LUT build), 1 thread and the
+        # host share of this GPU (16 threads at most), 2 s each
+        threads = max(1, min(16, os.cpu_count() or 1))
+        var = {}
+        for tag, path in (("scalar", ref.LIB_SCALAR), ("avx2", ref.LIB_AVX2)):
+            if not ref.available(path):
+                continue
+            R2 = ref.RefLinear(d["codebook"], d["codes"], d["scales"], None, d["csr"], path=path)
+            for nt in sorted({1, threads}):
+                for _ in range(5):
+                    R2.forward(x, nt)
+                k, t1 = 0, time.perf_counter()
+                while time.perf_counter() - t1 < min(2.0, seconds) and k < 1000:
+                    R2.forward(x, nt)
+                    k += 1
+                var[f"{tag}_{nt}t"] = round((time.perf_counter() - t1) / k * 1e6, 2)
+        out["variants_us_per_call"] = var
+        out["variants_threads"] = threads
+    return out
 
 
 def bench_sustained(pkg, torch, handles, x, code_bytes, all_bytes, steps):
