@@ -7,11 +7,11 @@
 //   per layer
 //     1. qkv  = LUT(Wqkv, RMSNorm(x, w_in))           lut_dec_kernel, RMSNorm prologue
 //     2. q    = RoPE(RMSNorm_head(q, w_qn));  k = RoPE(RMSNorm_head(k, w_kn));
-//        k, v encoded into the layer's paged code cache at `pos`   attn_prep_kernel
-//     3. attn = softmax(q K^T / sqrt(hd)) V over pos + 1 tokens   kv_decode_small_kernel + merge
-//     4. x   += LUT(Wo, attn)                          residual epilogue
-//     5. gu   = LUT(Wgu, RMSNorm(x, w_post))           RMSNorm prologue (gate rows, then up rows)
-//     6. x   += LUT(Wdown, silu(gate) * up)            SwiGLU prologue, residual epilogue
+//        k, v encoded into the layer's paged code cache at `pos`;
+//        attn = softmax(q K^T / sqrt(hd)) V over pos + 1 tokens  attn_decode_kernel + merge
+//     3. x   += LUT(Wo, attn)                          residual epilogue
+//     4. gu   = LUT(Wgu, RMSNorm(x, w_post))           RMSNorm prologue (gate rows, then up rows)
+//     5. x   += LUT(Wdown, silu(gate) * up)            SwiGLU prologue, residual epilogue
 //   head: logits = LUT(Wlm, RMSNorm(x, w_final)); argmax_embed_kernel picks the
 //   token (ties to the lower id), stores it, loads its embedding row into x
 //   and advances the position.
@@ -24,7 +24,6 @@
 #include <vector>
 
 #include "common.h"
-#include "kv_encode.h"
 
 namespace ojx {
 
@@ -35,65 +34,254 @@ constexpr int kG = kHd / kBd;     // KV code groups per head
 constexpr int kArgNT = 1024;
 }  // namespace
 
-struct AttnPrepParams {
+struct AttnParams {
     const float *qkv;             // [Hq*hd | Hkv*hd (k) | Hkv*hd (v)]
     const float *qn_w, *kn_w;     // [hd]
     const float *cos_t, *sin_t;   // [max_ctx][hd/2]
     const int *state;             // state[0] = position of the new token
-    const int *bt;                // block table
+    const int *bt;                // block table, ceil(max_ctx / P) entries
     const float *kcb, *vcb;       // [Hkv][256][16]
-    float *q_out;                 // [Hq][hd]
     uint8_t *kc, *vc;             // [pages][Hkv][P][G]
     float *ks, *vs;               // [pages][Hkv][P]
-    int Hq, Hkv, P, max_ctx;
-    float eps;
+    float *part_o, *part_ml;      // [Hq][n_chunks][hd], [Hq][n_chunks][2]
+    float *out;                   // [Hq][hd], written here when n_chunks == 1
+    int Hq, Hkv, P, max_ctx, n_chunks;
+    float eps, sf;
 };
 
-// Workgroup b < Hq: query head b; otherwise kv head b - Hq.  Thread d < hd
-// owns dimension d: the per-head RMSNorm (wave sums), then RoPE with the
-// partner dimension from LDS.  Query heads store q; kv heads encode the
-// rotated k and the raw v into the cache (all 256 threads, kv_encode.h).
-__global__ __launch_bounds__(kEncNT) void attn_prep_kernel(AttnPrepParams p) {
-    __shared__ float xs[2 * kHd];    // encoder scratch
-    __shared__ float xn[kHd];        // normalised row
-    __shared__ float kr[kHd];        // rotated k
-    __shared__ float red[kEncNW];
-    const int b = blockIdx.x, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    const bool is_q = b < p.Hq;
-    const int h = is_q ? b : b - p.Hq;
-    float kreg[kBd], vreg[kBd];
-    const float *kcb = (!is_q && p.kcb) ? p.kcb + (size_t)h * 256 * kBd : nullptr;
-    const float *vcb = (!is_q && p.vcb) ? p.vcb + (size_t)h * 256 * kBd : nullptr;
-    if (kcb) enc_load_centroids<kBd>(kcb, vcb, kreg, vreg);
+constexpr int kAttnNT = 256;
+constexpr int kAttnC = 64;        // tokens per chunk, one per lane
+
+// Attention of the new token at pos = state[0] over the pos + 1 cached tokens,
+// prologue included.  Workgroup = (chunk c of 64 tokens, kv head h, slice z of
+// up to 4 of its query heads); wave j < nj owns query head h*R + 4z + j.
+//   q: lane l holds dimensions l and l + 64 (a RoPE pair): per-head RMSNorm by
+//      a wave sum, then the rotation, into LDS.
+//   The chunk holding pos also prepares the new token: wave 2 normalises and
+//   rotates k, wave 3 takes v as is, each scaled by max|.| / 127; thread t then
+//   holds centroid t of the head's K and V codebooks for the nearest-centroid
+//   search of each 16-dimension group (ties to the lower index).  Slice z = 0
+//   stores the codes and scales into the cache; every slice uses them for the
+//   token itself, so no workgroup reads the slot being written.
+//   Decode: lane l scores token 64c + l for each query head from the K
+//   codebook in LDS, the chunk's softmax statistics by wave reductions, then
+//   lane l accumulates output dimensions 2l, 2l + 1 from the V codebook.
+// Partials (o, max, sum) per query head and chunk; the caller merges them.
+__global__ __launch_bounds__(kAttnNT) void attn_decode_kernel(AttnParams p) {
+    __shared__ float4 ck4[256 * 4];      // K codebook [256][16]
+    __shared__ float4 cv4[256 * 4];      // V codebook [256][16]
+    __shared__ float4 q4s[4 * 32];       // rotated q [4][128]
+    __shared__ float xs[2 * kHd];        // new token: k / s_k, v / s_v
+    __shared__ float nscale[2];          // its scales
+    __shared__ int npage;                // its page
+    __shared__ float wd[2][kG][4];       // per-wave nearest distance
+    __shared__ int wi[2][kG][4];         // and its lowest centroid
+    __shared__ uint2 ncode[2];           // its K and V codes
+    __shared__ uint2 kcw[kAttnC], vcw[kAttnC];
+    __shared__ float wsc[4][kAttnC];     // K scale * sf and V scale, then p_jt * vs_t
+    const int tid = threadIdx.x, lane = tid & 63, j = tid >> 6;
+    const int R = p.Hq / p.Hkv;
+    const int h = blockIdx.y;
+    const int j0 = h * R + blockIdx.z * 4;
+    const int nj = min(4, R - (int)blockIdx.z * 4);
+    const int c = blockIdx.x;
+    // ---- round trip 1: the position, codebooks, the q / k / v rows and norm
+    // weights, wave 0's block-table entry (the table covers max_ctx)
     const int pos = min(p.state[0], p.max_ctx - 1);
-    const float *src = p.qkv + (is_q ? (size_t)h * kHd : (size_t)(p.Hq + h) * kHd);
-    const float *wn = is_q ? p.qn_w : p.kn_w;
-    const float v = tid < kHd ? src[tid] : 0.f;
-    const float wv = tid < kHd ? wn[tid] : 0.f;
-    constexpr int half = kHd / 2;
-    const float c = tid < kHd ? p.cos_t[(size_t)pos * half + (tid % half)] : 0.f;
-    const float s = tid < kHd ? p.sin_t[(size_t)pos * half + (tid % half)] : 0.f;
-    const int page = is_q ? 0 : p.bt[pos / p.P];   // with the row loads, not after the rotation
-    const float ss = wave_sum_f(v * v);
-    if (lane == 0) red[w] = ss;
-    __syncthreads();
-    const float var = ((red[0] + red[1]) + (red[2] + red[3])) / (float)kHd;
-    const float rn = 1.0f / sqrtf(var + p.eps);
-    const float xv = (v * rn) * wv;
-    if (tid < kHd) xn[tid] = xv;
-    __syncthreads();
-    float out = 0.f;
-    if (tid < kHd) out = tid < half ? xv * c - xn[tid + half] * s : xv * c + xn[tid - half] * s;
-    if (is_q) {
-        if (tid < kHd) p.q_out[(size_t)h * kHd + tid] = out;
-        return;                                  // whole workgroup
+    const float4 *gk = reinterpret_cast<const float4 *>(p.kcb + (size_t)h * 256 * 16);
+    const float4 *gv = reinterpret_cast<const float4 *>(p.vcb + (size_t)h * 256 * 16);
+    float4 a[4], b[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        a[u] = gk[tid + u * kAttnNT];
+        b[u] = gv[tid + u * kAttnNT];
     }
-    if (tid < kHd) kr[tid] = out;
+    float r0 = 0.f, r1 = 0.f, w0 = 0.f, w1 = 0.f;   // q row and q_norm weights
+    if (j < nj) {
+        const float *src = p.qkv + (size_t)(j0 + j) * kHd;
+        r0 = src[lane];
+        r1 = src[lane + 64];
+        w0 = p.qn_w[lane];
+        w1 = p.qn_w[lane + 64];
+    }
+    float e0 = 0.f, e1 = 0.f, u0 = 0.f, u1 = 0.f;   // k (wave 2, k_norm weights) / v (wave 3)
+    if (j >= 2) {
+        const float *src = p.qkv + (size_t)(p.Hq + (j - 2) * p.Hkv + h) * kHd;
+        e0 = src[lane];
+        e1 = src[lane + 64];
+        if (j == 2) {
+            u0 = p.kn_w[lane];
+            u1 = p.kn_w[lane + 64];
+        }
+    }
+    const int tw = c * kAttnC + lane;            // wave 0's token
+    const int pg = j == 0 ? p.bt[min(tw, p.max_ctx - 1) / p.P] : 0;
+    const int T = pos + 1;
+    if (c * kAttnC >= T) return;                 // whole workgroup: a chunk past the context
+    const bool fresh = pos / kAttnC == c;        // this chunk holds the new token
+    // ---- round trip 2: cos / sin at pos, codes and scales of the cached tokens
+    const float cs = p.cos_t[(size_t)pos * (kHd / 2) + lane];
+    const float sn = p.sin_t[(size_t)pos * (kHd / 2) + lane];
+    uint2 kw = make_uint2(0, 0), vw = make_uint2(0, 0);
+    float ksv = 0.f, vsv = 0.f;
+    if (j == 0 && tw < pos) {
+        const size_t slot = ((size_t)pg * p.Hkv + h) * p.P + (tw % p.P);
+        kw = *reinterpret_cast<const uint2 *>(p.kc + slot * kG);
+        vw = *reinterpret_cast<const uint2 *>(p.vc + slot * kG);
+        ksv = p.ks[slot];
+        vsv = p.vs[slot];
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        ck4[tid + u * kAttnNT] = a[u];
+        cv4[tid + u * kAttnNT] = b[u];
+    }
+    if (j < nj) {
+        const float rn = 1.0f / sqrtf(wave_sum_f(r0 * r0 + r1 * r1) / (float)kHd + p.eps);
+        const float x0 = (r0 * rn) * w0, x1 = (r1 * rn) * w1;
+        float *qf = reinterpret_cast<float *>(q4s) + j * kHd;
+        qf[lane] = x0 * cs - x1 * sn;
+        qf[lane + 64] = x1 * cs + x0 * sn;
+    }
+    if (fresh) {
+        if (j == 2) {
+            const float rn = 1.0f / sqrtf(wave_sum_f(e0 * e0 + e1 * e1) / (float)kHd + p.eps);
+            const float x0 = (e0 * rn) * u0, x1 = (e1 * rn) * u1;
+            e0 = x0 * cs - x1 * sn;
+            e1 = x1 * cs + x0 * sn;
+        }
+        if (j >= 2) {
+            const float s = fmaxf(1e-8f, wave_max_f(fmaxf(fabsf(e0), fabsf(e1)))) / 127.0f;
+            xs[(j - 2) * kHd + lane] = e0 / s;
+            xs[(j - 2) * kHd + lane + 64] = e1 / s;
+            if (lane == 0) nscale[j - 2] = s;
+        }
+        if (j == 0 && tw == pos) npage = pg;
+    }
     __syncthreads();
-    const size_t row = ((size_t)page * p.Hkv + h) * p.P + (pos % p.P);
-    const float *vr = p.qkv + (size_t)(p.Hq + p.Hkv + h) * kHd;
-    encode_kv_token<kBd>(kr, vr, kcb, vcb, kreg, vreg, kHd, kBd, kG, p.kc + row * kG,
-                         p.vc + row * kG, p.ks + row, p.vs + row, xs);
+    if (fresh) {
+        float ck[kBd], cv[kBd];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const float4 ka = ck4[tid * 4 + u], va = cv4[tid * 4 + u];
+            ck[4 * u] = ka.x, ck[4 * u + 1] = ka.y, ck[4 * u + 2] = ka.z, ck[4 * u + 3] = ka.w;
+            cv[4 * u] = va.x, cv[4 * u + 1] = va.y, cv[4 * u + 2] = va.z, cv[4 * u + 3] = va.w;
+        }
+#pragma unroll
+        for (int g = 0; g < kG; ++g) {
+            float dk = 0.f, dv = 0.f;
+#pragma unroll
+            for (int d = 0; d < kBd; ++d) {
+                const float fk = xs[g * kBd + d] - ck[d];
+                const float fv = xs[kHd + g * kBd + d] - cv[d];
+                dk = fmaf(fk, fk, dk);
+                dv = fmaf(fv, fv, dv);
+            }
+            const float mk = wave_min_f(dk), mv = wave_min_f(dv);
+            const int ik = wave_min_i(dk == mk ? tid : 0x7fffffff);
+            const int iv = wave_min_i(dv == mv ? tid : 0x7fffffff);
+            if (lane == 0) {
+                wd[0][g][j] = mk;
+                wi[0][g][j] = ik;
+                wd[1][g][j] = mv;
+                wi[1][g][j] = iv;
+            }
+        }
+        __syncthreads();
+        if (tid < 2 * kG) {
+            const int kv = tid >= kG, g = tid - kv * kG;
+            float bm = wd[kv][g][0];
+            int bi = wi[kv][g][0];
+#pragma unroll
+            for (int q = 1; q < 4; ++q)
+                if (wd[kv][g][q] < bm) {   // strictly smaller: earlier waves hold lower indices
+                    bm = wd[kv][g][q];
+                    bi = wi[kv][g][q];
+                }
+            reinterpret_cast<uint8_t *>(ncode)[kv * kG + g] = (uint8_t)bi;
+            if (blockIdx.z == 0) {
+                const size_t row = ((size_t)npage * p.Hkv + h) * p.P + (pos % p.P);
+                (kv ? p.vc : p.kc)[row * kG + g] = (uint8_t)bi;
+                if (g == 0) (kv ? p.vs : p.ks)[row] = nscale[kv];
+            }
+        }
+        __syncthreads();
+        if (j == 0 && tw == pos) {
+            kw = ncode[0];
+            vw = ncode[1];
+            ksv = nscale[0];
+            vsv = nscale[1];
+        }
+    }
+    if (j == 0) {
+        kcw[lane] = kw;
+        vcw[lane] = vw;
+        wsc[0][lane] = tw < T ? ksv * p.sf : 0.f;
+        wsc[1][lane] = tw < T ? vsv : 0.f;
+    }
+    __syncthreads();
+    const float kf = wsc[0][lane], vf = wsc[1][lane];
+    const uint2 kwl = kcw[lane];
+    __syncthreads();   // wsc is rewritten with the weights below
+
+    // ---- score of token tw for head j: sum_g <q_j,g, Ck[code_g]> * ks * sf
+    float sc = -INFINITY;
+    if (j < nj) {
+        const uint32_t kd[2] = {kwl.x, kwl.y};
+        float acc = 0.f;
+#pragma unroll
+        for (int g = 0; g < kG; ++g) {
+            const uint32_t code = (kd[g >> 2] >> ((g & 3) * 8)) & 0xffu;
+            const float4 *cr = ck4 + code * 4;
+            const float4 *qr = q4s + j * 32 + g * 4;
+            float dot = 0.f;
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+                const float4 cq = cr[w], qq = qr[w];
+                dot = fmaf(qq.x, cq.x, dot);
+                dot = fmaf(qq.y, cq.y, dot);
+                dot = fmaf(qq.z, cq.z, dot);
+                dot = fmaf(qq.w, cq.w, dot);
+            }
+            acc += dot;
+        }
+        if (tw < T) sc = acc * kf;
+    }
+    const float m = wave_max_f(sc);
+    const float e = (sc == -INFINITY) ? 0.f : expf(sc - m);
+    wsc[j][lane] = e * vf;
+    const float l = wave_sum_f(e);
+    __syncthreads();
+
+    // ---- V: lane owns dims 2*lane, 2*lane+1 (group g = lane / 8)
+    if (j < nj) {
+        const int g = lane >> 3, d0 = (lane & 7) * 2;
+        const float *cvf = reinterpret_cast<const float *>(cv4);
+        float o0 = 0.f, o1 = 0.f;
+#pragma unroll 8
+        for (int tl = 0; tl < kAttnC; ++tl) {
+            const uint2 cw = vcw[tl];
+            const uint32_t code = ((g < 4 ? cw.x : cw.y) >> ((g & 3) * 8)) & 0xffu;
+            const float2 cvv = *reinterpret_cast<const float2 *>(cvf + code * 16 + d0);
+            const float w = wsc[j][tl];
+            o0 = fmaf(w, cvv.x, o0);
+            o1 = fmaf(w, cvv.y, o1);
+        }
+        const int od = lane * 2;
+        if (p.n_chunks == 1) {
+            p.out[(size_t)(j0 + j) * kHd + od] = o0 / l;
+            p.out[(size_t)(j0 + j) * kHd + od + 1] = o1 / l;
+        } else {
+            float *po = p.part_o + ((size_t)(j0 + j) * p.n_chunks + c) * kHd + od;
+            po[0] = o0;
+            po[1] = o1;
+            if (lane == 0) {
+                float *ml = p.part_ml + ((size_t)(j0 + j) * p.n_chunks + c) * 2;
+                ml[0] = m;
+                ml[1] = l;
+            }
+        }
+    }
 }
 
 // Greedy pick over V logits (first maximum), then the picked token's
@@ -183,8 +371,8 @@ struct Decoder {
     float eps = 0.f, theta = 0.f;
     std::vector<DecoderLayer> L;
     void *lm = nullptr;
-    DevBuf final_norm, emb, cos_t, sin_t, bt, x, qkv, q, attn, gu, logits, part_o, part_ml,
-        state, tokens;
+    DevBuf final_norm, emb, cos_t, sin_t, bt, x, qkv, attn, gu, logits, part_o, part_ml, state,
+        tokens;
     hipStream_t stream = nullptr;
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
@@ -198,12 +386,12 @@ struct Decoder {
             for (DevBuf *b : {&l.in_norm, &l.post_norm, &l.q_norm, &l.k_norm, &l.kcb, &l.vcb, &l.kc,
                               &l.ks, &l.vc, &l.vs})
                 b->release();
-        for (DevBuf *b : {&final_norm, &emb, &cos_t, &sin_t, &bt, &x, &qkv, &q, &attn, &gu, &logits,
+        for (DevBuf *b : {&final_norm, &emb, &cos_t, &sin_t, &bt, &x, &qkv, &attn, &gu, &logits,
                           &part_o, &part_ml, &state, &tokens})
             b->release();
     }
 
-    int n_chunks() const { return (max_ctx + 63) / 64; }
+    int n_chunks() const { return (max_ctx + kAttnC - 1) / kAttnC; }
 
     // One token step on `st` (device-resident position and token).
     int step(hipStream_t st) {
@@ -215,18 +403,19 @@ struct Decoder {
             rc = linear_forward_fused(ly.qkv, x.as<float>(), qkv.as<float>(), 1,
                                       ly.in_norm.as<float>(), eps, nullptr, st);
             if (rc) return rc;
-            AttnPrepParams ap{qkv.as<float>(), ly.q_norm.as<float>(), ly.k_norm.as<float>(),
-                              cos_t.as<float>(), sin_t.as<float>(), pos, bt.as<int>(),
-                              ly.kcb.as<float>(), ly.vcb.as<float>(), q.as<float>(),
-                              ly.kc.as<uint8_t>(), ly.vc.as<uint8_t>(), ly.ks.as<float>(),
-                              ly.vs.as<float>(), Hq, Hkv, P, max_ctx, eps};
-            OJX_LAUNCH(attn_prep_kernel, dim3(Hq + Hkv), dim3(kEncNT), 0, st, ap);
-            rc = kv_decode_device_len(q.as<float>(), ly.kc.as<uint8_t>(), ly.ks.as<float>(),
-                                      ly.vc.as<uint8_t>(), ly.vs.as<float>(), ly.kcb.as<float>(),
-                                      ly.vcb.as<float>(), bt.as<int>(), pos, 1, max_ctx, P, Hq,
-                                      Hkv, sf, part_o.as<float>(), part_ml.as<float>(),
-                                      attn.as<float>(), st);
-            if (rc) return rc;
+            AttnParams ap{qkv.as<float>(), ly.q_norm.as<float>(), ly.k_norm.as<float>(),
+                          cos_t.as<float>(), sin_t.as<float>(), pos, bt.as<int>(),
+                          ly.kcb.as<float>(), ly.vcb.as<float>(), ly.kc.as<uint8_t>(),
+                          ly.vc.as<uint8_t>(), ly.ks.as<float>(), ly.vs.as<float>(),
+                          part_o.as<float>(), part_ml.as<float>(), attn.as<float>(), Hq, Hkv, P,
+                          max_ctx, n_chunks(), eps, sf};
+            OJX_LAUNCH(attn_decode_kernel, dim3(n_chunks(), Hkv, (Hq / Hkv + 3) / 4),
+                       dim3(kAttnNT), 0, st, ap);
+            if (n_chunks() > 1) {
+                rc = kv_merge_device_len(part_o.as<float>(), part_ml.as<float>(), n_chunks(),
+                                         kAttnC, Hq, pos, 1, attn.as<float>(), st);
+                if (rc) return rc;
+            }
             rc = linear_forward_fused(ly.o, attn.as<float>(), x.as<float>(), 0, nullptr, 0.f,
                                       x.as<float>(), st);
             if (rc) return rc;
@@ -333,7 +522,6 @@ OJASX_API OjasxDecoderHandle ojasx_create_decoder(int hidden, int layers, int q_
     const size_t qkv_n = (size_t)(q_heads + 2 * kv_heads) * kHd;
     if (!rc) rc = d->x.ensure((size_t)hidden * 4);
     if (!rc) rc = d->qkv.ensure(qkv_n * 4);
-    if (!rc) rc = d->q.ensure((size_t)q_heads * kHd * 4);
     if (!rc) rc = d->attn.ensure((size_t)q_heads * kHd * 4);
     if (!rc) rc = d->gu.ensure((size_t)2 * intermediate * 4);
     if (!rc) rc = d->logits.ensure((size_t)vocab * 4);

@@ -630,9 +630,24 @@ __global__ __launch_bounds__(kNT) void kv_merge_kernel(const float *part_o, cons
     const int n_chunks =
         len_dev ? min(stride_chunks, (*len_dev + len_add + chunk - 1) / chunk) : stride_chunks;
     if (n_chunks <= 0) return;                      // empty context: out untouched
+    // The statistics of chunk tid first, then the partials of the first
+    // 2 * kMergePre chunks for the two-threads-per-coordinate sum (even and odd
+    // chunks) used when 2 * hd <= kNT.  Every load is unconditional, at clamped
+    // indices, so the code stays straight-line and the max reduction waits
+    // for the statistics only (vmcnt counts loads in issue order).
     const float *ml = part_ml + (size_t)j * stride_chunks * 2;
-    float m = -INFINITY;
-    for (int c = tid; c < n_chunks; c += kNT) m = fmaxf(m, ml[2 * c]);
+    float2 st0 = *reinterpret_cast<const float2 *>(ml + 2 * min(tid, n_chunks - 1));
+    constexpr int kMergePre = 36;
+    const bool pair = 2 * hd <= kNT;
+    const int hf = tid / hd, d = tid - hf * hd;
+    const float *po = part_o + (size_t)j * stride_chunks * hd + d;
+    float pre[kMergePre];
+#pragma unroll
+    for (int u = 0; u < kMergePre; ++u)
+        pre[u] = po[(size_t)min(min(hf, 1) + 2 * u, n_chunks - 1) * hd];
+    if (tid >= n_chunks) st0 = make_float2(-INFINITY, 0.f);
+    float m = st0.x;
+    for (int c = tid + kNT; c < n_chunks; c += kNT) m = fmaxf(m, ml[2 * c]);
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
     if (lane == 0) red[wv] = m;
@@ -642,7 +657,12 @@ __global__ __launch_bounds__(kNT) void kv_merge_kernel(const float *part_o, cons
     for (int q = 1; q < kNT / 64; ++q) m = fmaxf(m, red[q]);
     __syncthreads();
     float l = 0.f;
-    for (int c = tid; c < n_chunks; c += kNT) {
+    if (tid < n_chunks) {
+        const float wc = st0.x == -INFINITY ? 0.f : expf(st0.x - m);
+        wsm[tid] = wc;
+        l = st0.y * wc;
+    }
+    for (int c = tid + kNT; c < n_chunks; c += kNT) {
         const float mc = ml[2 * c];
         const float wc = mc == -INFINITY ? 0.f : expf(mc - m);
         wsm[c] = wc;
@@ -656,15 +676,18 @@ __global__ __launch_bounds__(kNT) void kv_merge_kernel(const float *part_o, cons
 #pragma unroll
     for (int q = 1; q < kNT / 64; ++q) l += red[q];
     const float inv = 1.f / l;
-    if (2 * hd <= kNT) {
-        // two threads per coordinate, even and odd chunks, 16 loads in flight each
+    if (pair) {
+        // the prefetched chunks, then the rest 16 loads in flight at a time
         __shared__ float half_sum[kNT / 2];
-        const int hf = tid / hd, d = tid - hf * hd;
         float acc = 0.f;
         if (hf < 2) {
-            const float *po = part_o + (size_t)j * stride_chunks * hd + d;
             float o[4] = {0.f, 0.f, 0.f, 0.f};
-            int c = hf;
+#pragma unroll
+            for (int u = 0; u < kMergePre; ++u) {
+                const int c = hf + 2 * u;
+                if (c < n_chunks) o[u & 3] = fmaf(pre[u], wsm[c], o[u & 3]);
+            }
+            int c = hf + 2 * kMergePre;
             for (; c + 30 < n_chunks; c += 32) {
                 float v[16];
 #pragma unroll
@@ -748,6 +771,18 @@ int kv_decode_device_len(const float *q, const uint8_t *kc, const float *ks, con
     if (n_chunks > 1)
         OJX_LAUNCH(kv_merge_kernel, dim3(Hq), dim3(kNT), (size_t)n_chunks * 4, st, part_o, part_ml,
                    n_chunks, 128, out, len_dev, len_add, C);
+    OJX_HIP(hipGetLastError());
+    return OJASX_OK;
+}
+
+int kv_merge_device_len(const float *part_o, const float *part_ml, int n_chunks, int chunk, int Hq,
+                        const int *len_dev, int len_add, float *out, hipStream_t st) {
+    if (n_chunks <= 1 || Hq <= 0 || chunk <= 0) {
+        set_error("invalid KV merge shape Hq=%d chunks=%d", Hq, n_chunks);
+        return OJASX_ERR_INVALID;
+    }
+    OJX_LAUNCH(kv_merge_kernel, dim3(Hq), dim3(kNT), (size_t)n_chunks * 4, st, part_o, part_ml,
+               n_chunks, 128, out, len_dev, len_add, chunk);
     OJX_HIP(hipGetLastError());
     return OJASX_OK;
 }
