@@ -8,13 +8,14 @@
 // A single batch-1 call is latency-bound and runs lut_dec_kernel, which dots
 // x with codebook rows read from LDS: 64 bytes of LDS per code byte, which
 // caps it near 1.2 TB/s of code bytes on a full chip.  Here a workgroup owns
-// 1024 rows of one instance and runs the MFMA-built LUT slice loop of
-// lut_slices.h over the handles' slice-major code tiles: 4 bytes of LDS per
-// code byte.  The MFMA build is a fixed 65,536 MACs per slice, so 1024 rows
-// per workgroup (4 per thread) amortise it over twice the codes of 512
-// (measured per slice, uncontended: build 0.55 us, gather 0.38 us for 2 rows
-// per thread; 160 x 2560->6912 in one launch: 79.6 us at 4 rows per thread,
-// 86-90 us at 2 or 8).
+// 768 rows (3 per thread) of one instance and runs the MFMA-built LUT slice
+// loop of lut_slices.h over the handles' slice-major code tiles: 4 bytes of
+// LDS per code byte.  The MFMA build is a fixed 65,536 MACs per slice per
+// workgroup, amortised over the workgroup's rows.  The grid is sized to run in
+// one round: 72 VGPRs (one slice of codes in flight) and 27 KB of LDS give 6
+// workgroups of 4 waves per CU, 1536 on the chip, and 160 x 2560->6912 is
+// 1440 workgroups (measured 68.2 us; 4 rows per thread and two slices in
+// flight: 1120 workgroups over 1024 places, 80.7 us; 5 or 6 rows: 74 or 84 us).
 #include <algorithm>
 #include <vector>
 
@@ -24,13 +25,13 @@
 namespace ojx {
 
 namespace {
-constexpr int kPF = 2;                  // slices of codes in flight
+constexpr int kPF = 1;                  // slices of codes in flight
 constexpr int kGNT = 256;               // threads per workgroup (4 waves)
-constexpr int kRPT = 4;                 // rows per thread
+constexpr int kRPT = 3;                 // rows per thread
 constexpr int kGRows = kGNT * kRPT;     // rows per workgroup
 }  // namespace
 
-__global__ __launch_bounds__(kGNT) __attribute__((amdgpu_waves_per_eu(4))) void lut_group_kernel(const GroupItem *__restrict__ items) {
+__global__ __launch_bounds__(kGNT) __attribute__((amdgpu_waves_per_eu(6))) void lut_group_kernel(const GroupItem *__restrict__ items) {
     __shared__ float L[slices::kLutFloats];
     extern __shared__ float xs[];                     // [S * 256], zero past K
     const GroupItem it = items[blockIdx.y];
