@@ -7,20 +7,29 @@
 // the sum over groups is a GEMM against W decoded from the codes: the
 // per-token LUTs grow with the batch (1 KB per group and token), W does not
 // (64 bytes per group and row, decoded in registers from the codebook in
-// LDS).  A workgroup owns 64 rows (16 per wave) and 16 tokens; per 256-wide
-// input slice it stages the 16 tokens' x in LDS (two buffers, the next
-// slice's loads in flight during the current one; codes kMmPF slices ahead,
-// since they come from HBM), and per group each wave
-// runs 4 MFMAs (v_mfma_f32_16x16x4f32) with
+// LDS).
+//
+// A wave computes one 16-row x 16-token tile over a quarter of the input: of
+// every 256-wide input slice (16 groups) wave q of a row tile takes groups
+// 4q .. 4q + 3, 4 MFMAs (v_mfma_f32_16x16x4f32) per group with
 //   A[m][k] = C[code(m, g)][4k + ks]   (one 16-byte LDS read of the codebook row),
 //   B[k][n] = x_n[16g + 4k + ks]       (one 16-byte LDS read of the staged x),
 // for ks = 0..3: MFMA ks covers dims 4k + ks of the group, so a lane's four
 // values are contiguous in both the codebook row and x.  Two accumulators
-// (even and odd groups) keep the MFMA chains independent.  The CSR outliers
-// of the workgroup's rows are staged in LDS; each lane adds those of its rows
-// whose columns fall in the current slice from the staged x (a row's entries
-// are sorted by column), so no x is read at random from memory.  The
-// epilogue applies the scale and the bias: (s_m * sum + bias) + outliers.
+// (even and odd groups) keep the MFMA chains independent.  The four quarter
+// sums of a tile meet in LDS at the end, added in quarter order.  Splitting
+// the input four ways gives four times the waves of a one-wave-per-tile
+// layout.  A workgroup holds RT row tiles (4 RT waves) of the same 16 tokens,
+// sharing the codebook and the staged x slices: two LDS buffers, and the x
+// loads kept Sh::kPX slices ahead in a register ring (a slice's 16 MFMAs per
+// wave are far shorter than a load's round trip); codes Sh::kPF slices ahead.
+//
+// The CSR outliers of the workgroup's rows are staged in LDS; wave q of a
+// tile adds those of row 4 (lane / 16) + q whose columns fall in the current
+// slice from the staged x (a row's entries are sorted by column), so no x is
+// read at random from memory; the outlier sums meet in LDS with the quarter
+// sums.  The epilogue applies the scale and the bias:
+// (s_m * sum + bias) + outliers.
 //
 // MFMA 16x16x4 fp32 operand layout: lane l supplies A[m = l % 16][k = l / 16]
 // and B[k = l / 16][n = l % 16]; the result's value v of lane l is
@@ -30,30 +39,45 @@
 namespace ojx {
 
 namespace {
-constexpr int kMmNT = 256;       // 4 waves
-constexpr int kMmRows = 64;      // rows per workgroup (16 per wave)
+constexpr int kQ = 4;            // waves splitting each slice's 16 groups
 constexpr int kMmTok = 16;       // tokens per workgroup
 constexpr int kXStride = 260;    // floats per staged x row (256 + pad)
-constexpr int kMmPF = 4;         // slices of codes in flight
-// CSR entries of a workgroup's 64 rows staged in LDS (columns as 16-bit:
-// in_features <= 65535 on this path); three workgroups still fit a CU
-constexpr int kCsrStage = 768;
 constexpr int kOutPass = 3;      // outlier candidates per row per pass
 typedef float v4f __attribute__((ext_vector_type(4)));
+
+// RT row tiles per workgroup.
+template <int RT>
+struct MmShape {
+    static constexpr int kNT = 64 * kQ * RT;        // threads
+    static constexpr int kRows = 16 * RT;           // rows
+    static constexpr int kXF = kMmTok * 256 / kNT;  // x floats staged per thread per slice
+    // slices of x and of codes in flight (kPX divides kPF): deeper where the
+    // registers allow, since few waves per SIMD leave a slice short
+    static constexpr int kPX = 2;
+    static constexpr int kPF = 4;
+    // CSR entries of the workgroup's rows staged in LDS (columns as 16-bit:
+    // in_features <= 65535 on this path): 16 per row, against 9.7 on average
+    // at 0.38 % of 2560 inputs; a denser block takes its outliers from memory
+    static constexpr int kCsr = kNT;
+    // waves per SIMD the register budget is cut for: 3 workgroups per CU
+    // (LDS) up to 2 row tiles, 2 at 4 row tiles
+    static constexpr int kWaves = RT == 1 ? 3 : RT == 2 ? 6 : 8;
+};
 }  // namespace
 
-// x of tokens n0..n0+15, inputs 256 s .. 256 s + 255 (zero past K and past B):
-// thread t loads token t / 16, inputs 16 (t % 16) .. + 15.
-template <typename T>
-__device__ __forceinline__ void mm_load_x(const MmParams &p, int n0, int s, float (&r)[16]) {
-    const int tt = threadIdx.x >> 4, k = s * 256 + (threadIdx.x & 15) * 16;
-    const int n = n0 + tt;
-    const bool ok = n < p.B && k < p.K;        // K is a multiple of 16
-    const T *src = static_cast<const T *>(p.x) + (size_t)min(n, p.B - 1) * p.K + min(k, p.K - 16);
+// x of tokens n0..n0+15, inputs 256 s .. 256 s + 255: thread t loads floats
+// t XF .. t XF + XF - 1 of the 16 x 256 slice, from clamped addresses (always
+// in bounds); mm_store_x zeroes them past K and past B.  The loads are not
+// touched until the store, so a prefetch is not waited for early.
+template <typename T, int XF>
+__device__ __forceinline__ void mm_load_x(const MmParams &p, int n0, int s, float (&r)[XF]) {
+    const int e = threadIdx.x * XF;
+    const int n = n0 + (e >> 8), k = s * 256 + (e & 255);
+    const T *src = static_cast<const T *>(p.x) + (size_t)min(n, p.B - 1) * p.K + min(k, p.K - XF);
     if constexpr (sizeof(T) == 4) {
         const float4 *s4 = reinterpret_cast<const float4 *>(src);
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
+        for (int u = 0; u < XF / 4; ++u) {
             const float4 f = gld(s4 + u);
             r[4 * u] = f.x;
             r[4 * u + 1] = f.y;
@@ -62,185 +86,223 @@ __device__ __forceinline__ void mm_load_x(const MmParams &p, int n0, int s, floa
         }
     } else {
 #pragma unroll
-        for (int u = 0; u < 16; ++u) r[u] = load_act(src, u);
-    }
-    if (!ok) {
-#pragma unroll
-        for (int u = 0; u < 16; ++u) r[u] = 0.f;
+        for (int u = 0; u < XF; ++u) r[u] = load_act(src, u);
     }
 }
 
-__device__ __forceinline__ void mm_store_x(float *xs, const float (&r)[16]) {
-    float4 *d = reinterpret_cast<float4 *>(xs + (threadIdx.x >> 4) * kXStride + (threadIdx.x & 15) * 16);
+// Store slice s's loaded x into an LDS buffer, zero past K and past B.
+template <int XF>
+__device__ __forceinline__ void mm_store_x(const MmParams &p, int n0, int s, float *xs, const float (&r)[XF]) {
+    const int e = threadIdx.x * XF;
+    const bool ok = n0 + (e >> 8) < p.B && s * 256 + (e & 255) < p.K;   // K is a multiple of 16, XF divides 16
+    float4 *d = reinterpret_cast<float4 *>(xs + (e >> 8) * kXStride + (e & 255));
 #pragma unroll
-    for (int u = 0; u < 4; ++u) d[u] = make_float4(r[4 * u], r[4 * u + 1], r[4 * u + 2], r[4 * u + 3]);
+    for (int u = 0; u < XF / 4; ++u)
+        d[u] = ok ? make_float4(r[4 * u], r[4 * u + 1], r[4 * u + 2], r[4 * u + 3])
+                  : make_float4(0.f, 0.f, 0.f, 0.f);
 }
 
-template <typename T>
-__global__ __launch_bounds__(kMmNT) void lut_mm_kernel(MmParams p) {
+__device__ __forceinline__ uint32_t mm_codes(const MmParams &p, int s, int row, int q) {
+    return gld(reinterpret_cast<const uint32_t *>(p.codes + ((size_t)s * p.Mp + row) * 16 + 4 * q));
+}
+
+template <typename T, int RT>
+__global__ __launch_bounds__(MmShape<RT>::kNT) __attribute__((amdgpu_waves_per_eu(MmShape<RT>::kWaves))) void lut_mm_kernel(MmParams p) {
+    using Sh = MmShape<RT>;
+    constexpr int NT = Sh::kNT, XF = Sh::kXF, NC = Sh::kCsr, PX = Sh::kPX, PF = Sh::kPF;
+    static_assert(PF % PX == 0, "the unrolled slice body covers both rings");
     __shared__ float4 cb4[256 * 4];                 // codebook [256][16]
-    __shared__ float xs[2][kMmTok * kXStride];      // staged x slices
-    __shared__ unsigned short lcol[kCsrStage];      // the workgroup's CSR outliers
-    __shared__ float lval[kCsrStage];
+    __shared__ __align__(16) float xs[2][kMmTok * kXStride];   // staged x slices; the quarter sums at the end
+    __shared__ unsigned short lcol[NC];             // the workgroup's CSR outliers
+    __shared__ float lval[NC];
+    static_assert(RT * ((kQ - 1) * 64 * 4 + kQ * 64) <= 2 * kMmTok * kXStride,
+                  "quarter and outlier sums fit the x buffers");
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int rt = w / kQ, q = w % kQ;              // row tile, input quarter
     const int ml = lane & 15, kk = lane >> 4;
-    const int mb = blockIdx.x * kMmRows;
-    const int m0 = mb + w * 16;
+    const int mb = blockIdx.x * Sh::kRows;
+    const int m0 = mb + rt * 16;
     const int n0 = blockIdx.y * kMmTok;
     const int row = min(m0 + ml, p.M - 1);          // rows past M: computed, never stored
+    const int mo = m0 + 4 * kk + q;                 // the lane's outlier row (one per quarter wave)
 
-    // ---- round trip 1: codebook, x slice 0, the CSR range of the rows, codes
-    float4 c4[4];
+    // ---- round trip 1: codebook, x slices 0 .. PX, the CSR range of the rows, codes
+    static_assert(1024 % NT == 0, "the codebook is staged in whole float4 rounds");
+    float4 c4[1024 / NT];
     const float4 *gcb = reinterpret_cast<const float4 *>(p.cb);
 #pragma unroll
-    for (int u = 0; u < 4; ++u) c4[u] = gld(gcb + tid + u * kMmNT);
-    float xr[16];
-    mm_load_x<T>(p, n0, 0, xr);
-    int e_lo = 0, e_hi = 0, j[4] = {0, 0, 0, 0}, je[4] = {0, 0, 0, 0};
+    for (int u = 0; u < 1024 / NT; ++u) c4[u] = gld(gcb + tid + u * NT);
+    float x0[XF];
+    mm_load_x<T, XF>(p, n0, 0, x0);
+    float xr[PX][XF];   // x of slices s + 1 .. s + PX, slot (slice % PX)
+#pragma unroll
+    for (int t = 1; t <= PX; ++t) mm_load_x<T, XF>(p, n0, min(t, p.S - 1), xr[t % PX]);
+    int e_lo = 0, e_hi = 0, j = 0, je = 0;
     if (p.rowp) {
         e_lo = gld(p.rowp + mb);
-        e_hi = gld(p.rowp + min(mb + kMmRows, p.M));
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-            const int m = min(m0 + 4 * kk + v, p.M - 1);
-            j[v] = gld(p.rowp + m);
-            je[v] = m0 + 4 * kk + v < p.M ? gld(p.rowp + m + 1) : j[v];
-        }
+        e_hi = gld(p.rowp + min(mb + Sh::kRows, p.M));
+        j = gld(p.rowp + min(mo, p.M - 1));
+        je = mo < p.M ? gld(p.rowp + mo + 1) : j;
     }
-    uint4 cr[kMmPF];   // codes of slices s .. s + kMmPF - 1, slot (s % kMmPF)
+    uint32_t cr[PF];   // codes of slices s .. s + PF - 1, slot (s % PF)
 #pragma unroll
-    for (int q = 0; q < kMmPF; ++q)
-        cr[q] = gld(reinterpret_cast<const uint4 *>(p.codes + ((size_t)min(q, p.S - 1) * p.Mp + row) * 16));
+    for (int u = 0; u < PF; ++u) cr[u] = mm_codes(p, min(u, p.S - 1), row, q);
     // ---- round trip 2: the CSR entries of the workgroup's rows into LDS when
     // they fit (the usual case: each row's entries sorted by column are then
     // added slice by slice from the staged x), else from memory at the end
-    const bool staged = e_hi - e_lo <= kCsrStage;
+    const bool staged = e_hi - e_lo <= NC;
     if (p.rowp && staged && e_hi > e_lo) {
-#pragma unroll
-        for (int u = 0; u < kCsrStage / kMmNT; ++u) {
-            const int e = min(e_lo + tid + u * kMmNT, e_hi - 1);   // an entry of these rows
-            const int c = gld(p.col + e);
-            const float v = gld(p.val + e);
-            if (e_lo + tid + u * kMmNT < e_hi) {
-                lcol[tid + u * kMmNT] = (unsigned short)c;
-                lval[tid + u * kMmNT] = v;
-            }
+        const int e = min(e_lo + tid, e_hi - 1);    // an entry of these rows
+        const int c = gld(p.col + e);
+        const float v = gld(p.val + e);
+        if (e_lo + tid < e_hi) {
+            lcol[tid] = (unsigned short)c;
+            lval[tid] = v;
         }
     }
 #pragma unroll
-    for (int u = 0; u < 4; ++u) cb4[tid + u * kMmNT] = c4[u];
-    mm_store_x(xs[0], xr);
+    for (int u = 0; u < 1024 / NT; ++u) cb4[tid + u * NT] = c4[u];
+    mm_store_x<XF>(p, n0, 0, xs[0], x0);
     __syncthreads();
 
     v4f acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
-    float o[4] = {0.f, 0.f, 0.f, 0.f};
+    float o = 0.f;
+    j -= e_lo;
+    je -= e_lo;
+    // Slice s uses code slot s % PF, and stores x slot (s + 1) % PX for the
+    // next slice: constants in the unrolled body (no register moves of loads
+    // in flight).  The slots are refilled with slices s + PF and s + 1 + PX,
+    // unconditionally (clamped to the last slice).  The main loop runs whole
+    // groups of PF slices with no branch in its body other than the
+    // outlier pass, so the wait counts for the rings stay exact across its
+    // back edge (a merge of differing paths makes the compiler wait for every
+    // load in flight); the last S % PF slices follow it.
+    auto slice = [&](const int s, const int u) __attribute__((always_inline)) {
+        const float *xt = xs[s & 1] + ml * kXStride;
+        const float *xb = xt + 4 * kk + 64 * q;
+        const uint32_t cw = cr[u];
 #pragma unroll
-    for (int v = 0; v < 4; ++v) {
-        j[v] -= e_lo;
-        je[v] -= e_lo;
-    }
-    // Slice s uses code slot s % kMmPF, a constant in the unrolled body (no
-    // register moves of loads in flight); the slot is refilled with slice
-    // s + kMmPF after its gathers, unconditionally (clamped to the last slice).
-    for (int sb = 0; sb < p.S; sb += kMmPF) {
-#pragma unroll
-        for (int q = 0; q < kMmPF; ++q) {
-            const int s = sb + q;
-            if (s >= p.S) break;
-            // the next slice's x in flight during this one (past the last
-            // slice: a reload of the last, unused)
-            mm_load_x<T>(p, n0, min(s + 1, p.S - 1), xr);
-            const float *xt = xs[s & 1] + ml * kXStride;
-            const float *xb = xt + 4 * kk;
-            const uint32_t wd[4] = {cr[q].x, cr[q].y, cr[q].z, cr[q].w};
-#pragma unroll
-            for (int g = 0; g < 16; ++g) {
-                const uint32_t code = (wd[g >> 2] >> ((g & 3) * 8)) & 0xffu;
-                const float4 a = cb4[code * 4 + kk];
-                const float4 b = *reinterpret_cast<const float4 *>(xb + 16 * g);
-                v4f &acc = (g & 1) ? acc1 : acc0;
-                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.x, b.x, acc, 0, 0, 0);
-                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.y, b.y, acc, 0, 0, 0);
-                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.z, b.z, acc, 0, 0, 0);
-                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.w, b.w, acc, 0, 0, 0);
-            }
-            // outliers of the lane's 4 rows whose columns fall in this slice:
-            // kOutPass candidates per row per pass, all reads of a pass in
-            // flight together (one pass covers a slice unless a row has more
-            // than kOutPass entries in it); added in column order
-            if (p.rowp && staged) {
-                const int lim = (s + 1) * 256;
-                bool more = true;
-                while (more) {
-                    int c[4][kOutPass];
-                    float vv[4][kOutPass], xv[4][kOutPass];
-                    bool in[4][kOutPass];
-#pragma unroll
-                    for (int v = 0; v < 4; ++v)
-#pragma unroll
-                        for (int u = 0; u < kOutPass; ++u) {
-                            const int e = min(j[v] + u, kCsrStage - 1);
-                            c[v][u] = lcol[e];
-                            vv[v][u] = lval[e];
-                        }
-#pragma unroll
-                    for (int v = 0; v < 4; ++v)
-#pragma unroll
-                        for (int u = 0; u < kOutPass; ++u) {
-                            in[v][u] = j[v] + u < je[v] && c[v][u] < lim && (u == 0 || in[v][u - 1]);
-                            xv[v][u] = xt[in[v][u] ? c[v][u] - s * 256 : 0];
-                        }
-                    more = false;
-#pragma unroll
-                    for (int v = 0; v < 4; ++v) {
-#pragma unroll
-                        for (int u = 0; u < kOutPass; ++u)
-                            if (in[v][u]) o[v] += vv[v][u] * xv[v][u];
-                        int took = 0;
-#pragma unroll
-                        for (int u = 0; u < kOutPass; ++u) took += in[v][u] ? 1 : 0;
-                        j[v] += took;
-                        more |= took == kOutPass;
-                    }
-                }
-            }
-            if (s + 1 < p.S) mm_store_x(xs[(s + 1) & 1], xr);
-            cr[q] = gld(reinterpret_cast<const uint4 *>(
-                p.codes + ((size_t)min(s + kMmPF, p.S - 1) * p.Mp + row) * 16));
-            __syncthreads();   // slice s + 1 staged; slice s's reads done before it is overwritten
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t code = (cw >> (8 * i)) & 0xffu;
+            const float4 a = cb4[code * 4 + kk];
+            const float4 b = *reinterpret_cast<const float4 *>(xb + 16 * i);
+            v4f &acc = (i & 1) ? acc1 : acc0;
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.x, b.x, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.y, b.y, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.z, b.z, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.w, b.w, acc, 0, 0, 0);
         }
+        // outliers of the lane's row mo whose columns fall in this slice:
+        // kOutPass candidates per pass, the reads of a pass in flight together
+        // (one pass covers a slice unless the row has more than kOutPass
+        // entries in it); added in column order
+        if (p.rowp && staged) {
+            const int lim = (s + 1) * 256;
+            bool more = true;
+            while (more) {
+                int c[kOutPass];
+                float vv[kOutPass];
+#pragma unroll
+                for (int k = 0; k < kOutPass; ++k) {
+                    const int e = min(j + k, NC - 1);
+                    c[k] = lcol[e];
+                    vv[k] = lval[e];
+                }
+                bool in = true;
+                int took = 0;
+#pragma unroll
+                for (int k = 0; k < kOutPass; ++k) {
+                    in = in && j + k < je && c[k] < lim;
+                    const float xv = xt[in ? c[k] - s * 256 : 0];
+                    if (in) o += vv[k] * xv;
+                    took += in ? 1 : 0;
+                }
+                j += took;
+                more = took == kOutPass;
+            }
+        }
+        // slice s + 1 into the other buffer (past the last slice: a clamped
+        // reload, never read), then the freed ring slots refilled
+        const int slot = (u + 1) % PX;
+        mm_store_x<XF>(p, n0, min(s + 1, p.S - 1), xs[(s + 1) & 1], xr[slot]);
+        mm_load_x<T, XF>(p, n0, min(s + 1 + PX, p.S - 1), xr[slot]);
+        cr[u] = mm_codes(p, min(s + PF, p.S - 1), row, q);
+        __syncthreads();   // slice s + 1 staged; slice s's reads done before it is overwritten
+    };
+    int s0 = 0;
+    for (; s0 + PF <= p.S; s0 += PF) {
+#pragma unroll
+        for (int u = 0; u < PF; ++u) slice(s0 + u, u);
+    }
+#pragma unroll
+    for (int u = 0; u < PF - 1; ++u)
+        if (s0 + u < p.S) slice(s0 + u, u);
+
+    // ---- a dense-outlier block: the row's entries and x from memory
+    const int n = n0 + ml;
+    const T *xn = static_cast<const T *>(p.x) + (size_t)min(n, p.B - 1) * p.K;
+    if (p.rowp && !staged && n < p.B)
+        for (int e = j; e < je; ++e) o += gld(p.val + e_lo + e) * load_act(xn, gld(p.col + e_lo + e));
+
+    // ---- the quarter sums and outlier sums of each tile through LDS (the x
+    // buffers are free: the last slice ended with a barrier); quarter 0 adds
+    // the quarter sums in order
+    float4 *red = reinterpret_cast<float4 *>(&xs[0][0]);                 // [RT][kQ - 1][64]
+    float *ored = &xs[0][0] + RT * (kQ - 1) * 64 * 4;                    // [RT][kQ][64]
+    const v4f part = acc0 + acc1;
+    if (q > 0) red[(rt * (kQ - 1) + q - 1) * 64 + lane] = make_float4(part[0], part[1], part[2], part[3]);
+    ored[(rt * kQ + q) * 64 + lane] = o;
+    __syncthreads();
+    if (q > 0) return;
+    float sum[4] = {part[0], part[1], part[2], part[3]};
+#pragma unroll
+    for (int r = 0; r < kQ - 1; ++r) {
+        const float4 t = red[(rt * (kQ - 1) + r) * 64 + lane];
+        sum[0] += t.x;
+        sum[1] += t.y;
+        sum[2] += t.z;
+        sum[3] += t.w;
     }
 
-    // ---- epilogue: lane holds rows m0 + 4 kk + v of token n0 + ml
-    const int n = n0 + ml;
+    // ---- epilogue: lane holds rows m0 + 4 kk + v of token n
     if (n >= p.B) return;
-    const T *xn = static_cast<const T *>(p.x) + (size_t)n * p.K;
     T *yn = static_cast<T *>(p.y) + (size_t)n * p.M;
-    if (p.rowp && !staged) {   // a dense-outlier block: entries and x from memory
-#pragma unroll
-        for (int v = 0; v < 4; ++v)
-            for (int e = j[v]; e < je[v]; ++e) o[v] += gld(p.val + e_lo + e) * load_act(xn, gld(p.col + e_lo + e));
-    }
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
         const int m = m0 + 4 * kk + v;
         if (m >= p.M) continue;
-        float yv = (acc0[v] + acc1[v]) * gld(p.scales + m);
+        float yv = sum[v] * gld(p.scales + m);
         if (p.bias) yv += gld(p.bias + m);
-        store_act(yn, (size_t)m, yv + o[v]);
+        store_act(yn, (size_t)m, yv + ored[(rt * kQ + v) * 64 + lane]);
     }
 }
 
+// Row tiles per workgroup by batch: small batches take one tile per
+// workgroup for the most workgroups, larger ones share the staged x among
+// more tiles.
+static int mm_row_tiles(int B) { return B <= 16 ? 1 : B <= 32 ? 2 : 4; }
+
+template <typename T>
+static void launch_mm_t(const MmParams &p, int rt, int gy, hipStream_t st) {
+    if (rt == 1)
+        OJX_LAUNCH((lut_mm_kernel<T, 1>), dim3((p.M + 15) / 16, gy), dim3(MmShape<1>::kNT), 0, st, p);
+    else if (rt == 2)
+        OJX_LAUNCH((lut_mm_kernel<T, 2>), dim3((p.M + 31) / 32, gy), dim3(MmShape<2>::kNT), 0, st, p);
+    else
+        OJX_LAUNCH((lut_mm_kernel<T, 4>), dim3((p.M + 63) / 64, gy), dim3(MmShape<4>::kNT), 0, st, p);
+}
+
 int launch_mm(const MmParams &p, int dtype, hipStream_t st) {
-    const dim3 grid((p.M + kMmRows - 1) / kMmRows, (p.B + kMmTok - 1) / kMmTok);
-    if (grid.y > 65535) {
+    const int gy = (p.B + kMmTok - 1) / kMmTok;
+    if (gy > 65535) {
         set_error("batch %d too large for the MFMA path", p.B);
         return OJASX_ERR_INVALID;
     }
+    const int rt = mm_row_tiles(p.B);
     if (dtype == OJASX_DTYPE_F32)
-        OJX_LAUNCH(lut_mm_kernel<float>, grid, dim3(kMmNT), 0, st, p);
+        launch_mm_t<float>(p, rt, gy, st);
     else
-        OJX_LAUNCH(lut_mm_kernel<__hip_bfloat16>, grid, dim3(kMmNT), 0, st, p);
+        launch_mm_t<__hip_bfloat16>(p, rt, gy, st);
     OJX_HIP(hipGetLastError());
     return OJASX_OK;
 }

@@ -80,7 +80,9 @@ def test_reference_t2(pkg):
                                    (257, 5120, 2),    # 20 slices: one or two per wave
                                    (64, 16, 7),       # one group, one wave
                                    (333, 2000, 35),   # MFMA path: ragged rows, tokens, slices
-                                   (70, 464, 33)])
+                                   (70, 464, 33),
+                                   (333, 2000, 13),   # MFMA, one row tile per workgroup
+                                   (517, 1040, 27)])  # MFMA, two row tiles per workgroup
 def test_integer_inputs_bit_exact(pkg, dev, M, K, B):
     import torch
     c = integer_case(M * 7 + B, M=M, K=K, B=B)
@@ -105,7 +107,12 @@ def test_baseline_configs_fp32(pkg, dev, M, K, B):
     (129, 4096, 40, 0, 0.02),
     (6912, 2560, 36, 1, 0.0038),   # outliers staged in LDS, added slice by slice
     (300, 256, 48, 1, 0.02),
-    (1000, 2560, 33, 0, 0.0038)])
+    (1000, 2560, 33, 0, 0.0038),
+    (333, 1040, 13, 0, 0.0038),    # one row tile per workgroup, 5 slices (a tail of 1)
+    (70, 4096, 16, 1, 0.02),       # one row tile, 16 slices (no tail)
+    (95, 2560, 14, 0, 0.05),       # one row tile, outliers past the LDS stage
+    (2049, 768, 20, 0, 0.0038),    # two row tiles, 3 slices (main loop skipped)
+    (517, 3072, 31, 1, 0.0038)])   # two row tiles, 12 slices
 def test_mfma_batched_shapes(pkg, dev, M, K, B, dt, density):
     """Many tokens (x . W^T on MFMA): ragged rows, tokens and slices, bias,
     outliers given with each row's columns shuffled (the handle sorts them),
