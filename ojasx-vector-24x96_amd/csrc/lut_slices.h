@@ -115,38 +115,45 @@ __device__ __forceinline__ void slice_loop(const float *xs, float *L, const floa
         build_store<NW>(L, w, lane, c);
         __syncthreads();
     }
-    // Slice s uses ring slot (s - s0) % PF, a constant in the unrolled body, so
-    // the ring never moves registers (a move of a register whose load is in
+    // Slice s uses ring slot q = (s - s0) % PF, a constant in the unrolled body,
+    // so the ring never moves registers (a move of a register whose load is in
     // flight would wait for that load); the slot is refilled with slice s + PF
     // once its gathers are issued, unconditionally (past the last slice it
     // reloads that slice: a conditional load would need a second copy of the
-    // slot).
-    for (int sb = s0; sb < s1; sb += PF) {
+    // slot).  With DB, slice s + 1's LUT is built unconditionally too (past the
+    // last slice: a rebuild of it into the idle buffer, never read).  The main
+    // loop runs whole groups of PF slices with no branch in its body, so the
+    // wait counts for the ring stay exact across its back edge (a loop body with
+    // several paths to its latch makes the compiler wait for every load in
+    // flight at the loop head); the last (s1 - s0) % PF slices follow it.
+    auto one = [&](const int s, const int q) __attribute__((always_inline)) {
+        __builtin_amdgcn_sched_barrier(0);   // each slice scheduled on its own
+        if constexpr (DB) {
+            build_issue<NW>(xs, min(s + 1, s1 - 1), lane, bop, c);
+            gather(L + ((s - s0) & 1) * kLutFloats, ring[q], acc);
 #pragma unroll
-        for (int q = 0; q < PF; ++q) {
-            const int s = sb + q;
-            if (s >= s1) break;
-            __builtin_amdgcn_sched_barrier(0);   // each slice scheduled on its own
-            if constexpr (DB) {
-                const bool nb = s + 1 < s1;
-                if (nb) build_issue<NW>(xs, s + 1, lane, bop, c);
-                gather(L + ((s - s0) & 1) * kLutFloats, ring[q], acc);
+            for (int r = 0; r < R; ++r) ring[q][r] = ld_code_row(codes, min(s + PF, s1 - 1), Mp, row[r]);
+            build_store<NW>(L + ((s + 1 - s0) & 1) * kLutFloats, w, lane, c);
+            __syncthreads();   // slice s + 1's LUT written, slice s's gathers done
+        } else {
+            build_issue<NW>(xs, s, lane, bop, c);
+            build_store<NW>(L, w, lane, c);
+            __syncthreads();
+            __builtin_amdgcn_sched_barrier(0);
+            gather(L, ring[q], acc);
 #pragma unroll
-                for (int r = 0; r < R; ++r) ring[q][r] = ld_code_row(codes, min(s + PF, s1 - 1), Mp, row[r]);
-                if (nb) build_store<NW>(L + ((s + 1 - s0) & 1) * kLutFloats, w, lane, c);
-                __syncthreads();   // slice s + 1's LUT written, slice s's gathers done
-            } else {
-                build_issue<NW>(xs, s, lane, bop, c);
-                build_store<NW>(L, w, lane, c);
-                __syncthreads();
-                __builtin_amdgcn_sched_barrier(0);
-                gather(L, ring[q], acc);
-#pragma unroll
-                for (int r = 0; r < R; ++r) ring[q][r] = ld_code_row(codes, min(s + PF, s1 - 1), Mp, row[r]);
-                __syncthreads();   // the gathers of slice s before the build of s + 1
-            }
+            for (int r = 0; r < R; ++r) ring[q][r] = ld_code_row(codes, min(s + PF, s1 - 1), Mp, row[r]);
+            __syncthreads();   // the gathers of slice s before the build of s + 1
         }
+    };
+    int sb = s0;
+    for (; sb + PF <= s1; sb += PF) {
+#pragma unroll
+        for (int q = 0; q < PF; ++q) one(sb + q, q);
     }
+#pragma unroll
+    for (int q = 0; q < PF - 1; ++q)
+        if (sb + q < s1) one(sb + q, q);
 }
 
 }  // namespace slices
