@@ -106,10 +106,13 @@ int kv_decode_device_len(const float *q, const uint8_t *kc, const float *ks, con
                          const int *len_dev, int len_add, int T_max, int P, int Hq, int Hkv,
                          float sf, float *part_o, float *part_ml, float *out, hipStream_t st,
                          int tpl = 0);
-// The log-sum-exp merge of such partials alone (n_chunks > 1 chunks of `chunk`
-// tokens, head dim 128): out [Hq][128].
-int kv_merge_device_len(const float *part_o, const float *part_ml, int n_chunks, int chunk, int Hq,
-                        const int *len_dev, int len_add, float *out, hipStream_t st);
+// The log-sum-exp merge of such partials alone (head dim 128): the first
+// ceil((*len_dev + len_add) / chunk) chunks of a stride of stride_chunks
+// slots, then, with extra set, the partial in the stride's last slot: out
+// [Hq][128].
+int kv_merge_device_len(const float *part_o, const float *part_ml, int stride_chunks, int chunk,
+                        int Hq, const int *len_dev, int len_add, int extra, float *out,
+                        hipStream_t st);
 
 // LUT[b][g][k] = <x_b[gD:(g+1)D], C[k]> for g < Gp (0 for g >= G) and all 256
 // centroids of the zero-padded codebook cb [256][D]; x [B][K] in dtype.

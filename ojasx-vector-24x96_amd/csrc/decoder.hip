@@ -9,6 +9,7 @@
 //     2. q    = RoPE(RMSNorm_head(q, w_qn));  k = RoPE(RMSNorm_head(k, w_kn));
 //        k, v encoded into the layer's paged code cache at `pos`;
 //        attn = softmax(q K^T / sqrt(hd)) V over pos + 1 tokens  attn_decode_kernel + merge
+//        (partials per 64-token chunk of the cached tokens and one for the new token)
 //     3. x   += LUT(Wo, attn)                          residual epilogue
 //     4. gu   = LUT(Wgu, RMSNorm(x, w_post))           RMSNorm prologue (gate rows, then up rows)
 //     5. x   += LUT(Wdown, silu(gate) * up)            SwiGLU prologue, residual epilogue
@@ -43,8 +44,7 @@ struct AttnParams {
     const float *kcb, *vcb;       // [Hkv][256][16]
     uint8_t *kc, *vc;             // [pages][Hkv][P][G]
     float *ks, *vs;               // [pages][Hkv][P]
-    float *part_o, *part_ml;      // [Hq][n_chunks][hd], [Hq][n_chunks][2]
-    float *out;                   // [Hq][hd], written here when n_chunks == 1
+    float *part_o, *part_ml;      // [Hq][n_chunks + 1][hd], [Hq][n_chunks + 1][2]
     int Hq, Hkv, P, max_ctx, n_chunks;
     float eps, sf;
 };
@@ -52,28 +52,30 @@ struct AttnParams {
 constexpr int kAttnNT = 256;
 constexpr int kAttnC = 64;        // tokens per chunk, one per lane
 
-// Attention of the new token at pos = state[0] over the pos + 1 cached tokens,
-// prologue included.  Workgroup = (chunk c of 64 tokens, kv head h, slice z of
-// up to 4 of its query heads); wave j < nj owns query head h*R + 4z + j.
-//   q: lane l holds dimensions l and l + 64 (a RoPE pair): per-head RMSNorm by
-//      a wave sum, then the rotation, into LDS.
-//   The chunk holding pos also prepares the new token: wave 2 normalises and
-//   rotates k, wave 3 takes v as is, each scaled by max|.| / 127; thread t then
-//   holds centroid t of the head's K and V codebooks for the nearest-centroid
-//   search of each 16-dimension group (ties to the lower index).  Slice z = 0
-//   stores the codes and scales into the cache; every slice uses them for the
-//   token itself, so no workgroup reads the slot being written.
-//   Decode: lane l scores token 64c + l for each query head from the K
-//   codebook in LDS, the chunk's softmax statistics by wave reductions, then
-//   lane l accumulates output dimensions 2l, 2l + 1 from the V codebook.
-// Partials (o, max, sum) per query head and chunk; the caller merges them.
+// Attention of the new token at pos = state[0] over the pos + 1 tokens of the
+// cache, prologue included, as partials (o, max, sum) per query head: one per
+// 64-token chunk of the tokens before pos, and the new token's own in the
+// last slot (index n_chunks); kv_merge_kernel combines them.
+// Workgroup (x, kv head h, slice z of up to 4 of its query heads); wave j < nj
+// owns query head h*R + 4z + j, whose q it normalises (RMSNorm by a wave sum)
+// and rotates itself: lane l holds dimensions l and l + 64, a RoPE pair.
+//   x < n_chunks: chunk x of the tokens before pos.  Lane l scores token
+//     64x + l for each query head from the K codebook in LDS, the chunk's
+//     softmax statistics are wave reductions, then lane l accumulates output
+//     dimensions 2l, 2l + 1 from the V codebook.
+//   x = n_chunks: the new token.  Wave 2 normalises and rotates k, wave 3
+//     takes v as is, each scaled by max|.| / 127; thread t holds centroid t of
+//     the head's K and V codebooks for the nearest-centroid search of each
+//     16-dimension group (ties to the lower index); slice z = 0 stores codes
+//     and scales into the cache.  Its partial: max = its score, sum = 1,
+//     o = v_scale * Cv[code].  No workgroup reads the slot being written, and
+//     the encoder's chain runs beside the chunks' instead of inside one.
 __global__ __launch_bounds__(kAttnNT) void attn_decode_kernel(AttnParams p) {
     __shared__ float4 ck4[256 * 4];      // K codebook [256][16]
     __shared__ float4 cv4[256 * 4];      // V codebook [256][16]
     __shared__ float4 q4s[4 * 32];       // rotated q [4][128]
     __shared__ float xs[2 * kHd];        // new token: k / s_k, v / s_v
     __shared__ float nscale[2];          // its scales
-    __shared__ int npage;                // its page
     __shared__ float wd[2][kG][4];       // per-wave nearest distance
     __shared__ int wi[2][kG][4];         // and its lowest centroid
     __shared__ uint2 ncode[2];           // its K and V codes
@@ -85,8 +87,10 @@ __global__ __launch_bounds__(kAttnNT) void attn_decode_kernel(AttnParams p) {
     const int j0 = h * R + blockIdx.z * 4;
     const int nj = min(4, R - (int)blockIdx.z * 4);
     const int c = blockIdx.x;
-    // ---- round trip 1: the position, codebooks, the q / k / v rows and norm
-    // weights, wave 0's block-table entry (the table covers max_ctx)
+    const bool fresh = c == p.n_chunks;          // the new token's workgroup
+    const int stride = p.n_chunks + 1;           // partial slots per query head
+    // ---- round trip 1: the position, codebooks, q rows and norm weights, the
+    // new token's k / v rows (its workgroup), wave 0's block-table entry
     const int pos = min(p.state[0], p.max_ctx - 1);
     const float4 *gk = reinterpret_cast<const float4 *>(p.kcb + (size_t)h * 256 * 16);
     const float4 *gv = reinterpret_cast<const float4 *>(p.vcb + (size_t)h * 256 * 16);
@@ -105,7 +109,7 @@ __global__ __launch_bounds__(kAttnNT) void attn_decode_kernel(AttnParams p) {
         w1 = p.qn_w[lane + 64];
     }
     float e0 = 0.f, e1 = 0.f, u0 = 0.f, u1 = 0.f;   // k (wave 2, k_norm weights) / v (wave 3)
-    if (j >= 2) {
+    if (fresh && j >= 2) {
         const float *src = p.qkv + (size_t)(p.Hq + (j - 2) * p.Hkv + h) * kHd;
         e0 = src[lane];
         e1 = src[lane + 64];
@@ -114,23 +118,23 @@ __global__ __launch_bounds__(kAttnNT) void attn_decode_kernel(AttnParams p) {
             u1 = p.kn_w[lane + 64];
         }
     }
-    const int tw = c * kAttnC + lane;            // wave 0's token
-    const int pg = j == 0 ? p.bt[min(tw, p.max_ctx - 1) / p.P] : 0;
-    const int T = pos + 1;
-    if (c * kAttnC >= T) return;                 // whole workgroup: a chunk past the context
-    const bool fresh = pos / kAttnC == c;        // this chunk holds the new token
-    // ---- round trip 2: cos / sin at pos, codes and scales of the cached tokens
+    const int tw = c * kAttnC + lane;            // wave 0's token (a chunk)
+    const int pg = (!fresh && j == 0) ? p.bt[min(tw, p.max_ctx - 1) / p.P] : 0;
+    if (!fresh && c * kAttnC >= pos) return;     // whole workgroup: a chunk past the cached tokens
+    // ---- round trip 2: cos / sin at pos; the chunk's codes and scales, or
+    // the new token's page
     const float cs = p.cos_t[(size_t)pos * (kHd / 2) + lane];
     const float sn = p.sin_t[(size_t)pos * (kHd / 2) + lane];
     uint2 kw = make_uint2(0, 0), vw = make_uint2(0, 0);
     float ksv = 0.f, vsv = 0.f;
-    if (j == 0 && tw < pos) {
+    if (!fresh && j == 0 && tw < pos) {
         const size_t slot = ((size_t)pg * p.Hkv + h) * p.P + (tw % p.P);
         kw = *reinterpret_cast<const uint2 *>(p.kc + slot * kG);
         vw = *reinterpret_cast<const uint2 *>(p.vc + slot * kG);
         ksv = p.ks[slot];
         vsv = p.vs[slot];
     }
+    const int npage = fresh ? p.bt[pos / p.P] : 0;
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
         ck4[tid + u * kAttnNT] = a[u];
@@ -143,6 +147,7 @@ __global__ __launch_bounds__(kAttnNT) void attn_decode_kernel(AttnParams p) {
         qf[lane] = x0 * cs - x1 * sn;
         qf[lane + 64] = x1 * cs + x0 * sn;
     }
+
     if (fresh) {
         if (j == 2) {
             const float rn = 1.0f / sqrtf(wave_sum_f(e0 * e0 + e1 * e1) / (float)kHd + p.eps);
@@ -156,10 +161,7 @@ __global__ __launch_bounds__(kAttnNT) void attn_decode_kernel(AttnParams p) {
             xs[(j - 2) * kHd + lane + 64] = e1 / s;
             if (lane == 0) nscale[j - 2] = s;
         }
-        if (j == 0 && tw == pos) npage = pg;
-    }
-    __syncthreads();
-    if (fresh) {
+        __syncthreads();
         float ck[kBd], cv[kBd];
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
@@ -206,13 +208,48 @@ __global__ __launch_bounds__(kAttnNT) void attn_decode_kernel(AttnParams p) {
             }
         }
         __syncthreads();
-        if (j == 0 && tw == pos) {
-            kw = ncode[0];
-            vw = ncode[1];
-            ksv = nscale[0];
-            vsv = nscale[1];
+        // the new token's partial for head j: its score (the chunk arithmetic
+        // for one token), sum 1, o = v_scale * Cv[code]
+        if (j < nj) {
+            const uint2 kn = ncode[0], vn = ncode[1];
+            const uint32_t kd[2] = {kn.x, kn.y};
+            float acc = 0.f;
+#pragma unroll
+            for (int g = 0; g < kG; ++g) {
+                const uint32_t code = (kd[g >> 2] >> ((g & 3) * 8)) & 0xffu;
+                const float4 *cr = ck4 + code * 4;
+                const float4 *qr = q4s + j * 32 + g * 4;
+                float dot = 0.f;
+#pragma unroll
+                for (int w = 0; w < 4; ++w) {
+                    const float4 cq = cr[w], qq = qr[w];
+                    dot = fmaf(qq.x, cq.x, dot);
+                    dot = fmaf(qq.y, cq.y, dot);
+                    dot = fmaf(qq.z, cq.z, dot);
+                    dot = fmaf(qq.w, cq.w, dot);
+                }
+                acc += dot;
+            }
+            const float sc = acc * (nscale[0] * p.sf);
+            const int g = lane >> 3, d0 = (lane & 7) * 2;
+            const uint32_t code = ((g < 4 ? vn.x : vn.y) >> ((g & 3) * 8)) & 0xffu;
+            const float2 cvv =
+                *reinterpret_cast<const float2 *>(reinterpret_cast<const float *>(cv4) + code * 16 + d0);
+            const float wv = nscale[1];
+            float *po = p.part_o + ((size_t)(j0 + j) * stride + p.n_chunks) * kHd + lane * 2;
+            po[0] = wv * cvv.x;
+            po[1] = wv * cvv.y;
+            if (lane == 0) {
+                float *ml = p.part_ml + ((size_t)(j0 + j) * stride + p.n_chunks) * 2;
+                ml[0] = sc;
+                ml[1] = 1.0f;
+            }
         }
+        return;
     }
+
+    // ---- a chunk of the tokens before pos
+    const int T = pos;
     if (j == 0) {
         kcw[lane] = kw;
         vcw[lane] = vw;
@@ -224,7 +261,7 @@ __global__ __launch_bounds__(kAttnNT) void attn_decode_kernel(AttnParams p) {
     const uint2 kwl = kcw[lane];
     __syncthreads();   // wsc is rewritten with the weights below
 
-    // ---- score of token tw for head j: sum_g <q_j,g, Ck[code_g]> * ks * sf
+    // score of token tw for head j: sum_g <q_j,g, Ck[code_g]> * ks * sf
     float sc = -INFINITY;
     if (j < nj) {
         const uint32_t kd[2] = {kwl.x, kwl.y};
@@ -253,7 +290,7 @@ __global__ __launch_bounds__(kAttnNT) void attn_decode_kernel(AttnParams p) {
     const float l = wave_sum_f(e);
     __syncthreads();
 
-    // ---- V: lane owns dims 2*lane, 2*lane+1 (group g = lane / 8)
+    // V: lane owns dims 2*lane, 2*lane+1 (group g = lane / 8)
     if (j < nj) {
         const int g = lane >> 3, d0 = (lane & 7) * 2;
         const float *cvf = reinterpret_cast<const float *>(cv4);
@@ -267,19 +304,13 @@ __global__ __launch_bounds__(kAttnNT) void attn_decode_kernel(AttnParams p) {
             o0 = fmaf(w, cvv.x, o0);
             o1 = fmaf(w, cvv.y, o1);
         }
-        const int od = lane * 2;
-        if (p.n_chunks == 1) {
-            p.out[(size_t)(j0 + j) * kHd + od] = o0 / l;
-            p.out[(size_t)(j0 + j) * kHd + od + 1] = o1 / l;
-        } else {
-            float *po = p.part_o + ((size_t)(j0 + j) * p.n_chunks + c) * kHd + od;
-            po[0] = o0;
-            po[1] = o1;
-            if (lane == 0) {
-                float *ml = p.part_ml + ((size_t)(j0 + j) * p.n_chunks + c) * 2;
-                ml[0] = m;
-                ml[1] = l;
-            }
+        float *po = p.part_o + ((size_t)(j0 + j) * stride + c) * kHd + lane * 2;
+        po[0] = o0;
+        po[1] = o1;
+        if (lane == 0) {
+            float *ml = p.part_ml + ((size_t)(j0 + j) * stride + c) * 2;
+            ml[0] = m;
+            ml[1] = l;
         }
     }
 }
@@ -407,15 +438,13 @@ struct Decoder {
                           cos_t.as<float>(), sin_t.as<float>(), pos, bt.as<int>(),
                           ly.kcb.as<float>(), ly.vcb.as<float>(), ly.kc.as<uint8_t>(),
                           ly.vc.as<uint8_t>(), ly.ks.as<float>(), ly.vs.as<float>(),
-                          part_o.as<float>(), part_ml.as<float>(), attn.as<float>(), Hq, Hkv, P,
-                          max_ctx, n_chunks(), eps, sf};
-            OJX_LAUNCH(attn_decode_kernel, dim3(n_chunks(), Hkv, (Hq / Hkv + 3) / 4),
+                          part_o.as<float>(), part_ml.as<float>(), Hq, Hkv, P, max_ctx,
+                          n_chunks(), eps, sf};
+            OJX_LAUNCH(attn_decode_kernel, dim3(n_chunks() + 1, Hkv, (Hq / Hkv + 3) / 4),
                        dim3(kAttnNT), 0, st, ap);
-            if (n_chunks() > 1) {
-                rc = kv_merge_device_len(part_o.as<float>(), part_ml.as<float>(), n_chunks(),
-                                         kAttnC, Hq, pos, 1, attn.as<float>(), st);
-                if (rc) return rc;
-            }
+            rc = kv_merge_device_len(part_o.as<float>(), part_ml.as<float>(), n_chunks() + 1,
+                                     kAttnC, Hq, pos, 0, 1, attn.as<float>(), st);
+            if (rc) return rc;
             rc = linear_forward_fused(ly.o, attn.as<float>(), x.as<float>(), 0, nullptr, 0.f,
                                       x.as<float>(), st);
             if (rc) return rc;
@@ -525,8 +554,8 @@ OJASX_API OjasxDecoderHandle ojasx_create_decoder(int hidden, int layers, int q_
     if (!rc) rc = d->attn.ensure((size_t)q_heads * kHd * 4);
     if (!rc) rc = d->gu.ensure((size_t)2 * intermediate * 4);
     if (!rc) rc = d->logits.ensure((size_t)vocab * 4);
-    if (!rc) rc = d->part_o.ensure((size_t)q_heads * d->n_chunks() * kHd * 4);
-    if (!rc) rc = d->part_ml.ensure((size_t)q_heads * d->n_chunks() * 2 * 4);
+    if (!rc) rc = d->part_o.ensure((size_t)q_heads * (d->n_chunks() + 1) * kHd * 4);
+    if (!rc) rc = d->part_ml.ensure((size_t)q_heads * (d->n_chunks() + 1) * 2 * 4);
     const int st0[4] = {0, 0, 0, 0};
     if (!rc) rc = upload(d->state, st0, sizeof(st0));
     if (!rc) rc = d->tokens.ensure((size_t)max_steps * 4);

@@ -620,23 +620,29 @@ __global__ __launch_bounds__(kNT) void kv_decode_small_kernel(KVParams p) {
 // (max, sum) pairs staged in LDS, max and normaliser by wave shuffles, then
 // each thread sums one output coordinate over the chunks.
 // With len_dev set, only the first ceil((*len_dev + len_add) / chunk) of the
-// n_chunks (the partials' stride) are merged.
+// chunks (the partials' stride) are merged.  With extra set, the stride's last
+// slot holds one more partial, merged after the live chunks (it is not one of
+// them).
 __global__ __launch_bounds__(kNT) void kv_merge_kernel(const float *part_o, const float *part_ml,
                                                       int stride_chunks, int hd, float *out,
-                                                      const int *len_dev, int len_add, int chunk) {
+                                                      const int *len_dev, int len_add, int chunk,
+                                                      int extra) {
     extern __shared__ float wsm[];   // [n_chunks] chunk weights
     __shared__ float red[kNT / 64];
     const int j = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    const int n_chunks =
-        len_dev ? min(stride_chunks, (*len_dev + len_add + chunk - 1) / chunk) : stride_chunks;
+    const int n_slots = stride_chunks - extra;
+    const int n_live =
+        len_dev ? min(n_slots, (*len_dev + len_add + chunk - 1) / chunk) : n_slots;
+    const int n_chunks = max(n_live, 0) + extra;   // chunk c < n_live at slot c, then the extra
     if (n_chunks <= 0) return;                      // empty context: out untouched
+    auto slot = [&](int c) { return c < n_live ? c : stride_chunks - 1; };
     // The statistics of chunk tid first, then the partials of the first
     // 2 * kMergePre chunks for the two-threads-per-coordinate sum (even and odd
     // chunks) used when 2 * hd <= kNT.  Every load is unconditional, at clamped
     // indices, so the code stays straight-line and the max reduction waits
     // for the statistics only (vmcnt counts loads in issue order).
     const float *ml = part_ml + (size_t)j * stride_chunks * 2;
-    float2 st0 = *reinterpret_cast<const float2 *>(ml + 2 * min(tid, n_chunks - 1));
+    float2 st0 = *reinterpret_cast<const float2 *>(ml + 2 * slot(min(tid, n_chunks - 1)));
     constexpr int kMergePre = 36;
     const bool pair = 2 * hd <= kNT;
     const int hf = tid / hd, d = tid - hf * hd;
@@ -644,10 +650,10 @@ __global__ __launch_bounds__(kNT) void kv_merge_kernel(const float *part_o, cons
     float pre[kMergePre];
 #pragma unroll
     for (int u = 0; u < kMergePre; ++u)
-        pre[u] = po[(size_t)min(min(hf, 1) + 2 * u, n_chunks - 1) * hd];
+        pre[u] = po[(size_t)slot(min(min(hf, 1) + 2 * u, n_chunks - 1)) * hd];
     if (tid >= n_chunks) st0 = make_float2(-INFINITY, 0.f);
     float m = st0.x;
-    for (int c = tid + kNT; c < n_chunks; c += kNT) m = fmaxf(m, ml[2 * c]);
+    for (int c = tid + kNT; c < n_chunks; c += kNT) m = fmaxf(m, ml[2 * slot(c)]);
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
     if (lane == 0) red[wv] = m;
@@ -663,10 +669,10 @@ __global__ __launch_bounds__(kNT) void kv_merge_kernel(const float *part_o, cons
         l = st0.y * wc;
     }
     for (int c = tid + kNT; c < n_chunks; c += kNT) {
-        const float mc = ml[2 * c];
+        const float mc = ml[2 * slot(c)];
         const float wc = mc == -INFINITY ? 0.f : expf(mc - m);
         wsm[c] = wc;
-        l += ml[2 * c + 1] * wc;
+        l += ml[2 * slot(c) + 1] * wc;
     }
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) l += __shfl_xor(l, off);
@@ -691,11 +697,11 @@ __global__ __launch_bounds__(kNT) void kv_merge_kernel(const float *part_o, cons
             for (; c + 30 < n_chunks; c += 32) {
                 float v[16];
 #pragma unroll
-                for (int u = 0; u < 16; ++u) v[u] = po[(size_t)(c + 2 * u) * hd];
+                for (int u = 0; u < 16; ++u) v[u] = po[(size_t)slot(c + 2 * u) * hd];
 #pragma unroll
                 for (int u = 0; u < 16; ++u) o[u & 3] = fmaf(v[u], wsm[c + 2 * u], o[u & 3]);
             }
-            for (; c < n_chunks; c += 2) o[0] = fmaf(po[(size_t)c * hd], wsm[c], o[0]);
+            for (; c < n_chunks; c += 2) o[0] = fmaf(po[(size_t)slot(c) * hd], wsm[c], o[0]);
             acc = (o[0] + o[1]) + (o[2] + o[3]);
             if (hf == 1) half_sum[d] = acc;
         }
@@ -710,11 +716,11 @@ __global__ __launch_bounds__(kNT) void kv_merge_kernel(const float *part_o, cons
         for (; c + 8 <= n_chunks; c += 8) {
             float v[8];
 #pragma unroll
-            for (int u = 0; u < 8; ++u) v[u] = po[(size_t)(c + u) * hd];
+            for (int u = 0; u < 8; ++u) v[u] = po[(size_t)slot(c + u) * hd];
 #pragma unroll
             for (int u = 0; u < 8; ++u) o[u] = fmaf(v[u], wsm[c + u], o[u]);
         }
-        for (; c < n_chunks; ++c) o[0] = fmaf(po[(size_t)c * hd], wsm[c], o[0]);
+        for (; c < n_chunks; ++c) o[0] = fmaf(po[(size_t)slot(c) * hd], wsm[c], o[0]);
         out[(size_t)j * hd + d] = (((o[0] + o[1]) + (o[2] + o[3])) + ((o[4] + o[5]) + (o[6] + o[7]))) * inv;
     }
 }
@@ -770,19 +776,20 @@ int kv_decode_device_len(const float *q, const uint8_t *kc, const float *ks, con
     else OJX_LAUNCH(kv_decode_small_kernel<4>, grid, dim3(kNT), 0, st, p);
     if (n_chunks > 1)
         OJX_LAUNCH(kv_merge_kernel, dim3(Hq), dim3(kNT), (size_t)n_chunks * 4, st, part_o, part_ml,
-                   n_chunks, 128, out, len_dev, len_add, C);
+                   n_chunks, 128, out, len_dev, len_add, C, 0);
     OJX_HIP(hipGetLastError());
     return OJASX_OK;
 }
 
-int kv_merge_device_len(const float *part_o, const float *part_ml, int n_chunks, int chunk, int Hq,
-                        const int *len_dev, int len_add, float *out, hipStream_t st) {
-    if (n_chunks <= 1 || Hq <= 0 || chunk <= 0) {
-        set_error("invalid KV merge shape Hq=%d chunks=%d", Hq, n_chunks);
+int kv_merge_device_len(const float *part_o, const float *part_ml, int stride_chunks, int chunk,
+                        int Hq, const int *len_dev, int len_add, int extra, float *out,
+                        hipStream_t st) {
+    if (stride_chunks < 1 + (extra ? 1 : 0) || Hq <= 0 || chunk <= 0) {
+        set_error("invalid KV merge shape Hq=%d chunks=%d", Hq, stride_chunks);
         return OJASX_ERR_INVALID;
     }
-    OJX_LAUNCH(kv_merge_kernel, dim3(Hq), dim3(kNT), (size_t)n_chunks * 4, st, part_o, part_ml,
-               n_chunks, 128, out, len_dev, len_add, chunk);
+    OJX_LAUNCH(kv_merge_kernel, dim3(Hq), dim3(kNT), (size_t)stride_chunks * 4, st, part_o, part_ml,
+               stride_chunks, 128, out, len_dev, len_add, chunk, extra ? 1 : 0);
     OJX_HIP(hipGetLastError());
     return OJASX_OK;
 }
@@ -820,7 +827,7 @@ int kv_decode(const float *q, const uint8_t *kc, const float *ks, const uint8_t 
             OJX_LAUNCH(kv_decode_small_kernel<1>, dim3(n_chunks, Hkv, nz), dim3(kNT), 0, st, p);
             if (n_chunks > 1)
                 OJX_LAUNCH(kv_merge_kernel, dim3(Hq), dim3(kNT), (size_t)n_chunks * 4, st,
-                           wk.o.as<float>(), wk.ml.as<float>(), n_chunks, hd, out, nullptr, 0, 1);
+                           wk.o.as<float>(), wk.ml.as<float>(), n_chunks, hd, out, nullptr, 0, 1, 0);
             OJX_HIP(hipGetLastError());
             return OJASX_OK;
         }
@@ -847,7 +854,7 @@ int kv_decode(const float *q, const uint8_t *kc, const float *ks, const uint8_t 
         OJX_LAUNCH(kv_decode_wide_kernel, dim3(n_chunks, Hkv, nz), dim3(kWideNT), lds, st, p);
         if (n_chunks > 1)
             OJX_LAUNCH(kv_merge_kernel, dim3(Hq), dim3(kNT), (size_t)n_chunks * 4, st,
-                       wk.o.as<float>(), wk.ml.as<float>(), n_chunks, hd, out, nullptr, 0, 1);
+                       wk.o.as<float>(), wk.ml.as<float>(), n_chunks, hd, out, nullptr, 0, 1, 0);
         OJX_HIP(hipGetLastError());
         return OJASX_OK;
     }
@@ -873,7 +880,7 @@ int kv_decode(const float *q, const uint8_t *kc, const float *ks, const uint8_t 
     const int nch = p.n_chunks;
     if (nch > 1)
         OJX_LAUNCH(kv_merge_kernel, dim3(Hq), dim3(kNT), (size_t)nch * 4, st,
-                           wk.o.as<float>(), wk.ml.as<float>(), nch, hd, out, nullptr, 0, 1);
+                           wk.o.as<float>(), wk.ml.as<float>(), nch, hd, out, nullptr, 0, 1, 0);
     OJX_HIP(hipGetLastError());
     return OJASX_OK;
 }
