@@ -100,8 +100,8 @@ OJASX_API void ojasx_destroy_linear(OjasxLinearHandle handle);
 
 /* Device variant of ref.h:72-78 (no reference counterpart): x [batch][in],
  * y [batch][out] in HBM, dtype OJASX_DTYPE_F32 or _BF16 for both, enqueued on
- * stream (a hipStream_t; NULL = default stream).  block_dim 16: below 13
- * tokens one in-place LUT kernel; from 13 tokens (in_features <= 65535, fp32
+ * stream (a hipStream_t; NULL = default stream).  block_dim 16: below 9
+ * tokens one in-place LUT kernel; from 9 tokens (in_features <= 65535, fp32
  * x 16-byte aligned) x . W^T on fp32 MFMA with W decoded from the codes. */
 OJASX_API int ojasx_linear_forward_device(OjasxLinearHandle handle, const void *x, void *y,
                                           int batch_size, int dtype, void *stream);

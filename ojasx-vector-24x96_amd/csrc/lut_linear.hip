@@ -709,9 +709,10 @@ int launch(Linear *L, const void *x, void *y, int B, hipStream_t st) {
 }
 
 // From this many tokens the block_dim-16 linear runs as x . W^T on MFMA:
-// measured (2560->6912, fp32) 19.3 vs 23.2 us at 14 tokens, 23.1 vs 39.6 at
-// 32; at 12 the in-place LUT kernel is faster (18.6 vs 19.4 us).
-constexpr int kMmMinBatch = 13;
+// measured (2560->6912, fp32) 17.0 vs 18.7 us at 10 tokens, 17.1 vs 23.7 at
+// 16, 22.8 vs 39.6 at 32; at 8 the in-place LUT kernel is faster (14.1 vs
+// 17.0 us).
+constexpr int kMmMinBatch = 9;
 
 int forward(Linear *L, const void *x, void *y, int B, int dtype, hipStream_t st) {
     if (B <= 0) return OJASX_OK;

@@ -39,15 +39,18 @@
 namespace ojx {
 
 namespace {
-constexpr int kQ = 4;            // waves splitting each slice's 16 groups
 constexpr int kMmTok = 16;       // tokens per workgroup
 constexpr int kXStride = 260;    // floats per staged x row (256 + pad)
 constexpr int kOutPass = 3;      // outlier candidates per row per pass
 typedef float v4f __attribute__((ext_vector_type(4)));
 
-// RT row tiles per workgroup.
+// RT row tiles per workgroup, each split over kQ waves (16 / kQ groups of
+// every slice per wave): 8 with one tile per workgroup (small batches, where
+// the waves are few), 4 otherwise.
 template <int RT>
 struct MmShape {
+    static constexpr int kQ = RT == 1 ? 8 : 4;
+    static constexpr int kGPW = 16 / kQ;            // groups per wave per slice
     static constexpr int kNT = 64 * kQ * RT;        // threads
     static constexpr int kRows = 16 * RT;           // rows
     static constexpr int kXF = kMmTok * 256 / kNT;  // x floats staged per thread per slice
@@ -61,7 +64,7 @@ struct MmShape {
     static constexpr int kCsr = kNT;
     // waves per SIMD the register budget is cut for: 3 workgroups per CU
     // (LDS) up to 2 row tiles, 2 at 4 row tiles
-    static constexpr int kWaves = RT == 1 ? 3 : RT == 2 ? 6 : 8;
+    static constexpr int kWaves = RT == 1 ? 5 : RT == 2 ? 6 : 8;
 };
 }  // namespace
 
@@ -102,21 +105,26 @@ __device__ __forceinline__ void mm_store_x(const MmParams &p, int n0, int s, flo
                   : make_float4(0.f, 0.f, 0.f, 0.f);
 }
 
+// Codes of groups GPW q .. GPW q + GPW - 1 of slice s for a row, as one word.
+template <int GPW>
 __device__ __forceinline__ uint32_t mm_codes(const MmParams &p, int s, int row, int q) {
-    return gld(reinterpret_cast<const uint32_t *>(p.codes + ((size_t)s * p.Mp + row) * 16 + 4 * q));
+    const uint8_t *src = p.codes + ((size_t)s * p.Mp + row) * 16 + GPW * q;
+    if constexpr (GPW == 4) return gld(reinterpret_cast<const uint32_t *>(src));
+    else return gld(reinterpret_cast<const unsigned short *>(src));
 }
 
 template <typename T, int RT>
 __global__ __launch_bounds__(MmShape<RT>::kNT) __attribute__((amdgpu_waves_per_eu(MmShape<RT>::kWaves))) void lut_mm_kernel(MmParams p) {
     using Sh = MmShape<RT>;
     constexpr int NT = Sh::kNT, XF = Sh::kXF, NC = Sh::kCsr, PX = Sh::kPX, PF = Sh::kPF;
+    constexpr int kQ = Sh::kQ, GPW = Sh::kGPW;
     static_assert(PF % PX == 0, "the unrolled slice body covers both rings");
     __shared__ float4 cb4[256 * 4];                 // codebook [256][16]
     __shared__ __align__(16) float xs[2][kMmTok * kXStride];   // staged x slices; the quarter sums at the end
     __shared__ unsigned short lcol[NC];             // the workgroup's CSR outliers
     __shared__ float lval[NC];
-    static_assert(RT * ((kQ - 1) * 64 * 4 + kQ * 64) <= 2 * kMmTok * kXStride,
-                  "quarter and outlier sums fit the x buffers");
+    static_assert(RT * ((kQ - 1) * 64 * 4 + 4 * 64) <= 2 * kMmTok * kXStride,
+                  "partial and outlier sums fit the x buffers");
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int rt = w / kQ, q = w % kQ;              // row tile, input quarter
     const int ml = lane & 15, kk = lane >> 4;
@@ -124,7 +132,8 @@ __global__ __launch_bounds__(MmShape<RT>::kNT) __attribute__((amdgpu_waves_per_e
     const int m0 = mb + rt * 16;
     const int n0 = blockIdx.y * kMmTok;
     const int row = min(m0 + ml, p.M - 1);          // rows past M: computed, never stored
-    const int mo = m0 + 4 * kk + q;                 // the lane's outlier row (one per quarter wave)
+    const int mo = m0 + 4 * kk + q;                 // the lane's outlier row (waves q < 4)
+    const bool outw = q < 4;
 
     // ---- round trip 1: codebook, x slices 0 .. PX, the CSR range of the rows, codes
     static_assert(1024 % NT == 0, "the codebook is staged in whole float4 rounds");
@@ -142,11 +151,11 @@ __global__ __launch_bounds__(MmShape<RT>::kNT) __attribute__((amdgpu_waves_per_e
         e_lo = gld(p.rowp + mb);
         e_hi = gld(p.rowp + min(mb + Sh::kRows, p.M));
         j = gld(p.rowp + min(mo, p.M - 1));
-        je = mo < p.M ? gld(p.rowp + mo + 1) : j;
+        je = outw && mo < p.M ? gld(p.rowp + mo + 1) : j;
     }
     uint32_t cr[PF];   // codes of slices s .. s + PF - 1, slot (s % PF)
 #pragma unroll
-    for (int u = 0; u < PF; ++u) cr[u] = mm_codes(p, min(u, p.S - 1), row, q);
+    for (int u = 0; u < PF; ++u) cr[u] = mm_codes<GPW>(p, min(u, p.S - 1), row, q);
     // ---- round trip 2: the CSR entries of the workgroup's rows into LDS when
     // they fit (the usual case: each row's entries sorted by column are then
     // added slice by slice from the staged x), else from memory at the end
@@ -179,10 +188,10 @@ __global__ __launch_bounds__(MmShape<RT>::kNT) __attribute__((amdgpu_waves_per_e
     // load in flight); the last S % PF slices follow it.
     auto slice = [&](const int s, const int u) __attribute__((always_inline)) {
         const float *xt = xs[s & 1] + ml * kXStride;
-        const float *xb = xt + 4 * kk + 64 * q;
+        const float *xb = xt + 4 * kk + 16 * GPW * q;
         const uint32_t cw = cr[u];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+        for (int i = 0; i < GPW; ++i) {
             const uint32_t code = (cw >> (8 * i)) & 0xffu;
             const float4 a = cb4[code * 4 + kk];
             const float4 b = *reinterpret_cast<const float4 *>(xb + 16 * i);
@@ -196,7 +205,7 @@ __global__ __launch_bounds__(MmShape<RT>::kNT) __attribute__((amdgpu_waves_per_e
         // kOutPass candidates per pass, the reads of a pass in flight together
         // (one pass covers a slice unless the row has more than kOutPass
         // entries in it); added in column order
-        if (p.rowp && staged) {
+        if (outw && p.rowp && staged) {
             const int lim = (s + 1) * 256;
             bool more = true;
             while (more) {
@@ -226,7 +235,7 @@ __global__ __launch_bounds__(MmShape<RT>::kNT) __attribute__((amdgpu_waves_per_e
         const int slot = (u + 1) % PX;
         mm_store_x<XF>(p, n0, min(s + 1, p.S - 1), xs[(s + 1) & 1], xr[slot]);
         mm_load_x<T, XF>(p, n0, min(s + 1 + PX, p.S - 1), xr[slot]);
-        cr[u] = mm_codes(p, min(s + PF, p.S - 1), row, q);
+        cr[u] = mm_codes<GPW>(p, min(s + PF, p.S - 1), row, q);
         __syncthreads();   // slice s + 1 staged; slice s's reads done before it is overwritten
     };
     int s0 = 0;
@@ -241,17 +250,17 @@ __global__ __launch_bounds__(MmShape<RT>::kNT) __attribute__((amdgpu_waves_per_e
     // ---- a dense-outlier block: the row's entries and x from memory
     const int n = n0 + ml;
     const T *xn = static_cast<const T *>(p.x) + (size_t)min(n, p.B - 1) * p.K;
-    if (p.rowp && !staged && n < p.B)
+    if (p.rowp && !staged && n < p.B && outw)
         for (int e = j; e < je; ++e) o += gld(p.val + e_lo + e) * load_act(xn, gld(p.col + e_lo + e));
 
-    // ---- the quarter sums and outlier sums of each tile through LDS (the x
-    // buffers are free: the last slice ended with a barrier); quarter 0 adds
-    // the quarter sums in order
+    // ---- the partial sums and outlier sums of each tile through LDS (the x
+    // buffers are free: the last slice ended with a barrier); wave 0 of the
+    // tile adds the partial sums in wave order
     float4 *red = reinterpret_cast<float4 *>(&xs[0][0]);                 // [RT][kQ - 1][64]
-    float *ored = &xs[0][0] + RT * (kQ - 1) * 64 * 4;                    // [RT][kQ][64]
+    float *ored = &xs[0][0] + RT * (kQ - 1) * 64 * 4;                    // [RT][4][64]
     const v4f part = acc0 + acc1;
     if (q > 0) red[(rt * (kQ - 1) + q - 1) * 64 + lane] = make_float4(part[0], part[1], part[2], part[3]);
-    ored[(rt * kQ + q) * 64 + lane] = o;
+    if (outw) ored[(rt * 4 + q) * 64 + lane] = o;
     __syncthreads();
     if (q > 0) return;
     float sum[4] = {part[0], part[1], part[2], part[3]};
@@ -273,7 +282,7 @@ __global__ __launch_bounds__(MmShape<RT>::kNT) __attribute__((amdgpu_waves_per_e
         if (m >= p.M) continue;
         float yv = sum[v] * gld(p.scales + m);
         if (p.bias) yv += gld(p.bias + m);
-        store_act(yn, (size_t)m, yv + ored[(rt * kQ + v) * 64 + lane]);
+        store_act(yn, (size_t)m, yv + ored[(rt * 4 + v) * 64 + lane]);
     }
 }
 
