@@ -325,9 +325,10 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(HO ? 8 : 1
 #pragma unroll
     for (int i = 0; i < RPL; ++i)
         cw[i] = *reinterpret_cast<const uint4 *>(p.codes + ((size_t)w * p.Mp + base + r + 16 * i) * kGS);
+    // the epilogue thread of (row tid % R, token tid / R) when tid < R * BT
     float sc = 0.f, bs = 0.f;
-    if (tid < R) {
-        const int mm = min(base + tid, p.M - 1);
+    if (tid < R * BT) {
+        const int mm = min(base + tid % R, p.M - 1);
         sc = p.scales[mm];
         bs = p.bias ? p.bias[mm] : 0.f;
     }
@@ -488,17 +489,17 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(HO ? 8 : 1
             }
         }
     __syncthreads();
-    if (tid >= R) return;
-    const int m = base + tid;
-    if (m >= p.M) return;
+    // ---- epilogue: one thread per (row, token), the waves' partials summed in
+    // wave order (a launch has at least 64 threads; R * BT may be more)
     T *y = static_cast<T *>(p.y);
-#pragma unroll
-    for (int t = 0; t < BT; ++t) {
-        if (t >= nt) break;
+    for (int e = tid; e < R * BT; e += nthr) {
+        const int rr = e % R, t = e / R;
+        const int m = base + rr;
+        if (t >= nt || m >= p.M) continue;
         float a = 0.f, o = 0.f;
         for (int k = 0; k < NW; ++k) {
-            a += part[0][k][tid][t];
-            o += part[1][k][tid][t];
+            a += part[0][k][rr][t];
+            o += part[1][k][rr][t];
         }
         if constexpr (PRO == kProRms) {
             float q = 0.f;
@@ -507,8 +508,9 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(HO ? 8 : 1
             a *= rn;
             o *= rn;
         }
-        float v = a * sc;
-        if (p.bias) v += bs;
+        const float scm = e < nthr ? sc : p.scales[m];
+        float v = a * scm;
+        if (p.bias) v += e < nthr ? bs : p.bias[m];
         v += o;
         const size_t yi = (size_t)(t0 + t) * p.M + m;
         if constexpr (RES) v = p.res[yi] + v;
@@ -644,11 +646,17 @@ template <typename T>
 int try_dec(Linear *L, const void *x, void *y, int B, hipStream_t st, const Fuse &f = Fuse{}) {
     const size_t align = sizeof(T) == 4 ? 16 : 8;
     if (L->D != 16 || (reinterpret_cast<uintptr_t>(x) % align)) return 1;
-    int bt = B >= 3 ? 4 : B;
+    // tokens per workgroup: all of them up to 8 (the codebook staged and the
+    // codes read once per row block), fewer where the staged x does not fit
+    // the LDS beside the per-wave partials (2 x 16 waves x 32 rows x bt floats)
+    int bt = B >= 5 ? 8 : B >= 3 ? 4 : B;
     const size_t xrow = (size_t)L->S * 256 * sizeof(float);
-    while (bt > 1 && kCB * 16 * sizeof(float) + bt * xrow > kMaxLds) bt /= 2;
+    auto lds_of = [&](int b) {
+        return kCB * 16 * sizeof(float) + b * xrow + (size_t)(2 * 16 * 32 + 16) * b * sizeof(float);
+    };
+    while (bt > 1 && lds_of(bt) > kMaxLds) bt /= 2;
+    if (lds_of(bt) > kMaxLds) return 1;
     const size_t lds = kCB * 16 * sizeof(float) + bt * xrow;
-    if (lds > kMaxLds) return 1;
     // 32-row workgroups when that still gives about one workgroup per CU
     const long wg32 = (long)((L->M + 31) / 32) * ((B + bt - 1) / bt);
     const bool r2 = wg32 >= 192;
@@ -658,7 +666,9 @@ int try_dec(Linear *L, const void *x, void *y, int B, hipStream_t st, const Fuse
         case 4: return launch_dec<T, 2, 1>(L, x, y, B, lds, st, f);
         case 5: return launch_dec<T, 2, 2>(L, x, y, B, lds, st, f);
         case 8: return launch_dec<T, 4, 1>(L, x, y, B, lds, st, f);
-        default: return launch_dec<T, 4, 2>(L, x, y, B, lds, st, f);
+        case 9: return launch_dec<T, 4, 2>(L, x, y, B, lds, st, f);
+        case 16: return launch_dec<T, 8, 1>(L, x, y, B, lds, st, f);
+        default: return launch_dec<T, 8, 2>(L, x, y, B, lds, st, f);
     }
 }
 
