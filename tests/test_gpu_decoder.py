@@ -100,10 +100,13 @@ def oracle_check_step(pkg, decoder, weights, cfg, pos, x_emb, dense):
     return logits
 
 
-def test_decoder_matches_oracle_and_graph_replay(pkg, dev):
+@pytest.mark.parametrize("context", [70, 0, 63, 64])
+def test_decoder_matches_oracle_and_graph_replay(pkg, dev, context):
+    """Three steps from `context` cached tokens: two 64-token chunks (70), the
+    new token alone (0), a step onto a chunk boundary (63 -> 64) and one
+    starting at it (64: the chunk holding the new token has no cached token)."""
     dec = pkg.decoder
     cfg = dec.DecoderConfig(**SMALL)
-    context = 70                                   # two 64-token decode chunks
     d, weights = dec.synthetic_decoder(cfg, context=context, seed=11, device=dev,
                                        keep_weights=True)
     emb = weights["embedding"]
@@ -123,7 +126,8 @@ def test_decoder_matches_oracle_and_graph_replay(pkg, dev):
     # the same three steps as one generate call, eager and graph: identical
     for use_graph in (False, True, True):
         for l, w in enumerate(weights["layers"]):
-            d.set_context(l, w["k_codes"], w["k_scales"], w["v_codes"], w["v_scales"], context)
+            if context:
+                d.set_context(l, w["k_codes"], w["k_scales"], w["v_codes"], w["v_scales"], context)
         d.reset(context)
         toks, logits = d.generate(7, 3, use_graph=use_graph, return_logits=True)
         assert toks.tolist() == eager_tokens, use_graph
