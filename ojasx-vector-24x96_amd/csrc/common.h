@@ -73,6 +73,9 @@ struct GroupItem {
     int K, M, Mp, S;
 };
 int linear_items(const void *h, GroupItem *it);
+// One tall batch-1 fp32 linear with the RMSNorm prologue (lut_group.hip):
+// it.x / it.y set, w the norm weight; both 16-byte aligned.
+int launch_tall_rms(const GroupItem &it, const float *w, float eps, hipStream_t st);
 
 // The block_dim-16 linear for many tokens on MFMA (lut_mm.hip): x [B][K] in
 // dtype (fp32 16-byte aligned, or bf16), y [B][M] in dtype.

@@ -110,6 +110,120 @@ __global__ __launch_bounds__(kGNT) __attribute__((amdgpu_waves_per_eu(6))) void 
     }
 }
 
+// One tall batch-1 fp32 linear with the RMSNorm prologue (a decoder's gate/up
+// and LM head): y[m] = ((s_m * r * sum_g LUT[g, code]) + bias_m) + r * outliers,
+// r = 1 / sqrt(mean(x^2) + eps), with the LUT built from x * w (r factors out of
+// the linear map, as in lut_dec_kernel's prologue).  Workgroup = 256 rows, one
+// per thread, on the shared slice loop with two LUT buffers (few workgroups
+// per CU: the build of slice s + 1 runs beside the gathers of s) and two
+// slices of codes in flight.  For tall matrices this builds each LUT slice once
+// per 256 rows instead of computing 64 bytes of codebook per code byte in
+// place.
+namespace {
+constexpr int kTNT = 256;               // threads, one row each
+constexpr int kTPF = 2;                 // slices of codes in flight
+}  // namespace
+
+__global__ __launch_bounds__(kTNT) void lut_tall_rms_kernel(GroupItem it, const float *w, float eps) {
+    __shared__ float L[slices::lut_bytes(true) / sizeof(float)];
+    extern __shared__ float xs[];                     // [S * 256]: x * w, zero past K
+    __shared__ float red[kTNT / 64];
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int base = (int)blockIdx.x * kTNT;
+    const int S = it.S, KS = S * 256, nx4 = KS / 4;
+    const bool outl = it.rowp != nullptr;
+    // ---- round trip 1: x and w (L2), the codebook operands, the row's CSR
+    //      range, scale and bias, then the codes of the first slices (HBM)
+    float4 xv[4], wv4[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        const int e = min(tid + u * kTNT, nx4 - 1) * 4;
+        xv[u] = gld(reinterpret_cast<const float4 *>(it.x + min(e, it.K - 4)));
+        wv4[u] = gld(reinterpret_cast<const float4 *>(w + min(e, it.K - 4)));
+    }
+    float bop[4][4];
+    slices::load_cb_operands<4>(it.cb, wv, lane, bop);
+    const int m = base + tid;
+    const int mc = min(m, it.M - 1);
+    int j0 = 0, j1 = 0;
+    if (outl) {
+        j0 = gld(it.rowp + mc);
+        j1 = gld(it.rowp + mc + 1);
+    }
+    const float sc = gld(it.scales + mc);
+    const float bs = it.bias ? gld(it.bias + mc) : 0.f;
+    int row[1] = {min(m, it.Mp - 1)};                 // rows past M: loaded, never stored
+    uint4 ring[kTPF][1];
+    slices::ring_start(it.codes, row, it.Mp, 0, S, ring);
+    // ---- x * w into LDS and the sum of x^2 (each element once)
+    float ss = 0.f;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        const int i = tid + u * kTNT;
+        if (i < nx4) {
+            const bool in = i * 4 < it.K;
+            const float4 v = in ? xv[u] : make_float4(0.f, 0.f, 0.f, 0.f);
+            ss += fmaf(v.w, v.w, fmaf(v.z, v.z, fmaf(v.y, v.y, v.x * v.x)));
+            reinterpret_cast<float4 *>(xs)[i] =
+                make_float4(v.x * wv4[u].x, v.y * wv4[u].y, v.z * wv4[u].z, v.w * wv4[u].w);
+        }
+    }
+    for (int i = tid + 4 * kTNT; i < nx4; i += kTNT) {   // K > 4096: the rest of x
+        const int e = i * 4;
+        float4 v = make_float4(0.f, 0.f, 0.f, 0.f), g = v;
+        if (e < it.K) {
+            v = gld(reinterpret_cast<const float4 *>(it.x + e));
+            g = gld(reinterpret_cast<const float4 *>(w + e));
+        }
+        ss += fmaf(v.w, v.w, fmaf(v.z, v.z, fmaf(v.y, v.y, v.x * v.x)));
+        reinterpret_cast<float4 *>(xs)[i] = make_float4(v.x * g.x, v.y * g.y, v.z * g.z, v.w * g.w);
+    }
+    ss = wave_sum_f(ss);
+    if (lane == 0) red[wv] = ss;
+    __syncthreads();
+    const float rn = 1.0f / sqrtf(((red[0] + red[1]) + (red[2] + red[3])) / (float)it.K + eps);
+
+    float acc[1] = {0.f};
+    slices::slice_loop<4, 1, true, kTPF>(xs, L, bop, it.codes, row, it.Mp, 0, S, wv, lane, ring, acc);
+
+    // ---- epilogue: ((r * sum) * s_m + bias) + r * outliers (4 loads in flight)
+    if (m >= it.M) return;
+    float o = 0.f;
+    if (outl) {
+        int j = j0;
+        for (; j + 4 <= j1; j += 4) {
+            int c[4];
+            float v[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                c[u] = gld(it.col + j + u);
+                v[u] = gld(it.val + j + u);
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) o += v[u] * xs[c[u]];
+        }
+        for (; j < j1; ++j) o += gld(it.val + j) * xs[gld(it.col + j)];
+    }
+    float y = (acc[0] * rn) * sc;
+    if (it.bias) y += bs;
+    it.y[m] = y + o * rn;
+}
+
+int launch_tall_rms(const GroupItem &it, const float *w, float eps, hipStream_t st) {
+    if ((reinterpret_cast<uintptr_t>(it.x) | reinterpret_cast<uintptr_t>(w)) & 15) {
+        set_error("tall linear: 16-byte aligned x and norm weight needed");
+        return OJASX_ERR_INVALID;
+    }
+    const size_t lds = (size_t)it.S * 256 * sizeof(float);
+    static size_t granted = 0;
+    int rc = ensure_dyn_lds(reinterpret_cast<const void *>(&lut_tall_rms_kernel),
+                            lds + slices::lut_bytes(true), &granted);
+    if (rc) return rc;
+    OJX_LAUNCH(lut_tall_rms_kernel, dim3((it.M + kTNT - 1) / kTNT), dim3(kTNT), lds, st, it, w, eps);
+    OJX_HIP(hipGetLastError());
+    return OJASX_OK;
+}
+
 // Per host thread: the staged item array.
 struct GroupWork {
     DevBuf items;

@@ -789,6 +789,13 @@ int linear_shape(const void *h, int *K, int *M, int *D) {
     return OJASX_OK;
 }
 
+// From this many output rows a batch-1 RMSNorm linear (no residual) runs on
+// lut_tall_rms_kernel: MFMA-built LUT slices, one build per 256 rows (an LM
+// head of 151936 rows: measured about 15 vs 37 us).  Below it the in-place
+// kernel is faster: each tall workgroup runs a chain of slices, and 19456
+// rows (76 workgroups) took 11.8 vs 11.3 us.
+constexpr int kTallMinRows = 65536;
+
 int linear_forward_fused(void *h, const float *x, float *y, int pro, const float *w, float eps,
                          const float *res, hipStream_t st) {
     Linear *L = static_cast<Linear *>(h);
@@ -800,6 +807,15 @@ int linear_forward_fused(void *h, const float *x, float *y, int pro, const float
     if (L->K % 4 || (pro == kProRms && (reinterpret_cast<uintptr_t>(w) & 15))) {
         set_error("fused linear: in_features %% 4 == 0 and a 16-byte aligned norm weight needed");
         return OJASX_ERR_INVALID;
+    }
+    if (pro == kProRms && !res && L->D == 16 && L->M >= kTallMinRows &&
+        !(reinterpret_cast<uintptr_t>(x) & 15)) {
+        GroupItem it{};
+        int rc = linear_items(h, &it);
+        if (rc) return rc;
+        it.x = x;
+        it.y = y;
+        return launch_tall_rms(it, w, eps, st);
     }
     Fuse f;
     f.pro = pro;

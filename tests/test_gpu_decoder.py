@@ -33,7 +33,11 @@ def make_linear(pkg, r, M, K, density=0.0038, scales="u"):
 
 @pytest.mark.parametrize("M,K,pro,res", [(700, 2560, 1, False), (300, 9728, 2, True),
                                          (2560, 4096, 0, True), (97, 512, 1, True),
-                                         (64, 9728, 2, False)])
+                                         (64, 9728, 2, False),
+                                         # tall RMSNorm linears (MFMA-built LUT slices):
+                                         # ragged rows; x longer than the first staging pass
+                                         (65600, 2560, 1, False), (65536, 5120, 1, False),
+                                         (65600, 512, 1, True)])   # with a residual: in place
 def test_fused_linear(pkg, dev, M, K, pro, res):
     import torch
     r = np.random.default_rng(M + K + pro)
