@@ -9,25 +9,26 @@
 // (64 bytes per group and row, decoded in registers from the codebook in
 // LDS).
 //
-// A wave computes one 16-row x 16-token tile over a quarter of the input: of
-// every 256-wide input slice (16 groups) wave q of a row tile takes groups
-// 4q .. 4q + 3, 4 MFMAs (v_mfma_f32_16x16x4f32) per group with
+// A wave computes one 16-row x 16-token tile over part of the input: the kQ
+// waves of a row tile split every 256-wide input slice (16 groups), wave q
+// taking groups GPW q .. GPW q + GPW - 1 (GPW = 16 / kQ; kQ = 8 with one tile
+// per workgroup, 4 otherwise), 4 MFMAs (v_mfma_f32_16x16x4f32) per group with
 //   A[m][k] = C[code(m, g)][4k + ks]   (one 16-byte LDS read of the codebook row),
 //   B[k][n] = x_n[16g + 4k + ks]       (one 16-byte LDS read of the staged x),
 // for ks = 0..3: MFMA ks covers dims 4k + ks of the group, so a lane's four
 // values are contiguous in both the codebook row and x.  Two accumulators
-// (even and odd groups) keep the MFMA chains independent.  The four quarter
-// sums of a tile meet in LDS at the end, added in quarter order.  Splitting
-// the input four ways gives four times the waves of a one-wave-per-tile
-// layout.  A workgroup holds RT row tiles (4 RT waves) of the same 16 tokens,
-// sharing the codebook and the staged x slices: two LDS buffers, and the x
-// loads kept Sh::kPX slices ahead in a register ring (a slice's 16 MFMAs per
-// wave are far shorter than a load's round trip); codes Sh::kPF slices ahead.
+// (even and odd groups) keep the MFMA chains independent.  The partial sums
+// of a tile meet in LDS at the end, added in wave order.  Splitting the input
+// gives kQ times the waves of a one-wave-per-tile layout.  A workgroup holds
+// RT row tiles (kQ RT waves) of the same 16 tokens, sharing the codebook and
+// the staged x slices: two LDS buffers, and the x loads kept Sh::kPX slices
+// ahead in a register ring (a slice's MFMAs per wave are far shorter than a
+// load's round trip); codes Sh::kPF slices ahead.
 //
-// The CSR outliers of the workgroup's rows are staged in LDS; wave q of a
+// The CSR outliers of the workgroup's rows are staged in LDS; wave q < 4 of a
 // tile adds those of row 4 (lane / 16) + q whose columns fall in the current
 // slice from the staged x (a row's entries are sorted by column), so no x is
-// read at random from memory; the outlier sums meet in LDS with the quarter
+// read at random from memory; the outlier sums meet in LDS with the partial
 // sums.  The epilogue applies the scale and the bias:
 // (s_m * sum + bias) + outliers.
 //
@@ -126,7 +127,7 @@ __global__ __launch_bounds__(MmShape<RT>::kNT) __attribute__((amdgpu_waves_per_e
     static_assert(RT * ((kQ - 1) * 64 * 4 + 4 * 64) <= 2 * kMmTok * kXStride,
                   "partial and outlier sums fit the x buffers");
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    const int rt = w / kQ, q = w % kQ;              // row tile, input quarter
+    const int rt = w / kQ, q = w % kQ;              // row tile, input part
     const int ml = lane & 15, kk = lane >> 4;
     const int mb = blockIdx.x * Sh::kRows;
     const int m0 = mb + rt * 16;
