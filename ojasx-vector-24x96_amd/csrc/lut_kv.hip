@@ -823,7 +823,7 @@ int kv_decode(const float *q, const uint8_t *kc, const float *ks, const uint8_t 
                 if (rc) return rc;
             }
             KVParams p{q, kc, vc, ks, vs, kcb, vcb, bt, wk.o.as<float>(), wk.ml.as<float>(), out, T, P,
-                       Hq, Hkv, hd, D, G, kSmallC, 4, n_chunks, sf};
+                       Hq, Hkv, hd, D, G, kSmallC, 4, n_chunks, sf, nullptr, 0};
             OJX_LAUNCH(kv_decode_small_kernel<1>, dim3(n_chunks, Hkv, nz), dim3(kNT), 0, st, p);
             if (n_chunks > 1)
                 OJX_LAUNCH(kv_merge_kernel, dim3(Hq), dim3(kNT), (size_t)n_chunks * 4, st,
@@ -845,7 +845,7 @@ int kv_decode(const float *q, const uint8_t *kc, const float *ks, const uint8_t 
             if (rc) return rc;
         }
         KVParams p{q, kc, vc, ks, vs, kcb, vcb, bt, wk.o.as<float>(), wk.ml.as<float>(), out, T, P,
-                   Hq, Hkv, hd, D, G, (int)C, 4, n_chunks, sf};
+                   Hq, Hkv, hd, D, G, (int)C, 4, n_chunks, sf, nullptr, 0};
         const size_t lds = (size_t)(4 * 128 + 256 * 16 + 4 * 8 * 256) * 4 + (size_t)kWideNT * 16 +
                            (size_t)kWideNT * 8 + (size_t)16 * 32 * 16 * 4;
         static size_t gw = 0;
@@ -871,7 +871,7 @@ int kv_decode(const float *q, const uint8_t *kc, const float *ks, const uint8_t 
         if (rc) return rc;
     }
     KVParams p{q, kc, vc, ks, vs, kcb, vcb, bt, wk.o.as<float>(), wk.ml.as<float>(), out, T, P,
-               Hq, Hkv, hd, D, G, kNT, RS, n_chunks, sf};
+               Hq, Hkv, hd, D, G, kNT, RS, n_chunks, sf, nullptr, 0};
     const size_t lds = ((size_t)RS * hd + 256 * D + (size_t)RS * G * 256) * 4 + (size_t)RS * G * kHP * 4;
     static size_t g0 = 0;
     rc = ensure_dyn_lds(reinterpret_cast<const void *>(&kv_decode_chunk_kernel<0, 0, 8, 1>), lds, &g0);
