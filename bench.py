@@ -254,7 +254,7 @@ def bench_moe(pkg, torch, steps, warmup, cpu_seconds, do_cpu):
 def bench_batched(pkg, torch, steps, warmup):
     """LUT-GEMV 2560->6912 at batch 8, 16, 32 and 64,
     fp32 and bf16 activations, on 32 distinct weight instances in round robin
-    (35 MB).  From 32 tokens the call runs as x . W^T on fp32 MFMA
+    (35 MB).  From 9 tokens the call runs as x . W^T on fp32 MFMA
     (lut_mm_kernel), below that the in-place LUT kernel (lut_dec_kernel).
     Per-token code bytes are the codes of one call (1,105,920 B)."""
     gen = pkg.synthetic
