@@ -808,7 +808,11 @@ int linear_forward_fused(void *h, const float *x, float *y, int pro, const float
         set_error("fused linear: in_features %% 4 == 0 and a 16-byte aligned norm weight needed");
         return OJASX_ERR_INVALID;
     }
-    if (pro == kProRms && !res && L->D == 16 && L->M >= kTallMinRows &&
+    // (the tall kernel stages x * w beside two LUT buffers: it fits the LDS up
+    // to about 31000 inputs)
+    const bool tall_fits = (size_t)L->S * 256 * sizeof(float) + 2 * 16 * 260 * sizeof(float) +
+                               64 <= kMaxLds;
+    if (pro == kProRms && !res && L->D == 16 && L->M >= kTallMinRows && tall_fits &&
         !(reinterpret_cast<uintptr_t>(x) & 15)) {
         GroupItem it{};
         int rc = linear_items(h, &it);
