@@ -409,9 +409,18 @@ struct Decoder {
     hipGraphExec_t exec = nullptr;
     bool ready_layers = false, ready_head = false;
 
-    ~Decoder() {
+    // The captured step holds the device pointers of every linear handle and
+    // buffer it launched on; replacing a handle makes it stale, so the next
+    // generate with use_graph captures again.
+    void drop_graph() {
         if (exec) (void)hipGraphExecDestroy(exec);
         if (graph) (void)hipGraphDestroy(graph);
+        exec = nullptr;
+        graph = nullptr;
+    }
+
+    ~Decoder() {
+        drop_graph();
         if (stream) (void)hipStreamDestroy(stream);
         for (DecoderLayer &l : L)
             for (DevBuf *b : {&l.in_norm, &l.post_norm, &l.q_norm, &l.k_norm, &l.kcb, &l.vcb, &l.kc,
@@ -588,6 +597,8 @@ OJASX_API int ojasx_decoder_set_layer(OjasxDecoderHandle handle, int layer,
         return OJASX_ERR_NULL;
     Decoder *d = static_cast<Decoder *>(handle);
     if (layer < 0 || layer >= d->layers) return OJASX_ERR_HEAD;
+    OJX_HIP(hipStreamSynchronize(d->stream));
+    d->drop_graph();
     const int qd = d->Hq * kHd, kvd = d->Hkv * kHd;
     int rc = check_linear(qkv, d->hidden, qd + 2 * kvd, "qkv");
     if (!rc) rc = check_linear(o, qd, d->hidden, "o");
@@ -619,6 +630,8 @@ OJASX_API int ojasx_decoder_set_head(OjasxDecoderHandle handle, OjasxLinearHandl
     Decoder *d = static_cast<Decoder *>(handle);
     int rc = check_linear(lm_head, d->hidden, d->vocab, "lm_head");
     if (rc) return rc;
+    OJX_HIP(hipStreamSynchronize(d->stream));
+    d->drop_graph();
     d->lm = lm_head;
     rc = copy_d2d(d->final_norm, final_norm, (size_t)d->hidden * 4);
     if (!rc) rc = copy_d2d(d->emb, embedding, (size_t)d->vocab * d->hidden * 4);

@@ -160,3 +160,33 @@ def test_decoder_errors(pkg, dev):
     with pytest.raises(pkg.OjasxError, match="position"):
         d.reset(96)
     d.close()
+
+
+def test_decoder_graph_recaptured_after_layer_swap(pkg, dev):
+    """A captured step holds the linear handles' device pointers: after
+    set_layer / set_head replace handles, graph generation must follow the
+    new weights (the decoder drops its graph and captures again)."""
+    dec = pkg.decoder
+    cfg = dec.DecoderConfig(**SMALL)
+    d, _ = dec.synthetic_decoder(cfg, context=20, seed=5, device=dev)
+    _, before = d.generate(7, 2, use_graph=True, return_logits=True)     # captures
+    r = np.random.default_rng(99)
+    qd, kvd = cfg.q_heads * 128, cfg.kv_heads * 128
+    shapes = ((qd + 2 * kvd, cfg.hidden), (cfg.hidden, qd), (2 * cfg.intermediate, cfg.hidden),
+              (cfg.hidden, cfg.intermediate))
+    lins = [dec._linear(r, M, K, 0.05, 0.0038, 0.05, False)[0] for M, K in shapes]
+    norms = [r.uniform(0.8, 1.2, size=n).astype(np.float32)
+             for n in (cfg.hidden, cfg.hidden, 128, 128)]
+    cbs = [r.normal(0, 40, size=(cfg.kv_heads, 256, 16)).astype(np.float32) for _ in range(2)]
+    d.set_layer(1, *lins, *norms, *cbs)
+    lm = dec._linear(r, cfg.vocab, cfg.hidden, 0.05, 0.0038, 0.05, False)[0]
+    d.set_head(lm, np.ones(cfg.hidden, np.float32),
+               r.normal(size=(cfg.vocab, cfg.hidden)).astype(np.float32))
+    res = {}
+    for use_graph in (False, True, True):
+        d.reset(20)
+        res[use_graph] = d.generate(7, 2, use_graph=use_graph, return_logits=True)
+    assert res[True][0].tolist() == res[False][0].tolist()
+    assert np.array_equal(res[True][1], res[False][1])
+    assert not np.array_equal(res[True][1], before)
+    d.close()
