@@ -160,6 +160,24 @@ OJASX_API int ojasx_kv_decode_paged_device(const float *q, const uint8_t *k_code
                                            int num_kv_heads, int head_dim, int block_dim,
                                            float scale_factor, float *out, void *stream);
 
+/* No counterpart in the reference: ojasx_kv_decode_paged_device for callers
+ * that cannot allocate device memory (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc).  Same arguments, kernels
+ * and results; the decode partials live in a fixed library scratch of
+ * 4 MiB + 64 KiB per GPU (held until the process ends) instead of a growable
+ * workspace, so num_q_heads x chunks (chunks = ceil(seq_len / 64) up to 4096
+ * tokens, at most 256 beyond) is limited to 4 MiB / (head_dim * 4 bytes):
+ * 8192 at head_dim 128.  Larger calls return OJASX_ERR_INVALID with a
+ * message.  All calls on one GPU share the scratch: calls that overlap in
+ * time on one GPU (other streams, other host threads) race. */
+OJASX_API int ojasx_kv_decode_paged_device_noalloc(const float *q, const uint8_t *k_codes,
+                                                   const float *k_scales, const uint8_t *v_codes,
+                                                   const float *v_scales, const float *k_cb,
+                                                   const float *v_cb, const int *block_table,
+                                                   int seq_len, int page_size, int num_q_heads,
+                                                   int num_kv_heads, int head_dim, int block_dim,
+                                                   float scale_factor, float *out, void *stream);
+
 /* Device append into the paged code layout above; replaces
  * HeadKVCache::append_token (ojasx_lut_kv_cache.cpp:16-65, ref.h:103-108) for
  * num_tokens tokens and all kv heads in one call.

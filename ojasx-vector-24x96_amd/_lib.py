@@ -43,6 +43,8 @@ SIGNATURES = {
     "ojasx_destroy_kv_cache": (None, [vp]),
     "ojasx_kv_decode_paged_device": (ci, [vp, vp, vp, vp, vp, vp, vp, vp, ci, ci, ci, ci, ci,
                                           ci, cf, vp, vp]),
+    "ojasx_kv_decode_paged_device_noalloc": (ci, [vp, vp, vp, vp, vp, vp, vp, vp, ci, ci, ci, ci,
+                                                  ci, ci, cf, vp, vp]),
     "ojasx_kv_decode_paged_device_len": (ci, [vp, vp, vp, vp, vp, vp, vp, vp, vp, ci, ci, ci, ci,
                                               ci, ci, cf, ci, vp, vp]),
     "ojasx_create_moe": (vp, [ci, ci, ci, ci, ci, vp, vp, vp, vp, vp, vp]),

@@ -37,6 +37,7 @@
 // [pages][Hkv][page] fp32, so a page of one kv head is contiguous.
 #include <algorithm>
 #include <cmath>
+#include <mutex>
 #include <vector>
 
 #include "common.h"
@@ -725,16 +726,49 @@ __global__ __launch_bounds__(kNT) void kv_merge_kernel(const float *part_o, cons
     }
 }
 
-// Workspace for the decode partials, one per thread of the host (device
-// entry points called from several host threads each get their own).
+// Workspace for the decode partials (part_o, part_ml), one per thread of the
+// host (device entry points called from several host threads each get their
+// own).  reserve() grows the buffers and sets po / pml; a workspace built on
+// fixed memory (fixed_o, non-null) never allocates and refuses a request
+// beyond its capacity instead.
 struct KVWork {
     DevBuf o, ml;
+    float *po = nullptr, *pml = nullptr;
+    float *fixed_o = nullptr, *fixed_ml = nullptr;
+    size_t fixed_o_bytes = 0, fixed_ml_bytes = 0;
+    int reserve(size_t o_bytes, size_t ml_bytes) {
+        if (fixed_o) {
+            if (o_bytes > fixed_o_bytes || ml_bytes > fixed_ml_bytes) {
+                set_error("decode partials need %zu + %zu bytes; the no-allocation scratch holds "
+                          "%zu + %zu (num_q_heads x chunks too large)",
+                          o_bytes, ml_bytes, fixed_o_bytes, fixed_ml_bytes);
+                return OJASX_ERR_INVALID;
+            }
+            po = fixed_o;
+            pml = fixed_ml;
+            return OJASX_OK;
+        }
+        int rc = o.ensure(o_bytes);
+        if (!rc) rc = ml.ensure(ml_bytes);
+        if (rc) return rc;
+        po = o.as<float>();
+        pml = ml.as<float>();
+        return OJASX_OK;
+    }
     ~KVWork() {
         o.release();
         ml.release();
     }
 };
 static thread_local KVWork t_work;
+
+// Scratch of the no-allocation decode (ojasx_kv_decode_paged_device_noalloc):
+// partial outputs [Hq][chunks][hd] fp32 in the first kScratchO bytes, then
+// partial (max, sum) pairs [Hq][chunks][2].  Every GPU holds its own copy
+// until the process ends; its device address is looked up once per device.
+constexpr size_t kScratchO = (size_t)4 << 20;
+constexpr size_t kScratchML = (size_t)64 << 10;
+static __device__ __align__(256) unsigned char scratch[kScratchO + kScratchML];
 
 // Decode with the context length read on the device (*len_dev + len_add, at
 // most T_max): the short-context kernel over ceil(T_max / 64) chunks, the
@@ -818,16 +852,15 @@ int kv_decode(const float *q, const uint8_t *kc, const float *ks, const uint8_t 
         if (T <= kSmallMaxT) {
             const int n_chunks = (T + kSmallC - 1) / kSmallC;
             if (n_chunks > 1) {
-                int rc = wk.o.ensure((size_t)Hq * n_chunks * hd * 4);
-                if (!rc) rc = wk.ml.ensure((size_t)Hq * n_chunks * 2 * 4);
+                const int rc = wk.reserve((size_t)Hq * n_chunks * hd * 4, (size_t)Hq * n_chunks * 2 * 4);
                 if (rc) return rc;
             }
-            KVParams p{q, kc, vc, ks, vs, kcb, vcb, bt, wk.o.as<float>(), wk.ml.as<float>(), out, T, P,
+            KVParams p{q, kc, vc, ks, vs, kcb, vcb, bt, wk.po, wk.pml, out, T, P,
                        Hq, Hkv, hd, D, G, kSmallC, 4, n_chunks, sf, nullptr, 0};
             OJX_LAUNCH(kv_decode_small_kernel<1>, dim3(n_chunks, Hkv, nz), dim3(kNT), 0, st, p);
             if (n_chunks > 1)
                 OJX_LAUNCH(kv_merge_kernel, dim3(Hq), dim3(kNT), (size_t)n_chunks * 4, st,
-                           wk.o.as<float>(), wk.ml.as<float>(), n_chunks, hd, out, nullptr, 0, 1, 0);
+                           wk.po, wk.pml, n_chunks, hd, out, nullptr, 0, 1, 0);
             OJX_HIP(hipGetLastError());
             return OJASX_OK;
         }
@@ -840,11 +873,10 @@ int kv_decode(const float *q, const uint8_t *kc, const float *ks, const uint8_t 
         if (T <= 1024 && units <= 16) C = std::max<long>(64, pow2(T));
         const int n_chunks = (int)((T + C - 1) / C);
         if (n_chunks > 1) {
-            int rc = wk.o.ensure((size_t)Hq * n_chunks * hd * 4);
-            if (!rc) rc = wk.ml.ensure((size_t)Hq * n_chunks * 2 * 4);
+            const int rc = wk.reserve((size_t)Hq * n_chunks * hd * 4, (size_t)Hq * n_chunks * 2 * 4);
             if (rc) return rc;
         }
-        KVParams p{q, kc, vc, ks, vs, kcb, vcb, bt, wk.o.as<float>(), wk.ml.as<float>(), out, T, P,
+        KVParams p{q, kc, vc, ks, vs, kcb, vcb, bt, wk.po, wk.pml, out, T, P,
                    Hq, Hkv, hd, D, G, (int)C, 4, n_chunks, sf, nullptr, 0};
         const size_t lds = (size_t)(4 * 128 + 256 * 16 + 4 * 8 * 256) * 4 + (size_t)kWideNT * 16 +
                            (size_t)kWideNT * 8 + (size_t)16 * 32 * 16 * 4;
@@ -854,7 +886,7 @@ int kv_decode(const float *q, const uint8_t *kc, const float *ks, const uint8_t 
         OJX_LAUNCH(kv_decode_wide_kernel, dim3(n_chunks, Hkv, nz), dim3(kWideNT), lds, st, p);
         if (n_chunks > 1)
             OJX_LAUNCH(kv_merge_kernel, dim3(Hq), dim3(kNT), (size_t)n_chunks * 4, st,
-                       wk.o.as<float>(), wk.ml.as<float>(), n_chunks, hd, out, nullptr, 0, 1, 0);
+                       wk.po, wk.pml, n_chunks, hd, out, nullptr, 0, 1, 0);
         OJX_HIP(hipGetLastError());
         return OJASX_OK;
     }
@@ -866,11 +898,10 @@ int kv_decode(const float *q, const uint8_t *kc, const float *ks, const uint8_t 
     const int n_chunks = (T + kNT - 1) / kNT;
     int rc = OJASX_OK;
     if (n_chunks > 1) {
-        rc = wk.o.ensure((size_t)Hq * n_chunks * hd * 4);
-        if (!rc) rc = wk.ml.ensure((size_t)Hq * n_chunks * 2 * 4);
+        rc = wk.reserve((size_t)Hq * n_chunks * hd * 4, (size_t)Hq * n_chunks * 2 * 4);
         if (rc) return rc;
     }
-    KVParams p{q, kc, vc, ks, vs, kcb, vcb, bt, wk.o.as<float>(), wk.ml.as<float>(), out, T, P,
+    KVParams p{q, kc, vc, ks, vs, kcb, vcb, bt, wk.po, wk.pml, out, T, P,
                Hq, Hkv, hd, D, G, kNT, RS, n_chunks, sf, nullptr, 0};
     const size_t lds = ((size_t)RS * hd + 256 * D + (size_t)RS * G * 256) * 4 + (size_t)RS * G * kHP * 4;
     static size_t g0 = 0;
@@ -880,11 +911,33 @@ int kv_decode(const float *q, const uint8_t *kc, const float *ks, const uint8_t 
     const int nch = p.n_chunks;
     if (nch > 1)
         OJX_LAUNCH(kv_merge_kernel, dim3(Hq), dim3(kNT), (size_t)nch * 4, st,
-                           wk.o.as<float>(), wk.ml.as<float>(), nch, hd, out, nullptr, 0, 1, 0);
+                           wk.po, wk.pml, nch, hd, out, nullptr, 0, 1, 0);
     OJX_HIP(hipGetLastError());
     return OJASX_OK;
 }
 
+
+// Device address of `scratch` on the current device, looked up once per
+// device with that device current (host code must never pass the array's
+// name itself: on the host it is only a stand-in for the symbol).
+static int scratch_address(unsigned char **out) {
+    static std::mutex mu;
+    static unsigned char *addr[64] = {};
+    int dev = 0;
+    OJX_HIP(hipGetDevice(&dev));
+    if (dev < 0 || dev >= 64) {
+        set_error("no-allocation scratch: device %d out of range", dev);
+        return OJASX_ERR_INVALID;
+    }
+    std::lock_guard<std::mutex> lock(mu);
+    if (!addr[dev]) {
+        void *p = nullptr;
+        OJX_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        addr[dev] = static_cast<unsigned char *>(p);
+    }
+    *out = addr[dev];
+    return OJASX_OK;
+}
 
 // ---- reference-API KV cache: one code stream per head ---------------------
 struct KVHead {
@@ -1061,6 +1114,30 @@ OJASX_API int ojasx_kv_decode_paged_device(const float *q, const uint8_t *k_code
                      static_cast<hipStream_t>(stream), t_work);
 }
 
+OJASX_API int ojasx_kv_decode_paged_device_noalloc(const float *q, const uint8_t *k_codes,
+                                                   const float *k_scales, const uint8_t *v_codes,
+                                                   const float *v_scales, const float *k_cb,
+                                                   const float *v_cb, const int *block_table,
+                                                   int seq_len, int page_size, int num_q_heads,
+                                                   int num_kv_heads, int head_dim, int block_dim,
+                                                   float scale_factor, float *out, void *stream) {
+    using namespace ojx;
+    if (!q || !k_codes || !k_scales || !v_codes || !v_scales || !k_cb || !v_cb || !block_table ||
+        !out)
+        return OJASX_ERR_NULL;
+    unsigned char *base = nullptr;
+    const int rc = scratch_address(&base);
+    if (rc) return rc;
+    KVWork wk;   // no DevBuf is touched: reserve() hands out the scratch only
+    wk.fixed_o = reinterpret_cast<float *>(base);
+    wk.fixed_ml = reinterpret_cast<float *>(base + kScratchO);
+    wk.fixed_o_bytes = kScratchO;
+    wk.fixed_ml_bytes = kScratchML;
+    return kv_decode(q, k_codes, k_scales, v_codes, v_scales, k_cb, v_cb, block_table, seq_len,
+                     page_size, num_q_heads, num_kv_heads, head_dim, block_dim, scale_factor, out,
+                     static_cast<hipStream_t>(stream), wk);
+}
+
 OJASX_API int ojasx_kv_decode_paged_device_len(const float *q, const uint8_t *k_codes,
                                                const float *k_scales, const uint8_t *v_codes,
                                                const float *v_scales, const float *k_cb,
@@ -1087,13 +1164,12 @@ OJASX_API int ojasx_kv_decode_paged_device_len(const float *q, const uint8_t *k_
         return OJASX_ERR_INVALID;
     }
     const int n = kv_device_len_chunks(max_seq_len, tokens_per_lane);
-    int rc = t_work.o.ensure((size_t)num_q_heads * n * 128 * 4);
-    if (!rc) rc = t_work.ml.ensure((size_t)num_q_heads * n * 2 * 4);
+    const int rc = t_work.reserve((size_t)num_q_heads * n * 128 * 4, (size_t)num_q_heads * n * 2 * 4);
     if (rc) return rc;
     if (scale_factor <= 0.f) scale_factor = 1.0f / sqrtf(128.f);
     return kv_decode_device_len(q, k_codes, k_scales, v_codes, v_scales, k_cb, v_cb, block_table,
                                 seq_len_dev, 0, max_seq_len, page_size, num_q_heads, num_kv_heads,
-                                scale_factor, t_work.o.as<float>(), t_work.ml.as<float>(), out,
+                                scale_factor, t_work.po, t_work.pml, out,
                                 static_cast<hipStream_t>(stream), tokens_per_lane);
 }
 
