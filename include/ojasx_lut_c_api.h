@@ -222,7 +222,10 @@ OJASX_API int ojasx_dequantize_int8_device(const int8_t *q, const void *scale_f1
  * max_seq_len (block_table holds ceil(max_seq_len / page_size) entries).  head_dim 128, block_dim 16, 16-byte aligned q and codebooks.
  * Chunks of 64 * tokens_per_lane tokens (1, 2 or 4; 0 picks by max_seq_len).
  * Workspace as ojasx_kv_decode_paged_device: call once outside a capture with
- * the same max_seq_len before capturing. */
+ * the same max_seq_len before capturing.  A later call that needs a larger
+ * workspace moves to a new one and keeps the old until the host thread exits,
+ * so graphs captured before stay valid; calls from one host thread on several
+ * streams share the workspace and must not overlap in time. */
 OJASX_API int ojasx_kv_decode_paged_device_len(const float *q, const uint8_t *k_codes,
                                                const float *k_scales, const uint8_t *v_codes,
                                                const float *v_scales, const float *k_cb,

@@ -748,16 +748,32 @@ struct KVWork {
             pml = fixed_ml;
             return OJASX_OK;
         }
-        int rc = o.ensure(o_bytes);
-        if (!rc) rc = ml.ensure(ml_bytes);
+        int rc = grow(o, o_bytes);
+        if (!rc) rc = grow(ml, ml_bytes);
         if (rc) return rc;
         po = o.as<float>();
         pml = ml.as<float>();
         return OJASX_OK;
     }
+    // A buffer that grows is retired, not freed, until the thread exits: a
+    // graph captured over an earlier (smaller) call still owns valid memory.
+    // Growth at least doubles, so the retired buffers total less than the
+    // live one.
+    std::vector<DevBuf> retired;
+    int grow(DevBuf &b, size_t n) {
+        if (n <= b.bytes && b.ptr) return OJASX_OK;
+        if (b.ptr) {
+            retired.push_back(b);
+            n = std::max(n, 2 * b.bytes);
+            b.ptr = nullptr;
+            b.bytes = 0;
+        }
+        return b.ensure(n);
+    }
     ~KVWork() {
         o.release();
         ml.release();
+        for (DevBuf &b : retired) b.release();
     }
 };
 static thread_local KVWork t_work;

@@ -828,7 +828,14 @@ int linear_forward_fused(void *h, const float *x, float *y, int pro, const float
     f.res = res;
     const int rc = try_dec<float>(L, x, y, 1, st, f);
     if (rc == 1) {
-        set_error("fused linear: block_dim 16 and a 16-byte aligned x needed");
+        if (L->D == 16 && !(reinterpret_cast<uintptr_t>(x) & 15))
+            set_error("fused linear: in_features %d does not fit the LDS: the staged input and "
+                      "codebook need %zu bytes, %zu available",
+                      L->K, kCB * 16 * sizeof(float) + (size_t)L->S * 256 * sizeof(float) +
+                                (size_t)(2 * 16 * 32 + 16) * sizeof(float),
+                      kMaxLds);
+        else
+            set_error("fused linear: block_dim 16 and a 16-byte aligned x needed");
         return OJASX_ERR_INVALID;
     }
     return rc;

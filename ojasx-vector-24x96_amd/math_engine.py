@@ -37,12 +37,24 @@ def _require_gpu(t, what):
         raise RuntimeError(f"{what}: the LUT engine runs on the GPU only (got a {t.device} tensor)")
 
 
+def _packed_geometry(shape, block: int, bits: int):
+    """(codes per row, total codes, packed bytes per stage) of a rows x columns
+    weight cut into block-wide vectors, one ``bits``-wide code each."""
+    rows, cols = shape
+    per_row = -(-cols // block)
+    count = rows * per_row
+    return per_row, count, -(-count * bits // 8)
+
+
 @dataclass
 class QuantizedWeight:
-    """Portable encoded representation of one rank-two weight matrix
-    (codec.py:77-174): ``stages`` residual stages, each a packed stream of
-    ``rows * ceil(columns / block_size)`` codes of ``bits_per_stage`` bits and a
-    ``[2^bits, block_size]`` fp32 codebook, plus fp32 row scales."""
+    """Encoded rank-two weight of the residual-VQ codec (ojasx_24x96/codec.py:77-174):
+    ``codebooks[s]`` is stage s's ``[2^bits, block_size]`` fp32 codebook,
+    ``packed_codes[s]`` its codes (one per ``block_size``-wide vector of a row,
+    rows in order, ``bits_per_stage`` bits each, little-endian within bytes),
+    ``row_scales`` the fp32 scale of every row.  Field names, properties and
+    exception types (ValueError for shapes, widths and devices, TypeError for
+    storage dtypes, IndexError for stage and code ranges) are the reference's."""
 
     original_shape: Tuple[int, int]
     block_size: int
@@ -54,34 +66,35 @@ class QuantizedWeight:
 
     def __post_init__(self) -> None:
         torch = _torch()
-        if len(self.original_shape) != 2:
-            raise ValueError("Only rank-two weights are supported")
+        shape = tuple(self.original_shape)
+        if len(shape) != 2 or min(shape) < 0:
+            raise ValueError(f"QuantizedWeight encodes a rank-two weight with nonnegative "
+                             f"dimensions, not shape {shape}")
         if self.bits_per_stage not in _SUPPORTED_WIDTHS:
-            raise ValueError("Unsupported code width")
-        if self.packed_codes.dtype != torch.uint8:
-            raise TypeError("packed_codes must be uint8")
-        if self.codebooks.dtype != torch.float32 or self.row_scales.dtype != torch.float32:
-            raise TypeError("Codebooks and scales use float32 storage")
-        if self.packed_codes.device != self.codebooks.device or (
-                self.packed_codes.device != self.row_scales.device):
-            raise ValueError("All encoded tensors must be on one device")
-        rows, columns = self.original_shape
-        if rows < 0 or columns < 0:
-            raise ValueError("Weight dimensions must be nonnegative")
-        blocks_per_row = (columns + self.block_size - 1) // self.block_size
-        vectors = rows * blocks_per_row
-        if self.codebooks.ndim != 3:
-            raise ValueError("Codebooks must be a rank-three tensor")
-        stages = self.codebooks.shape[0]
-        if stages < 1:
-            raise ValueError("An encoded weight requires at least one residual stage")
-        expected_packed = (vectors * self.bits_per_stage + 7) // 8
-        if tuple(self.codebooks.shape[1:]) != (1 << self.bits_per_stage, self.block_size):
-            raise ValueError("Codebook shape is inconsistent with the codec")
-        if tuple(self.packed_codes.shape) != (stages, expected_packed):
-            raise ValueError("Packed-code shape is inconsistent with the weight shape")
-        if tuple(self.row_scales.shape) != (rows,):
-            raise ValueError("Row-scale shape is inconsistent with the weight shape")
+            raise ValueError(f"code width {self.bits_per_stage} is not one of "
+                             f"{_SUPPORTED_WIDTHS}")
+        # storage dtypes first (TypeError), then one device, then the shapes
+        for name, want in (("packed_codes", torch.uint8), ("codebooks", torch.float32),
+                           ("row_scales", torch.float32)):
+            got = getattr(self, name).dtype
+            if got != want:
+                raise TypeError(f"{name} is stored as {got}; the codec stores {want}")
+        devices = {t.device for t in (self.packed_codes, self.codebooks, self.row_scales)}
+        if len(devices) != 1:
+            raise ValueError(f"encoded tensors span several devices: {sorted(map(str, devices))}")
+        if self.codebooks.ndim != 3 or self.codebooks.shape[0] < 1:
+            raise ValueError(f"codebooks must be [stages >= 1, 2^bits, block_size], got "
+                             f"{tuple(self.codebooks.shape)}")
+        _, _, nbytes = _packed_geometry(shape, self.block_size, self.bits_per_stage)
+        expected = {"codebooks": (self.stages, 1 << self.bits_per_stage, self.block_size),
+                    "packed_codes": (self.stages, nbytes),
+                    "row_scales": (shape[0],)}
+        for name, want in expected.items():
+            got = tuple(getattr(self, name).shape)
+            if got != want:
+                raise ValueError(f"{name} has shape {got}; a {shape[0]} x {shape[1]} weight with "
+                                 f"block {self.block_size} and {self.bits_per_stage}-bit codes "
+                                 f"needs {want}")
 
     @property
     def stages(self) -> int:
@@ -89,17 +102,16 @@ class QuantizedWeight:
 
     @property
     def blocks_per_row(self) -> int:
-        return (self.original_shape[1] + self.block_size - 1) // self.block_size
+        return _packed_geometry(self.original_shape, self.block_size, self.bits_per_stage)[0]
 
     @property
     def vector_count(self) -> int:
-        return self.original_shape[0] * self.blocks_per_row
+        return _packed_geometry(self.original_shape, self.block_size, self.bits_per_stage)[1]
 
     @property
     def storage_bytes(self) -> int:
-        return (self.packed_codes.numel()
-                + self.codebooks.numel() * self.codebooks.element_size()
-                + self.row_scales.numel() * self.row_scales.element_size())
+        return sum(t.numel() * t.element_size()
+                   for t in (self.packed_codes, self.codebooks, self.row_scales))
 
     @property
     def nominal_bits_per_weight(self) -> float:
@@ -107,31 +119,35 @@ class QuantizedWeight:
 
     @property
     def measured_bits_per_weight(self) -> float:
-        elements = self.original_shape[0] * self.original_shape[1]
-        return 8.0 * self.storage_bytes / elements if elements else 0.0
+        rows, cols = self.original_shape
+        return 8.0 * self.storage_bytes / (rows * cols) if rows * cols else 0.0
+
+    def _stage(self, stage: int) -> int:
+        if stage < 0 or stage >= self.stages:
+            raise IndexError(f"stage {stage} outside [0, {self.stages})")
+        return stage
 
     def codes(self, stage: int):
-        if not 0 <= stage < self.stages:
-            raise IndexError("Invalid residual stage")
-        return unpack_codes(self.packed_codes[stage], self.bits_per_stage, self.vector_count)
+        """All codes of one stage, uint8, in vector order."""
+        return unpack_codes(self.packed_codes[self._stage(stage)], self.bits_per_stage,
+                            self.vector_count)
 
     def codes_range(self, stage: int, start: int, count: int):
-        """Unpack a bounded logical code range, including unaligned bit offsets."""
+        """Codes start .. start + count - 1 of one stage.  A byte holds
+        8 / bits whole codes, so only the bytes covering the range are
+        unpacked and the codes before ``start`` in its first byte dropped."""
         torch = _torch()
-        if not 0 <= stage < self.stages:
-            raise IndexError("Invalid residual stage")
+        s = self._stage(stage)
         if start < 0 or count < 0 or start + count > self.vector_count:
-            raise IndexError("Invalid logical code range")
+            raise IndexError(f"code range [{start}, {start + count}) outside "
+                             f"[0, {self.vector_count})")
         if count == 0:
             return torch.empty(0, dtype=torch.uint8, device=self.packed_codes.device)
-        bits = self.bits_per_stage
-        per_byte = 8 // bits
-        first_byte = (start * bits) // 8
-        final_byte = ((start + count) * bits + 7) // 8
-        window = self.packed_codes[stage, first_byte:final_byte]
-        window_codes = unpack_codes(window, bits, window.numel() * per_byte)
-        offset = start - first_byte * per_byte
-        return window_codes[offset:offset + count]
+        per = 8 // self.bits_per_stage
+        lo, hi = start // per, -(-(start + count) // per)
+        unpacked = unpack_codes(self.packed_codes[s, lo:hi], self.bits_per_stage, (hi - lo) * per)
+        skip = start - lo * per
+        return unpacked[skip:skip + count]
 
 
 def pack_codes(codes, bits: int):

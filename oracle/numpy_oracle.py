@@ -300,15 +300,59 @@ def lut_dense(w):
     return dequantize(w["codebook"], w["codes"], np.ones(w["codes"].shape[0]), csr=w["csr"])
 
 
-def decoder_step(x, weights, cfg, pos, caches, dense=None):
+def engine_forward_rows(x, codebook, codes, scales=None, csr=None, bias=None, row_block=4096):
+    """SplitManifoldLUTLinear.forward for one token in fp64 without a dense
+    matrix (split_manifold_engine.py:202-250): LUT[g, k] = <x_g, C[k]>, then
+    y_m = s_m * sum_g LUT[g, codes[m, g]] + sum_j val_j * x[col_j] (+ bias),
+    gathered ``row_block`` rows at a time so [M, G] fp64 never materialises."""
+    x = np.asarray(x, np.float64).reshape(-1)
+    cb = np.asarray(codebook, np.float64)
+    d = cb.shape[1]
+    lut = x.reshape(-1, d) @ cb.T                           # [G, 256]
+    M, G = codes.shape
+    gi = np.arange(G)[None, :]
+    y = np.empty(M, np.float64)
+    for r0 in range(0, M, row_block):
+        blk = np.asarray(codes[r0:r0 + row_block]).astype(np.intp)
+        y[r0:r0 + blk.shape[0]] = lut[gi, blk].sum(axis=1)
+    if scales is not None:
+        y *= np.asarray(scales, np.float64)
+    if csr is not None and np.asarray(csr[2]).size:
+        rp, cl, vl = csr
+        rows = np.repeat(np.arange(M), np.diff(np.asarray(rp, np.int64)))
+        y += np.bincount(rows, weights=x[np.asarray(cl, np.int64)] * np.asarray(vl, np.float64),
+                         minlength=M)
+    if bias is not None:
+        y += np.asarray(bias, np.float64)
+    return y
+
+
+class LUTOp:
+    """A LUT linear {codebook, codes, csr} with unit scales that applies as
+    ``op @ x`` through engine_forward_rows: the decoder oracle's linear at
+    sizes where a dense fp64 matrix would not fit in memory."""
+
+    def __init__(self, w):
+        self.w = w
+
+    def __matmul__(self, x):
+        w = self.w
+        return engine_forward_rows(x, w["codebook"], w["codes"], None, w["csr"])
+
+
+def decoder_step(x, weights, cfg, pos, caches, dense=None, linear="dense"):
     """One greedy step of the LUT decoder in fp64 from the residual x (the
     token's embedding row) at position `pos`.  caches[l] = (kc, ks, vc, vs)
     holds every layer's code cache for tokens 0..pos in the paged layout with
     the identity block table, including the new token's codes (written by the
-    step under test).  Returns (logits, new_kv) with new_kv[l] = (k_rot, v) of
+    step under test).  ``linear`` = "dense" applies each LUT linear as its
+    dense fp64 matrix, "lut" through engine_forward_rows (same values to fp64
+    rounding, for shapes whose dense matrices would not fit in memory).
+    Returns (logits, new_kv) with new_kv[l] = (k_rot, v) of
     the new token per kv head, for checking its codes."""
     hd, Hq, Hkv = cfg.head_dim, cfg.q_heads, cfg.kv_heads
     R = Hq // Hkv
+    make = lut_dense if linear == "dense" else LUTOp
     cos, sin = rope_tables(pos + 1, hd, cfg.rope_theta)
     dense = dense if dense is not None else {}
     x = np.asarray(x, np.float64)
@@ -318,7 +362,7 @@ def decoder_step(x, weights, cfg, pos, caches, dense=None):
         W = {k: dense.get((l, k)) for k in ("qkv", "o", "gate_up", "down")}
         for k in W:
             if W[k] is None:
-                W[k] = dense[(l, k)] = lut_dense(w[k])
+                W[k] = dense[(l, k)] = make(w[k])
         h = rmsnorm(x, w["input_norm"], cfg.rms_eps)
         qkv = W["qkv"] @ h
         q = qkv[:Hq * hd].reshape(Hq, hd)
@@ -346,7 +390,7 @@ def decoder_step(x, weights, cfg, pos, caches, dense=None):
         x = x + W["down"] @ a
     Wl = dense.get("lm")
     if Wl is None:
-        Wl = dense["lm"] = lut_dense(weights["lm_head"])
+        Wl = dense["lm"] = make(weights["lm_head"])
     logits = Wl @ rmsnorm(x, weights["final_norm"], cfg.rms_eps)
     return logits, new_kv
 

@@ -81,3 +81,57 @@ def test_decoder_config_validation(pkg):
                             intermediate=128, vocab=10, max_context=32)
     with pytest.raises(RuntimeError, match="head_dim must be 128"):
         dec.LUTDecoder(bad, device="cpu")
+
+
+def _lut_linear(r, M, K, density=0.01):
+    from oracle import gen
+    return dict(codebook=r.normal(0, 0.1, size=(256, 16)).astype(np.float32),
+                codes=r.integers(0, 256, size=(M, K // 16), dtype=np.uint8),
+                csr=gen.csr_outliers(r, M, K, density))
+
+
+def test_engine_forward_rows_equals_dense():
+    """The row-blocked fp64 LUT gather equals the dense x . W^T (the identity
+    LUT-gather = x . W^T), across row blocks, with scales, CSR and bias; an
+    off-by-one code (planted) is far outside the bar."""
+    r = np.random.default_rng(5)
+    for M, K, blk in ((300, 256, 64), (1000, 4096, 4096), (77, 48, 10)):
+        w = _lut_linear(r, M, K)
+        sc = r.uniform(0.5, 1.5, size=M)
+        bias = r.normal(size=M)
+        x = r.normal(size=K)
+        got = no.engine_forward_rows(x, w["codebook"], w["codes"], sc, w["csr"], bias, blk)
+        want = no.linear_fp64(x, w["codebook"], w["codes"], sc, bias, w["csr"])[0]
+        assert np.allclose(got, want, rtol=1e-12, atol=1e-12 * np.abs(want).max())
+        assert np.allclose(no.LUTOp(w) @ x, no.lut_dense(w) @ x, rtol=1e-12,
+                           atol=1e-12 * np.abs(want).max())
+        bad = dict(w, codes=(w["codes"].astype(np.int64) + 1).astype(np.uint8) % 255)
+        assert np.abs(no.LUTOp(bad) @ x - no.lut_dense(w) @ x).max() > 1e-3 * np.abs(want).max()
+
+
+def test_decoder_step_lut_equals_dense():
+    class C:
+        head_dim, q_heads, kv_heads, rms_eps, rope_theta = 128, 4, 2, 1e-6, 1e6
+
+    r = np.random.default_rng(6)
+    hid, inter, T = 64, 96, 40
+    layers = []
+    caches = []
+    for _ in range(2):
+        layers.append(dict(qkv=_lut_linear(r, 8 * 128, hid), o=_lut_linear(r, hid, 512),
+                           gate_up=_lut_linear(r, 2 * inter, hid), down=_lut_linear(r, hid, inter),
+                           input_norm=r.uniform(0.8, 1.2, hid), post_norm=r.uniform(0.8, 1.2, hid),
+                           q_norm=r.uniform(0.8, 1.2, 128), k_norm=r.uniform(0.8, 1.2, 128),
+                           k_codebook=r.normal(size=(2, 256, 16)),
+                           v_codebook=r.normal(size=(2, 256, 16))))
+        kc = r.integers(0, 256, size=(3, 2, 16, 8), dtype=np.uint8)
+        vc = r.integers(0, 256, size=(3, 2, 16, 8), dtype=np.uint8)
+        caches.append((kc, r.uniform(0.01, 0.03, size=(3, 2, 16)), vc,
+                       r.uniform(0.01, 0.03, size=(3, 2, 16))))
+    weights = dict(layers=layers, lm_head=_lut_linear(r, 50, hid), final_norm=np.ones(hid))
+    x = r.normal(size=hid)
+    a, kv_a = no.decoder_step(x, weights, C, T - 1, caches)
+    b, kv_b = no.decoder_step(x, weights, C, T - 1, caches, linear="lut")
+    assert np.allclose(a, b, rtol=1e-10, atol=1e-10 * np.abs(a).max())
+    for (ka, va), (kb, vb) in zip(kv_a, kv_b):
+        assert np.allclose(ka, kb, rtol=1e-10) and np.allclose(va, vb, rtol=1e-10)

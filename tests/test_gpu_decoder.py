@@ -63,6 +63,43 @@ def test_fused_linear(pkg, dev, M, K, pro, res):
     assert rel_err(out.cpu().numpy(), want) < 1e-5
 
 
+def test_fused_linear_tall_beyond_tall_kernel_lds(pkg, dev):
+    """A tall RMSNorm linear whose input is too long for the tall kernel's LDS
+    (x * w staged beside two LUT buffers: about 31000 inputs) runs on the
+    in-place kernel instead: 65536 rows x 32768 inputs against the fp64 LUT
+    gather (no dense matrix); one past the in-place kernel's LDS is refused
+    with the LDS sizes named."""
+    import torch
+    r = np.random.default_rng(65536)
+    M, K = 65536, 32768
+    cb = r.normal(0, 0.05, size=(256, 16)).astype(np.float32)
+    codes = r.integers(0, 256, size=(M, K // 16), dtype=np.uint8)
+    sc = r.uniform(0.5, 1.5, size=M).astype(np.float32)
+    csr = pkg.synthetic.csr_outliers(r, M, K, 2e-5)
+    lin = pkg.native.NativeSplitManifoldLinear(K, M, 16, 256)
+    lin.initialize_weights(cb, codes, sc)
+    lin.set_outliers(*csr)
+    xin = r.normal(size=K).astype(np.float32) * 3.0
+    w = r.uniform(0.5, 1.5, size=K).astype(np.float32)
+    x_t = torch.from_numpy(xin).to(dev)
+    w_t = torch.from_numpy(w).to(dev)
+    out = torch.empty(M, device=dev)
+    L = pkg.lib()
+    rc = L.ojasx_linear_forward_fused_device(lin.handle, vp(x_t), vp(out), 1, vp(w_t), 1e-6,
+                                             None, None)
+    assert rc == 0, L.ojasx_get_last_error()
+    torch.cuda.synchronize()
+    want = no.engine_forward_rows(no.rmsnorm(xin.astype(np.float64), w, 1e-6), cb, codes, sc, csr)
+    assert rel_err(out.cpu().numpy(), want) < 1e-5
+    big, _ = make_linear(pkg, r, 64, 40960)
+    xb = torch.zeros(40960, device=dev)
+    wb = torch.ones(40960, device=dev)
+    yb = torch.zeros(64, device=dev)
+    assert L.ojasx_linear_forward_fused_device(big.handle, vp(xb), vp(yb), 1, vp(wb), 1e-6, None,
+                                               None) == -3
+    assert b"does not fit the LDS" in L.ojasx_get_last_error()
+
+
 def test_fused_linear_errors(pkg, dev):
     import torch
     r = np.random.default_rng(3)
@@ -79,10 +116,10 @@ SMALL = dict(hidden=256, layers=2, q_heads=4, kv_heads=2, head_dim=128, intermed
              vocab=500, max_context=96, page_size=16, max_steps=8, rms_eps=1e-6, rope_theta=1e6)
 
 
-def oracle_check_step(pkg, decoder, weights, cfg, pos, x_emb, dense):
+def oracle_check_step(pkg, decoder, weights, cfg, pos, x_emb, dense, linear="dense"):
     """Compare the decoder state after the step at `pos` with the oracle step."""
     caches = [decoder.read_kv(l, 0, pos + 1) for l in range(cfg.layers)]
-    logits, new_kv = no.decoder_step(x_emb, weights, cfg, pos, caches, dense)
+    logits, new_kv = no.decoder_step(x_emb, weights, cfg, pos, caches, dense, linear)
     pg, off = divmod(pos, cfg.page_size)
     for l in range(cfg.layers):
         kc, ks, vc, vs = caches[l]
@@ -136,6 +173,42 @@ def test_decoder_matches_oracle_and_graph_replay(pkg, dev, context):
         toks, logits = d.generate(7, 3, use_graph=use_graph, return_logits=True)
         assert toks.tolist() == eager_tokens, use_graph
         assert np.array_equal(logits, eager_logits), use_graph
+    d.close()
+
+
+@pytest.mark.timeout(600)
+def test_decoder_full_size_matches_oracle(pkg, dev):
+    """BASELINE.json configs[4] at full size: hidden 2560, 36 layers, 32 q /
+    8 kv heads, MLP 9728, vocab 151936, every linear LUT with 0.38 % CSR, a
+    4096-token code context.  One eager step, then two more in one graph
+    generate (an eager step, the capture, a replay); the first and the last
+    step are checked against the fp64 oracle step, whose linears gather from
+    the LUT in fp64 (engine_forward_rows) and whose attention reads the codes
+    the GPU wrote: logits rel <= 1e-4 after 36 layers of fp32 arithmetic,
+    tokens equal where the top-2 margin allows, new KV codes equal to the
+    oracle encoder's away from near ties."""
+    dec = pkg.decoder
+    ctx = 4096
+    cfg = dec.DecoderConfig(max_steps=4, max_context=ctx + 8)
+    print(f"full-size decoder: build, context {ctx}", flush=True)
+    d, weights = dec.synthetic_decoder(cfg, context=ctx, seed=3, device=dev, keep_weights=True)
+    emb = weights["embedding"]
+    ops = {}
+
+    def check(pos, token_in, logits, token_out):
+        want = oracle_check_step(pkg, d, weights, cfg, pos, emb[token_in], ops, linear="lut")
+        err = rel_err(logits, want)
+        print(f"full-size decoder: step at {pos}: logits rel err {err:.3e}", flush=True)
+        assert err < 1e-4, pos
+        top2 = np.sort(want)[-2:]
+        if top2[1] - top2[0] > 1e-3 * np.abs(want).max():
+            assert token_out == int(np.argmax(want)), pos
+
+    toks, logits = d.generate(1, 1, use_graph=False, return_logits=True)
+    check(ctx, 1, logits, int(toks[0]))
+    t1 = int(toks[0])
+    toks2, logits2 = d.generate(t1, 2, use_graph=True, return_logits=True)
+    check(ctx + 2, int(toks2[0]), logits2, int(toks2[1]))
     d.close()
 
 

@@ -106,6 +106,14 @@ def test_pack_unpack_bit_exact(pkg, dev, bits):
     # 7 rows x 143 blocks = 1001 codes in one stage: codes_range over unaligned bits
     enc = me.QuantizedWeight((7, 143 * bits), bits, bits, packed[None, :].clone(),
                              torch.zeros(1, 1 << bits, bits, device=dev), torch.ones(7, device=dev), {})
-    assert np.array_equal(enc.codes_range(0, 333, 100).cpu().numpy(), codes[333:433].astype(np.uint8))
+    for start, count in ((333, 100), (0, 1), (1, 7), (7, 9), (995, 6), (1000, 1), (5, 0), (0, 1001)):
+        got = enc.codes_range(0, start, count).cpu().numpy()
+        assert np.array_equal(got, codes[start:start + count].astype(np.uint8)), (start, count)
+    assert np.array_equal(enc.codes(0).cpu().numpy(), codes.astype(np.uint8))
+    for bad in ((-1, 2), (1000, 2), (3, -1)):
+        with pytest.raises(IndexError):
+            enc.codes_range(0, *bad)
+    with pytest.raises(IndexError):
+        enc.codes(1)
     with pytest.raises(ValueError, match="exceeds"):
         me.pack_codes(ct + (1 << bits), bits)
