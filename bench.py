@@ -5,8 +5,12 @@
 Workload: LUT-GEMV 2560 -> 6912 (MLP gate/up),
 batch 1, fp32 activations, d = 16 / 256 centroids, 0.38 % CSR outliers.  A
 step is one call of the fused LUT-GEMV kernel on one of N distinct weight
-instances (round robin), all resident in HBM; N is sized so the working set
-exceeds the 256 MB Infinity Cache and the codes really stream from HBM.
+instances (round robin, 262 MB at N = 160, above the 256 MB Infinity Cache).
+
+HBM residency: before every timed pass (events, kernel timing, every extra
+leg) a 512 MiB buffer is read and written, which evicts the Infinity Cache
+and the L2s, so the first N calls of a pass read their codes from HBM
+whatever K is; longer passes cycle through a working set above 256 MB.
 
 Printed: one JSON line.  ``value`` is microseconds per call (lower is
 better), measured with HIP events on the launch stream over the K timed
@@ -18,12 +22,12 @@ end on the launch stream); ``traffic`` is the HBM bytes per launch from the
 rocprofv3 FETCH_SIZE/WRITE_SIZE summary under profiles/ when present.
 ``cpu_baseline`` times the reference's own C++ engine (compiled from its
 sources into oracle/_ref when present, else the repo's C restatement) on the
-host, one thread, on the same inputs.  ``sustained`` runs the same call on
-all N instances in one grouped launch (the sustained rate).  Extra fields
-give the MoE, KV-decode, KV-append and 4B-shaped decoder figures of the same
-run.  Before the timed region one 64 MiB device-to-device copy runs: a
-kernel of known traffic that calibrates the PMC byte counters of a profiled
-run of this script.
+host, one thread, on the same inputs.  Extra fields (each with its own
+timing, roofline fraction and CPU figure where the reference has one): the
+2560 -> 2560 linear, bf16 at batch 1 and the batched linear
+(configs[1]), the grouped launch (the sustained form), the MoE layer
+(configs[2]), the KV decode and the 4B-shaped decoder
+(configs[4]), plus a measured device-to-device copy rate and the host CPU.
 """
 import argparse
 import ctypes
@@ -41,9 +45,11 @@ import numpy as np  # noqa: E402
 HBM_PEAK_GBS = 8000.0
 M_GU, K_GU = 6912, 2560
 CAL_COPY_BYTES = 64 << 20
-TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "lut_dec_kernel_2560x6912_b1_hbm_traffic.md")
-GROUP_TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles",
-                                     "lut_group_kernel_160x2560x6912_hbm_traffic.md")
+FLUSH_BYTES = 512 << 20
+PROFILES = os.path.join(ROOT, "profiles")
+TRAFFIC_SUMMARY = os.path.join(PROFILES, "lut_dec_kernel_2560x6912_b1_hbm_traffic.md")
+GROUP_TRAFFIC_SUMMARY = os.path.join(PROFILES, "lut_group_kernel_160x2560x6912_hbm_traffic.md")
+VP = ctypes.c_void_p
 
 
 def measured_traffic(path=TRAFFIC_SUMMARY):
@@ -57,17 +63,100 @@ def measured_traffic(path=TRAFFIC_SUMMARY):
         return None
 
 
-def timed_kernels(pkg, run):
-    """Run `run()` with the library's per-kernel start/stop events on and
-    return {kernel: {"calls", "avg_us"}}."""
-    pkg._lib.kernel_timing_enable(True)
+def host_info():
+    model = None
     try:
-        run()
-        rep = pkg._lib.kernel_timing_report()
-    finally:
-        pkg._lib.kernel_timing_enable(False)
-    rep.pop("_dropped", None)
-    return rep
+        with open("/proc/cpuinfo") as f:
+            m = re.search(r"model name\s*:\s*(.+)", f.read())
+            model = m.group(1).strip() if m else None
+    except OSError:
+        pass
+    try:
+        usable = len(os.sched_getaffinity(0))
+    except AttributeError:
+        usable = os.cpu_count()
+    return {"cpu_model": model, "logical_cpus": os.cpu_count(), "usable_cpus": usable}
+
+
+def cpu_threads():
+    """Threads for the multi-threaded CPU variants: the host share of one GPU
+    on the box (16), at most what this process may use."""
+    return max(1, min(16, host_info()["usable_cpus"] or 1))
+
+
+def timed_cpu(call, seconds, max_calls, warm=3):
+    """Mean seconds per call of ``call`` over at most ``seconds`` / ``max_calls``
+    after ``warm`` untimed calls (ojasx_run.cpp's steady-clock method)."""
+    for _ in range(warm):
+        call()
+    n, t0 = 0, time.perf_counter()
+    while True:
+        call()
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= seconds or n >= max_calls:
+            return el / n, n
+
+
+class Bench:
+    """Device, stream, library and the cache flush shared by every leg."""
+
+    def __init__(self, torch, pkg):
+        self.torch = torch
+        self.pkg = pkg
+        self.L = pkg.lib()
+        self.dev = torch.device("cuda:0")
+        self.stream = torch.cuda.current_stream()
+        self.sp = VP(self.stream.cuda_stream)
+        self.fbuf = torch.zeros(FLUSH_BYTES // 4, device=self.dev)
+
+    def flush(self):
+        """Read and write 512 MiB: evicts the Infinity Cache and every L2."""
+        self.fbuf.add_(1.0)
+        self.torch.cuda.synchronize()
+
+    def events_us(self, fn, n):
+        """Average µs per call of fn(i), i < n, from HIP events on the launch
+        stream, after a flush."""
+        torch = self.torch
+        self.flush()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(self.stream)
+        for i in range(n):
+            fn(i)
+        e1.record(self.stream)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1e3 / n
+
+    def kernels(self, fn, n):
+        """{kernel: {"calls", "avg_us"}} of fn(i), i < n, from the library's
+        start/stop events, after a flush."""
+        self.flush()
+        lib = self.pkg._lib
+        lib.kernel_timing_enable(True)
+        try:
+            for i in range(n):
+                fn(i)
+            rep = lib.kernel_timing_report()
+        finally:
+            lib.kernel_timing_enable(False)
+        rep.pop("_dropped", None)
+        return rep
+
+
+def roofline(code_bytes, all_bytes, kernel_us, kernel, calls, traffic=None):
+    ach = code_bytes / (kernel_us * 1e-6) / 1e9
+    return {"bound": "hbm", "achieved": round(ach, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(ach / HBM_PEAK_GBS, 5), "traffic": traffic, "kernel": kernel,
+            "kernel_avg_us": round(kernel_us, 4), "kernel_launches_timed": calls,
+            "algorithmic_bytes_per_launch": int(code_bytes),
+            "all_compulsory_bytes_per_launch": int(all_bytes),
+            "achieved_all_bytes_GBs": round(all_bytes / (kernel_us * 1e-6) / 1e9, 2),
+            "frac_all_bytes": round(all_bytes / (kernel_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 5)}
+
+
+def dominant(kern):
+    return max(kern, key=lambda k: kern[k]["calls"] * kern[k]["avg_us"])
 
 
 def parse():
@@ -79,113 +168,171 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true",
-                    help="skip the MoE, KV and decoder figures")
-    ap.add_argument("--extra", default="batched,moe,kv,decoder",
-                    help="comma-separated extra figures to run (batched, moe, kv, decoder)")
+                    help="skip every extra figure (headline only)")
+    ap.add_argument("--extra", default="copy,linear2560,bf16,batched,sustained,moe,kv,decoder",
+                    help="comma-separated extra figures to run")
     return ap.parse_args()
 
 
-def time_cpu_linear(d, seconds, y_gpu):
-    """Reference C++ engine (or the C restatement) on the host, 1 thread,
-    ojasx_run.cpp's method: 50 warm-up calls, then timed calls.  Its output on
-    the benchmarked instance is also the parity check of the GPU result
-    (``parity_rel_err``, max |GPU - CPU| / max |CPU|)."""
+# --- linear legs ------------------------------------------------------------------
+
+def make_instances(b, M, K, n, seed):
+    """n LUT-GEMV handles M x K: one seeded codebook, scales, CSR and x, codes
+    drawn per instance.  Returns (handles, base inputs, device bytes per handle)."""
+    L = b.L
+    base = b.pkg.synthetic.linear(M, K, B=64, seed=seed)
+    r = np.random.default_rng(seed + 1)
+    p = lambda a: a.ctypes.data_as(VP)
+    rp, cl, vl = base["csr"]
+    hs, wbytes = [], 0
+    for i in range(n):
+        codes = base["codes"] if i == 0 else r.integers(0, 256, size=base["codes"].shape,
+                                                        dtype=np.uint8)
+        h = L.ojasx_create_linear(K, M, 16, 256, p(base["codebook"]), p(codes),
+                                  p(base["scales"]), None)
+        assert h, L.ojasx_get_last_error()
+        assert L.ojasx_set_linear_outliers(h, vl.size, p(rp), p(cl), p(vl)) == 0
+        hs.append(h)
+        wbytes = L.ojasx_linear_device_weight_bytes(h)
+    return hs, base, wbytes
+
+
+def cpu_linear(base, B, seconds, y_gpu=None, threads=(1,)):
+    """Reference C++ engine (or the C restatement) on the host for one call of
+    B tokens: µs per call per thread count; its output on instance 0 is the
+    parity check of the GPU result (max |GPU - CPU| / max |CPU|)."""
     from oracle import ref, cpu
-    x = d["x"]
+    x = base["x"][:B]
     if ref.available():
-        R = ref.RefLinear(d["codebook"], d["codes"], d["scales"], None, d["csr"])
-        call = lambda: R.forward(x, 1)
+        R = ref.RefLinear(base["codebook"], base["codes"], base["scales"], None, base["csr"])
+        mk = lambda nt: (lambda: R.forward(x, nt))
         kind = "reference"
     else:
-        call = lambda: cpu.linear_forward(x, d["codebook"], d["codes"], d["scales"], None, *d["csr"])
+        mk = lambda nt: (lambda: cpu.linear_forward(x, base["codebook"], base["codes"],
+                                                    base["scales"], None, *base["csr"]))
         kind = "port"
-    y_cpu = np.asarray(call(), np.float64).reshape(-1)
-    rel = float(np.abs(np.asarray(y_gpu, np.float64).reshape(-1) - y_cpu).max() / np.abs(y_cpu).max())
-    for _ in range(50):
-        call()
-    n, t0 = 0, time.perf_counter()
-    while True:
-        call()
-        n += 1
-        el = time.perf_counter() - t0
-        if el > seconds or n >= 1000:
-            break
-    out = dict(value=el / n * 1e6, unit="us/call", cores=1, kind=kind,
-               sample=f"{n} calls of LUT-GEMV 2560->6912 B=1 fp32 with CSR, 1 thread, "
-                      f"after 50 warm-up calls", parity_rel_err=rel)
-    if kind == "reference":
-        # the reference's other builds and thread counts: scalar (its Makefile
-        # flags) and -march=x86-64-v3 (its AVX2 LUT build), 1 thread and the
-        # host share of this GPU (16 threads at most), 2 s each
-        threads = max(1, min(16, os.cpu_count() or 1))
-        var = {}
-        for tag, path in (("scalar", ref.LIB_SCALAR), ("avx2", ref.LIB_AVX2)):
-            if not ref.available(path):
-                continue
-            R2 = ref.RefLinear(d["codebook"], d["codes"], d["scales"], None, d["csr"], path=path)
-            for nt in sorted({1, threads}):
-                for _ in range(5):
-                    R2.forward(x, nt)
-                k, t1 = 0, time.perf_counter()
-                while time.perf_counter() - t1 < min(2.0, seconds) and k < 1000:
-                    R2.forward(x, nt)
-                    k += 1
-                var[f"{tag}_{nt}t"] = round((time.perf_counter() - t1) / k * 1e6, 2)
-        out["variants_us_per_call"] = var
-        out["variants_threads"] = threads
+        threads = (1,)
+    out = {"kind": kind, "unit": "us/call", "batch": B}
+    if y_gpu is not None:
+        y_cpu = np.asarray(mk(1)(), np.float64).reshape(-1)
+        out["parity_rel_err"] = float(np.abs(np.asarray(y_gpu, np.float64).reshape(-1) - y_cpu).max()
+                                      / np.abs(y_cpu).max())
+    for nt in threads:
+        s, n = timed_cpu(mk(nt), seconds, 1000)
+        out[f"us_{nt}t"] = round(s * 1e6, 2)
+        out[f"calls_{nt}t"] = n
     return out
 
 
-def bench_sustained(pkg, torch, handles, x, code_bytes, all_bytes, steps):
+def linear_leg(b, hs, base, wbytes, M, K, B, dt, steps, warmup):
+    """µs per call (events) and kernel roofline of ``B``-token calls over the
+    instances in round robin (flushed before each pass)."""
+    torch, L = b.torch, b.L
+    n = len(hs)
+    x = torch.from_numpy(base["x"][:B]).to(b.dev)
+    if dt:
+        x = x.to(torch.bfloat16)
+    y = torch.empty(B, M, device=b.dev, dtype=x.dtype)
+    xp, yp = VP(x.data_ptr()), VP(y.data_ptr())
+    call = lambda i: L.ojasx_linear_forward_device(hs[i % n], xp, yp, B, dt, b.sp)
+    assert call(0) == 0, L.ojasx_get_last_error()
+    for i in range(warmup):
+        call(i)
+    torch.cuda.synchronize()
+    us = b.events_us(call, steps)
+    kern = b.kernels(call, steps)
+    name = dominant(kern)
+    code_bytes = M * (K // 16)
+    all_bytes = wbytes + B * K * x.element_size() + B * M * x.element_size()
+    out = {"us_per_call": round(us, 4), "us_per_token": round(us / B, 4), "instances": n,
+           "working_set_MB": round(n * wbytes / 2**20, 1),
+           "timed_pass_bytes_touched_MB": round(min(steps, n) * wbytes / 2**20, 1),
+           "roofline": roofline(code_bytes, all_bytes, kern[name]["avg_us"], name,
+                                kern[name]["calls"])}
+    out["useful_TFLOPs"] = round(2.0 * M * K * B / (kern[name]["avg_us"] * 1e-6) / 1e12, 3)
+    assert L.ojasx_linear_forward_device(hs[0], xp, yp, B, dt, b.sp) == 0
+    torch.cuda.synchronize()
+    return out, y.float().cpu().numpy()
+
+
+def bench_linear2560(b, args):
+    """LUT linear 2560 -> 2560, batch 1, fp32, 0.38 %
+    CSR, over 400 instances (268 MB), with the reference engine's CPU time."""
+    M = K = 2560
+    hs, base, wbytes = make_instances(b, M, K, 400, 2040)
+    try:
+        res, y0 = linear_leg(b, hs, base, wbytes, M, K, 1, 0, args.steps, args.warmup)
+        if not args.no_cpu:
+            res["cpu_baseline"] = cpu_linear(base, 1, min(2.0, args.cpu_seconds), y0,
+                                             threads=(1, cpu_threads()))
+    finally:
+        for h in hs:
+            b.L.ojasx_destroy_linear(h)
+    return res
+
+
+def bench_sustained(b, handles, base, wbytes, steps):
     """The same LUT-GEMV on all N weight instances in one grouped launch
-    (ojasx_linear_forward_grouped_device: MFMA-built LUT slices, gathered
-    per row): the sustained rate over a working set above the Infinity
-    Cache, the persistent-launch form of the sustained-GB/s measurement."""
-    L = pkg.lib()
-    vp = ctypes.c_void_p
+    (ojasx_linear_forward_grouped_device): the sustained rate over a working
+    set above the Infinity Cache."""
+    torch, L = b.torch, b.L
     n = len(handles)
-    dev = x.device
-    st = torch.cuda.current_stream()
-    sp = vp(st.cuda_stream)
-    ys = torch.empty(n, M_GU, device=dev)
-    H = (vp * n)(*handles)
-    X = (vp * n)(*([x.data_ptr()] * n))
-    Y = (vp * n)(*[ys[i].data_ptr() for i in range(n)])
-    call = lambda: L.ojasx_linear_forward_grouped_device(H, n, X, Y, sp)
-    for _ in range(5):
-        assert call() == 0, L.ojasx_get_last_error()
+    x = torch.from_numpy(base["x"][:1]).to(b.dev)
+    ys = torch.empty(n, M_GU, device=b.dev)
+    H = (VP * n)(*handles)
+    X = (VP * n)(*([x.data_ptr()] * n))
+    Y = (VP * n)(*[ys[i].data_ptr() for i in range(n)])
+    call = lambda i: L.ojasx_linear_forward_grouped_device(H, n, X, Y, b.sp)
+    for _ in range(3):
+        assert call(0) == 0, L.ojasx_get_last_error()
     torch.cuda.synchronize()
-    reps = max(20, steps // 50)
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record(st)
-    for _ in range(reps):
-        call()
-    e1.record(st)
-    torch.cuda.synchronize()
-    us = e0.elapsed_time(e1) * 1e3 / reps
-    kern = timed_kernels(pkg, lambda: [call() for _ in range(reps)])
+    reps = max(10, min(steps, 200))
+    us = b.events_us(call, reps)
+    kern = b.kernels(call, reps)
     kus = kern["lut_group_kernel"]["avg_us"]
-    ach = n * code_bytes / (kus * 1e-6) / 1e9
-    ach_all = n * all_bytes / (kus * 1e-6) / 1e9
-    return {"kernel": "lut_group_kernel", "instances": n, "launches": reps,
-            "us_per_launch": round(us, 3), "kernel_avg_us": round(kus, 3),
-            "us_per_linear": round(kus / n, 4),
-            "achieved_code_GBs": round(ach, 1), "frac_code": round(ach / HBM_PEAK_GBS, 4),
-            "achieved_all_bytes_GBs": round(ach_all, 1),
-            "frac_all_bytes": round(ach_all / HBM_PEAK_GBS, 4),
-            "algorithmic_bytes_per_launch": n * code_bytes,
-            "traffic": measured_traffic(GROUP_TRAFFIC_SUMMARY) if n == 160 else None}
+    code_bytes = M_GU * (K_GU // 16)
+    all_bytes = wbytes + K_GU * 4 + M_GU * 4
+    rf = roofline(n * code_bytes, n * all_bytes, kus, "lut_group_kernel",
+                  kern["lut_group_kernel"]["calls"],
+                  measured_traffic(GROUP_TRAFFIC_SUMMARY) if n == 160 else None)
+    return {"instances": n, "us_per_launch": round(us, 3), "us_per_linear": round(kus / n, 4),
+            "roofline": rf}
 
 
-def bench_moe(pkg, torch, steps, warmup, cpu_seconds, do_cpu):
+def bench_batched(b, handles, base, wbytes, args):
+    """LUT-GEMV 2560->6912 at batch 8, 16, 32 and 64 (BASELINE.json configs[1]),
+    fp32 and bf16 activations, over the headline's instances (flushed before
+    each pass).  From 9 tokens the call runs as x . W^T on fp32 MFMA
+    (lut_mm_kernel), below that the in-place LUT kernel (lut_dec_kernel).
+    CPU: the reference engine at 8 and 64 tokens (it loops tokens)."""
+    res = {}
+    n = max(50, min(args.steps, 400))
+    y8 = {}
+    for dt, tag in ((0, "fp32"), (1, "bf16")):
+        for B in (8, 16, 32, 64):
+            r, y0 = linear_leg(b, handles, base, wbytes, M_GU, K_GU, B, dt, n, min(args.warmup, 20))
+            res[f"{tag}_B{B}"] = r
+            if dt == 0:
+                y8[B] = y0
+    if not args.no_cpu:
+        for B in (8, 64):
+            res[f"cpu_baseline_fp32_B{B}"] = cpu_linear(base, B, min(1.5, args.cpu_seconds),
+                                                        y8[B], threads=(1, cpu_threads()))
+    return res
+
+
+# --- MoE ----------------------------------------------------------------------------
+
+def bench_moe(b, args):
     """512-expert top-10 MoE layer (H 2048, I 768), T = 1 and 16 tokens.  Two
     expert banks (2 x 151 MB, above the 256 MB Infinity Cache) alternate and
-    every step has its own routing, so routed experts' codes come from HBM."""
+    every step has its own routing (routed on the device); code bytes count
+    the distinct experts a call reads.  CPU: the reference engine, whose API
+    is one token per call (16 calls for T = 16)."""
     from oracle import ref
-    gen = pkg.synthetic
-    L = pkg.lib()
-    vp = ctypes.c_void_p
-    p = lambda a: a.ctypes.data_as(vp)
+    torch, L = b.torch, b.L
+    gen = b.pkg.synthetic
+    p = lambda a: a.ctypes.data_as(VP)
     E, H, I, K = 512, 2048, 768, 10
     banks = []
     for seed in (11, 12):
@@ -194,211 +341,180 @@ def bench_moe(pkg, torch, steps, warmup, cpu_seconds, do_cpu):
                                p(m["gu_scales"]), p(m["dn_codes"]), p(m["dn_scales"]))
         assert h, L.ojasx_get_last_error()
         banks.append((h, m))
-    dev = torch.device("cuda:0")
-    st = torch.cuda.current_stream()
-    sp = vp(st.cuda_stream)
     res = {}
     per_expert = 2 * I * (H // 16) + H * (I // 16)
-    for T in (1, 16):
-        nsteps = steps
-        r = np.random.default_rng(T)
-        logits = torch.from_numpy(r.normal(size=(nsteps, T, E)).astype(np.float32)).to(dev)
-        idx = torch.empty(nsteps, T, K, dtype=torch.int32, device=dev)
-        w = torch.empty(nsteps, T, K, dtype=torch.float32, device=dev)
-        for i in range(nsteps):
-            assert L.ojasx_moe_route_device(vp(logits[i].data_ptr()), T, E, K, 0,
-                                            vp(idx[i].data_ptr()), vp(w[i].data_ptr()), sp) == 0
-        torch.cuda.synchronize()
-        distinct = np.array([len(np.unique(a)) for a in idx.cpu().numpy().reshape(nsteps, -1)])
-        x = torch.from_numpy(banks[0][1]["x"][:T]).to(dev)
-        y = torch.empty(T, H, device=dev)
-        fwd = lambda i: L.ojasx_moe_forward_device(banks[i % 2][0], vp(x.data_ptr()),
-                                                   vp(idx[i].data_ptr()), vp(w[i].data_ptr()),
-                                                   vp(y.data_ptr()), T, K, 0, sp)
-        for i in range(min(warmup, nsteps)):
-            fwd(i)
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record(st)
-        for i in range(nsteps):
-            fwd(i)
-        e1.record(st)
-        torch.cuda.synchronize()
-        us = e0.elapsed_time(e1) * 1e3 / nsteps
-        code_bytes = float(distinct.mean()) * per_expert
-        kern = timed_kernels(pkg, lambda: [fwd(i) for i in range(min(nsteps, 200))])
-        res[f"T{T}"] = {"us_per_call": round(us, 3), "distinct_experts_mean": float(distinct.mean()),
-                        "code_bytes_per_call": int(code_bytes),
-                        "achieved_GBs": round(code_bytes / (us * 1e-6) / 1e9, 2),
-                        "frac_of_8TBs": round(code_bytes / (us * 1e-6) / 8e12, 5),
-                        "kernels_avg_us": {k: v["avg_us"] for k, v in kern.items()}}
-    if do_cpu and ref.available():
-        m = banks[0][1]
-        R = ref.RefMoE(m["cb_in"], m["cb_down"], m["gu_codes"], m["gu_scales"], m["dn_codes"],
-                       m["dn_scales"])
-        ii = idx[0, 0].cpu().numpy()
-        ww = w[0, 0].cpu().numpy()
-        for _ in range(3):
-            R.forward(m["x"][0], ii, ww)
-        n, t0 = 0, time.perf_counter()
-        while time.perf_counter() - t0 < cpu_seconds and n < 100:
-            R.forward(m["x"][0], ii, ww)
-            n += 1
-        res["cpu_reference_T1_us"] = round((time.perf_counter() - t0) / n * 1e6, 2)
-        res["cpu_reference_sample"] = f"{n} single-token calls, 1 thread (reference engine)"
-    for h, _ in banks:
-        L.ojasx_destroy_moe(h)
+    per_expert_scales = (2 * I + H) * 4
+    nsteps = max(50, min(args.steps, 400))
+    try:
+        for T in (1, 16):
+            r = np.random.default_rng(T)
+            logits = torch.from_numpy(r.normal(size=(nsteps, T, E)).astype(np.float32)).to(b.dev)
+            idx = torch.empty(nsteps, T, K, dtype=torch.int32, device=b.dev)
+            w = torch.empty(nsteps, T, K, dtype=torch.float32, device=b.dev)
+            for i in range(nsteps):
+                assert L.ojasx_moe_route_device(VP(logits[i].data_ptr()), T, E, K, 0,
+                                                VP(idx[i].data_ptr()), VP(w[i].data_ptr()),
+                                                b.sp) == 0
+            torch.cuda.synchronize()
+            distinct = np.array([len(np.unique(a))
+                                 for a in idx.cpu().numpy().reshape(nsteps, -1)])
+            x = torch.from_numpy(banks[0][1]["x"][:T]).to(b.dev)
+            y = torch.empty(T, H, device=b.dev)
+            fwd = lambda i: L.ojasx_moe_forward_device(banks[i % 2][0], VP(x.data_ptr()),
+                                                       VP(idx[i].data_ptr()), VP(w[i].data_ptr()),
+                                                       VP(y.data_ptr()), T, K, 0, b.sp)
+            for i in range(min(args.warmup, nsteps)):
+                fwd(i)
+            torch.cuda.synchronize()
+            us = b.events_us(fwd, nsteps)
+            kern = b.kernels(fwd, nsteps)
+            code_bytes = float(distinct.mean()) * per_expert
+            all_bytes = float(distinct.mean()) * (per_expert + per_expert_scales) + 2 * T * H * 4
+            res[f"T{T}"] = {"us_per_call": round(us, 3),
+                            "distinct_experts_mean": float(distinct.mean()),
+                            "code_bytes_per_call": int(code_bytes),
+                            "achieved_code_GBs": round(code_bytes / (us * 1e-6) / 1e9, 2),
+                            "frac_code": round(code_bytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 5),
+                            "achieved_all_bytes_GBs": round(all_bytes / (us * 1e-6) / 1e9, 2),
+                            "kernels_avg_us": {k: v["avg_us"] for k, v in kern.items()}}
+            if not args.no_cpu and ref.available():
+                m = banks[0][1]
+                R = ref.RefMoE(m["cb_in"], m["cb_down"], m["gu_codes"], m["gu_scales"],
+                               m["dn_codes"], m["dn_scales"])
+                ii = idx[0].cpu().numpy()
+                ww = w[0].cpu().numpy()
+                call = lambda: [R.forward(m["x"][t], ii[t], ww[t]) for t in range(T)]
+                s, n = timed_cpu(call, min(2.0, args.cpu_seconds), 100, warm=1)
+                res[f"T{T}"]["cpu_baseline"] = {
+                    "value": round(s * 1e6, 1), "unit": "us/call", "cores": 1, "kind": "reference",
+                    "sample": f"{n} calls of {T} token(s) (one reference call per token), 1 thread"}
+    finally:
+        for h, _ in banks:
+            L.ojasx_destroy_moe(h)
     return res
 
 
-def bench_batched(pkg, torch, steps, warmup):
-    """LUT-GEMV 2560->6912 at batch 8, 16, 32 and 64 (BASELINE.json configs[1]),
-    fp32 and bf16 activations, on 32 distinct weight instances in round robin
-    (35 MB).  From 9 tokens the call runs as x . W^T on fp32 MFMA
-    (lut_mm_kernel), below that the in-place LUT kernel (lut_dec_kernel).
-    Per-token code bytes are the codes of one call (1,105,920 B)."""
-    gen = pkg.synthetic
-    L = pkg.lib()
-    vp = ctypes.c_void_p
-    p = lambda a: a.ctypes.data_as(vp)
-    base = gen.linear(M_GU, K_GU, B=64, seed=2027)
-    r = np.random.default_rng(8)
-    hs = []
-    for i in range(32):
-        codes = base["codes"] if i == 0 else r.integers(0, 256, size=base["codes"].shape,
-                                                        dtype=np.uint8)
-        h = L.ojasx_create_linear(K_GU, M_GU, 16, 256, p(base["codebook"]), p(codes),
-                                  p(base["scales"]), None)
-        assert h, L.ojasx_get_last_error()
-        rp, cl, vl = base["csr"]
-        assert L.ojasx_set_linear_outliers(h, vl.size, p(rp), p(cl), p(vl)) == 0
-        hs.append(h)
-    dev = torch.device("cuda:0")
-    st = torch.cuda.current_stream()
-    sp = vp(st.cuda_stream)
-    code_bytes = M_GU * (K_GU // 16)
-    res = {}
-    n = max(50, min(steps, 400))
-    for dt, tag in ((0, "fp32"), (1, "bf16")):
-        for B in (8, 16, 32, 64):
-            x = torch.from_numpy(base["x"][:B]).to(dev)
-            if dt:
-                x = x.to(torch.bfloat16)
-            y = torch.empty(B, M_GU, device=dev, dtype=x.dtype)
-            call = lambda i: L.ojasx_linear_forward_device(hs[i % 32], vp(x.data_ptr()),
-                                                           vp(y.data_ptr()), B, dt, sp)
-            for i in range(min(warmup, 50)):
-                assert call(i) == 0, L.ojasx_get_last_error()
-            torch.cuda.synchronize()
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            e0.record(st)
-            for i in range(n):
-                call(i)
-            e1.record(st)
-            torch.cuda.synchronize()
-            us = e0.elapsed_time(e1) * 1e3 / n
-            kern = timed_kernels(pkg, lambda: [call(i) for i in range(min(n, 200))])
-            name, kv = next(iter(kern.items()))
-            mfma = 2.0 * M_GU * K_GU * B / (kv["avg_us"] * 1e-6) / 1e12
-            res[f"{tag}_B{B}"] = {"us_per_call": round(us, 3), "us_per_token": round(us / B, 3),
-                                  "kernel": name, "kernel_avg_us": kv["avg_us"],
-                                  "code_GBs": round(code_bytes / (kv["avg_us"] * 1e-6) / 1e9, 1),
-                                  "useful_TFLOPs": round(mfma, 2)}
-    for h in hs:
-        L.ojasx_destroy_linear(h)
-    return res
+# --- KV decode ----------------------------------------------------------------------
 
-
-def bench_kv(pkg, torch, steps, do_cpu=True):
-    """Paged code-domain decode: 8 kv / 32 q heads, head_dim 128, page 16."""
-    gen = pkg.synthetic
-    L = pkg.lib()
-    vp = ctypes.c_void_p
-    dev = torch.device("cuda:0")
-    st = torch.cuda.current_stream()
+def bench_kv(b, args):
+    """Paged code-domain decode, 8 kv / 32 q heads, head_dim 128, page 16, at
+    2048 and 32768 tokens.  Every call reads another layer's cache (codes,
+    scales and codebooks of its own), over more than 256 MB of caches, after a
+    flush.  CPU: the reference engine's ojasx_kv_cache_attention for the 32
+    query heads (one call per query head, its kv head j // 4; the reference
+    re-reads each kv head's codes for every query head) over the same number
+    of tokens appended by its scalar quantiser."""
+    from oracle import ref
+    torch, L = b.torch, b.L
     res = {}
+    Hkv, Hq, hd, P = 8, 32, 128, 16
+    g = torch.Generator(device=b.dev).manual_seed(5)
     for T in (2048, 32768):
-        d = gen.kv(H_kv=8, H_q=32, T=T, seed=5, shuffle_pages=True)
-        t = {k: torch.from_numpy(np.ascontiguousarray(d[k])).to(dev)
-             for k in ("q", "k_codes", "k_scales", "v_codes", "v_scales", "k_cb", "v_cb",
-                       "block_table")}
-        out = torch.empty(32, 128, device=dev)
-        call = lambda: L.ojasx_kv_decode_paged_device(
-            vp(t["q"].data_ptr()), vp(t["k_codes"].data_ptr()), vp(t["k_scales"].data_ptr()),
-            vp(t["v_codes"].data_ptr()), vp(t["v_scales"].data_ptr()), vp(t["k_cb"].data_ptr()),
-            vp(t["v_cb"].data_ptr()), vp(t["block_table"].data_ptr()), T, 16, 32, 8, 128, 16,
-            -1.0, vp(out.data_ptr()), vp(st.cuda_stream))
-        for _ in range(20):
-            call()
+        pages = T // P
+        per_layer = 2 * pages * Hkv * P * 8 + 2 * pages * Hkv * P * 4 + 2 * Hkv * 256 * 16 * 4
+        layers = max(2, -(-(300 << 20) // per_layer))
+        kc = torch.randint(0, 256, (layers, pages, Hkv, P, 8), dtype=torch.uint8, device=b.dev,
+                           generator=g)
+        vc = torch.randint(0, 256, (layers, pages, Hkv, P, 8), dtype=torch.uint8, device=b.dev,
+                           generator=g)
+        ks = torch.rand(layers, pages, Hkv, P, device=b.dev, generator=g) + 0.5
+        vs = torch.rand(layers, pages, Hkv, P, device=b.dev, generator=g) + 0.5
+        kcb = torch.randn(layers, Hkv, 256, 16, device=b.dev, generator=g)
+        vcb = torch.randn(layers, Hkv, 256, 16, device=b.dev, generator=g)
+        bt = torch.randperm(pages, device=b.dev, generator=g).to(torch.int32)
+        q = torch.randn(Hq, hd, device=b.dev, generator=g)
+        out = torch.empty(Hq, hd, device=b.dev)
+        ptr = lambda t, l: VP(t[l].data_ptr())
+        call = lambda i: L.ojasx_kv_decode_paged_device(
+            VP(q.data_ptr()), ptr(kc, i % layers), ptr(ks, i % layers), ptr(vc, i % layers),
+            ptr(vs, i % layers), ptr(kcb, i % layers), ptr(vcb, i % layers), VP(bt.data_ptr()),
+            T, P, Hq, Hkv, hd, 16, -1.0, VP(out.data_ptr()), b.sp)
+        assert call(0) == 0, L.ojasx_get_last_error()
+        for i in range(min(args.warmup, 20)):
+            call(i)
         torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        n = max(50, steps // 4)
-        e0.record(st)
-        for _ in range(n):
-            call()
-        e1.record(st)
-        torch.cuda.synchronize()
-        us = e0.elapsed_time(e1) * 1e3 / n
-        code_bytes = 2 * T * 8 * 8
-        all_bytes = code_bytes + 2 * T * 8 * 4
-        kern = timed_kernels(pkg, lambda: [call() for _ in range(200)])
-        res[f"T{T}"] = {"us_per_call": round(us, 3), "code_bytes": code_bytes,
+        n = max(50, min(args.steps, 400))
+        us = b.events_us(call, n)
+        kern = b.kernels(call, n)
+        code_bytes = 2 * T * Hkv * 8
+        all_bytes = code_bytes + 2 * T * Hkv * 4 + 2 * Hkv * 256 * 16 * 4
+        name = dominant(kern)
+        res[f"T{T}"] = {"us_per_call": round(us, 3), "layers_rotated": layers,
+                        "working_set_MB": round(layers * per_layer / 2**20, 1),
+                        "code_bytes": code_bytes, "all_compulsory_bytes": all_bytes,
                         "achieved_code_GBs": round(code_bytes / (us * 1e-6) / 1e9, 2),
                         "achieved_all_GBs": round(all_bytes / (us * 1e-6) / 1e9, 2),
-                        "kernels_avg_us": {k: v["avg_us"] for k, v in kern.items()}}
-    res["append"] = bench_kv_append(pkg, torch, steps, do_cpu)
+                        "frac_all_bytes_per_call": round(all_bytes / (us * 1e-6) / 1e9
+                                                         / HBM_PEAK_GBS, 5),
+                        "kernels_avg_us": {k: v["avg_us"] for k, v in kern.items()},
+                        "dominant_kernel_roofline": roofline(
+                            code_bytes, all_bytes, kern[name]["avg_us"], name,
+                            kern[name]["calls"])}
+        del kc, vc, ks, vs, kcb, vcb
+        if not args.no_cpu and ref.available():
+            R = ref.RefKV(Hkv, hd, T, 16)
+            r = np.random.default_rng(T)
+            kv = r.normal(size=(T, 2, Hkv, hd)).astype(np.float32)
+            for t in range(T):
+                for h in range(Hkv):
+                    R.append(h, kv[t, 0, h], kv[t, 1, h])
+            qh = r.normal(size=(Hq, hd)).astype(np.float32)
+            outh = np.zeros(hd, np.float32)
+            pq = [qh[j].ctypes.data_as(VP) for j in range(Hq)]
+            po = outh.ctypes.data_as(VP)
+            RL = ref.lib()
+            call_cpu = lambda: [RL.ojasx_kv_cache_attention(R.h, j // (Hq // Hkv), pq[j], po, -1.0)
+                                for j in range(Hq)]
+            s, n = timed_cpu(call_cpu, min(2.0, args.cpu_seconds), 1000)
+            res[f"T{T}"]["cpu_baseline"] = {
+                "value": round(s * 1e6, 1), "unit": "us/call", "cores": 1, "kind": "reference",
+                "sample": f"{n} decodes of 32 query heads over {T} tokens x 8 kv heads "
+                          "(reference scalar-quantised cache), 1 thread"}
+            del R
+    res["append"] = bench_kv_append(b, args)
     return res
 
 
-def bench_kv_append(pkg, torch, steps, do_cpu, cpu_seconds=2.0):
+def bench_kv_append(b, args, cpu_seconds=2.0):
     """Device KV append (encode + paged write) for 8 kv heads x 128, per call
     of 1 or 16 tokens, with the 256 x 16 codebooks (nearest centroid) and with
     the reference's scalar quantiser; each call writes fresh slots of a
     4096-page pool.  Beside it the reference engine's ojasx_kv_cache_append
     on the host, 8 heads per token."""
     from oracle import ref
-    L = pkg.lib()
-    vp = ctypes.c_void_p
-    dev = torch.device("cuda:0")
-    st = torch.cuda.current_stream()
+    torch, L = b.torch, b.L
     Hkv, hd, D, P, pages = 8, 128, 16, 16, 4096
     r = np.random.default_rng(17)
-    kc = torch.zeros(pages, Hkv, P, hd // D, dtype=torch.uint8, device=dev)
+    kc = torch.zeros(pages, Hkv, P, hd // D, dtype=torch.uint8, device=b.dev)
     vc = torch.zeros_like(kc)
-    ks = torch.zeros(pages, Hkv, P, device=dev)
+    ks = torch.zeros(pages, Hkv, P, device=b.dev)
     vs = torch.zeros_like(ks)
-    cb = torch.from_numpy(r.normal(0, 30, size=(2, Hkv, 256, D)).astype(np.float32)).to(dev)
+    cb = torch.from_numpy(r.normal(0, 30, size=(2, Hkv, 256, D)).astype(np.float32)).to(b.dev)
     res = {}
-    n = max(50, steps // 4)
+    n = max(50, min(args.steps, 400))
     for tokens in (1, 16):
-        kv = torch.from_numpy(r.normal(size=(2, n, tokens, Hkv, hd)).astype(np.float32)).to(dev)
-        slots = torch.arange(n * tokens, dtype=torch.int32, device=dev).view(n, tokens)
+        kv = torch.from_numpy(r.normal(size=(2, n, tokens, Hkv, hd)).astype(np.float32)).to(b.dev)
+        slots = torch.arange(n * tokens, dtype=torch.int32, device=b.dev).view(n, tokens)
         for mode in ("codebook", "scalar"):
-            cbk = vp(cb[0].data_ptr()) if mode == "codebook" else None
-            cbv = vp(cb[1].data_ptr()) if mode == "codebook" else None
+            cbk = VP(cb[0].data_ptr()) if mode == "codebook" else None
+            cbv = VP(cb[1].data_ptr()) if mode == "codebook" else None
             call = lambda i: L.ojasx_kv_encode_append_device(
-                vp(kv[0, i].data_ptr()), vp(kv[1, i].data_ptr()), tokens, Hkv, hd, D, cbk, cbv,
-                vp(slots[i].data_ptr()), P, pages, vp(kc.data_ptr()), vp(ks.data_ptr()),
-                vp(vc.data_ptr()), vp(vs.data_ptr()), vp(st.cuda_stream))
+                VP(kv[0, i].data_ptr()), VP(kv[1, i].data_ptr()), tokens, Hkv, hd, D, cbk, cbv,
+                VP(slots[i].data_ptr()), P, pages, VP(kc.data_ptr()), VP(ks.data_ptr()),
+                VP(vc.data_ptr()), VP(vs.data_ptr()), b.sp)
             for i in range(min(n, 20)):
                 call(i)
             torch.cuda.synchronize()
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            e0.record(st)
-            for i in range(n):
-                call(i)
-            e1.record(st)
-            torch.cuda.synchronize()
-            us = e0.elapsed_time(e1) * 1e3 / n
-            kern = timed_kernels(pkg, lambda: [call(i) for i in range(n)])
+            us = b.events_us(call, n)
+            kern = b.kernels(call, n)
             res[f"{mode}_{tokens}tok"] = {
                 "us_per_call": round(us, 3), "us_per_token": round(us / tokens, 3),
                 "kernels_avg_us": {k: v["avg_us"] for k, v in kern.items()}}
-    if do_cpu and ref.available():
+    if not args.no_cpu and ref.available():
         R = ref.lib()
         h = R.ojasx_create_kv_cache(Hkv, hd, 1 << 17, D)
         k = r.normal(size=(Hkv, hd)).astype(np.float32)
-        p = lambda a: a.ctypes.data_as(vp)
+        p = lambda a: a.ctypes.data_as(VP)
         count, t0 = 0, time.perf_counter()
         while time.perf_counter() - t0 < cpu_seconds and count < 100000:
             for head in range(Hkv):
@@ -411,15 +527,38 @@ def bench_kv_append(pkg, torch, steps, do_cpu, cpu_seconds=2.0):
     return res
 
 
-def bench_decoder(pkg, torch, n_tokens=128, context=4096):
+# --- decoder ------------------------------------------------------------------------
+
+class _CpuLinear:
+    """One LUT linear through the C restatement of the reference engine's
+    forward (oracle/lut_oracle.c), 1 thread, as ``op @ x``."""
+
+    def __init__(self, w):
+        self.w = w
+
+    def __matmul__(self, x):
+        from oracle import cpu
+        w = self.w
+        return cpu.linear_forward(np.asarray(x, np.float32), w["codebook"], w["codes"], None, None,
+                                  *w["csr"]).astype(np.float64)
+
+
+def bench_decoder(b, args, n_tokens=128, context=4096):
     """The 4B-shaped LUT decoder (hidden 2560, 36 layers, 32 q / 8 kv heads,
     MLP 9728, LUT LM head over 151936 tokens): greedy decode of n_tokens at a
     4096-token code KV context, one HIP graph per token and eager launches.
-    Seeded random weights and context (synthetic_decoder)."""
-    decm = pkg.decoder
+    Seeded random weights and context (synthetic_decoder).  Bytes per token:
+    codes + CSR of every linear, the KV codes and scales read, and the
+    embedding row.  CPU: one token of the same decoder on the host (the C
+    restatement of the reference engine for every linear, 1 thread; NumPy
+    norms, RoPE and attention); the reference has no decoder of its own."""
+    from oracle import numpy_oracle as no
+    decm = b.pkg.decoder
     cfg = decm.DecoderConfig(max_steps=n_tokens, max_context=context + n_tokens)
     t0 = time.perf_counter()
-    d, _ = decm.synthetic_decoder(cfg, context=context, seed=3, device="cuda:0")
+    keep = not args.no_cpu
+    d, weights = decm.synthetic_decoder(cfg, context=context, seed=3, device="cuda:0",
+                                        keep_weights=keep)
     t_build = time.perf_counter() - t0
     res = {"config": "hidden 2560, 36 layers, 32 q / 8 kv heads, head_dim 128, MLP 9728, "
                      f"vocab {cfg.vocab}, all linears LUT d=16/256 + 0.38% CSR, "
@@ -430,6 +569,7 @@ def bench_decoder(pkg, torch, n_tokens=128, context=4096):
         d.reset(context)
         d.generate(1, 4, use_graph=graph)          # warm-up (captures the graph)
         d.reset(context)
+        b.flush()
         t0 = time.perf_counter()
         toks = d.generate(1, n_tokens, use_graph=graph)
         el = time.perf_counter() - t0
@@ -438,16 +578,67 @@ def bench_decoder(pkg, torch, n_tokens=128, context=4096):
                      "ms_per_token": round(el / n_tokens * 1e3, 4)}
     res["graph_equals_eager"] = bool(np.array_equal(runs["graph"], runs["eager"]))
     d.reset(context)
-    kern = timed_kernels(pkg, lambda: d.generate(1, 8, use_graph=False))
-    res["kernels_per_token_us"] = {k: round(v["avg_us"] * v["calls"] / 8, 2)
-                                   for k, v in sorted(kern.items(), key=lambda kv: -kv[1]["avg_us"] * kv[1]["calls"])}
-    per_layer_codes = (6144 * 160 + 2560 * 256 + 19456 * 160 + 2560 * 608)
-    code_bytes = 36 * per_layer_codes + cfg.vocab * 160
+    b.flush()
+    b.pkg._lib.kernel_timing_enable(True)
+    try:
+        d.generate(1, 8, use_graph=False)
+        kern = b.pkg._lib.kernel_timing_report()
+    finally:
+        b.pkg._lib.kernel_timing_enable(False)
+    kern.pop("_dropped", None)
+    res["kernels_per_token_us"] = {
+        k: round(v["avg_us"] * v["calls"] / 8, 2)
+        for k, v in sorted(kern.items(), key=lambda kv: -kv[1]["avg_us"] * kv[1]["calls"])}
+    qkv, o, gu, dn = 6144, 2560, 19456, 2560
+    shapes = [(qkv, 2560), (o, 4096), (gu, 2560), (dn, 9728)]
+    dens = 0.0038
+    per_layer_codes = sum(M * K // 16 for M, K in shapes)
+    per_layer_csr = sum(round(dens * M * K) * 8 + (M + 1) * 4 for M, K in shapes)
+    lm_codes = cfg.vocab * 160
+    lm_csr = round(dens * cfg.vocab * 2560) * 8 + (cfg.vocab + 1) * 4
+    kv_bytes = 36 * 8 * (context + n_tokens // 2) * (2 * 8 + 2 * 4)
+    code_bytes = 36 * per_layer_codes + lm_codes
+    all_bytes = code_bytes + 36 * per_layer_csr + lm_csr + kv_bytes
     ms = res["graph"]["ms_per_token"]
-    res["code_bytes_per_token"] = code_bytes
-    res["achieved_code_GBs"] = round(code_bytes / (ms * 1e-3) / 1e9, 2)
+    res.update({"code_bytes_per_token": code_bytes, "all_bytes_per_token": int(all_bytes),
+                "achieved_code_GBs": round(code_bytes / (ms * 1e-3) / 1e9, 2),
+                "achieved_all_GBs": round(all_bytes / (ms * 1e-3) / 1e9, 2),
+                "frac_all_bytes": round(all_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 5)})
+    if keep:
+        emb = weights["embedding"]
+        caches = [d.read_kv(l, 0, context + 1) for l in range(cfg.layers)]
+        t0 = time.perf_counter()
+        no.decoder_step(emb[1], weights, cfg, context, caches, {}, linear=_CpuLinear)
+        el = time.perf_counter() - t0
+        res["cpu_baseline"] = {"value": round(el * 1e3, 1), "unit": "ms/token", "cores": 1,
+                               "kind": "port",
+                               "sample": "one greedy token at 4096 context: every linear on the "
+                                         "C restatement of the reference engine (1 thread), "
+                                         "norms / RoPE / attention in NumPy fp64"}
     d.close()
     return res
+
+
+def copy_peak(b):
+    """Device-to-device copy of 1 GiB (read + write counted): a measured HBM
+    rate beside the 8 TB/s spec."""
+    torch = b.torch
+    n = (1 << 30) // 4
+    src = torch.ones(n, device=b.dev)
+    dst = torch.empty_like(src)
+    for _ in range(2):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(b.stream)
+    for _ in range(10):
+        dst.copy_(src)
+    e1.record(b.stream)
+    torch.cuda.synchronize()
+    s = e0.elapsed_time(e1) * 1e-3 / 10
+    del src, dst
+    return {"bytes_moved": 2 << 30, "GBs": round((2 << 30) / s / 1e9, 1),
+            "frac_of_8TBs": round((2 << 30) / s / 1e9 / HBM_PEAK_GBS, 4)}
 
 
 def main():
@@ -461,34 +652,20 @@ def main():
     import __graft_entry__
 
     pkg = __graft_entry__.load_package()
-    gen = pkg.synthetic
-    L = pkg.lib()
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    b = Bench(torch, pkg)
+    L = b.L
 
-    # --- weights: N distinct instances, shared x --------------------------------
-    base = gen.linear(M_GU, K_GU, B=1, seed=2026)
-    r = np.random.default_rng(7)
-    handles, wbytes = [], 0
-    p = lambda a: a.ctypes.data_as(ctypes.c_void_p)
-    for i in range(args.instances):
-        codes = base["codes"] if i == 0 else r.integers(0, 256, size=base["codes"].shape,
-                                                        dtype=np.uint8)
-        h = L.ojasx_create_linear(K_GU, M_GU, 16, 256, p(base["codebook"]), p(codes),
-                                  p(base["scales"]), None)
-        assert h, L.ojasx_get_last_error()
-        rp, cl, vl = base["csr"]
-        assert L.ojasx_set_linear_outliers(h, vl.size, p(rp), p(cl), p(vl)) == 0
-        handles.append(h)
-        wbytes = L.ojasx_linear_device_weight_bytes(h)
-    x = torch.from_numpy(base["x"]).to(dev)
+    # --- headline: N distinct 2560 -> 6912 instances, shared x --------------------
+    handles, base, wbytes = make_instances(b, M_GU, K_GU, args.instances, 2026)
+    n = len(handles)
+    x = torch.from_numpy(base["x"][:1]).to(dev)
     y = torch.empty(1, M_GU, device=dev)
-    stream = torch.cuda.current_stream()
-    sp = ctypes.c_void_p(stream.cuda_stream)
-    xp, yp = ctypes.c_void_p(x.data_ptr()), ctypes.c_void_p(y.data_ptr())
+    xp, yp = VP(x.data_ptr()), VP(y.data_ptr())
     fwd = L.ojasx_linear_forward_device
-
-    assert fwd(handles[0], xp, yp, 1, 0, sp) == 0
+    call = lambda i: fwd(handles[i % n], xp, yp, 1, 0, b.sp)
+    assert call(0) == 0, L.ojasx_get_last_error()
     torch.cuda.synchronize()
     y_bench = y.cpu().numpy()
 
@@ -499,29 +676,19 @@ def main():
     torch.cuda.synchronize()
     del cal_src, cal_dst
 
-    n = len(handles)
     for i in range(args.warmup):
-        fwd(handles[i % n], xp, yp, 1, 0, sp)
+        call(i)
     torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t_wall = time.perf_counter()
-    e0.record(stream)
-    for i in range(args.steps):
-        fwd(handles[i % n], xp, yp, 1, 0, sp)
-    e1.record(stream)
-    torch.cuda.synchronize()
+    us_call = b.events_us(call, args.steps)
     t_wall = time.perf_counter() - t_wall
-    ms = e0.elapsed_time(e1)
-    us_call = ms * 1e3 / args.steps
-
     code_bytes = M_GU * (K_GU // 16)
     all_bytes = wbytes + K_GU * 4 + M_GU * 4
-    # the kernel's own duration, same calls, library start/stop events
-    kern = timed_kernels(pkg, lambda: [fwd(handles[i % n], xp, yp, 1, 0, sp)
-                                       for i in range(args.steps)])
-    kname = max(kern, key=lambda k: kern[k]["calls"] * kern[k]["avg_us"])
-    kernel_us = kern[kname]["avg_us"]
-    achieved = code_bytes / (kernel_us * 1e-6) / 1e9
+    kern = b.kernels(call, args.steps)
+    kname = dominant(kern)
+    rf = roofline(code_bytes, all_bytes, kern[kname]["avg_us"], kname, kern[kname]["calls"],
+                  measured_traffic())
+    rf["call_period_GBs"] = round(code_bytes / (us_call * 1e-6) / 1e9, 2)
 
     out = {
         "metric": "LUT-GEMV 2560->6912 us/call (HBM GB/s on code bytes alongside)",
@@ -530,7 +697,7 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(ms / args.steps, 6),
+        "ms_per_step": round(us_call / 1e3, 6),
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,
@@ -539,34 +706,56 @@ def main():
         "config": {"workload": "LUT-GEMV 2560->6912 gate/up, B=1, fp32, d=16/256 centroids, "
                                "0.38% CSR outliers", "batch": 1, "in_features": K_GU,
                    "out_features": M_GU, "weight_instances": n,
-                   "working_set_MB": round(n * wbytes / 2**20, 1)},
-        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 5),
-                     "traffic": measured_traffic(),
-                     "kernel": kname, "kernel_avg_us": round(kernel_us, 4),
-                     "kernel_launches_timed": kern[kname]["calls"],
-                     "algorithmic_bytes_per_launch": code_bytes,
-                     "all_compulsory_bytes_per_launch": all_bytes,
-                     "achieved_all_bytes_GBs": round(all_bytes / (kernel_us * 1e-6) / 1e9, 2),
-                     "call_period_GBs": round(code_bytes / (us_call * 1e-6) / 1e9, 2)},
+                   "working_set_MB": round(n * wbytes / 2**20, 1),
+                   "timed_pass_bytes_touched_MB": round(min(args.steps, n) * wbytes / 2**20, 1),
+                   "cache_flush_before_each_pass_MiB": FLUSH_BYTES >> 20},
+        "roofline": rf,
         "pmc_calibration_copy_bytes": CAL_COPY_BYTES,
         "wall_s_timed": round(t_wall, 3),
+        "host": host_info(),
     }
-    out["sustained"] = bench_sustained(pkg, torch, handles, x, code_bytes, all_bytes, args.steps)
     if not args.no_cpu:
-        out["cpu_baseline"] = time_cpu_linear(base, args.cpu_seconds, y_bench)
-    for h in handles:
-        L.ojasx_destroy_linear(h)
+        c = cpu_linear(base, 1, args.cpu_seconds, y_bench, threads=(1,))
+        out["cpu_baseline"] = {"value": c["us_1t"], "unit": "us/call", "cores": 1,
+                               "kind": c["kind"],
+                               "sample": f"{c['calls_1t']} calls of LUT-GEMV 2560->6912 B=1 fp32 "
+                                         "with CSR, 1 thread, after 3 warm-up calls",
+                               "parity_rel_err": c["parity_rel_err"]}
+        if c["kind"] == "reference":
+            from oracle import ref
+            var = {}
+            for tag, path in (("scalar", ref.LIB_SCALAR), ("avx2", ref.LIB_AVX2)):
+                if not ref.available(path):
+                    continue
+                R = ref.RefLinear(base["codebook"], base["codes"], base["scales"], None,
+                                  base["csr"], path=path)
+                for nt in sorted({1, cpu_threads()}):
+                    s, _ = timed_cpu(lambda: R.forward(base["x"][:1], nt),
+                                     min(2.0, args.cpu_seconds), 1000)
+                    var[f"{tag}_{nt}t"] = round(s * 1e6, 2)
+            out["cpu_baseline"]["variants_us_per_call"] = var
     extra = set() if args.no_extra else set(args.extra.split(","))
-    if "batched" in extra:
-        out["lut_gemv_batched"] = bench_batched(pkg, torch, args.steps, args.warmup)
+    try:
+        if "copy" in extra:
+            out["hbm_copy_peak"] = copy_peak(b)
+        if "bf16" in extra:
+            out["lut_gemv_bf16_b1"], _ = linear_leg(b, handles, base, wbytes, M_GU, K_GU, 1, 1,
+                                                    args.steps, args.warmup)
+        if "sustained" in extra:
+            out["sustained"] = bench_sustained(b, handles, base, wbytes, args.steps)
+        if "batched" in extra:
+            out["lut_gemv_batched"] = bench_batched(b, handles, base, wbytes, args)
+    finally:
+        for h in handles:
+            L.ojasx_destroy_linear(h)
+    if "linear2560" in extra:
+        out["lut_linear_2560x2560_b1"] = bench_linear2560(b, args)
     if "moe" in extra:
-        out["moe_512x_top10"] = bench_moe(pkg, torch, min(args.steps, 400), args.warmup,
-                                          args.cpu_seconds / 2, not args.no_cpu)
+        out["moe_512x_top10"] = bench_moe(b, args)
     if "kv" in extra:
-        out["kv_decode_gqa4"] = bench_kv(pkg, torch, args.steps, not args.no_cpu)
+        out["kv_decode_gqa4"] = bench_kv(b, args)
     if "decoder" in extra:
-        out["decoder_4b_shaped"] = bench_decoder(pkg, torch)
+        out["decoder_4b_shaped"] = bench_decoder(b, args)
     print(json.dumps(out))
 
 

@@ -347,12 +347,13 @@ def decoder_step(x, weights, cfg, pos, caches, dense=None, linear="dense"):
     the identity block table, including the new token's codes (written by the
     step under test).  ``linear`` = "dense" applies each LUT linear as its
     dense fp64 matrix, "lut" through engine_forward_rows (same values to fp64
-    rounding, for shapes whose dense matrices would not fit in memory).
+    rounding, for shapes whose dense matrices would not fit in memory), or a
+    callable w -> op with ``op @ x`` (another implementation of the linear).
     Returns (logits, new_kv) with new_kv[l] = (k_rot, v) of
     the new token per kv head, for checking its codes."""
     hd, Hq, Hkv = cfg.head_dim, cfg.q_heads, cfg.kv_heads
     R = Hq // Hkv
-    make = lut_dense if linear == "dense" else LUTOp
+    make = {"dense": lut_dense, "lut": LUTOp}.get(linear, linear)
     cos, sin = rope_tables(pos + 1, hd, cfg.rope_theta)
     dense = dense if dense is not None else {}
     x = np.asarray(x, np.float64)

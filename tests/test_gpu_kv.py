@@ -82,6 +82,7 @@ def test_paged_decode_gqa(pkg, dev, T, shuffle):
     sums), so against the oracle the bar is 1e-5 plus the oracle's own error."""
     d = gen.kv(H_kv=8, H_q=32, T=T, seed=T, shuffle_pages=shuffle)
     out = decode(pkg, d, T, 32, 8)
+    worst = dict(exact=0.0, oracle=0.0, oracle_vs_exact=0.0)
     for j in range(32):
         h = j // 4
         kc, ks, vc, vs = gen.kv_logical(d, h)
@@ -89,8 +90,14 @@ def test_paged_decode_gqa(pkg, dev, T, shuffle):
         Kd = d["k_cb"][h][kc.astype(np.int64)].reshape(T, -1) * ks[:, None].astype(np.float64)
         Vd = d["v_cb"][h][vc.astype(np.int64)].reshape(T, -1) * vs[:, None].astype(np.float64)
         exact = no.full_softmax_attention(d["q"][j], Kd, Vd)
-        assert rel_err(out[j], exact) < 1e-5, j
-        assert rel_err(out[j], want) < 1e-5 + rel_err(want, exact), j
+        e_exact, e_orc, e_oe = rel_err(out[j], exact), rel_err(out[j], want), rel_err(want, exact)
+        for k, v in (("exact", e_exact), ("oracle", e_orc), ("oracle_vs_exact", e_oe)):
+            worst[k] = max(worst[k], v)
+        assert e_exact < 1e-5, j
+        assert e_orc < 1e-5 + e_oe, j
+    print(f"KV decode T={T}: worst rel err vs exact fp64 {worst['exact']:.3e}, vs the oracle "
+          f"{worst['oracle']:.3e} (bar 1e-5 + the oracle's own {worst['oracle_vs_exact']:.3e})",
+          flush=True)
 
 
 def test_reference_codebook_special_case(pkg, dev):

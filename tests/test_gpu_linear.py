@@ -269,6 +269,39 @@ def test_engine_module(pkg, dev, dtype):
     assert rel_err(f(y).reshape(6, 640), f(x).reshape(6, 1024) @ W.T + f(layer.bias)) < tol * 10
 
 
+@pytest.mark.parametrize("B", [1, 8, 64])
+def test_bf16_matches_reference_bf16_module(pkg, dev, B):
+    """bf16 parity against the reference's own bf16 path: outputs of its
+    PyTorch module with bf16 buffers (split_manifold_engine.py:22-250, LUT
+    matmul and gather sum in bf16), written in the build container by
+    tests/golden/make_bf16_golden.py from the same seeded inputs.  The HIP
+    path keeps the LUT and its sums in fp32, so it agrees to the bf16 bar
+    (rel 1e-2, max-abs error over max |ref|) rather than bit for bit."""
+    import sys
+    import torch
+    sys.path.insert(0, GOLDEN)
+    from make_bf16_golden import M, K, bf16_inputs
+    g = np.load(os.path.join(GOLDEN, "engine_bf16_2560x6912.npz"))
+    t = bf16_inputs()
+    layer = pkg.engine.SplitManifoldLUTLinear(K, M, bias=True, dtype=torch.bfloat16).to(dev)
+    with torch.no_grad():
+        for k in ("codebook", "codes", "scales"):
+            getattr(layer, k).copy_(t[k])
+        layer.bias.data.copy_(t["bias"])
+    layer.outlier_indices = t["outlier_indices"].to(dev)
+    layer.outlier_values = t["outlier_values"].to(dev)
+    layer.num_outliers = int(t["outlier_values"].numel())
+    y = layer(t["x"][:B].to(dev))
+    assert y.dtype == torch.bfloat16
+    y = y.float().cpu().numpy()
+    if B == 64:
+        y = y[:, ::int(g["col_stride_b64"])]
+    want = torch.from_numpy(g[f"y_b{B}"].view(np.int16)).view(torch.bfloat16).float().numpy()
+    err = rel_err(y, want)
+    print(f"bf16 2560->6912 B={B}: rel err vs the reference bf16 module {err:.2e}", flush=True)
+    assert err < BF16_TOL
+
+
 def test_cpu_tensor_fails_loudly(pkg):
     import torch
     layer = pkg.engine.SplitManifoldLUTLinear(32, 8)

@@ -308,3 +308,13 @@ def test_oracle_equals_compiled_reference(seed):
         y = cpu.moe_forward(m["x"][t], m["cb_in"], m["cb_down"], m["gu_codes"], m["gu_scales"],
                             m["dn_codes"], m["dn_scales"], idx[t], w[t])
         assert np.array_equal(y, M.forward(m["x"][t], idx[t], w[t]))
+
+
+def test_bf16_fixture_inputs_regenerate():
+    """The bf16 reference-module fixture stores a digest of its inputs, not the
+    inputs: the seeded generator must still produce them byte for byte."""
+    import sys
+    sys.path.insert(0, GOLDEN)
+    from make_bf16_golden import bf16_inputs, digest
+    g = np.load(os.path.join(GOLDEN, "engine_bf16_2560x6912.npz"))
+    assert digest(bf16_inputs()) == str(g["inputs_sha256"])
