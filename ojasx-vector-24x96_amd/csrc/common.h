@@ -62,6 +62,7 @@ int linear_shape(const void *h, int *K, int *M, int *D);
 // One linear of a grouped launch (lut_group.hip).
 struct GroupItem {
     const uint8_t *codes;     // [S][Mp][16]
+    const uint8_t *codes_b;   // bank layout [ceil(M/64)][S32][32][64] (lut_bank.hip)
     const float *cb;          // [256][16]
     const float *scales;      // [M]
     const float *bias;        // [M] or null
@@ -70,9 +71,21 @@ struct GroupItem {
     const float *val;
     const float *x;           // [K], 16-byte aligned
     float *y;                 // [M]
-    int K, M, Mp, S;
+    int K, M, Mp, S, S32;     // S32 = ceil(G / 32)
 };
 int linear_items(const void *h, GroupItem *it);
+// Grouped batch-1 LUT-GEMV with bank-aligned gathers (lut_bank.hip): items
+// staged in device memory, work[t] = (item, first row of a 512-row block) in
+// item-major order, max_K the largest input length.
+constexpr int kBankRows = 512;
+int launch_bank(const GroupItem *items_dev, const int2 *work_dev, int n_work, int max_K,
+                hipStream_t st);
+// Bank layout of [M][G] codes: tile (row block b of 64 rows, slice s of 32
+// groups, group g) holds the 64 rows' codes of that group; 0 past M and G.
+void pack_bank_codes(const uint8_t *codes, int M, int G, uint8_t *out);
+inline size_t bank_codes_bytes(int M, int G) {
+    return (size_t)((M + 63) / 64) * ((G + 31) / 32) * 2048;
+}
 // One tall batch-1 fp32 linear with the RMSNorm prologue (lut_group.hip):
 // it.x / it.y set, w the norm weight; both 16-byte aligned.
 int launch_tall_rms(const GroupItem &it, const float *w, float eps, hipStream_t st);

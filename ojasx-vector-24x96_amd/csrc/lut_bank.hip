@@ -1,0 +1,348 @@
+// lut_bank.hip -- many independent batch-1 LUT linears (block_dim 16, 256
+// centroids, fp32) in one launch, with gathers that never conflict in LDS.
+//
+// y_i[m] = (s_m * sum_g LUT_i[g, codes_i[m, g]] + bias_i[m]) + sum_j val_j x_i[col_j]
+// with LUT_i[g, k] = <x_i[16g .. 16g + 16), C_i[k]> (ojasx_lut_cpu.cpp:18-206).
+//
+// The LDS has 32 banks of 4 bytes; a wave's 4-byte reads run as two halves
+// of 32 lanes, and each half takes as many cycles as the most requests any
+// one bank receives.  A lane-per-row gather reads LUT[g][code] at random
+// banks (measured on gfx950: 7.5 cycles per wave read against 2.4 when every
+// lane of a half reads its own bank).  Here a lane owns a GROUP instead:
+//  * the LUT of a slice of 32 groups is stored code-major, word
+//    code * 64 + 32 * buffer + g, so group g lives in bank g whatever the code
+//    and the 32 lanes of a half-wave (groups 0..31) never share a bank;
+//  * lane (h, g) of a wave gathers group g of 32 rows (half h of the wave's 64
+//    rows), one accumulator per row, over the slices in order;
+//  * after the last slice a butterfly across the 32 lanes of each half
+//    (v_permlane16_swap, then DPP row mirror, half mirror and quad permutes;
+//    at each stage a lane keeps the half of its rows its lane bit selects)
+//    leaves row r's sum in lane r.
+// The byte address of an entry, code * 256 + 4 g + 128 * buffer, is one
+// v_perm_b32 of the code word and a per-lane constant.
+//
+// LUT build: per slice, LUT^T[256 x 32] = C[256 x 16] . X_s^T[16 x 32], wave
+// w computing centroids 32w .. 32w + 31 on v_mfma_f32_32x32x16_bf16 over an
+// exact three-way bf16 split of both operands (six products, fp32 sums:
+// fp32 accuracy at 2.7x fewer matrix cycles than eight fp32 32x32x2 steps).
+// Its output lane (h, n) holds rows 8(r/4) + 4h + r%4 of column n, so the
+// stores of each half-wave hit 32 distinct banks.  Lane half h supplies input
+// dimensions 8h .. 8h + 7 of both operands: 8 contiguous floats of x and of
+// its codebook row.
+// Two LUT buffers in the 64-word rows: slice s + 1 is built while slice s is
+// gathered, one barrier per slice.
+//
+// Codes come from the handle's bank layout [row block of 64][slice][group]
+// [64 rows]: a lane's 32 codes of a slice are 32 contiguous bytes, a wave's
+// 2 KB contiguous; kBPF slices are in flight in a register ring.
+// x is staged in LDS once (rows of 20 words per group, so the B operand's
+// 16-byte reads are conflict-free).  Outliers: after the slice loop the
+// workgroup's CSR range (its rows are contiguous) is loaded coalesced, the
+// products val * x[col] staged in the then free LUT space, and each lane adds
+// its row's products in CSR order.
+#include <algorithm>
+
+#include "common.h"
+
+namespace ojx {
+
+namespace {
+constexpr int kBW = 8;                  // waves per workgroup
+constexpr int kBNT = kBW * 64;          // threads per workgroup
+constexpr int kBRows = kBW * 64;        // rows per workgroup: 32 per half-wave
+constexpr int kBPF = 2;                 // slices of codes in flight
+constexpr int kLutRow = 64;             // words per code in the LUT: two buffers of 32 groups
+constexpr int kStagePT = 12;            // CSR entries staged per thread
+constexpr int kStage = kStagePT * kBNT; // per workgroup (4 B each, in the 64 KB LUT space)
+typedef float v16f __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ void bank_codes(const uint8_t *cp, int s, uint4 (&c)[2]) {
+    const uint4 *p = reinterpret_cast<const uint4 *>(cp + (size_t)s * 2048);
+    c[0] = gld(p);
+    c[1] = gld(p + 1);
+}
+
+// x staged in LDS with a row of kXRow words per group (16 used): the b128
+// reads of 8 lanes at groups g .. g + 7 then start at banks 20 g mod 32, 32
+// distinct banks.
+constexpr int kXRow = 20;
+__device__ __forceinline__ int xs_index(int k) { return (k >> 4) * kXRow + (k & 15); }
+
+// MFMA B operand of slice s: x[16 (32 s + g) + 8 h .. + 8) from the staged x,
+// the group clamped into the input (columns of groups past G are zeroed at
+// the store).
+__device__ __forceinline__ void bank_xop(const float *xs, int G, int s, int g, int h, float (&b)[8]) {
+    const float4 *p = reinterpret_cast<const float4 *>(xs + min(32 * s + g, G - 1) * kXRow + 8 * h);
+    const float4 u = p[0], v = p[1];
+    b[0] = u.x; b[1] = u.y; b[2] = u.z; b[3] = u.w;
+    b[4] = v.x; b[5] = v.y; b[6] = v.z; b[7] = v.w;
+}
+
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+
+// v = v1 + v2 + v3 exactly: v1 = bf16(v), v2 = bf16(v - v1), v3 = v - v1 - v2
+// (an fp32 value has 24 significant bits, each bf16 piece takes 8; the
+// remainders are exact in fp32).
+__device__ __forceinline__ void split3(const float (&v)[8], v8bf (&p)[3]) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const __bf16 h1 = (__bf16)v[i];
+        const float r1 = v[i] - (float)h1;
+        const __bf16 h2 = (__bf16)r1;
+        p[0][i] = h1;
+        p[1][i] = h2;
+        p[2][i] = (__bf16)(r1 - (float)h2);
+    }
+}
+
+// LUT tile = C_tile . X_s^T on v_mfma_f32_32x32x16_bf16 (16 input dims in one
+// step): with C = c1 + c2 + c3 and x = x1 + x2 + x3 split exactly into bf16
+// pieces, the six products c_i x_j with i + j <= 4 (each exact in fp32) are
+// accumulated in fp32, smallest first; the three left out are below 2^-24 of
+// the result.  A lane's 8 values are dimensions 8h .. 8h + 7 in both operands.
+__device__ __forceinline__ v16f bank_build(const v8bf (&a)[3], const v8bf (&b)[3]) {
+    v16f d = {};
+    d = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0], b[2], d, 0, 0, 0);
+    d = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[1], b[1], d, 0, 0, 0);
+    d = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[2], b[0], d, 0, 0, 0);
+    d = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0], b[1], d, 0, 0, 0);
+    d = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[1], b[0], d, 0, 0, 0);
+    d = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0], b[0], d, 0, 0, 0);
+    return d;
+}
+
+// LUT[32 w + m][g] of buffer buf <- column g of the wave's tile (0 for a group past G).
+__device__ __forceinline__ void bank_store(float *L, int buf, int w, int g, int h, bool gv,
+                                           const v16f &d) {
+    float *p = L + (32 * w + 4 * h) * kLutRow + 32 * buf + g;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) p[(8 * (r / 4) + (r % 4)) * kLutRow] = gv ? d[r] : 0.f;
+}
+
+// acc[j] += LUT[code of row j][g] for the 32 rows of the lane's half.
+__device__ __forceinline__ void bank_gather(const float *L, uint32_t gsel, const uint4 (&c)[2],
+                                            float (&acc)[32]) {
+    const uint32_t wd[8] = {c[0].x, c[0].y, c[0].z, c[0].w, c[1].x, c[1].y, c[1].z, c[1].w};
+    const char *Lb = reinterpret_cast<const char *>(L);
+    // eight reads in flight at a time: addresses, then the reads, then the adds
+#pragma unroll
+    for (int q2 = 0; q2 < 4; ++q2) {
+        float v[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            // byte 1 <- the code (byte i % 4 of its word), byte 0 <- 4 g + 128 buffer
+            const uint32_t a = __builtin_amdgcn_perm(wd[2 * q2 + i / 4], gsel,
+                                                     0x0c0c0400u + ((i % 4) << 8));
+            v[i] = *reinterpret_cast<const float *>(Lb + a);
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[8 * q2 + i] += v[i];
+    }
+}
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+
+// Sum of acc[r] over the 32 lanes of each half-wave, returned in lane r.
+__device__ __forceinline__ float bank_reduce(const float (&acc)[32], int lane) {
+    float a16[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {   // lanes 16..31 <-> 0..15: rows j (low lanes), j + 16 (high)
+        const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(acc[j]),
+                                                        __float_as_uint(acc[j + 16]), false, false);
+        a16[j] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    }
+    const bool b3 = lane & 8, b2 = lane & 4, b1 = lane & 2, b0 = lane & 1;
+    float a8[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {    // row mirror: lane i <-> 15 - i (bit 3 flips)
+        const float lo = a16[j] + dpp_f<0x140>(a16[j]);
+        const float hi = a16[j + 8] + dpp_f<0x140>(a16[j + 8]);
+        a8[j] = b3 ? hi : lo;
+    }
+    float a4[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {    // half mirror: lane i <-> 7 - i within 8 (bit 2 flips)
+        const float lo = a8[j] + dpp_f<0x141>(a8[j]);
+        const float hi = a8[j + 4] + dpp_f<0x141>(a8[j + 4]);
+        a4[j] = b2 ? hi : lo;
+    }
+    float a2[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {    // quad_perm [2,3,0,1]: bit 1 flips
+        const float lo = a4[j] + dpp_f<0x4E>(a4[j]);
+        const float hi = a4[j + 2] + dpp_f<0x4E>(a4[j + 2]);
+        a2[j] = b1 ? hi : lo;
+    }
+    const float lo = a2[0] + dpp_f<0xB1>(a2[0]);    // quad_perm [1,0,3,2]: bit 0 flips
+    const float hi = a2[1] + dpp_f<0xB1>(a2[1]);
+    return b0 ? hi : lo;
+}
+}  // namespace
+
+__global__ __launch_bounds__(kBNT) void lut_bank_kernel(const GroupItem *__restrict__ items,
+                                                        const int2 *__restrict__ work) {
+    __shared__ float L[256 * kLutRow];               // two LUT buffers; then the products
+    extern __shared__ float xs[];                    // [G][kXRow]: x (the B operands, outliers)
+    const int2 wk = work[blockIdx.x];                // (item, first row of the block)
+    const GroupItem it = items[wk.x];
+    const int base = wk.y;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, h = lane >> 5, g = lane & 31;
+    const int S = it.S32, K = it.K, G = K >> 4;
+    const int rb = min((base >> 6) + w, ((it.M + 63) >> 6) - 1);   // past M: a real block, unused
+    const uint8_t *cp = it.codes_b + ((size_t)rb * S * 32 + g) * 64 + 32 * h;
+    const int m = base + 64 * w + 32 * h + g;        // the row this lane finishes
+    const int mc = min(m, it.M - 1);
+    const bool outl = it.rowp != nullptr;
+
+    // ---- round trip 1: L2-resident operands first, then the HBM codes
+    float af[8];
+    {
+        const float4 *p = reinterpret_cast<const float4 *>(it.cb + (32 * w + g) * 16 + 8 * h);
+        const float4 u = gld(p), v = gld(p + 1);
+        af[0] = u.x; af[1] = u.y; af[2] = u.z; af[3] = u.w;
+        af[4] = v.x; af[5] = v.y; af[6] = v.z; af[7] = v.w;
+    }
+    const float sc = gld(it.scales + mc);
+    const float bs = it.bias ? gld(it.bias + mc) : 0.f;
+    int j0 = 0, j1 = 0, e0 = 0, e1 = 0;
+    if (outl) {
+        j0 = gld(it.rowp + mc);
+        j1 = m < it.M ? gld(it.rowp + mc + 1) : j0;
+        e0 = gld(it.rowp + base);
+        e1 = gld(it.rowp + min(base + kBRows, it.M));
+    }
+    uint4 ring[kBPF][2];
+#pragma unroll
+    for (int q = 0; q < kBPF; ++q) bank_codes(cp, min(q, S - 1), ring[q]);
+    {   // x: float4 i holds dims 4(i%4).. of group i/4; two loads in flight per thread
+        const float4 *x4 = reinterpret_cast<const float4 *>(it.x);
+        float4 *xs4 = reinterpret_cast<float4 *>(xs);
+        for (int i = tid; i < K / 4; i += 2 * kBNT) {
+            const int i2 = min(i + kBNT, K / 4 - 1);
+            const float4 u = gld(x4 + i), v = gld(x4 + i2);
+            xs4[(i >> 2) * (kXRow / 4) + (i & 3)] = u;
+            xs4[(i2 >> 2) * (kXRow / 4) + (i2 & 3)] = v;
+        }
+    }
+    const uint32_t gsel0 = 4u * g, gsel1 = 4u * g + 128u;
+    __syncthreads();
+
+    // ---- slice 0 into buffer 0
+    v8bf a[3], b[3];
+    split3(af, a);
+    float bf[8];
+    bank_xop(xs, G, 0, g, h, bf);
+    split3(bf, b);
+    {
+        const v16f d = bank_build(a, b);
+        bank_store(L, 0, w, g, h, g < G, d);
+    }
+    bank_xop(xs, G, min(1, S - 1), g, h, bf);
+    split3(bf, b);
+    __syncthreads();
+
+    // the outliers' loads (the workgroup's CSR range, coalesced) go out now
+    // and are consumed after the last slice, their latency under the slices
+    const int ne = min(e1 - e0, kStage);
+    int cl[kStagePT];
+    float vl[kStagePT];
+    if (ne > 0) {
+#pragma unroll
+        for (int i = 0; i < kStagePT; ++i) {
+            const int e = e0 + min(tid + i * kBNT, ne - 1);
+            cl[i] = gld(it.col + e);
+            vl[i] = gld(it.val + e);
+        }
+    }
+    float acc[32];
+#pragma unroll
+    for (int j = 0; j < 32; ++j) acc[j] = 0.f;
+    // Slice s uses ring slot q = s % kBPF, a constant in the unrolled body (no
+    // register moves of loads in flight); refills run unconditionally, clamped
+    // to the last slice (past it: a reload), so the loop body has no branch
+    // and the wait counts for the ring stay exact.  Slices 0 .. S-2 build the
+    // next slice's LUT beside their gathers; the last slice builds nothing.
+    auto one = [&](const int s, const int q) __attribute__((always_inline)) {
+        __builtin_amdgcn_sched_barrier(0);
+        const v16f d = bank_build(a, b);                         // slice s + 1
+        bank_gather(L, (s & 1) ? gsel1 : gsel0, ring[q], acc);   // slice s
+        bank_codes(cp, min(s + kBPF, S - 1), ring[q]);
+        bank_xop(xs, G, min(s + 2, S - 1), g, h, bf);
+        bank_store(L, (s + 1) & 1, w, g, h, 32 * (s + 1) + g < G, d);
+        split3(bf, b);
+        __syncthreads();
+    };
+    int sb = 0;
+    for (; sb + kBPF <= S - 1; sb += kBPF) {
+#pragma unroll
+        for (int q = 0; q < kBPF; ++q) one(sb + q, q);
+    }
+#pragma unroll
+    for (int q = 0; q < kBPF - 1; ++q)
+        if (sb + q < S - 1) one(sb + q, q);
+    __builtin_amdgcn_sched_barrier(0);
+    if ((S - 1) % kBPF == 0)                                     // the last slice
+        bank_gather(L, ((S - 1) & 1) ? gsel1 : gsel0, ring[0], acc);
+    else
+        bank_gather(L, ((S - 1) & 1) ? gsel1 : gsel0, ring[1], acc);
+    static_assert(kBPF == 2, "the last slice's ring slot is picked from two");
+    __syncthreads();
+
+    // ---- outliers: each staged entry's product val * x[col] goes to the LUT
+    //      space, then every lane sums its row's products in CSR order (the
+    //      entries past the stage from memory)
+    float *sp = L;
+    const float tot = bank_reduce(acc, lane);
+    if (ne > 0) {
+#pragma unroll
+        for (int i = 0; i < kStagePT; ++i)
+            if (tid + i * kBNT < ne) sp[tid + i * kBNT] = vl[i] * xs[xs_index(cl[i])];
+        __syncthreads();
+    }
+    float o = 0.f;
+    const int js = max(j0, min(j1, e0 + ne));
+    int j = j0;
+    for (; j + 4 <= js; j += 4) {
+        float pr[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) pr[u] = sp[j + u - e0];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) o += pr[u];
+    }
+    for (; j < js; ++j) o += sp[j - e0];
+    for (; j < j1; ++j) o += gld(it.val + j) * xs[xs_index(gld(it.col + j))];
+    float y = tot * sc;
+    if (it.bias) y += bs;
+    if (m < it.M) it.y[m] = y + o;
+}
+
+int launch_bank(const GroupItem *items_dev, const int2 *work_dev, int n_work, int max_K,
+                hipStream_t st) {
+    const size_t lds = (size_t)(max_K / 16) * kXRow * sizeof(float);
+    // The attribute bounds the dynamic part; with the 64 KB of static LUT the
+    // total passes the 64 KB default for any input.
+    static size_t granted = 0;
+    if (lds > granted) {
+        OJX_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(&lut_bank_kernel),
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+        granted = lds;
+    }
+    OJX_LAUNCH(lut_bank_kernel, dim3(n_work), dim3(kBNT), lds, st, items_dev, work_dev);
+    OJX_HIP(hipGetLastError());
+    return OJASX_OK;
+}
+
+void pack_bank_codes(const uint8_t *codes, int M, int G, uint8_t *out) {
+    const int S32 = (G + 31) / 32;
+    for (int m = 0; m < M; ++m) {
+        const uint8_t *row = codes + (size_t)m * G;
+        const size_t rb = (size_t)(m / 64), r = (size_t)(m % 64);
+        for (int gg = 0; gg < G; ++gg)
+            out[((rb * S32 + gg / 32) * 32 + gg % 32) * 64 + r] = row[gg];
+    }
+}
+
+}  // namespace ojx

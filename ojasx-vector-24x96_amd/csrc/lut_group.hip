@@ -1,114 +1,14 @@
-// lut_group.hip -- many independent LUT linears (block_dim 16, batch 1, fp32)
-// in one launch: the sustained-throughput path.
-//
-// y_i[m] = (s_m * sum_g LUT_i[g, codes_i[m, g]] + bias_i[m]) + sum_j val_j x_i[col_j]
-// for every instance i, with LUT_i[g, k] = <x_i[16g..16g+16), C_i[k]> (the
-// formula and epilogue order of ojasx_lut_cpu.cpp:18-206).
-//
-// A single batch-1 call is latency-bound and runs lut_dec_kernel, which dots
-// x with codebook rows read from LDS: 64 bytes of LDS per code byte, which
-// caps it near 1.2 TB/s of code bytes on a full chip.  Here a workgroup owns
-// 768 rows (3 per thread) of one instance and runs the MFMA-built LUT slice
-// loop of lut_slices.h over the handles' slice-major code tiles: 4 bytes of
-// LDS per code byte.  The MFMA build is a fixed 65,536 MACs per slice per
-// workgroup, amortised over the workgroup's rows.  The grid is sized to run in
-// one round: 72 VGPRs (one slice of codes in flight) and 27 KB of LDS give 6
-// workgroups of 4 waves per CU, 1536 on the chip, and 160 x 2560->6912 is
-// 1440 workgroups (measured 68.2 us; 4 rows per thread and two slices in
-// flight: 1120 workgroups over 1024 places, 80.7 us; 5 or 6 rows: 74 or 84 us).
+// lut_group.hip -- the grouped batch-1 LUT-GEMV entry point (its kernel is
+// lut_bank_kernel in lut_bank.hip) and the tall RMSNorm linear of the decoder
+// (lut_tall_rms_kernel, on the LUT slice loop of lut_slices.h).
 #include <algorithm>
+#include <cstring>
 #include <vector>
 
 #include "common.h"
 #include "lut_slices.h"
 
 namespace ojx {
-
-namespace {
-constexpr int kPF = 1;                  // slices of codes in flight
-constexpr int kGNT = 256;               // threads per workgroup (4 waves)
-constexpr int kRPT = 3;                 // rows per thread
-constexpr int kGRows = kGNT * kRPT;     // rows per workgroup
-}  // namespace
-
-__global__ __launch_bounds__(kGNT) __attribute__((amdgpu_waves_per_eu(6))) void lut_group_kernel(const GroupItem *__restrict__ items) {
-    __shared__ float L[slices::kLutFloats];
-    extern __shared__ float xs[];                     // [S * 256], zero past K
-    const GroupItem it = items[blockIdx.y];
-    const int base = (int)blockIdx.x * kGRows;
-    if (base >= it.M) return;                         // whole workgroup
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    const int S = it.S, KS = S * 256;
-    const bool outl = it.rowp != nullptr;
-
-    // ---- round trip 1, L2-resident data first (vmcnt counts in order, so the
-    //      x stores into LDS then do not wait for the HBM code loads): x, the
-    //      codebook operands (wave w: centroid tiles 4w..4w+3), row bounds
-    const int nx4 = KS / 4;
-    float4 xv[4];
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-        const int e = min(tid + u * kGNT, nx4 - 1) * 4;
-        xv[u] = gld(reinterpret_cast<const float4 *>(it.x + min(e, it.K - 4)));
-        if (e >= it.K) xv[u] = make_float4(0.f, 0.f, 0.f, 0.f);
-    }
-    float bop[4][4];
-    slices::load_cb_operands<4>(it.cb, w, lane, bop);
-    int j0[kRPT] = {}, j1[kRPT] = {};               // the rows' CSR ranges
-    if (outl) {
-#pragma unroll
-        for (int r2 = 0; r2 < kRPT; ++r2) {
-            const int m = min(base + tid + kGNT * r2, it.M - 1);
-            j0[r2] = gld(it.rowp + m);
-            j1[r2] = gld(it.rowp + m + 1);
-        }
-    }
-    // ---- then HBM: codes of slices 0..kPF-1 (rows past Mp clamp: loaded, never stored)
-    int row[kRPT];
-#pragma unroll
-    for (int r2 = 0; r2 < kRPT; ++r2) row[r2] = min(base + tid + kGNT * r2, it.Mp - 1);
-    uint4 ring[kPF][kRPT];
-    slices::ring_start(it.codes, row, it.Mp, 0, S, ring);
-#pragma unroll
-    for (int u = 0; u < 4; ++u)
-        if (tid + u * kGNT < nx4) reinterpret_cast<float4 *>(xs)[tid + u * kGNT] = xv[u];
-    for (int i = tid + 4 * kGNT; i < nx4; i += kGNT) {   // K > 4096: the rest of x
-        const int e = i * 4;
-        reinterpret_cast<float4 *>(xs)[i] =
-            e < it.K ? gld(reinterpret_cast<const float4 *>(it.x + e)) : make_float4(0.f, 0.f, 0.f, 0.f);
-    }
-    __syncthreads();
-
-    float acc[kRPT] = {};
-    slices::slice_loop<4, kRPT, false, kPF>(xs, L, bop, it.codes, row, it.Mp, 0, S, w, lane, ring, acc);
-
-    // ---- epilogue: (s_m * sum + bias) + the row's CSR outliers (4 loads in
-    //      flight; batching both rows' entries measured slower)
-#pragma unroll
-    for (int r2 = 0; r2 < kRPT; ++r2) {
-        const int m = base + tid + kGNT * r2;
-        if (m >= it.M) continue;
-        float o = 0.f;
-        if (outl) {
-            int j = j0[r2];
-            for (; j + 4 <= j1[r2]; j += 4) {
-                int c[4];
-                float v[4];
-#pragma unroll
-                for (int u = 0; u < 4; ++u) {
-                    c[u] = gld(it.col + j + u);
-                    v[u] = gld(it.val + j + u);
-                }
-#pragma unroll
-                for (int u = 0; u < 4; ++u) o += v[u] * xs[c[u]];
-            }
-            for (; j < j1[r2]; ++j) o += gld(it.val + j) * xs[gld(it.col + j)];
-        }
-        float y = acc[r2] * gld(it.scales + m);
-        if (it.bias) y += gld(it.bias + m);
-        it.y[m] = y + o;
-    }
-}
 
 // One tall batch-1 fp32 linear with the RMSNorm prologue (a decoder's gate/up
 // and LM head): y[m] = ((s_m * r * sum_g LUT[g, code]) + bias_m) + r * outliers,
@@ -224,11 +124,51 @@ int launch_tall_rms(const GroupItem &it, const float *w, float eps, hipStream_t 
     return OJASX_OK;
 }
 
-// Per host thread: the staged item array.
+// Per host thread: the item arrays of the last kGroupRing calls, written in
+// pinned host memory and copied to the device asynchronously (a pageable
+// source would make every call wait for its copy).  Slot k is reused only
+// after the event recorded behind the launch that read it has completed, so
+// neither its host nor its device copy is overwritten while in use, whatever
+// stream the calls run on.
+// A call whose item array equals the last one uploaded (same handles, x and y
+// pointers: the steady state of a serving loop) launches on that device copy
+// without a new upload.
+// An upload is the item array followed by the work list of the bank kernel
+// ((item, first row) per 512-row block).
+constexpr int kGroupRing = 4;
 struct GroupWork {
-    DevBuf items;
-    std::vector<GroupItem> host;
-    ~GroupWork() { items.release(); }
+    DevBuf items;                       // [kGroupRing][cap] bytes on the device
+    unsigned char *pinned = nullptr;    // [kGroupRing][cap] bytes of pinned host memory
+    size_t cap = 0;
+    hipEvent_t ev[kGroupRing] = {};
+    int slot = 0;
+    int last_slot = -1;                 // the slot holding the last upload
+    size_t last_bytes = 0;
+    std::vector<unsigned char> host;
+    int reserve(size_t bytes) {
+        if (bytes <= cap) return OJASX_OK;
+        for (hipEvent_t &e : ev)
+            if (e) OJX_HIP(hipEventSynchronize(e));
+        if (pinned) (void)hipHostFree(pinned);
+        pinned = nullptr;
+        cap = 0;
+        const size_t n = round_up(std::max<size_t>(bytes, 64 << 10), 256);
+        OJX_HIP(hipHostMalloc(reinterpret_cast<void **>(&pinned), n * kGroupRing,
+                              hipHostMallocDefault));
+        last_slot = -1;
+        const int rc = items.ensure(n * kGroupRing);
+        if (rc) return rc;
+        for (hipEvent_t &e : ev)
+            if (!e) OJX_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming));
+        cap = n;
+        return OJASX_OK;
+    }
+    ~GroupWork() {
+        items.release();
+        if (pinned) (void)hipHostFree(pinned);
+        for (hipEvent_t e : ev)
+            if (e) (void)hipEventDestroy(e);
+    }
 };
 static thread_local GroupWork t_group;
 
@@ -247,13 +187,15 @@ OJASX_API int ojasx_linear_forward_grouped_device(const OjasxLinearHandle *handl
         return OJASX_ERR_INVALID;
     }
     GroupWork &gw = t_group;
-    gw.host.resize(count);
-    int max_blocks = 0;
-    size_t lds = 0;
+    const size_t item_bytes = round_up(sizeof(GroupItem) * count, 16);
+    gw.host.assign(item_bytes, 0);                   // padding bytes too, for the comparison
+    GroupItem *host = reinterpret_cast<GroupItem *>(gw.host.data());
+    int rc = OJASX_OK;
+    int max_K = 0;
     for (int i = 0; i < count; ++i) {
         if (!handles[i] || !xs[i] || !ys[i]) return OJASX_ERR_NULL;
-        GroupItem &it = gw.host[i];
-        int rc = linear_items(handles[i], &it);
+        GroupItem &it = host[i];
+        rc = linear_items(handles[i], &it);
         if (rc) return rc;
         if (reinterpret_cast<uintptr_t>(xs[i]) & 15) {
             set_error("grouped linear %d: x must be 16-byte aligned", i);
@@ -261,22 +203,37 @@ OJASX_API int ojasx_linear_forward_grouped_device(const OjasxLinearHandle *handl
         }
         it.x = xs[i];
         it.y = ys[i];
-        max_blocks = std::max(max_blocks, (it.M + kGRows - 1) / kGRows);
-        lds = std::max(lds, (size_t)it.S * 256 * sizeof(float));
+        max_K = std::max(max_K, it.K);
     }
+    // the bank kernel's work list: every 512-row block of every item, item-major
+    int n_work = 0;
+    for (int i = 0; i < count; ++i) n_work += (host[i].M + kBankRows - 1) / kBankRows;
+    const size_t bytes = item_bytes + sizeof(int2) * (size_t)n_work;
+    gw.host.resize(bytes);
+    host = reinterpret_cast<GroupItem *>(gw.host.data());
+    int2 *wl = reinterpret_cast<int2 *>(gw.host.data() + item_bytes);
+    for (int i = 0, t = 0; i < count; ++i)
+        for (int b = 0; b < host[i].M; b += kBankRows) wl[t++] = make_int2(i, b);
+    rc = gw.reserve(bytes);
+    if (rc) return rc;
     hipStream_t st = static_cast<hipStream_t>(stream);
-    int rc = gw.items.ensure(sizeof(GroupItem) * count);
+    int k = gw.last_slot;
+    if (k < 0 || gw.last_bytes != bytes ||
+        memcmp(gw.pinned + (size_t)k * gw.cap, gw.host.data(), bytes) != 0) {
+        k = gw.slot;
+        gw.slot = (k + 1) % kGroupRing;
+        if (gw.ev[k]) OJX_HIP(hipEventSynchronize(gw.ev[k]));   // slot k's last launch is done
+        memcpy(gw.pinned + (size_t)k * gw.cap, gw.host.data(), bytes);
+        OJX_HIP(hipMemcpyAsync(gw.items.as<unsigned char>() + (size_t)k * gw.cap,
+                               gw.pinned + (size_t)k * gw.cap, bytes, hipMemcpyHostToDevice, st));
+        gw.last_slot = k;
+        gw.last_bytes = bytes;
+    }
+    GroupItem *dev = reinterpret_cast<GroupItem *>(gw.items.as<unsigned char>() + (size_t)k * gw.cap);
+    const int2 *dev_work = reinterpret_cast<const int2 *>(reinterpret_cast<unsigned char *>(dev) + item_bytes);
+    rc = launch_bank(dev, dev_work, n_work, max_K, st);
     if (rc) return rc;
-    OJX_HIP(hipMemcpyAsync(gw.items.ptr, gw.host.data(), sizeof(GroupItem) * count,
-                           hipMemcpyHostToDevice, st));
-    // the limit covers the static LUT buffers too (their sum passes 64 KB for K > 7000)
-    static size_t granted = 0;
-    rc = ensure_dyn_lds(reinterpret_cast<const void *>(&lut_group_kernel),
-                        lds + slices::lut_bytes(false), &granted);
-    if (rc) return rc;
-    OJX_LAUNCH(lut_group_kernel, dim3(max_blocks, count), dim3(kGNT), lds, st,
-               gw.items.as<GroupItem>());
-    OJX_HIP(hipGetLastError());
+    OJX_HIP(hipEventRecord(gw.ev[k], st));
     return OJASX_OK;
 }
 

@@ -539,11 +539,11 @@ struct Linear {
     int K = 0, M = 0, D = 0, Kcb = 0, G = 0, S = 0, Mp = 0;
     bool has_bias = false;
     size_t nnz = 0;
-    DevBuf codes, codebook, scales, bias, rowp, col, val;
+    DevBuf codes, codes_b, codebook, scales, bias, rowp, col, val;
     DevBuf lut, xstage, ystage;
     ~Linear() {
-        for (DevBuf *b : {&codes, &codebook, &scales, &bias, &rowp, &col, &val, &lut, &xstage,
-                          &ystage})
+        for (DevBuf *b : {&codes, &codes_b, &codebook, &scales, &bias, &rowp, &col, &val, &lut,
+                          &xstage, &ystage})
             b->release();
     }
 };
@@ -768,6 +768,8 @@ int linear_items(const void *h, GroupItem *it) {
         return OJASX_ERR_INVALID;
     }
     it->codes = L->codes.as<uint8_t>();
+    it->codes_b = L->codes_b.as<uint8_t>();
+    it->S32 = (L->G + 31) / 32;
     it->cb = L->codebook.as<float>();
     it->scales = L->scales.as<float>();
     it->bias = L->has_bias ? L->bias.as<float>() : nullptr;
@@ -899,6 +901,11 @@ OJASX_API OjasxLinearHandle ojasx_create_linear(int in_features, int out_feature
     std::vector<float> sc(L->M, 1.f);
     if (scales_data) memcpy(sc.data(), scales_data, sizeof(float) * L->M);
     int rc = upload(L->codes, packed.data(), packed.size());
+    if (!rc && L->D == 16) {   // the grouped kernel's layout (block_dim 16 only)
+        std::vector<uint8_t> bank(bank_codes_bytes(L->M, L->G), 0);
+        if (codes_data) pack_bank_codes(codes_data, L->M, L->G, bank.data());
+        rc = upload(L->codes_b, bank.data(), bank.size());
+    }
     if (!rc) rc = upload(L->codebook, cb.data(), cb.size() * sizeof(float));
     if (!rc) rc = upload(L->scales, sc.data(), sc.size() * sizeof(float));
     if (!rc && bias_data) {
