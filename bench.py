@@ -323,12 +323,69 @@ def bench_batched(b, handles, base, wbytes, args):
 
 # --- MoE ----------------------------------------------------------------------------
 
+def moe_sustained(b, banks, E, K, per_expert, T, n_layers=16, replays=5):
+    """n_layers MoE layers, each on the next of the two alternating expert
+    banks with its own device routing, layer i's output the input of layer
+    i + 1, captured as one HIP graph and replayed after a flush: the steady
+    state of a deep MoE stack (302 MB of banks per pair of layers).  The
+    replay's output is compared with an eager run of the same layers."""
+    torch, L = b.torch, b.L
+    H = banks[0][1]["x"].shape[1]
+    r = np.random.default_rng(1000 + T)
+    logits = torch.from_numpy(r.normal(size=(n_layers, T, E)).astype(np.float32)).to(b.dev)
+    idx = torch.empty(n_layers, T, K, dtype=torch.int32, device=b.dev)
+    w = torch.empty(n_layers, T, K, dtype=torch.float32, device=b.dev)
+    for i in range(n_layers):
+        assert L.ojasx_moe_route_device(VP(logits[i].data_ptr()), T, E, K, 0, VP(idx[i].data_ptr()),
+                                        VP(w[i].data_ptr()), b.sp) == 0
+    torch.cuda.synchronize()
+    distinct = np.array([len(np.unique(a)) for a in idx.cpu().numpy().reshape(n_layers, -1)])
+    xs = [torch.zeros(T, H, device=b.dev) for _ in range(n_layers + 1)]
+    xs[0].copy_(torch.from_numpy(banks[0][1]["x"][:T]))
+
+    def layers(sp):
+        for i in range(n_layers):
+            rc = L.ojasx_moe_forward_device(banks[i % 2][0], VP(xs[i].data_ptr()),
+                                            VP(idx[i].data_ptr()), VP(w[i].data_ptr()),
+                                            VP(xs[i + 1].data_ptr()), T, K, 0, sp)
+            assert rc == 0, L.ojasx_get_last_error()
+
+    layers(b.sp)                                     # eager: sizes every workspace
+    torch.cuda.synchronize()
+    eager = xs[n_layers].clone()
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s), torch.cuda.graph(g, stream=s):
+        layers(VP(s.cuda_stream))
+    torch.cuda.synchronize()
+    g.replay()
+    torch.cuda.synchronize()
+    same = bool(torch.equal(xs[n_layers], eager))
+    b.flush()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(b.stream)
+    for _ in range(replays):
+        g.replay()
+    e1.record(b.stream)
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / (replays * n_layers)
+    code = float(distinct.mean()) * per_expert
+    del g
+    return {"us_per_layer": round(us, 3), "layers": n_layers, "replays": replays,
+            "distinct_experts_mean": float(distinct.mean()), "code_bytes_per_layer": int(code),
+            "achieved_code_GBs": round(code / (us * 1e-6) / 1e9, 2),
+            "frac_code": round(code / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 5),
+            "graph_equals_eager": same}
+
+
 def bench_moe(b, args):
     """512-expert top-10 MoE layer (H 2048, I 768), T = 1 and 16 tokens.  Two
     expert banks (2 x 151 MB, above the 256 MB Infinity Cache) alternate and
     every step has its own routing (routed on the device); code bytes count
     the distinct experts a call reads.  CPU: the reference engine, whose API
-    is one token per call (16 calls for T = 16)."""
+    is one token per call (16 calls for T = 16).  "sustained": 16 layers of
+    T = 16, 64 and 256 tokens in one HIP graph."""
     from oracle import ref
     torch, L = b.torch, b.L
     gen = b.pkg.synthetic
@@ -336,7 +393,7 @@ def bench_moe(b, args):
     E, H, I, K = 512, 2048, 768, 10
     banks = []
     for seed in (11, 12):
-        m = gen.moe(E=E, H=H, I=I, T=16, seed=seed)
+        m = gen.moe(E=E, H=H, I=I, T=256, seed=seed)
         h = L.ojasx_create_moe(E, H, I, K, 16, p(m["cb_in"]), p(m["cb_down"]), p(m["gu_codes"]),
                                p(m["gu_scales"]), p(m["dn_codes"]), p(m["dn_scales"]))
         assert h, L.ojasx_get_last_error()
@@ -388,6 +445,8 @@ def bench_moe(b, args):
                 res[f"T{T}"]["cpu_baseline"] = {
                     "value": round(s * 1e6, 1), "unit": "us/call", "cores": 1, "kind": "reference",
                     "sample": f"{n} calls of {T} token(s) (one reference call per token), 1 thread"}
+        res["sustained"] = {f"T{T}": moe_sustained(b, banks, E, K, per_expert, T)
+                            for T in (16, 64, 256)}
     finally:
         for h, _ in banks:
             L.ojasx_destroy_moe(h)

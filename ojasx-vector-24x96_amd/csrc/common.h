@@ -80,12 +80,28 @@ int linear_items(const void *h, GroupItem *it);
 constexpr int kBankRows = 512;
 int launch_bank(const GroupItem *items_dev, const int2 *work_dev, int n_work, int max_K,
                 hipStream_t st);
-// Bank layout of [M][G] codes: tile (row block b of 64 rows, slice s of 32
-// groups, group g) holds the 64 rows' codes of that group; 0 past M and G.
+// Bank layout of [M][G] codes: [row block of 64 rows][group][64 rows], 0 past M.
 void pack_bank_codes(const uint8_t *codes, int M, int G, uint8_t *out);
-inline size_t bank_codes_bytes(int M, int G) {
-    return (size_t)((M + 63) / 64) * ((G + 31) / 32) * 2048;
-}
+inline size_t bank_codes_bytes(int M, int G) { return (size_t)((M + 63) / 64) * G * 64; }
+// Readable bytes allocated after the last block: a partial last slice reads up
+// to 31 groups x 64 bytes past its block.
+constexpr size_t kBankSlack = 2048;
+// MoE stages on the bank kernel (lut_bank.hip): the plan (routed pairs sorted
+// by expert into work lists of (pair, first row)), then one launch per stage.
+int launch_moe_plan(const int *idx, const float *w, int P, int E, int nb_gu, int nb_dn,
+                    int2 *work_gu, int2 *work_dn, int *n_work, hipStream_t st);
+struct MoEBankLaunch {
+    const uint8_t *codes_b;     // [E][bank layout]
+    size_t expert_bytes;
+    const float *cb, *scales;   // [256][16], [E][M]
+    const void *x;              // xs 0: [T][K] fp32, 1: bf16, 2: [P][2K] fp32 gate|up rows
+    float *y;                   // [P][M]
+    const int *idx;
+    const int2 *work;
+    const int *n_work;          // device count of work entries
+    int M, K, k, max_work, xs;
+};
+int launch_moe_bank(const MoEBankLaunch &l, hipStream_t st);
 // One tall batch-1 fp32 linear with the RMSNorm prologue (lut_group.hip):
 // it.x / it.y set, w the norm weight; both 16-byte aligned.
 int launch_tall_rms(const GroupItem &it, const float *w, float eps, hipStream_t st);

@@ -56,8 +56,13 @@ constexpr int kStagePT = 12;            // CSR entries staged per thread
 constexpr int kStage = kStagePT * kBNT; // per workgroup (4 B each, in the 64 KB LUT space)
 typedef float v16f __attribute__((ext_vector_type(16)));
 
+// Codes of slice s for lane (h, g) from the block's bank layout [G][64 rows]:
+// cp points at group g, rows 32h...  In a partial last slice the lanes past G
+// read the bytes after the block (the next block's, or the kBankSlack bytes
+// allocated after the last one): their LUT column is 0, so any code adds 0.
+// (A clamp here would cost the loop its immediate load offsets.)
 __device__ __forceinline__ void bank_codes(const uint8_t *cp, int s, uint4 (&c)[2]) {
-    const uint4 *p = reinterpret_cast<const uint4 *>(cp + (size_t)s * 2048);
+    const uint4 *p = reinterpret_cast<const uint4 *>(cp + 2048 * s);
     c[0] = gld(p);
     c[1] = gld(p + 1);
 }
@@ -182,51 +187,82 @@ __device__ __forceinline__ float bank_reduce(const float (&acc)[32], int lane) {
 }
 }  // namespace
 
-__global__ __launch_bounds__(kBNT) void lut_bank_kernel(const GroupItem *__restrict__ items,
-                                                        const int2 *__restrict__ work) {
-    __shared__ float L[256 * kLutRow];               // two LUT buffers; then the products
-    extern __shared__ float xs[];                    // [G][kXRow]: x (the B operands, outliers)
-    const int2 wk = work[blockIdx.x];                // (item, first row of the block)
-    const GroupItem it = items[wk.x];
-    const int base = wk.y;
+// One 512-row block of one matrix: its bank-layout codes, codebook, scales,
+// optional bias and CSR outliers, input and output.
+struct BankBlock {
+    const uint8_t *codes_b;     // the matrix's bank layout [ceil(M/64)][G][64]
+    const float *cb;            // [256][16]
+    const float *scales;        // [M]
+    const float *bias;          // [M] or null
+    const int *rowp;            // [M + 1] or null
+    const int *col;
+    const float *val;
+    const void *x;              // XS_F32: [K] fp32; XS_BF16: [K] bf16; XS_SWIGLU: [2K] fp32
+    float *y;                   // [M]
+    int K, M, base;
+};
+enum { XS_F32 = 0, XS_BF16 = 1, XS_SWIGLU = 2 };
+
+// x (or silu(gate) * up, silu(v) = v / (1 + exp(-v))) into LDS, float4 i
+// holding dims 4(i%4).. of group i/4; two loads in flight per thread.
+template <int XS>
+__device__ __forceinline__ void bank_stage_x(const void *x, int K, float *xs, int tid) {
+    float4 *xs4 = reinterpret_cast<float4 *>(xs);
+    for (int i = tid; i < K / 4; i += 2 * kBNT) {
+        const int i2 = min(i + kBNT, K / 4 - 1);
+        float4 u, v;
+        if constexpr (XS == XS_F32) {
+            const float4 *x4 = static_cast<const float4 *>(x);
+            u = gld(x4 + i);
+            v = gld(x4 + i2);
+        } else if constexpr (XS == XS_BF16) {
+            const __hip_bfloat16 *xb = static_cast<const __hip_bfloat16 *>(x);
+            u = load4_act(xb, (size_t)4 * i);
+            v = load4_act(xb, (size_t)4 * i2);
+        } else {
+            const float4 *g4 = static_cast<const float4 *>(x), *u4 = g4 + K / 4;
+            const float4 ga = gld(g4 + i), ua = gld(u4 + i), gb = gld(g4 + i2), ub = gld(u4 + i2);
+            auto sw = [](float gg, float uu) { return gg / (1.f + expf(-gg)) * uu; };
+            u = make_float4(sw(ga.x, ua.x), sw(ga.y, ua.y), sw(ga.z, ua.z), sw(ga.w, ua.w));
+            v = make_float4(sw(gb.x, ub.x), sw(gb.y, ub.y), sw(gb.z, ub.z), sw(gb.w, ub.w));
+        }
+        xs4[(i >> 2) * (kXRow / 4) + (i & 3)] = u;
+        xs4[(i2 >> 2) * (kXRow / 4) + (i2 & 3)] = v;
+    }
+}
+
+template <int XS>
+__device__ __forceinline__ void bank_block(const BankBlock &bb, float *L, float *xs) {
+    const int base = bb.base;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, h = lane >> 5, g = lane & 31;
-    const int S = it.S32, K = it.K, G = K >> 4;
-    const int rb = min((base >> 6) + w, ((it.M + 63) >> 6) - 1);   // past M: a real block, unused
-    const uint8_t *cp = it.codes_b + ((size_t)rb * S * 32 + g) * 64 + 32 * h;
+    const int K = bb.K, G = K >> 4, S = (G + 31) >> 5;
+    const int rb = min((base >> 6) + w, ((bb.M + 63) >> 6) - 1);   // past M: a real block, unused
+    const uint8_t *cp = bb.codes_b + ((size_t)rb * G + g) * 64 + 32 * h;
     const int m = base + 64 * w + 32 * h + g;        // the row this lane finishes
-    const int mc = min(m, it.M - 1);
-    const bool outl = it.rowp != nullptr;
+    const int mc = min(m, bb.M - 1);
+    const bool outl = bb.rowp != nullptr;
 
     // ---- round trip 1: L2-resident operands first, then the HBM codes
     float af[8];
     {
-        const float4 *p = reinterpret_cast<const float4 *>(it.cb + (32 * w + g) * 16 + 8 * h);
+        const float4 *p = reinterpret_cast<const float4 *>(bb.cb + (32 * w + g) * 16 + 8 * h);
         const float4 u = gld(p), v = gld(p + 1);
         af[0] = u.x; af[1] = u.y; af[2] = u.z; af[3] = u.w;
         af[4] = v.x; af[5] = v.y; af[6] = v.z; af[7] = v.w;
     }
-    const float sc = gld(it.scales + mc);
-    const float bs = it.bias ? gld(it.bias + mc) : 0.f;
+    const float sc = gld(bb.scales + mc);
+    const float bs = bb.bias ? gld(bb.bias + mc) : 0.f;
     int j0 = 0, j1 = 0, e0 = 0, e1 = 0;
     if (outl) {
-        j0 = gld(it.rowp + mc);
-        j1 = m < it.M ? gld(it.rowp + mc + 1) : j0;
-        e0 = gld(it.rowp + base);
-        e1 = gld(it.rowp + min(base + kBRows, it.M));
+        j0 = gld(bb.rowp + mc);
+        j1 = m < bb.M ? gld(bb.rowp + mc + 1) : j0;
+        e0 = gld(bb.rowp + base);
+        e1 = gld(bb.rowp + min(base + kBRows, bb.M));
     }
     uint4 ring[kBPF][2];
 #pragma unroll
     for (int q = 0; q < kBPF; ++q) bank_codes(cp, min(q, S - 1), ring[q]);
-    {   // x: float4 i holds dims 4(i%4).. of group i/4; two loads in flight per thread
-        const float4 *x4 = reinterpret_cast<const float4 *>(it.x);
-        float4 *xs4 = reinterpret_cast<float4 *>(xs);
-        for (int i = tid; i < K / 4; i += 2 * kBNT) {
-            const int i2 = min(i + kBNT, K / 4 - 1);
-            const float4 u = gld(x4 + i), v = gld(x4 + i2);
-            xs4[(i >> 2) * (kXRow / 4) + (i & 3)] = u;
-            xs4[(i2 >> 2) * (kXRow / 4) + (i2 & 3)] = v;
-        }
-    }
+    bank_stage_x<XS>(bb.x, K, xs, tid);
     const uint32_t gsel0 = 4u * g, gsel1 = 4u * g + 128u;
     __syncthreads();
 
@@ -253,8 +289,8 @@ __global__ __launch_bounds__(kBNT) void lut_bank_kernel(const GroupItem *__restr
 #pragma unroll
         for (int i = 0; i < kStagePT; ++i) {
             const int e = e0 + min(tid + i * kBNT, ne - 1);
-            cl[i] = gld(it.col + e);
-            vl[i] = gld(it.val + e);
+            cl[i] = gld(bb.col + e);
+            vl[i] = gld(bb.val + e);
         }
     }
     float acc[32];
@@ -313,35 +349,204 @@ __global__ __launch_bounds__(kBNT) void lut_bank_kernel(const GroupItem *__restr
         for (int u = 0; u < 4; ++u) o += pr[u];
     }
     for (; j < js; ++j) o += sp[j - e0];
-    for (; j < j1; ++j) o += gld(it.val + j) * xs[xs_index(gld(it.col + j))];
+    for (; j < j1; ++j) o += gld(bb.val + j) * xs[xs_index(gld(bb.col + j))];
     float y = tot * sc;
-    if (it.bias) y += bs;
-    if (m < it.M) it.y[m] = y + o;
+    if (bb.bias) y += bs;
+    if (m < bb.M) bb.y[m] = y + o;
 }
+
+// The grouped linear call: workgroup i takes work[i] = (item, first row).
+__global__ __launch_bounds__(kBNT) void lut_bank_kernel(const GroupItem *__restrict__ items,
+                                                        const int2 *__restrict__ work) {
+    __shared__ float L[256 * kLutRow];               // two LUT buffers; then the products
+    extern __shared__ float xs[];                    // [G][kXRow]: x (the B operands, outliers)
+    const int2 wk = work[blockIdx.x];
+    const GroupItem it = items[wk.x];
+    const BankBlock bb{it.codes_b, it.cb, it.scales, it.bias, it.rowp, it.col, it.val,
+                       it.x, it.y, it.K, it.M, wk.y};
+    bank_block<XS_F32>(bb, L, xs);
+}
+
+// MoE stages on the routed pairs (no outliers, no bias): gate/up (x = the
+// pair's token row, M = 2I gate then up rows) or down (x = silu(gate) * up of
+// the pair's gate/up row, M = H).  work[] = (pair, first row) comes from the
+// plan kernel, sorted by expert; workgroup i takes position
+// (i % 8) * ceil(n / 8) + i / 8, so each of the 8 XCDs (workgroups go to XCD
+// i % 8) walks a contiguous stretch of the sorted list and the pairs of one
+// expert read its codes back to back through one L2.
+struct MoEBankParams {
+    const uint8_t *codes_b;     // [E][bank layout of M x G]
+    size_t expert_bytes;
+    const float *cb;            // [256][16]
+    const float *scales;        // [E][M]
+    const void *x;              // gate/up: [T][K]; down: [P][2K] fp32
+    float *y;                   // [P][M]
+    const int *idx;             // [P] expert of each pair
+    const int2 *work;           // [n] (pair, first row)
+    const int *n_work;          // n
+    int M, K, k;                // rows, inputs, slots per token
+};
+
+template <int XS>
+__global__ __launch_bounds__(kBNT) void moe_bank_kernel(MoEBankParams p) {
+    __shared__ float L[256 * kLutRow];
+    extern __shared__ float xs[];
+    const int n = *p.n_work;
+    const int q = (n + 7) >> 3;
+    const int pos = (int)(blockIdx.x & 7) * q + (int)(blockIdx.x >> 3);
+    if (pos >= n || (int)(blockIdx.x >> 3) >= q) return;
+    const int2 wk = p.work[pos];
+    const int pr = wk.x, e = p.idx[pr];
+    const void *x;
+    if constexpr (XS == XS_SWIGLU)
+        x = static_cast<const float *>(p.x) + (size_t)pr * 2 * p.K;
+    else if constexpr (XS == XS_BF16)
+        x = static_cast<const __hip_bfloat16 *>(p.x) + (size_t)(pr / p.k) * p.K;
+    else
+        x = static_cast<const float *>(p.x) + (size_t)(pr / p.k) * p.K;
+    const BankBlock bb{p.codes_b + (size_t)e * p.expert_bytes, p.cb,
+                       p.scales + (size_t)e * p.M, nullptr, nullptr, nullptr, nullptr,
+                       x, p.y + (size_t)pr * p.M, p.K, p.M, wk.y};
+    bank_block<XS>(bb, L, xs);
+}
+
+// The MoE plan, one workgroup: the valid routed pairs (expert id in [0, E),
+// |w| >= 1e-8) sorted by expert (counting sort; the order within an expert
+// does not change any result), expanded into the gate/up and down work lists
+// ordered (expert, row block, pair); n_work[0] / n_work[1] = their lengths.
+__global__ __launch_bounds__(1024) void moe_plan_kernel(const int *idx, const float *w, int P, int E,
+                                                        int nb_gu, int nb_dn, int2 *work_gu,
+                                                        int2 *work_dn, int *n_work) {
+    extern __shared__ int sh[];
+    int *cnt = sh, *start = sh + E, *cur = sh + 2 * E, *sorted = sh + 3 * E;
+    __shared__ int wsum[16], total;
+    const int tid = threadIdx.x, NT = blockDim.x, lane = tid & 63, wv = tid >> 6;
+    for (int e = tid; e < E; e += NT) cnt[e] = 0;
+    __syncthreads();
+    for (int q = tid; q < P; q += NT) {
+        const int e = idx[q];
+        if (e >= 0 && e < E && fabsf(w[q]) >= 1e-8f) atomicAdd(&cnt[e], 1);
+    }
+    __syncthreads();
+    // exclusive prefix over the experts: thread tid owns a run of per experts;
+    // run sums scanned within each wave (shuffles), then across the waves
+    const int per = (E + NT - 1) / NT, e0 = min(E, tid * per), e1 = min(E, e0 + per);
+    int s = 0;
+    for (int e = e0; e < e1; ++e) s += cnt[e];
+    int incl = s;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const int v = __shfl_up(incl, d, 64);
+        if (lane >= d) incl += v;
+    }
+    if (lane == 63) wsum[wv] = incl;
+    __syncthreads();
+    if (tid == 0) {
+        int run = 0;
+        for (int i = 0; i < NT / 64; ++i) {
+            const int v = wsum[i];
+            wsum[i] = run;
+            run += v;
+        }
+        total = run;
+        n_work[0] = run * nb_gu;
+        n_work[1] = run * nb_dn;
+    }
+    __syncthreads();
+    int run = wsum[wv] + incl - s;
+    for (int e = e0; e < e1; ++e) {
+        start[e] = run;
+        cur[e] = run;
+        run += cnt[e];
+    }
+    __syncthreads();
+    for (int q = tid; q < P; q += NT) {
+        const int e = idx[q];
+        if (e >= 0 && e < E && fabsf(w[q]) >= 1e-8f) sorted[atomicAdd(&cur[e], 1)] = q;
+    }
+    __syncthreads();
+    const int nv = total;
+    for (int i = tid; i < nv * nb_gu; i += NT) {
+        const int kk = i / nb_gu, b = i % nb_gu;
+        const int pr = sorted[kk], e = idx[pr];
+        work_gu[nb_gu * start[e] + b * cnt[e] + (kk - start[e])] = make_int2(pr, b * kBRows);
+    }
+    for (int i = tid; i < nv * nb_dn; i += NT) {
+        const int kk = i / nb_dn, b = i % nb_dn;
+        const int pr = sorted[kk], e = idx[pr];
+        work_dn[nb_dn * start[e] + b * cnt[e] + (kk - start[e])] = make_int2(pr, b * kBRows);
+    }
+}
+
+namespace {
+template <typename F>
+int set_dyn_lds(F *fn, size_t lds, size_t *granted) {
+    // The attribute bounds the dynamic part; with the 64 KB of static LUT the
+    // total passes the 64 KB default for any input.
+    if (lds > *granted) {
+        OJX_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(fn),
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+        *granted = lds;
+    }
+    return OJASX_OK;
+}
+}  // namespace
 
 int launch_bank(const GroupItem *items_dev, const int2 *work_dev, int n_work, int max_K,
                 hipStream_t st) {
     const size_t lds = (size_t)(max_K / 16) * kXRow * sizeof(float);
-    // The attribute bounds the dynamic part; with the 64 KB of static LUT the
-    // total passes the 64 KB default for any input.
     static size_t granted = 0;
-    if (lds > granted) {
-        OJX_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(&lut_bank_kernel),
-                                    hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-        granted = lds;
-    }
+    int rc = set_dyn_lds(&lut_bank_kernel, lds, &granted);
+    if (rc) return rc;
     OJX_LAUNCH(lut_bank_kernel, dim3(n_work), dim3(kBNT), lds, st, items_dev, work_dev);
     OJX_HIP(hipGetLastError());
     return OJASX_OK;
 }
 
+int launch_moe_plan(const int *idx, const float *w, int P, int E, int nb_gu, int nb_dn,
+                    int2 *work_gu, int2 *work_dn, int *n_work, hipStream_t st) {
+    const size_t lds = (size_t)(3 * E + P) * sizeof(int);
+    static size_t granted = 0;
+    if (lds > 65536 && lds > granted) {
+        OJX_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(&moe_plan_kernel),
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+        granted = lds;
+    }
+    OJX_LAUNCH(moe_plan_kernel, dim3(1), dim3(1024), lds, st, idx, w, P, E, nb_gu, nb_dn, work_gu,
+               work_dn, n_work);
+    OJX_HIP(hipGetLastError());
+    return OJASX_OK;
+}
+
+int launch_moe_bank(const MoEBankLaunch &l, hipStream_t st) {
+    MoEBankParams p{l.codes_b, l.expert_bytes, l.cb, l.scales, l.x, l.y, l.idx, l.work,
+                    l.n_work, l.M, l.K, l.k};
+    const size_t lds = (size_t)(l.K / 16) * kXRow * sizeof(float);
+    const int grid = 8 * ((l.max_work + 7) / 8);
+    int rc = OJASX_OK;
+    if (l.xs == XS_SWIGLU) {
+        static size_t gr = 0;
+        rc = set_dyn_lds(&moe_bank_kernel<XS_SWIGLU>, lds, &gr);
+        if (!rc) OJX_LAUNCH(moe_bank_kernel<XS_SWIGLU>, dim3(grid), dim3(kBNT), lds, st, p);
+    } else if (l.xs == XS_BF16) {
+        static size_t gr = 0;
+        rc = set_dyn_lds(&moe_bank_kernel<XS_BF16>, lds, &gr);
+        if (!rc) OJX_LAUNCH(moe_bank_kernel<XS_BF16>, dim3(grid), dim3(kBNT), lds, st, p);
+    } else {
+        static size_t gr = 0;
+        rc = set_dyn_lds(&moe_bank_kernel<XS_F32>, lds, &gr);
+        if (!rc) OJX_LAUNCH(moe_bank_kernel<XS_F32>, dim3(grid), dim3(kBNT), lds, st, p);
+    }
+    if (rc) return rc;
+    OJX_HIP(hipGetLastError());
+    return OJASX_OK;
+}
+
 void pack_bank_codes(const uint8_t *codes, int M, int G, uint8_t *out) {
-    const int S32 = (G + 31) / 32;
     for (int m = 0; m < M; ++m) {
         const uint8_t *row = codes + (size_t)m * G;
         const size_t rb = (size_t)(m / 64), r = (size_t)(m % 64);
-        for (int gg = 0; gg < G; ++gg)
-            out[((rb * S32 + gg / 32) * 32 + gg % 32) * 64 + r] = row[gg];
+        for (int gg = 0; gg < G; ++gg) out[(rb * G + gg) * 64 + r] = row[gg];
     }
 }
 

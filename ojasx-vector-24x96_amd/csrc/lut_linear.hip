@@ -902,7 +902,7 @@ OJASX_API OjasxLinearHandle ojasx_create_linear(int in_features, int out_feature
     if (scales_data) memcpy(sc.data(), scales_data, sizeof(float) * L->M);
     int rc = upload(L->codes, packed.data(), packed.size());
     if (!rc && L->D == 16) {   // the grouped kernel's layout (block_dim 16 only)
-        std::vector<uint8_t> bank(bank_codes_bytes(L->M, L->G), 0);
+        std::vector<uint8_t> bank(bank_codes_bytes(L->M, L->G) + kBankSlack, 0);
         if (codes_data) pack_bank_codes(codes_data, L->M, L->G, bank.data());
         rc = upload(L->codes_b, bank.data(), bank.size());
     }

@@ -11,22 +11,28 @@
 // zeroed when k_active > 0, untouched otherwise).  Only routed experts' codes
 // are ever read.
 //
-// Three paths, none with cross-workgroup synchronisation inside a kernel (a
+// Four paths, none with cross-workgroup synchronisation inside a kernel (a
 // "pair" is one routed (token, slot)):
 //  * block_dim 16, fewer than kGroupMinTokens tokens (latency-bound): two
 //    launches that compute LUT entries where they are used, <v_g, C[code]>,
 //    from the codebook and the input vector staged in LDS -- moe_up_dec
 //    (gate/up + SwiGLU per (pair, 32 intermediate rows)) and moe_down_dec
 //    (down + combine per (token, hidden rows), slots summed in slot order).
-//  * block_dim 16, more tokens: the pairs as grouped LUT GEMVs, each
-//    workgroup building its 16-group LUT slices with MFMA -- moe_gu_group
-//    (gate/up + SwiGLU), moe_dn_group (down, scaled), moe_combine.
+//  * block_dim 16, kGroupMinTokens up to kBankMinTokens tokens: the pairs as
+//    grouped LUT GEMVs in slot order, each workgroup building its 16-group
+//    LUT slices with MFMA -- moe_gu_group (gate/up + SwiGLU), moe_dn_group
+//    (down, scaled), moe_combine.
+//  * block_dim 16, more tokens, aligned activations: the pairs grouped by
+//    expert (moe_plan, a counting sort) on the bank-layout LUT-GEMV of
+//    lut_bank.hip -- moe_bank (gate/up), moe_bank (SwiGLU input, down),
+//    moe_combine -- so each distinct expert's codes stream from HBM once.
 //  * other block sizes: LUT_in build, moe_gateup (gathers from the L2-resident
 //    LUT, SwiGLU, LUT_down rows), moe_down, moe_combine.
 // Every path sums slots in slot order, so results are deterministic.
 //  Router: moe_route, one workgroup per token.
 #include <algorithm>
 #include <cstring>
+#include <type_traits>
 #include <vector>
 
 #include "common.h"
@@ -47,11 +53,15 @@ struct MoE {
     int E = 0, H = 0, I = 0, top_k = 0, D = 0;
     int Gin = 0, Gi = 0, Sin = 0, Si = 0, Ip = 0, Hp = 0;
     DevBuf cb_in, cb_dn, gu, dn, gus, dns;
+    DevBuf gub, dnb;                    // bank layouts per expert (block_dim 16)
+    size_t gub_bytes = 0, dnb_bytes = 0;
     DevBuf lut_in, lut_dn, dout, inter, gu_part, xstage, ystage, istage, wstage;
+    DevBuf work, nwork, gu_out;         // bank path: plan output, gate/up rows per pair
     size_t lut_dn_pairs = 0;
     ~MoE() {
-        for (DevBuf *b : {&cb_in, &cb_dn, &gu, &dn, &gus, &dns, &lut_in, &lut_dn, &dout, &inter,
-                          &gu_part, &xstage, &ystage, &istage, &wstage})
+        for (DevBuf *b : {&cb_in, &cb_dn, &gu, &dn, &gus, &dns, &gub, &dnb, &lut_in, &lut_dn,
+                          &dout, &inter, &gu_part, &xstage, &ystage, &istage, &wstage, &work,
+                          &nwork, &gu_out})
             b->release();
     }
 };
@@ -758,6 +768,13 @@ constexpr size_t kMaxLds = 160 * 1024;
 // measured 18.4 vs 21.6 us at 3 tokens, 16.9 vs 18.2 us at 2 (the 512-expert
 // H 2048 / I 768 top-10 layer).
 constexpr int kGroupMinTokens = 3;
+// From this many tokens the routed pairs run grouped by expert on the bank
+// kernel (up to kBankMaxPairs pairs per call: the plan's LDS).  Measured on
+// the 512-expert H 2048 / I 768 top-10 layer, per call, two alternating
+// 151 MB banks: 33.4 vs 34.2 us at 16 tokens, 48.2 vs 51.9 at 32, 85.4 vs
+// 87.1 at 64, 264 vs 286 at 256 (bank vs grouped per slot); 27.1 vs 26.7 at 8.
+constexpr int kBankMinTokens = 16;
+constexpr size_t kBankMaxPairs = 16384;
 
 template <typename T>
 int moe_forward_dec(MoE *m, const void *x, const int *idx, const float *w, void *y, int T_, int k,
@@ -905,6 +922,70 @@ int moe_forward_group(MoE *m, const void *x, const int *idx, const float *w, voi
     return OJASX_OK;
 }
 
+// Routed pairs grouped by expert on the bank kernel (lut_bank.hip): a plan
+// launch sorts the valid pairs by expert into work lists of (pair, 512-row
+// block); gate/up then writes s_m * (gate | up) rows per pair, down stages
+// silu(gate) * up as its input and writes s_dn * down per pair, and the
+// ordered combine sums w_j * down_j over the slots.  The pairs of one expert
+// run back to back on one XCD, so its codes stream through one L2.
+template <typename T>
+int moe_forward_bank(MoE *m, const void *x, const int *idx, const float *w, void *y, int T_, int k,
+                     hipStream_t st) {
+    const size_t P = (size_t)T_ * k;
+    const int nb_gu = (2 * m->I + kBankRows - 1) / kBankRows, nb_dn = (m->H + kBankRows - 1) / kBankRows;
+    int rc = m->work.ensure(P * (nb_gu + nb_dn) * sizeof(int2));
+    if (!rc) rc = m->nwork.ensure(2 * sizeof(int));
+    if (!rc) rc = m->gu_out.ensure(P * 2 * m->I * sizeof(float));
+    if (!rc) rc = m->dout.ensure(P * m->H * sizeof(float));
+    if (rc) return rc;
+    int2 *work_gu = m->work.as<int2>(), *work_dn = work_gu + P * nb_gu;
+    rc = launch_moe_plan(idx, w, (int)P, m->E, nb_gu, nb_dn, work_gu, work_dn, m->nwork.as<int>(), st);
+    if (rc) return rc;
+    MoEBankLaunch l{};
+    l.codes_b = m->gub.as<uint8_t>();
+    l.expert_bytes = m->gub_bytes;
+    l.cb = m->cb_in.as<float>();
+    l.scales = m->gus.as<float>();
+    l.x = x;
+    l.y = m->gu_out.as<float>();
+    l.idx = idx;
+    l.work = work_gu;
+    l.n_work = m->nwork.as<int>();
+    l.M = 2 * m->I;
+    l.K = m->H;
+    l.k = k;
+    l.max_work = (int)(P * nb_gu);
+    l.xs = std::is_same<T, float>::value ? 0 : 1;
+    rc = launch_moe_bank(l, st);
+    if (rc) return rc;
+    l.codes_b = m->dnb.as<uint8_t>();
+    l.expert_bytes = m->dnb_bytes;
+    l.cb = m->cb_dn.as<float>();
+    l.scales = m->dns.as<float>();
+    l.x = m->gu_out.as<float>();
+    l.y = m->dout.as<float>();
+    l.work = work_dn;
+    l.n_work = m->nwork.as<int>() + 1;
+    l.M = m->H;
+    l.K = m->I;
+    l.max_work = (int)(P * nb_dn);
+    l.xs = 2;
+    rc = launch_moe_bank(l, st);
+    if (rc) return rc;
+    MoEParams cp{};
+    cp.dout = m->dout.as<float>();
+    cp.idx = idx;
+    cp.w = w;
+    cp.y = y;
+    cp.E = m->E;
+    cp.H = m->H;
+    cp.T = T_;
+    cp.k = k;
+    OJX_LAUNCH((moe_combine_kernel<T>), dim3((m->H + kNT - 1) / kNT, T_), dim3(kNT), 0, st, cp);
+    OJX_HIP(hipGetLastError());
+    return OJASX_OK;
+}
+
 int moe_forward(MoE *m, const void *x, const int *idx, const float *w, void *y, int T_, int k,
                 int dtype, hipStream_t st) {
     if (k <= 0 || T_ <= 0) return OJASX_OK;
@@ -920,10 +1001,14 @@ int moe_forward(MoE *m, const void *x, const int *idx, const float *w, void *y, 
         // single-kernel-per-stage path: block_dim 16, aligned activations,
         // the staged vectors fit LDS
         const size_t align = dtype == OJASX_DTYPE_F32 ? 16 : 8;
-        const bool ok = m->D == 16 && k <= 32 && m->H % 4 == 0 && m->I % 4 == 0 &&
-                        reinterpret_cast<uintptr_t>(x) % align == 0 &&
+        const bool aligned = m->H % 4 == 0 && m->I % 4 == 0 &&
+                             reinterpret_cast<uintptr_t>(x) % align == 0;
+        const bool ok = m->D == 16 && k <= 32 && aligned &&
                         (size_t)(kCB * 16 + (size_t)k * m->Si * 256) * 4 <= kMaxLds &&
                         (size_t)(kCB * 16 + m->Sin * 256) * 4 <= kMaxLds;
+        if (m->D == 16 && aligned && T_ >= kBankMinTokens && m->gub.ptr && (size_t)T_ * k <= kBankMaxPairs)
+            return dtype == OJASX_DTYPE_F32 ? moe_forward_bank<float>(m, x, idx, w, y, T_, k, st)
+                                            : moe_forward_bank<__hip_bfloat16>(m, x, idx, w, y, T_, k, st);
         if (m->D == 16 && T_ >= kGroupMinTokens)
             return dtype == OJASX_DTYPE_F32 ? moe_forward_group<float>(m, x, idx, w, y, T_, k, st)
                                             : moe_forward_group<__hip_bfloat16>(m, x, idx, w, y, T_, k, st);
@@ -1046,6 +1131,21 @@ OJASX_API OjasxMoEHandle ojasx_create_moe(int num_experts, int hidden_dim, int i
     if (down_scales) memcpy(dns.data(), down_scales, sizeof(float) * dns.size());
     int rc = upload(m->gu, gu.data(), gu.size());
     if (!rc) rc = upload(m->dn, dn.data(), dn.size());
+    if (!rc && block_dim == 16) {   // the bank kernel's layouts, expert after expert
+        m->gub_bytes = bank_codes_bytes(2 * intermediate_dim, m->Gin);
+        m->dnb_bytes = bank_codes_bytes(hidden_dim, m->Gi);
+        std::vector<uint8_t> gb(E * m->gub_bytes + kBankSlack, 0), db(E * m->dnb_bytes + kBankSlack, 0);
+        if (gate_up_codes)
+            for (size_t e = 0; e < E; ++e)
+                pack_bank_codes(gate_up_codes + e * 2 * I * m->Gin, 2 * intermediate_dim, m->Gin,
+                                gb.data() + e * m->gub_bytes);
+        if (down_codes)
+            for (size_t e = 0; e < E; ++e)
+                pack_bank_codes(down_codes + e * H * m->Gi, hidden_dim, m->Gi,
+                                db.data() + e * m->dnb_bytes);
+        rc = upload(m->gub, gb.data(), gb.size());
+        if (!rc) rc = upload(m->dnb, db.data(), db.size());
+    }
     if (!rc) rc = upload(m->cb_in, cbi.data(), cbi.size() * 4);
     if (!rc) rc = upload(m->cb_dn, cbd.data(), cbd.size() * 4);
     if (!rc) rc = upload(m->gus, gus.data(), gus.size() * 4);

@@ -79,12 +79,12 @@ def test_router_bit_exact_indices(pkg, dev, renorm):
 
 @pytest.fixture(scope="module")
 def baseline_moe(pkg):
-    m = gen.moe(E=512, H=2048, I=768, T=16, seed=2024, scales="u")
+    m = gen.moe(E=512, H=2048, I=768, T=32, seed=2024, scales="u")
     nat = make_native(pkg, m, 512, 2048, 768)
     return m, nat
 
 
-@pytest.mark.parametrize("T", [1, 16])
+@pytest.mark.parametrize("T", [1, 16, 32])
 def test_baseline_moe_fp32(pkg, dev, baseline_moe, T):
     import torch
     m, nat = baseline_moe
@@ -124,7 +124,7 @@ def test_baseline_moe_bf16(pkg, dev, baseline_moe):
         assert rel_err(y[t].float().cpu().numpy(), want) < 1e-2
 
 
-@pytest.mark.parametrize("T", [1, 4])   # the in-place path and the grouped path
+@pytest.mark.parametrize("T", [1, 4, 20])   # in-place, grouped-per-slot and by-expert paths
 def test_repeat_deterministic_and_skips(pkg, dev, baseline_moe, T):
     """Skipped slots (id out of range, |w| < 1e-8) and repeated experts within a
     token; repeated calls return identical bits."""
@@ -163,7 +163,9 @@ def device_moe(pkg, dev, nat, x_t, idx, w, k, dtype_tag=0):
     return y.float().cpu().numpy()
 
 
-@pytest.mark.parametrize("T", [2, 6])   # below / from the token count that selects the grouped path
+# below / from the token count that selects the grouped path; from the one
+# that groups the routed pairs by expert (bank kernel: partial slices, rows)
+@pytest.mark.parametrize("T", [2, 6, 20])
 @pytest.mark.parametrize("E,H,I,k,D", [
     (40, 480, 208, 20, 16),    # partial input/intermediate slices; 20 slots > 16 waves
     (64, 512, 256, 32, 16),    # the largest k of the single-kernel stages
@@ -200,3 +202,24 @@ def test_moe_unaligned_activations(pkg, dev, baseline_moe, dtype_tag):
         want = cpu.moe_forward(xr[t], m["cb_in"], m["cb_down"], m["gu_codes"], m["gu_scales"],
                                m["dn_codes"], m["dn_scales"], idx[t], w[t])
         assert rel_err(y[t], want) < (1e-5 if dtype_tag == 0 else 1e-2)
+
+
+@pytest.mark.parametrize("dtype_tag", [0, 1])
+def test_moe_by_expert_many_pairs_per_expert(pkg, dev, dtype_tag):
+    """256 routed pairs over 8 experts (32 pairs each on average, the plan's
+    expert-sorted work lists), with skipped slots, fp32 and bf16 inputs."""
+    import torch
+    E, H, I, k, T = 8, 256, 96, 4, 64
+    m = gen.moe(E=E, H=H, I=I, T=T, seed=77, scales="u")
+    nat = make_native(pkg, m, E, H, I, k)
+    idx, w = cpu.router_topk(m["logits"], k, renorm=True)
+    idx[3, 2] = E + 5                                # out of range: skipped
+    w[7, 1] = 0.0                                    # below 1e-8: skipped
+    tdt = torch.float32 if dtype_tag == 0 else torch.bfloat16
+    xt = torch.from_numpy(m["x"]).to(dev).to(tdt)
+    y = device_moe(pkg, dev, nat, xt, idx, w, k, dtype_tag)
+    xr = xt.float().cpu().numpy()
+    for t in range(T):
+        want = cpu.moe_forward(xr[t], m["cb_in"], m["cb_down"], m["gu_codes"], m["gu_scales"],
+                               m["dn_codes"], m["dn_scales"], idx[t], w[t])
+        assert rel_err(y[t], want) < (1e-5 if dtype_tag == 0 else 1e-2), t
