@@ -169,7 +169,7 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true",
                     help="skip every extra figure (headline only)")
-    ap.add_argument("--extra", default="copy,linear2560,bf16,batched,sustained,moe,kv,decoder",
+    ap.add_argument("--extra", default="copy,linear2560,bf16,batched,sustained,moe,kv,attn,decoder",
                     help="comma-separated extra figures to run")
     return ap.parse_args()
 
@@ -534,6 +534,69 @@ def bench_kv(b, args):
     return res
 
 
+def bench_attn_pages(b, args, T=32768, page=256, n_caches=4):
+    """OnlineSoftmaxBlockAttention.forward_stream over the int8 pages of a
+    PagedCompressedKVCache read in place: 32 query / 8 kv heads, head_dim 128,
+    one decode query, T tokens in pages of 256, fp64 state.  Calls rotate over
+    n_caches caches (more than 256 MB) after a flush; each call is the whole
+    Python face (init, update, merge, finalize and the report's max_logsumexp,
+    which synchronises).  CPU: the fp64 NumPy restatement of forward_stream
+    over the same cache's dequantised pages, 1 thread."""
+    from oracle import numpy_oracle as no
+    torch = b.torch
+    lc = b.pkg.long_context
+    B, Hq, Hkv, D = 1, 32, 8, 128
+    caches = []
+    g = torch.Generator(device=b.dev).manual_seed(77)
+    for _ in range(n_caches):
+        c = lc.PagedCompressedKVCache(page_size=page, max_resident_pages=T // page + 2,
+                                      sink_pages=2)
+        for t0 in range(0, T, 4096):
+            c.append(torch.randn(B, Hkv, 4096, D, device=b.dev, generator=g),
+                     torch.randn(B, Hkv, 4096, D, device=b.dev, generator=g))
+        caches.append(c)
+    attn = lc.OnlineSoftmaxBlockAttention(Hq, Hkv, D, causal=False)
+    q = torch.randn(B, Hq, 1, D, device=b.dev, generator=g, dtype=torch.float32)
+    call = lambda i: attn.forward_stream(q, caches[i % n_caches])
+    for i in range(min(args.warmup, 8)):
+        call(i)
+    torch.cuda.synchronize()
+    n = max(40, min(args.steps, 200))
+    us = b.events_us(call, n)
+    kern = b.kernels(call, n)
+    code = T * Hkv * 2 * D
+    all_bytes = code + T * Hkv * 2 * 2
+    tile = [k for k in kern if k.startswith("attn_tile_kernel")][0]
+    res = {"tokens": T, "page_size": page, "caches_rotated": n_caches,
+           "working_set_MB": round(n_caches * all_bytes / 2**20, 1),
+           "us_per_call": round(us, 3), "int8_bytes": code, "all_compulsory_bytes": all_bytes,
+           "achieved_all_GBs_per_call": round(all_bytes / (us * 1e-6) / 1e9, 2),
+           "kernels_avg_us": {k: v["avg_us"] for k, v in kern.items()},
+           "tile_kernel_roofline": roofline(code, all_bytes, kern[tile]["avg_us"], tile,
+                                            kern[tile]["calls"]),
+           "tile_kernel_fp64_TFLOPs": round(4 * T * Hq * D / (kern[tile]["avg_us"] * 1e-6)
+                                            / 1e12, 3)}
+    if not args.no_cpu:
+        from threadpoolctl import threadpool_limits
+        c = caches[0]
+        pages = [(no.paged_dequantize_int8(qk.cpu().numpy(), sk.cpu().numpy()),
+                  no.paged_dequantize_int8(qv.cpu().numpy(), sv.cpu().numpy()))
+                 for qk, sk, qv, sv in c._pages]
+        qn = q.double().cpu().numpy()
+        with threadpool_limits(1):
+            s, m = timed_cpu(lambda: no.block_attention_stream(qn, pages, False),
+                             min(10.0, args.cpu_seconds), 5, warm=1)
+        want = no.block_attention_stream(qn, pages, False)[0]
+        got = attn.forward_stream(q.double(), c)[0].cpu().numpy()
+        res["cpu_baseline"] = {"value": round(s * 1e6, 1), "unit": "us/call", "cores": 1,
+                               "kind": "port",
+                               "sample": f"{m} calls over the first cache's {T} tokens "
+                                         "(NumPy fp64 forward_stream over its dequantised pages)",
+                               "parity_rel_err_fp64_query": float(np.abs(got - want).max()
+                                                                  / np.abs(want).max())}
+    return res
+
+
 def bench_kv_append(b, args, cpu_seconds=2.0):
     """Device KV append (encode + paged write) for 8 kv heads x 128, per call
     of 1 or 16 tokens, with the 256 x 16 codebooks (nearest centroid) and with
@@ -813,6 +876,8 @@ def main():
         out["moe_512x_top10"] = bench_moe(b, args)
     if "kv" in extra:
         out["kv_decode_gqa4"] = bench_kv(b, args)
+    if "attn" in extra:
+        out["attn_stream_int8_pages"] = bench_attn_pages(b, args)
     if "decoder" in extra:
         out["decoder_4b_shaped"] = bench_decoder(b, args)
     print(json.dumps(out))

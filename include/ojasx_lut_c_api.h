@@ -50,8 +50,15 @@ enum {
     OJASX_ERR_OOM = -5
 };
 
-/* Activation / output element types of the device entry points. */
-enum { OJASX_DTYPE_F32 = 0, OJASX_DTYPE_BF16 = 1, OJASX_DTYPE_F16 = 2 };
+/* Activation / output element types of the device entry points (F64 and
+ * INT8 only where an entry point says so). */
+enum {
+    OJASX_DTYPE_F32 = 0,
+    OJASX_DTYPE_BF16 = 1,
+    OJASX_DTYPE_F16 = 2,
+    OJASX_DTYPE_F64 = 3,
+    OJASX_DTYPE_INT8 = 4
+};
 
 /* ---- metadata (ref.h:40-41) ------------------------------------------- */
 OJASX_API const char *ojasx_get_version(void);
@@ -234,6 +241,46 @@ OJASX_API int ojasx_kv_decode_paged_device_len(const float *q, const uint8_t *k_
                                                int page_size, int num_q_heads, int num_kv_heads,
                                                int head_dim, int block_dim, float scale_factor,
                                                int tokens_per_lane, float *out, void *stream);
+
+/* ---- streamed exact attention (ojasx_24x96/long_context.py:92-176) ------ */
+/* OnlineSoftmaxBlockAttention.forward_stream on device, fp64 state, in three
+ * calls: init (state <- query), update (fold tiles in), finalize (output).
+ * Query rows are [batch][num_heads][q_len] (row = (b * num_heads + h) * q_len
+ * + s), each of head_dim elements; head h attends kv head
+ * h / (num_heads / num_kv_heads).  state: [rows][2 * head_dim + 2] fp64 =
+ * (query, acc, m, l) per row; head_dim a multiple of 8, at most 256. */
+typedef struct OjasxAttnTile {
+    const void *k, *v;            /* [batch][kv heads][n_tokens][head_dim], strided */
+    const void *k_scale, *v_scale; /* OJASX_DTYPE_INT8 tiles: fp16 per-token scales */
+    long long n_tokens;
+    long long batch_stride, head_stride, token_stride;       /* elements, k and v */
+    long long scale_batch_stride, scale_head_stride, scale_token_stride;
+} OjasxAttnTile;
+/* long_context.py:117-127: state <- (q as fp64, acc 0, m -inf, l 0); q
+ * [rows][head_dim] contiguous, q_dtype F32, BF16, F16 or F64. */
+OJASX_API int ojasx_attention_stream_init_device(double *state, const void *q, int q_dtype,
+                                                 int rows, int head_dim, void *stream);
+/* long_context.py:129-163 for n_tiles tiles in order (the tiles' device
+ * descriptors are staged by the library; the host array may be reused on
+ * return).  Token t of the stream (kv_offset + tokens of earlier tiles + t)
+ * is hidden from query s when causal != 0 and t > query_start_pos + s.
+ * kv_dtype F32, BF16, F16, F64, or INT8 (the paged cache's pages: value =
+ * int8 * fp16 scale of its token, exact; head_dim a multiple of 16).  Scores
+ * (q . k) * scale, in fp64.  k and v 16-byte aligned with strides that keep
+ * every row 16-byte aligned (float v: 4-element aligned), rows contiguous.
+ * Calls from one host thread share a workspace: serialise them (one stream). */
+OJASX_API int ojasx_attention_stream_update_device(double *state, int batch, int num_heads,
+                                                   int num_kv_heads, int q_len, int head_dim,
+                                                   const OjasxAttnTile *tiles, int n_tiles,
+                                                   int kv_dtype, int causal,
+                                                   long long query_start_pos, long long kv_offset,
+                                                   double scale, void *stream);
+/* long_context.py:165-167: out [rows][head_dim] = acc / l (l = 0 -> 1) in
+ * out_dtype (F32, BF16, F16 or F64; bf16 and fp16 rounded through fp32 as
+ * torch's .to() from fp64), lse [rows] = m + log(l) (NULL: not written). */
+OJASX_API int ojasx_attention_stream_finalize_device(const double *state, int rows, int head_dim,
+                                                     void *out, int out_dtype, double *lse,
+                                                     void *stream);
 
 /* ---- MoE (ref.h:125-150) ---------------------------------------------- */
 OJASX_API OjasxMoEHandle ojasx_create_moe(int num_experts, int hidden_dim,

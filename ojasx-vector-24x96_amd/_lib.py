@@ -71,10 +71,29 @@ SIGNATURES = {
     "ojasx_decoder_generate": (ci, [vp, ci, ci, ci, vp, vp]),
     "ojasx_decoder_read_kv": (ci, [vp, ci, ci, ci, vp, vp, vp, vp]),
     "ojasx_linear_forward_fused_device": (ci, [vp, vp, vp, ci, vp, cf, vp, vp]),
+    "ojasx_attention_stream_init_device": (ci, [vp, vp, ci, ci, ci, vp]),
+    "ojasx_attention_stream_update_device": (ci, [vp, ci, ci, ci, ci, ci, vp, ci, ci, ci,
+                                                  ctypes.c_longlong, ctypes.c_longlong,
+                                                  ctypes.c_double, vp]),
+    "ojasx_attention_stream_finalize_device": (ci, [vp, ci, ci, vp, ci, vp, vp]),
 }
+
+
+class AttnTile(ctypes.Structure):
+    """OjasxAttnTile: one K/V tile of a streamed attention (element strides)."""
+    _fields_ = [("k", vp), ("v", vp), ("k_scale", vp), ("v_scale", vp),
+                ("n_tokens", ctypes.c_longlong),
+                ("batch_stride", ctypes.c_longlong), ("head_stride", ctypes.c_longlong),
+                ("token_stride", ctypes.c_longlong),
+                ("scale_batch_stride", ctypes.c_longlong),
+                ("scale_head_stride", ctypes.c_longlong),
+                ("scale_token_stride", ctypes.c_longlong)]
 
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
+DTYPE_F16 = 2
+DTYPE_F64 = 3
+DTYPE_INT8 = 4
 
 
 class OjasxError(RuntimeError):

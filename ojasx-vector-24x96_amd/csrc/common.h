@@ -38,6 +38,31 @@ struct DevBuf {
 
 int upload(DevBuf &buf, const void *host, size_t n);  // ensure + memcpy
 
+// Small per-call argument arrays (work lists, descriptors) staged for a
+// launch: kSlots slots of pinned host memory and their device copies, so the
+// upload is an asynchronous copy (a pageable source would make every call wait
+// for it).  A slot is rewritten only after the event recorded behind the last
+// launch that read it has completed, whatever stream the calls run on.  With
+// reuse, a call whose bytes equal the last upload's launches on that device
+// copy without a new upload.  One ring per host thread (thread_local).
+struct StagingRing {
+    static constexpr int kSlots = 4;
+    DevBuf dev;                         // [kSlots][cap] bytes
+    unsigned char *pinned = nullptr;    // [kSlots][cap] bytes
+    size_t cap = 0;
+    hipEvent_t ev[kSlots] = {};
+    int next = 0, cur = -1;             // the slot of the current call
+    int last = -1;                      // the slot holding the last upload
+    size_t last_bytes = 0;
+    int reserve(size_t bytes);
+    // Uploads bytes from host (or reuses the last upload) on st; *dev_out is
+    // the device copy, valid for launches on st until launched() is called.
+    int stage(const void *host, size_t bytes, bool reuse, hipStream_t st, void **dev_out);
+    // Records the current slot's event on st, behind the launches that read it.
+    int launched(hipStream_t st);
+    ~StagingRing();
+};
+
 // Optional per-kernel timing (ojasx_kernel_timing_*): when enabled, launches
 // record start/stop events at the kernel's own begin and end
 // (hipExtLaunchKernelGGL), kept per kernel name until the report.

@@ -2,7 +2,6 @@
 // lut_bank_kernel in lut_bank.hip) and the tall RMSNorm linear of the decoder
 // (lut_tall_rms_kernel, on the LUT slice loop of lut_slices.h).
 #include <algorithm>
-#include <cstring>
 #include <vector>
 
 #include "common.h"
@@ -124,51 +123,13 @@ int launch_tall_rms(const GroupItem &it, const float *w, float eps, hipStream_t 
     return OJASX_OK;
 }
 
-// Per host thread: the item arrays of the last kGroupRing calls, written in
-// pinned host memory and copied to the device asynchronously (a pageable
-// source would make every call wait for its copy).  Slot k is reused only
-// after the event recorded behind the launch that read it has completed, so
-// neither its host nor its device copy is overwritten while in use, whatever
-// stream the calls run on.
-// A call whose item array equals the last one uploaded (same handles, x and y
-// pointers: the steady state of a serving loop) launches on that device copy
-// without a new upload.
-// An upload is the item array followed by the work list of the bank kernel
-// ((item, first row) per 512-row block).
-constexpr int kGroupRing = 4;
+// Per host thread: the item array and the bank kernel's work list ((item,
+// first row) per 512-row block) of a call, staged for upload.  A call whose
+// arrays equal the last upload (same handles, x and y pointers: the steady
+// state of a serving loop) launches on that device copy without a new upload.
 struct GroupWork {
-    DevBuf items;                       // [kGroupRing][cap] bytes on the device
-    unsigned char *pinned = nullptr;    // [kGroupRing][cap] bytes of pinned host memory
-    size_t cap = 0;
-    hipEvent_t ev[kGroupRing] = {};
-    int slot = 0;
-    int last_slot = -1;                 // the slot holding the last upload
-    size_t last_bytes = 0;
+    StagingRing ring;
     std::vector<unsigned char> host;
-    int reserve(size_t bytes) {
-        if (bytes <= cap) return OJASX_OK;
-        for (hipEvent_t &e : ev)
-            if (e) OJX_HIP(hipEventSynchronize(e));
-        if (pinned) (void)hipHostFree(pinned);
-        pinned = nullptr;
-        cap = 0;
-        const size_t n = round_up(std::max<size_t>(bytes, 64 << 10), 256);
-        OJX_HIP(hipHostMalloc(reinterpret_cast<void **>(&pinned), n * kGroupRing,
-                              hipHostMallocDefault));
-        last_slot = -1;
-        const int rc = items.ensure(n * kGroupRing);
-        if (rc) return rc;
-        for (hipEvent_t &e : ev)
-            if (!e) OJX_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming));
-        cap = n;
-        return OJASX_OK;
-    }
-    ~GroupWork() {
-        items.release();
-        if (pinned) (void)hipHostFree(pinned);
-        for (hipEvent_t e : ev)
-            if (e) (void)hipEventDestroy(e);
-    }
 };
 static thread_local GroupWork t_group;
 
@@ -214,27 +175,15 @@ OJASX_API int ojasx_linear_forward_grouped_device(const OjasxLinearHandle *handl
     int2 *wl = reinterpret_cast<int2 *>(gw.host.data() + item_bytes);
     for (int i = 0, t = 0; i < count; ++i)
         for (int b = 0; b < host[i].M; b += kBankRows) wl[t++] = make_int2(i, b);
-    rc = gw.reserve(bytes);
-    if (rc) return rc;
     hipStream_t st = static_cast<hipStream_t>(stream);
-    int k = gw.last_slot;
-    if (k < 0 || gw.last_bytes != bytes ||
-        memcmp(gw.pinned + (size_t)k * gw.cap, gw.host.data(), bytes) != 0) {
-        k = gw.slot;
-        gw.slot = (k + 1) % kGroupRing;
-        if (gw.ev[k]) OJX_HIP(hipEventSynchronize(gw.ev[k]));   // slot k's last launch is done
-        memcpy(gw.pinned + (size_t)k * gw.cap, gw.host.data(), bytes);
-        OJX_HIP(hipMemcpyAsync(gw.items.as<unsigned char>() + (size_t)k * gw.cap,
-                               gw.pinned + (size_t)k * gw.cap, bytes, hipMemcpyHostToDevice, st));
-        gw.last_slot = k;
-        gw.last_bytes = bytes;
-    }
-    GroupItem *dev = reinterpret_cast<GroupItem *>(gw.items.as<unsigned char>() + (size_t)k * gw.cap);
-    const int2 *dev_work = reinterpret_cast<const int2 *>(reinterpret_cast<unsigned char *>(dev) + item_bytes);
+    void *staged = nullptr;
+    rc = gw.ring.stage(gw.host.data(), bytes, true, st, &staged);
+    if (rc) return rc;
+    GroupItem *dev = static_cast<GroupItem *>(staged);
+    const int2 *dev_work = reinterpret_cast<const int2 *>(static_cast<unsigned char *>(staged) + item_bytes);
     rc = launch_bank(dev, dev_work, n_work, max_K, st);
     if (rc) return rc;
-    OJX_HIP(hipEventRecord(gw.ev[k], st));
-    return OJASX_OK;
+    return gw.ring.launched(st);
 }
 
 }  // extern "C"

@@ -3,6 +3,7 @@
 // Metadata entry points mirror split_manifold_lut_experiment/native/src/
 // ojasx_lut_c_api.cpp:17-31 (version and backend strings); the strings name
 // this engine instead of the reference's CPU backends.
+#include <algorithm>
 #include <cstdarg>
 #include <cstring>
 #include <map>
@@ -51,6 +52,55 @@ int upload(DevBuf &buf, const void *host, size_t n) {
     if (rc) return rc;
     if (n) OJX_HIP(hipMemcpy(buf.ptr, host, n, hipMemcpyHostToDevice));
     return OJASX_OK;
+}
+
+int StagingRing::reserve(size_t bytes) {
+    if (bytes <= cap) return OJASX_OK;
+    for (hipEvent_t &e : ev)
+        if (e) OJX_HIP(hipEventSynchronize(e));
+    if (pinned) (void)hipHostFree(pinned);
+    pinned = nullptr;
+    cap = 0;
+    last = -1;
+    const size_t n = round_up(std::max<size_t>(bytes, 64 << 10), 256);
+    OJX_HIP(hipHostMalloc(reinterpret_cast<void **>(&pinned), n * kSlots, hipHostMallocDefault));
+    const int rc = dev.ensure(n * kSlots);
+    if (rc) return rc;
+    for (hipEvent_t &e : ev)
+        if (!e) OJX_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming));
+    cap = n;
+    return OJASX_OK;
+}
+
+int StagingRing::stage(const void *host, size_t bytes, bool reuse, hipStream_t st, void **dev_out) {
+    int rc = reserve(bytes);
+    if (rc) return rc;
+    int k = last;
+    if (!reuse || k < 0 || last_bytes != bytes || memcmp(pinned + (size_t)k * cap, host, bytes) != 0) {
+        k = next;
+        next = (k + 1) % kSlots;
+        OJX_HIP(hipEventSynchronize(ev[k]));             // slot k's last launch is done
+        memcpy(pinned + (size_t)k * cap, host, bytes);
+        OJX_HIP(hipMemcpyAsync(dev.as<unsigned char>() + (size_t)k * cap, pinned + (size_t)k * cap,
+                               bytes, hipMemcpyHostToDevice, st));
+        last = k;
+        last_bytes = bytes;
+    }
+    cur = k;
+    *dev_out = dev.as<unsigned char>() + (size_t)k * cap;
+    return OJASX_OK;
+}
+
+int StagingRing::launched(hipStream_t st) {
+    if (cur >= 0) OJX_HIP(hipEventRecord(ev[cur], st));
+    return OJASX_OK;
+}
+
+StagingRing::~StagingRing() {
+    dev.release();
+    if (pinned) (void)hipHostFree(pinned);
+    for (hipEvent_t e : ev)
+        if (e) (void)hipEventDestroy(e);
 }
 
 // ---- kernel timing -------------------------------------------------------

@@ -18,12 +18,22 @@ csrc/lut_kv.hip.
   ``max_resident_pages`` evicts the oldest page after the ``sink_pages`` first
   ones (the reference's eviction rule, long_context.py:255-257).
 
-Everything runs on the GPU; CPU tensors raise.
+* ``OnlineSoftmaxBlockAttention`` mirrors long_context.py:47-209: exact
+  attention over streamed (K, V) tiles with fp64 online-softmax state, on the
+  kernels of csrc/attn_stream.hip.  ``forward_stream`` takes any iterable of
+  tiles (one device update per tile, tiles moved to the query's device as the
+  reference moves them) or a ``PagedCompressedKVCache`` itself, whose int8
+  pages are then read in place and dequantised in registers, all pages in
+  one update.
+
+Everything runs on the GPU; CPU queries raise.
 """
 from __future__ import annotations
 
 import ctypes
-from typing import Iterator, List, Optional, Tuple
+import math
+from dataclasses import dataclass
+from typing import Iterable, Iterator, List, Optional, Tuple
 
 import numpy as np
 
@@ -92,6 +102,8 @@ class PagedCompressedKVCache:
         self._buffers: List[Tuple] = []  # (qk, sk, qv, sv) page buffers
         self._free: List[int] = []
         self._layout = None              # (B, H, D, device) of the first append
+        self._version = 0                # bumped by every append
+        self._tiles = None               # (version, attention tile array, tokens, max page)
 
     @staticmethod
     def _quantize_int8(t):
@@ -154,6 +166,7 @@ class PagedCompressedKVCache:
         elif layout != self._layout:
             raise ValueError(f"chunk layout {layout[:3]} differs from the cache's {self._layout[:3]}")
         self.total_tokens_seen += S
+        self._version += 1
         key, value = key.contiguous(), value.contiguous()
         for start in range(0, S, self.page_size):
             n = min(start + self.page_size, S) - start
@@ -188,6 +201,221 @@ class PagedCompressedKVCache:
             for t in page:
                 total += t.numel() * t.element_size()
         return total
+
+
+@dataclass(frozen=True)
+class BlockAttentionReport:
+    """Telemetry of an online-softmax pass (long_context.py:36-44)."""
+
+    query_tokens: int
+    kv_tokens: int
+    num_kv_blocks: int
+    peak_tile_elements: int
+    max_logsumexp: float
+
+
+def _attn_tag(dtype):
+    torch = _torch()
+    return {torch.float32: _lib.DTYPE_F32, torch.bfloat16: _lib.DTYPE_BF16,
+            torch.float16: _lib.DTYPE_F16, torch.float64: _lib.DTYPE_F64}.get(dtype)
+
+
+def _float_tile(k, v, keep):
+    """AttnTile of float K/V blocks [B, H_kv, S, D] (k and v of one dtype,
+    rows contiguous and aligned; otherwise contiguous copies, kept alive in
+    ``keep`` until the update is enqueued)."""
+    torch = _torch()
+    if k.dtype != v.dtype or _attn_tag(k.dtype) is None:
+        k, v = k.to(torch.float64), v.to(torch.float64)
+    es = k.element_size()
+    ak, av = min(16, 8 * es), min(16, 4 * es)
+
+    def fits(t, a):
+        return (t.stride(-1) == 1 and t.data_ptr() % a == 0 and
+                all((st * es) % ak == 0 for st in t.stride()[:3]) and t.stride(2) >= t.shape[3])
+
+    if not fits(k, ak) or not fits(v, av) or k.stride() != v.stride():
+        k, v = k.contiguous(), v.contiguous()
+    keep.extend((k, v))
+    tile = _lib.AttnTile(k.data_ptr(), v.data_ptr(), None, None, k.shape[2],
+                         k.stride(0), k.stride(1), k.stride(2), 0, 0, 0)
+    return tile, _attn_tag(k.dtype)
+
+
+class OnlineSoftmaxBlockAttention:
+    """Exact attention of queries over streamed (K, V) tiles with fp64
+    (m, l, acc) state (long_context.py:47-209): MHA, GQA and MQA, optional
+    causal masking.  Constructor arguments, validation and the scale
+    1/sqrt(head_dim) follow the reference; the arithmetic runs on the GPU
+    (scores and state in fp64, tiles read in their own type)."""
+
+    def __init__(self, num_heads: int, num_kv_heads: Optional[int] = None, head_dim: int = 64,
+                 *, q_block_size: int = 128, kv_block_size: int = 256,
+                 causal: bool = True) -> None:
+        if min(num_heads, head_dim, q_block_size, kv_block_size) <= 0:
+            raise ValueError("Attention dimensions and block sizes must be positive")
+        self.num_heads = int(num_heads)
+        self.num_kv_heads = int(num_kv_heads or num_heads)
+        if self.num_heads % self.num_kv_heads != 0:
+            raise ValueError(f"num_heads ({self.num_heads}) must be divisible by num_kv_heads "
+                             f"({self.num_kv_heads})")
+        self.num_queries_per_kv = self.num_heads // self.num_kv_heads
+        self.head_dim = int(head_dim)
+        self.q_block_size = int(q_block_size)
+        self.kv_block_size = int(kv_block_size)
+        self.causal = bool(causal)
+        self.scale = 1.0 / math.sqrt(self.head_dim)
+
+    def _expand_kv_heads(self, tensor):
+        """[B, H_kv, S, D] -> [B, H_q, S, D], each kv head repeated for its
+        query heads (a view)."""
+        if self.num_queries_per_kv == 1:
+            return tensor
+        B, H_kv, S, D = tensor.shape
+        return tensor.unsqueeze(2).expand(B, H_kv, self.num_queries_per_kv, S, D).reshape(
+            B, self.num_heads, S, D)
+
+    def _check_query(self, query):
+        if query.dim() != 4:
+            raise ValueError(f"Expected query [B, H, S_q, D], got {tuple(query.shape)}")
+        B, H_q, S_q, D = query.shape
+        if H_q != self.num_heads or D != self.head_dim:
+            raise ValueError(f"Expected query heads={self.num_heads}, dim={self.head_dim}, "
+                             f"got ({H_q}, {D})")
+        _require_gpu(query, "OnlineSoftmaxBlockAttention")
+        if _attn_tag(query.dtype) is None:
+            raise TypeError(f"unsupported query dtype {query.dtype}: float32, bfloat16, "
+                            "float16 or float64")
+
+    def _init(self, query):
+        torch = _torch()
+        B, H_q, S_q, D = query.shape
+        rows = B * H_q * S_q
+        state = torch.empty(rows, 2 * D + 2, dtype=torch.float64, device=query.device)
+        q = query.contiguous()
+        rc = _lib.lib().ojasx_attention_stream_init_device(_vp(state), _vp(q), _attn_tag(q.dtype),
+                                                          rows, D, _stream())
+        _lib.check(rc, "ojasx_attention_stream_init_device")
+        return state
+
+    def _page_tiles(self, cache, query):
+        """The cache's resident pages as int8 attention tiles, rebuilt only
+        after an append: (tile array, resident tokens, longest page)."""
+        if cache._tiles is not None and cache._tiles[0] == cache._version:
+            return cache._tiles[1:]
+        tiles = []
+        for qk, sk, qv, sv in cache._pages:
+            if qk.device != query.device:
+                raise ValueError("the cache's pages live on another device than the query")
+            self._check_block(qk, query.shape[0], "key")
+            if qk.shape[2]:
+                tiles.append(_lib.AttnTile(qk.data_ptr(), qv.data_ptr(), sk.data_ptr(),
+                                           sv.data_ptr(), qk.shape[2], qk.stride(0), qk.stride(1),
+                                           qk.stride(2), sk.stride(0), sk.stride(1), sk.stride(2)))
+        arr = (_lib.AttnTile * len(tiles))(*tiles)
+        cache._tiles = (cache._version, arr, sum(t.n_tokens for t in tiles),
+                        max((t.n_tokens for t in tiles), default=0))
+        return cache._tiles[1:]
+
+    def _update(self, state, query, tiles, kv_tag, query_start_pos, kv_offset):
+        B, H_q, S_q, D = query.shape
+        arr = tiles if isinstance(tiles, ctypes.Array) else (_lib.AttnTile * len(tiles))(*tiles)
+        rc = _lib.lib().ojasx_attention_stream_update_device(
+            _vp(state), B, H_q, self.num_kv_heads, S_q, D, arr, len(tiles), kv_tag,
+            int(self.causal), int(query_start_pos), int(kv_offset), float(self.scale), _stream())
+        _lib.check(rc, "ojasx_attention_stream_update_device")
+
+    def _finalize(self, state, query, lse=None):
+        torch = _torch()
+        out = torch.empty(query.shape, dtype=query.dtype, device=query.device)
+        rc = _lib.lib().ojasx_attention_stream_finalize_device(
+            _vp(state), state.shape[0], query.shape[3], _vp(out), _attn_tag(query.dtype),
+            _vp(lse) if lse is not None else None, _stream())
+        _lib.check(rc, "ojasx_attention_stream_finalize_device")
+        return out
+
+    def _check_block(self, t, B, name):
+        if t.dim() != 4 or t.shape[0] != B or t.shape[1] != self.num_kv_heads or \
+                t.shape[3] != self.head_dim:
+            raise ValueError(f"Expected {name} block [B={B}, H_kv={self.num_kv_heads}, S, "
+                             f"D={self.head_dim}], got {tuple(t.shape)}")
+
+    def forward_stream(self, query, kv_stream, *, query_start_pos: int = 0):
+        """Attention of ``query`` [B, H_q, S_q, D] over a stream of
+        ``(K_block, V_block)`` tiles [B, H_kv, S_k, D] (long_context.py:92-176),
+        or over every resident page of a ``PagedCompressedKVCache`` passed
+        as the stream.  Returns ``(out, BlockAttentionReport)``; ``out`` has
+        the query's dtype."""
+        torch = _torch()
+        self._check_query(query)
+        B, H_q, S_q, D = query.shape
+        state = self._init(query)
+        kv_offset = num_blocks = peak = 0
+        if isinstance(kv_stream, PagedCompressedKVCache) and kv_stream._pages and \
+                kv_stream._pages[0][0].shape[3] % 16 == 0:
+            self._check_block(kv_stream._pages[0][0], B, "key")
+            arr, kv_offset, max_n = self._page_tiles(kv_stream, query)
+            num_blocks = len(arr)
+            peak = B * H_q * S_q * max_n
+            self._update(state, query, arr, _lib.DTYPE_INT8, query_start_pos, 0)
+        else:
+            if isinstance(kv_stream, PagedCompressedKVCache):
+                kv_stream = kv_stream.iter_dequantized_pages()   # head_dim not a multiple of 16
+
+            for k_blk, v_blk in kv_stream:
+                k_blk = k_blk.to(device=query.device)
+                v_blk = v_blk.to(device=query.device)
+                self._check_block(k_blk, B, "key")
+                self._check_block(v_blk, B, "value")
+                if k_blk.shape[2] != v_blk.shape[2]:
+                    raise ValueError("key and value blocks differ in length")
+                S_k = k_blk.shape[2]
+                if S_k == 0:
+                    continue
+                keep = []
+                tile, tag = _float_tile(k_blk, v_blk, keep)
+                self._update(state, query, [tile], tag, query_start_pos, kv_offset)
+                num_blocks += 1
+                peak = max(peak, B * H_q * S_q * S_k)
+                kv_offset += S_k
+        lse = torch.empty(state.shape[0], dtype=torch.float64, device=query.device)
+        out = self._finalize(state, query, lse)
+        max_lse = float(lse.max().item()) if kv_offset > 0 else 0.0
+        return out, BlockAttentionReport(query_tokens=S_q, kv_tokens=kv_offset,
+                                         num_kv_blocks=num_blocks, peak_tile_elements=peak,
+                                         max_logsumexp=max_lse)
+
+    def forward(self, query, key, value, *, query_start_pos: int = 0):
+        """Tiled exact attention of ``query`` over ``key`` / ``value``
+        [B, H_kv, S_k, D] (long_context.py:178-209): query blocks of
+        q_block_size, each over the kv blocks of kv_block_size its causal
+        horizon reaches, all of a query block's kv blocks in one update."""
+        torch = _torch()
+        self._check_query(query)
+        B, H_q, S_q, D = query.shape
+        key = key.to(device=query.device)
+        value = value.to(device=query.device)
+        self._check_block(key, B, "key")
+        self._check_block(value, B, "value")
+        S_k = key.shape[2]
+        outs = []
+        for q_start in range(0, S_q, self.q_block_size):
+            q_stop = min(q_start + self.q_block_size, S_q)
+            q_chunk = query[:, :, q_start:q_stop, :]
+            eff_k = min(S_k, query_start_pos + q_stop) if self.causal else S_k
+            state = self._init(q_chunk)
+            keep, tiles, tag = [], [], None
+            for k_start in range(0, max(eff_k, 0), self.kv_block_size):
+                k_stop = min(k_start + self.kv_block_size, eff_k)
+                tile, tag = _float_tile(key[:, :, k_start:k_stop, :],
+                                        value[:, :, k_start:k_stop, :], keep)
+                tiles.append(tile)
+            if tiles:
+                self._update(state, q_chunk, tiles, tag, query_start_pos + q_start, 0)
+            outs.append(self._finalize(state, q_chunk))
+        return torch.cat(outs, dim=2)
+
+    __call__ = forward
 
 
 def _group_stride(t):

@@ -143,6 +143,73 @@ def online_softmax_attention(q, k_tiles, v_tiles, scale=None):
     return acc / (l if l > 0 else 1.0)
 
 
+def block_attention_stream(q, tiles, causal=True, query_start_pos=0, scale=None):
+    """fp64 OnlineSoftmaxBlockAttention.forward_stream (long_context.py:92-176)
+    for q [B, Hq, Sq, D] over (K, V) tiles [B, Hkv, S_k, D] in order, query
+    head h reading kv head h // (Hq // Hkv) (:80-89).  Per tile: scores
+    (q @ K^T) * scale, -inf where key position > query position when causal
+    (:133-139), then the running (m, l, acc) update with the -inf guards
+    (:141-163).  Returns (out [B, Hq, Sq, D] fp64, lse [B, Hq, Sq] fp64 =
+    m + log(l) with l = 0 -> 1, kv tokens, tiles)."""
+    q = np.asarray(q, np.float64)
+    B, Hq, Sq, D = q.shape
+    scale = 1.0 / math.sqrt(D) if scale is None else scale
+    m = np.full((B, Hq, Sq, 1), -np.inf)
+    l = np.zeros((B, Hq, Sq, 1))
+    acc = np.zeros((B, Hq, Sq, D))
+    qpos = (query_start_pos + np.arange(Sq)).reshape(1, 1, Sq, 1)
+    off = n_tiles = 0
+    for K, V in tiles:
+        K = np.asarray(K, np.float64)
+        V = np.asarray(V, np.float64)
+        S = K.shape[2]
+        if S == 0:
+            continue
+        n_tiles += 1
+        rep = Hq // K.shape[1]
+        K = np.repeat(K, rep, axis=1)
+        V = np.repeat(V, rep, axis=1)
+        s = (q @ np.swapaxes(K, -1, -2)) * scale
+        if causal:
+            kpos = (off + np.arange(S)).reshape(1, 1, 1, S)
+            s = np.where(kpos > qpos, -np.inf, s)
+        m_new = np.maximum(m, s.max(axis=-1, keepdims=True))
+        safe = np.where(np.isinf(m_new), 0.0, m_new)
+        with np.errstate(invalid="ignore"):
+            alpha = np.where(np.isinf(m), 0.0, np.exp(m - safe))
+            p = np.where(np.isinf(s), 0.0, np.exp(s - safe))
+        l = alpha * l + p.sum(axis=-1, keepdims=True)
+        acc = alpha * acc + p @ V
+        m = m_new
+        off += S
+    sl = np.where(l > 0.0, l, 1.0)
+    with np.errstate(invalid="ignore"):
+        lse = (m + np.log(sl))[..., 0]
+    return acc / sl, lse, off, n_tiles
+
+
+def masked_full_attention(q, K, V, causal=True, query_start_pos=0, scale=None):
+    """fp64 full-matrix attention with the causal mask and GQA head mapping
+    (tests/test_m13_ultra_long_context_10m.py:49-103): rows whose keys are
+    all hidden give 0."""
+    q = np.asarray(q, np.float64)
+    B, Hq, Sq, D = q.shape
+    scale = 1.0 / math.sqrt(D) if scale is None else scale
+    rep = Hq // np.asarray(K).shape[1]
+    K = np.repeat(np.asarray(K, np.float64), rep, axis=1)
+    V = np.repeat(np.asarray(V, np.float64), rep, axis=1)
+    s = (q @ np.swapaxes(K, -1, -2)) * scale
+    if causal:
+        kpos = np.arange(K.shape[2]).reshape(1, 1, 1, -1)
+        qpos = (query_start_pos + np.arange(Sq)).reshape(1, 1, Sq, 1)
+        s = np.where(kpos > qpos, -np.inf, s)
+    mx = s.max(axis=-1, keepdims=True)
+    safe = np.where(np.isinf(mx), 0.0, mx)
+    e = np.where(np.isinf(s), 0.0, np.exp(s - safe))
+    tot = e.sum(axis=-1, keepdims=True)
+    return (e / np.where(tot > 0.0, tot, 1.0)) @ V
+
+
 def full_softmax_attention(q, K, V, scale=None):
     """fp64 full-softmax reference (tests/test_m13_ultra_long_context_10m.py:49-103)."""
     q = np.asarray(q, np.float64).reshape(-1)

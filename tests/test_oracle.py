@@ -288,6 +288,45 @@ def test_online_softmax_matches_full():
     assert np.abs(o - no.full_softmax_attention(q, K, V)).max() < 1e-12
 
 
+def test_block_attention_stream_matches_masked_full():
+    """The batched stream restatement against the full-matrix fp64 attention
+    of the reference's M13 tests: causal GQA with a query offset, uneven
+    tiles, an empty tile, and rows whose keys are all hidden (output 0)."""
+    r = gen.rng(13)
+    B, Hq, Hkv, Sq, D, S = 2, 8, 2, 5, 16, 300
+    q = r.normal(size=(B, Hq, Sq, D))
+    K = r.normal(size=(B, Hkv, S, D))
+    V = r.normal(size=(B, Hkv, S, D))
+    cuts = [0, 37, 37, 190, 256, 300]
+    tiles = [(K[:, :, a:b], V[:, :, a:b]) for a, b in zip(cuts, cuts[1:])]
+    for causal, qsp in ((True, 150), (False, 0), (True, -3)):
+        o, lse, n, nt = no.block_attention_stream(q, tiles, causal, qsp)
+        want = no.masked_full_attention(q, K, V, causal, qsp)
+        assert np.abs(o - want).max() < 1e-12, (causal, qsp)
+        assert n == S and nt == 4
+    assert np.all(o[:, :, :3] == 0) and np.isinf(lse[:, :, :3]).all()   # qsp -3: rows 0..2 see nothing
+
+
+def test_block_attention_stream_closed_forms():
+    """Head mapping h -> h // (Hq / Hkv) (kv head j holds V = j + 1 everywhere:
+    every output of query head h is h // 4 + 1), a single visible key (out =
+    its V row), and n identical tiles (same output, lse + log n)."""
+    r = gen.rng(14)
+    B, Hq, Hkv, D = 1, 8, 2, 8
+    q = r.normal(size=(B, Hq, 3, D))
+    K = r.normal(size=(B, Hkv, 40, D))
+    V = np.ones((B, Hkv, 40, D)) * np.arange(1, Hkv + 1).reshape(1, Hkv, 1, 1)
+    o, _, _, _ = no.block_attention_stream(q, [(K, V)], causal=False)
+    assert np.allclose(o, (np.arange(Hq) // 4 + 1).reshape(1, Hq, 1, 1), atol=1e-14)
+    V2 = r.normal(size=(B, Hkv, 40, D))
+    o, _, _, _ = no.block_attention_stream(q, [(K, V2)], causal=True, query_start_pos=0)
+    assert np.array_equal(o[:, :, 0], np.repeat(V2[:, :, 0], 4, axis=1))
+    o1, l1, _, _ = no.block_attention_stream(q, [(K, V2)], causal=False)
+    o5, l5, n5, _ = no.block_attention_stream(q, [(K, V2)] * 5, causal=False)
+    assert n5 == 200
+    assert np.abs(o5 - o1).max() < 1e-13 and np.abs(l5 - (l1 + np.log(5))).max() < 1e-12
+
+
 # ------------------------------------------- the compiled reference (optional) --
 
 needs_ref = pytest.mark.skipif(not ref.available(), reason="reference engine not built here")
