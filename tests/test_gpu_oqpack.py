@@ -41,3 +41,18 @@ def test_package_layers_on_gpu(pkg, dev, tmp_path):
     assert rel_err(nat.forward(x), want) < 1e-5
     with pytest.raises(ValueError, match="one 8-bit stage"):
         loaded["a"].native_linear()
+
+
+def test_reference_written_package_on_gpu(pkg, dev):
+    """The reference's own package (tests/golden/make_oqpack_golden.py): its
+    layers on the GPU reproduce the reference modules' outputs, through the
+    math-engine kernel and, for the 8-bit block-16 layer, the LUT-GEMV handle."""
+    import os
+    import torch
+    from conftest import GOLDEN
+    exp = np.load(os.path.join(GOLDEN, "oqpack_ref_expected.npz"))
+    layers, _ = pkg.oqpack.load_lut_layers(os.path.join(GOLDEN, "oqpack_ref_small"), device=dev)
+    for name, x, y in (("0", exp["x0"], exp["y0"]), ("2", exp["x2"], exp["y2"])):
+        got = layers[name](torch.from_numpy(x).to(dev)).cpu().numpy()
+        assert rel_err(got, y) < 1e-5, name
+    assert rel_err(layers["0"].native_linear().forward(exp["x0"]), exp["y0"]) < 1e-5

@@ -132,3 +132,61 @@ def test_non_lut_layers_skipped_or_strict(pkg, package):
     assert "experts" not in layers and len(layers) == 3
     with pytest.raises(oq.OQPackValidationError, match="not a LUT layer"):
         oq.load_lut_layers(package["dir"], device="cpu", strict=True)
+
+
+# --- a package written by the reference's own save_oqpack ---------------------------
+# tests/golden/oqpack_ref_small/ and oqpack_ref_expected.npz come from
+# tests/golden/make_oqpack_golden.py (the reference's quantize_model + save_oqpack,
+# ojasx_24x96/oqpack.py:383-548, and its modules' forward outputs).
+
+def _ref_package():
+    import os
+    from conftest import GOLDEN
+    return os.path.join(GOLDEN, "oqpack_ref_small"), np.load(os.path.join(GOLDEN,
+                                                                        "oqpack_ref_expected.npz"))
+
+
+def test_reference_package_verifies_and_loads(pkg):
+    """This build's verifier and reader accept the reference's package; the
+    loaded layers through the NumPy oracle reproduce the reference modules'
+    outputs (rel 1e-5)."""
+    from conftest import rel_err
+    oq = pkg.oqpack
+    path, exp = _ref_package()
+    m = oq.verify_oqpack_integrity(path)
+    assert m.format_version == "oqpack.v1" and m.model_id == "ojasx-lut-interchange-fixture"
+    assert sorted(m.layer_specs) == ["0", "2"]
+    layers, _ = oq.load_lut_layers(path, device="cpu")
+    assert [layers[k].weight.stages for k in ("0", "2")] == list(exp["stages"])
+    for name, x, y in (("0", exp["x0"], exp["y0"]), ("2", exp["x2"], exp["y2"])):
+        w, b = layers[name].weight, layers[name].bias
+        rows, cols = w.original_shape
+        got = no.subspace_lut_rvq_gemm(x, w.codebooks.numpy(), w.packed_codes.numpy(),
+                                       w.bits_per_stage, rows, cols, w.block_size,
+                                       w.row_scales.numpy(), None if b is None else b.numpy())
+        assert rel_err(got, y) < 1e-5, name
+
+
+def test_reference_package_tamper_detected(pkg, tmp_path):
+    """A flipped byte in the reference's shard fails the checksum check."""
+    import shutil
+    oq = pkg.oqpack
+    path, _ = _ref_package()
+    bad = tmp_path / "bad"
+    shutil.copytree(path, bad)
+    shard = next(bad.glob("shard-*.safetensors"))
+    data = bytearray(shard.read_bytes())
+    data[-5] ^= 0x40
+    shard.write_bytes(bytes(data))
+    with pytest.raises(oq.OQPackValidationError):
+        oq.verify_oqpack_integrity(bad)
+
+
+def test_reference_reads_our_package():
+    """Recorded at fixture generation: the reference's
+    load_quantized_model_from_oqpack (ojasx_24x96/oqpack.py:688-754) read the
+    package this build's save_oqpack wrote from the same layers, and its
+    modules gave the reference package's outputs bit for bit."""
+    _, exp = _ref_package()
+    assert np.array_equal(exp["ours_by_ref_y0"], exp["y0"])
+    assert np.array_equal(exp["ours_by_ref_y2"], exp["y2"])
