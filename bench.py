@@ -48,7 +48,7 @@ CAL_COPY_BYTES = 64 << 20
 FLUSH_BYTES = 512 << 20
 PROFILES = os.path.join(ROOT, "profiles")
 TRAFFIC_SUMMARY = os.path.join(PROFILES, "lut_dec_kernel_2560x6912_b1_hbm_traffic.md")
-GROUP_TRAFFIC_SUMMARY = os.path.join(PROFILES, "lut_group_kernel_160x2560x6912_hbm_traffic.md")
+GROUP_TRAFFIC_SUMMARY = os.path.join(PROFILES, "lut_bank_kernel_160x2560x6912_hbm_traffic.md")
 VP = ctypes.c_void_p
 
 
@@ -289,11 +289,11 @@ def bench_sustained(b, handles, base, wbytes, steps):
     reps = max(10, min(steps, 200))
     us = b.events_us(call, reps)
     kern = b.kernels(call, reps)
-    kus = kern["lut_group_kernel"]["avg_us"]
+    kname = dominant(kern)
+    kus = kern[kname]["avg_us"]
     code_bytes = M_GU * (K_GU // 16)
     all_bytes = wbytes + K_GU * 4 + M_GU * 4
-    rf = roofline(n * code_bytes, n * all_bytes, kus, "lut_group_kernel",
-                  kern["lut_group_kernel"]["calls"],
+    rf = roofline(n * code_bytes, n * all_bytes, kus, kname, kern[kname]["calls"],
                   measured_traffic(GROUP_TRAFFIC_SUMMARY) if n == 160 else None)
     return {"instances": n, "us_per_launch": round(us, 3), "us_per_linear": round(kus / n, 4),
             "roofline": rf}
