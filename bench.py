@@ -115,12 +115,21 @@ class Bench:
         self.fbuf.add_(1.0)
         self.torch.cuda.synchronize()
 
+    def gate(self, n):
+        """Hold the stream with a bounded spin kernel (about 15 µs per call to
+        come) while the host enqueues the timed calls, so the timed region
+        measures the GPU running them back to back, not the host issuing the
+        first ones."""
+        if hasattr(self.torch.cuda, "_sleep"):
+            self.torch.cuda._sleep(int(min(n * 15, 200000) * 2400))
+
     def events_us(self, fn, n):
         """Average µs per call of fn(i), i < n, from HIP events on the launch
-        stream, after a flush."""
+        stream, after a flush, the calls enqueued behind a gate."""
         torch = self.torch
         self.flush()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        self.gate(n)
         e0.record(self.stream)
         for i in range(n):
             fn(i)

@@ -53,6 +53,7 @@ constexpr int kBRows = kBW * 64;        // rows per workgroup: 32 per half-wave
 constexpr int kBPF = 2;                 // slices of codes in flight
 constexpr int kLutRow = 64;             // words per code in the LUT: two buffers of 32 groups
 constexpr int kStagePT = 12;            // CSR entries staged per thread
+constexpr int kEarlyPT = 10;            // of which loaded before the slice loop
 constexpr int kStage = kStagePT * kBNT; // per workgroup (4 B each, in the 64 KB LUT space)
 typedef float v16f __attribute__((ext_vector_type(16)));
 
@@ -67,23 +68,30 @@ __device__ __forceinline__ void bank_codes(const uint8_t *cp, int s, uint4 (&c)[
     c[1] = gld(p + 1);
 }
 
-// x staged in LDS with a row of kXRow words per group (16 used): the b128
-// reads of 8 lanes at groups g .. g + 7 then start at banks 20 g mod 32, 32
-// distinct banks.
-constexpr int kXRow = 20;
-__device__ __forceinline__ int xs_index(int k) { return (k >> 4) * kXRow + (k & 15); }
-
-// MFMA B operand of slice s: x[16 (32 s + g) + 8 h .. + 8) from the staged x,
-// the group clamped into the input (columns of groups past G are zeroed at
-// the store).
-__device__ __forceinline__ void bank_xop(const float *xs, int G, int s, int g, int h, float (&b)[8]) {
-    const float4 *p = reinterpret_cast<const float4 *>(xs + min(32 * s + g, G - 1) * kXRow + 8 * h);
-    const float4 u = p[0], v = p[1];
-    b[0] = u.x; b[1] = u.y; b[2] = u.z; b[3] = u.w;
-    b[4] = v.x; b[5] = v.y; b[6] = v.z; b[7] = v.w;
-}
+// x staged in LDS once per workgroup, already split into its three bf16
+// pieces (x = x1 + x2 + x3 exactly, see split3): a row of kXRow words per
+// group, piece p in words 8p .. 8p + 7 (16 bf16), no padding (two
+// workgroups per CU up to K = 2560: 64 KB of LUT + 96 B per group each).  x
+// itself is (x1 + x2) + x3 in fp32, exact (24 significant bits).
+constexpr int kXRow = 24;
 
 typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+
+// MFMA B operand of slice s: the three pieces of x[16 (32 s + g) + 8 h .. + 8)
+// from the staged x, the group clamped into the input (columns of groups past
+// G are zeroed at the store).
+__device__ __forceinline__ void bank_xop(const float *xs, int G, int s, int g, int h, v8bf (&b)[3]) {
+    const v8bf *p = reinterpret_cast<const v8bf *>(xs + min(32 * s + g, G - 1) * kXRow + 4 * h);
+    b[0] = p[0];
+    b[1] = p[2];
+    b[2] = p[4];
+}
+
+// x[k] from its staged pieces.
+__device__ __forceinline__ float xs_value(const float *xs, int k) {
+    const __bf16 *r = reinterpret_cast<const __bf16 *>(xs + (k >> 4) * kXRow) + (k & 15);
+    return ((float)r[0] + (float)r[16]) + (float)r[32];
+}
 
 // v = v1 + v2 + v3 exactly: v1 = bf16(v), v2 = bf16(v - v1), v3 = v - v1 - v2
 // (an fp32 value has 24 significant bits, each bf16 piece takes 8; the
@@ -205,9 +213,30 @@ enum { XS_F32 = 0, XS_BF16 = 1, XS_SWIGLU = 2 };
 
 // x (or silu(gate) * up, silu(v) = v / (1 + exp(-v))) into LDS, float4 i
 // holding dims 4(i%4).. of group i/4; two loads in flight per thread.
+// Dims 4 (i % 4) .. + 3 of group i / 4 into the staged rows, as three pieces.
+__device__ __forceinline__ void bank_put_x(float *xs, int i, float4 v) {
+    const float f[4] = {v.x, v.y, v.z, v.w};
+    __bf16 pc[3][4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const __bf16 h1 = (__bf16)f[k];
+        const float r1 = f[k] - (float)h1;
+        const __bf16 h2 = (__bf16)r1;
+        pc[0][k] = h1;
+        pc[1][k] = h2;
+        pc[2][k] = (__bf16)(r1 - (float)h2);
+    }
+    uint2 *row = reinterpret_cast<uint2 *>(xs + (i >> 2) * kXRow) + (i & 3);
+#pragma unroll
+    for (int p = 0; p < 3; ++p) {
+        uint2 w;
+        __builtin_memcpy(&w, pc[p], 8);
+        row[4 * p] = w;
+    }
+}
+
 template <int XS>
 __device__ __forceinline__ void bank_stage_x(const void *x, int K, float *xs, int tid) {
-    float4 *xs4 = reinterpret_cast<float4 *>(xs);
     for (int i = tid; i < K / 4; i += 2 * kBNT) {
         const int i2 = min(i + kBNT, K / 4 - 1);
         float4 u, v;
@@ -226,8 +255,8 @@ __device__ __forceinline__ void bank_stage_x(const void *x, int K, float *xs, in
             u = make_float4(sw(ga.x, ua.x), sw(ga.y, ua.y), sw(ga.z, ua.z), sw(ga.w, ua.w));
             v = make_float4(sw(gb.x, ub.x), sw(gb.y, ub.y), sw(gb.z, ub.z), sw(gb.w, ub.w));
         }
-        xs4[(i >> 2) * (kXRow / 4) + (i & 3)] = u;
-        xs4[(i2 >> 2) * (kXRow / 4) + (i2 & 3)] = v;
+        bank_put_x(xs, i, u);
+        bank_put_x(xs, i2, v);
     }
 }
 
@@ -269,25 +298,24 @@ __device__ __forceinline__ void bank_block(const BankBlock &bb, float *L, float 
     // ---- slice 0 into buffer 0
     v8bf a[3], b[3];
     split3(af, a);
-    float bf[8];
-    bank_xop(xs, G, 0, g, h, bf);
-    split3(bf, b);
+    bank_xop(xs, G, 0, g, h, b);
     {
         const v16f d = bank_build(a, b);
         bank_store(L, 0, w, g, h, g < G, d);
     }
-    bank_xop(xs, G, min(1, S - 1), g, h, bf);
-    split3(bf, b);
+    bank_xop(xs, G, min(1, S - 1), g, h, b);
     __syncthreads();
 
-    // the outliers' loads (the workgroup's CSR range, coalesced) go out now
-    // and are consumed after the last slice, their latency under the slices
+    // The outliers' loads (the workgroup's CSR range, coalesced): the first
+    // kEarlyPT per thread go out now, under the slices; the rest, needed only
+    // by ranges longer than kEarlyPT * 512 entries, before the last slice
+    // (all of them here would hold 24 registers across the slice loop).
     const int ne = min(e1 - e0, kStage);
     int cl[kStagePT];
     float vl[kStagePT];
     if (ne > 0) {
 #pragma unroll
-        for (int i = 0; i < kStagePT; ++i) {
+        for (int i = 0; i < kEarlyPT; ++i) {
             const int e = e0 + min(tid + i * kBNT, ne - 1);
             cl[i] = gld(bb.col + e);
             vl[i] = gld(bb.val + e);
@@ -306,9 +334,9 @@ __device__ __forceinline__ void bank_block(const BankBlock &bb, float *L, float 
         const v16f d = bank_build(a, b);                         // slice s + 1
         bank_gather(L, (s & 1) ? gsel1 : gsel0, ring[q], acc);   // slice s
         bank_codes(cp, min(s + kBPF, S - 1), ring[q]);
-        bank_xop(xs, G, min(s + 2, S - 1), g, h, bf);
+        __builtin_amdgcn_sched_barrier(0);                       // b is read by the build above
+        bank_xop(xs, G, min(s + 2, S - 1), g, h, b);
         bank_store(L, (s + 1) & 1, w, g, h, 32 * (s + 1) + g < G, d);
-        split3(bf, b);
         __syncthreads();
     };
     int sb = 0;
@@ -319,6 +347,14 @@ __device__ __forceinline__ void bank_block(const BankBlock &bb, float *L, float 
 #pragma unroll
     for (int q = 0; q < kBPF - 1; ++q)
         if (sb + q < S - 1) one(sb + q, q);
+    if (ne > kEarlyPT * kBNT) {
+#pragma unroll
+        for (int i = kEarlyPT; i < kStagePT; ++i) {
+            const int e = e0 + min(tid + i * kBNT, ne - 1);
+            cl[i] = gld(bb.col + e);
+            vl[i] = gld(bb.val + e);
+        }
+    }
     __builtin_amdgcn_sched_barrier(0);
     if ((S - 1) % kBPF == 0)                                     // the last slice
         bank_gather(L, ((S - 1) & 1) ? gsel1 : gsel0, ring[0], acc);
@@ -335,7 +371,7 @@ __device__ __forceinline__ void bank_block(const BankBlock &bb, float *L, float 
     if (ne > 0) {
 #pragma unroll
         for (int i = 0; i < kStagePT; ++i)
-            if (tid + i * kBNT < ne) sp[tid + i * kBNT] = vl[i] * xs[xs_index(cl[i])];
+            if (tid + i * kBNT < ne) sp[tid + i * kBNT] = vl[i] * xs_value(xs, cl[i]);
         __syncthreads();
     }
     float o = 0.f;
@@ -349,7 +385,7 @@ __device__ __forceinline__ void bank_block(const BankBlock &bb, float *L, float 
         for (int u = 0; u < 4; ++u) o += pr[u];
     }
     for (; j < js; ++j) o += sp[j - e0];
-    for (; j < j1; ++j) o += gld(bb.val + j) * xs[xs_index(gld(bb.col + j))];
+    for (; j < j1; ++j) o += gld(bb.val + j) * xs_value(xs, gld(bb.col + j));
     float y = tot * sc;
     if (bb.bias) y += bs;
     if (m < bb.M) bb.y[m] = y + o;
