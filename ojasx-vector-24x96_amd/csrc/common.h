@@ -112,7 +112,8 @@ inline size_t bank_codes_bytes(int M, int G) { return (size_t)((M + 63) / 64) * 
 // to 31 groups x 64 bytes past its block.
 constexpr size_t kBankSlack = 2048;
 // MoE stages on the bank kernel (lut_bank.hip): the plan (routed pairs sorted
-// by expert into work lists of (pair, first row)), then one launch per stage.
+// by expert into work lists of (pair, 512-row block << 16 | expert); E at
+// most 65535), then one launch per stage.
 int launch_moe_plan(const int *idx, const float *w, int P, int E, int nb_gu, int nb_dn,
                     int2 *work_gu, int2 *work_dn, int *n_work, hipStream_t st);
 struct MoEBankLaunch {

@@ -405,8 +405,8 @@ __global__ __launch_bounds__(kBNT) void lut_bank_kernel(const GroupItem *__restr
 
 // MoE stages on the routed pairs (no outliers, no bias): gate/up (x = the
 // pair's token row, M = 2I gate then up rows) or down (x = silu(gate) * up of
-// the pair's gate/up row, M = H).  work[] = (pair, first row) comes from the
-// plan kernel, sorted by expert; workgroup i takes position
+// the pair's gate/up row, M = H).  work[] = (pair, 512-row block << 16 |
+// expert) comes from the plan kernel, sorted by expert; workgroup i takes position
 // (i % 8) * ceil(n / 8) + i / 8, so each of the 8 XCDs (workgroups go to XCD
 // i % 8) walks a contiguous stretch of the sorted list and the pairs of one
 // expert read its codes back to back through one L2.
@@ -418,7 +418,7 @@ struct MoEBankParams {
     const void *x;              // gate/up: [T][K]; down: [P][2K] fp32
     float *y;                   // [P][M]
     const int *idx;             // [P] expert of each pair
-    const int2 *work;           // [n] (pair, first row)
+    const int2 *work;           // [n] (pair, block << 16 | expert)
     const int *n_work;          // n
     int M, K, k;                // rows, inputs, slots per token
 };
@@ -432,7 +432,7 @@ __global__ __launch_bounds__(kBNT) void moe_bank_kernel(MoEBankParams p) {
     const int pos = (int)(blockIdx.x & 7) * q + (int)(blockIdx.x >> 3);
     if (pos >= n || (int)(blockIdx.x >> 3) >= q) return;
     const int2 wk = p.work[pos];
-    const int pr = wk.x, e = p.idx[pr];
+    const int pr = wk.x, e = wk.y & 0xffff;          // the expert travels with the entry
     const void *x;
     if constexpr (XS == XS_SWIGLU)
         x = static_cast<const float *>(p.x) + (size_t)pr * 2 * p.K;
@@ -442,7 +442,7 @@ __global__ __launch_bounds__(kBNT) void moe_bank_kernel(MoEBankParams p) {
         x = static_cast<const float *>(p.x) + (size_t)(pr / p.k) * p.K;
     const BankBlock bb{p.codes_b + (size_t)e * p.expert_bytes, p.cb,
                        p.scales + (size_t)e * p.M, nullptr, nullptr, nullptr, nullptr,
-                       x, p.y + (size_t)pr * p.M, p.K, p.M, wk.y};
+                       x, p.y + (size_t)pr * p.M, p.K, p.M, (wk.y >> 16) * kBRows};
     bank_block<XS>(bb, L, xs);
 }
 
@@ -505,12 +505,12 @@ __global__ __launch_bounds__(1024) void moe_plan_kernel(const int *idx, const fl
     for (int i = tid; i < nv * nb_gu; i += NT) {
         const int kk = i / nb_gu, b = i % nb_gu;
         const int pr = sorted[kk], e = idx[pr];
-        work_gu[nb_gu * start[e] + b * cnt[e] + (kk - start[e])] = make_int2(pr, b * kBRows);
+        work_gu[nb_gu * start[e] + b * cnt[e] + (kk - start[e])] = make_int2(pr, (b << 16) | e);
     }
     for (int i = tid; i < nv * nb_dn; i += NT) {
         const int kk = i / nb_dn, b = i % nb_dn;
         const int pr = sorted[kk], e = idx[pr];
-        work_dn[nb_dn * start[e] + b * cnt[e] + (kk - start[e])] = make_int2(pr, b * kBRows);
+        work_dn[nb_dn * start[e] + b * cnt[e] + (kk - start[e])] = make_int2(pr, (b << 16) | e);
     }
 }
 
