@@ -78,10 +78,10 @@ constexpr int kXRow = 24;
 typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
 
 // MFMA B operand of slice s: the three pieces of x[16 (32 s + g) + 8 h .. + 8)
-// from the staged x, the group clamped into the input (columns of groups past
-// G are zeroed at the store).
-__device__ __forceinline__ void bank_xop(const float *xs, int G, int s, int g, int h, v8bf (&b)[3]) {
-    const v8bf *p = reinterpret_cast<const v8bf *>(xs + min(32 * s + g, G - 1) * kXRow + 4 * h);
+// from the staged x (zero rows for the groups past G up to the slice's end,
+// so their LUT columns come out 0).
+__device__ __forceinline__ void bank_xop(const float *xs, int s, int g, int h, v8bf (&b)[3]) {
+    const v8bf *p = reinterpret_cast<const v8bf *>(xs + (32 * s + g) * kXRow + 4 * h);
     b[0] = p[0];
     b[1] = p[2];
     b[2] = p[4];
@@ -124,12 +124,11 @@ __device__ __forceinline__ v16f bank_build(const v8bf (&a)[3], const v8bf (&b)[3
     return d;
 }
 
-// LUT[32 w + m][g] of buffer buf <- column g of the wave's tile (0 for a group past G).
-__device__ __forceinline__ void bank_store(float *L, int buf, int w, int g, int h, bool gv,
-                                           const v16f &d) {
+// LUT[32 w + m][g] of buffer buf <- column g of the wave's tile.
+__device__ __forceinline__ void bank_store(float *L, int buf, int w, int g, int h, const v16f &d) {
     float *p = L + (32 * w + 4 * h) * kLutRow + 32 * buf + g;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) p[(8 * (r / 4) + (r % 4)) * kLutRow] = gv ? d[r] : 0.f;
+    for (int r = 0; r < 16; ++r) p[(8 * (r / 4) + (r % 4)) * kLutRow] = d[r];
 }
 
 // acc[j] += LUT[code of row j][g] for the 32 rows of the lane's half.
@@ -258,6 +257,10 @@ __device__ __forceinline__ void bank_stage_x(const void *x, int K, float *xs, in
         bank_put_x(xs, i, u);
         bank_put_x(xs, i2, v);
     }
+    // zero rows for groups G .. 32 S - 1 (the last slice's missing groups)
+    const int G = K >> 4, GS = ((G + 31) >> 5) << 5;
+    float4 *z = reinterpret_cast<float4 *>(xs + G * kXRow);
+    for (int i = tid; i < (GS - G) * (kXRow / 4); i += kBNT) z[i] = make_float4(0.f, 0.f, 0.f, 0.f);
 }
 
 template <int XS>
@@ -298,12 +301,12 @@ __device__ __forceinline__ void bank_block(const BankBlock &bb, float *L, float 
     // ---- slice 0 into buffer 0
     v8bf a[3], b[3];
     split3(af, a);
-    bank_xop(xs, G, 0, g, h, b);
+    bank_xop(xs, 0, g, h, b);
     {
         const v16f d = bank_build(a, b);
-        bank_store(L, 0, w, g, h, g < G, d);
+        bank_store(L, 0, w, g, h, d);
     }
-    bank_xop(xs, G, min(1, S - 1), g, h, b);
+    bank_xop(xs, min(1, S - 1), g, h, b);
     __syncthreads();
 
     // The outliers' loads (the workgroup's CSR range, coalesced): the first
@@ -335,8 +338,8 @@ __device__ __forceinline__ void bank_block(const BankBlock &bb, float *L, float 
         bank_gather(L, (s & 1) ? gsel1 : gsel0, ring[q], acc);   // slice s
         bank_codes(cp, min(s + kBPF, S - 1), ring[q]);
         __builtin_amdgcn_sched_barrier(0);                       // b is read by the build above
-        bank_xop(xs, G, min(s + 2, S - 1), g, h, b);
-        bank_store(L, (s + 1) & 1, w, g, h, 32 * (s + 1) + g < G, d);
+        bank_xop(xs, min(s + 2, S - 1), g, h, b);
+        bank_store(L, (s + 1) & 1, w, g, h, d);
         __syncthreads();
     };
     int sb = 0;
@@ -395,7 +398,7 @@ __device__ __forceinline__ void bank_block(const BankBlock &bb, float *L, float 
 __global__ __launch_bounds__(kBNT) void lut_bank_kernel(const GroupItem *__restrict__ items,
                                                         const int2 *__restrict__ work) {
     __shared__ float L[256 * kLutRow];               // two LUT buffers; then the products
-    extern __shared__ float xs[];                    // [G][kXRow]: x (the B operands, outliers)
+    extern __shared__ float xs[];                    // [32 S][kXRow]: x pieces (B operands, outliers)
     const int2 wk = work[blockIdx.x];
     const GroupItem it = items[wk.x];
     const BankBlock bb{it.codes_b, it.cb, it.scales, it.bias, it.rowp, it.col, it.val,
@@ -530,7 +533,7 @@ int set_dyn_lds(F *fn, size_t lds, size_t *granted) {
 
 int launch_bank(const GroupItem *items_dev, const int2 *work_dev, int n_work, int max_K,
                 hipStream_t st) {
-    const size_t lds = (size_t)(max_K / 16) * kXRow * sizeof(float);
+    const size_t lds = round_up((size_t)(max_K / 16), 32) * kXRow * sizeof(float);
     static size_t granted = 0;
     int rc = set_dyn_lds(&lut_bank_kernel, lds, &granted);
     if (rc) return rc;
@@ -557,7 +560,7 @@ int launch_moe_plan(const int *idx, const float *w, int P, int E, int nb_gu, int
 int launch_moe_bank(const MoEBankLaunch &l, hipStream_t st) {
     MoEBankParams p{l.codes_b, l.expert_bytes, l.cb, l.scales, l.x, l.y, l.idx, l.work,
                     l.n_work, l.M, l.K, l.k};
-    const size_t lds = (size_t)(l.K / 16) * kXRow * sizeof(float);
+    const size_t lds = round_up((size_t)(l.K / 16), 32) * kXRow * sizeof(float);
     const int grid = 8 * ((l.max_work + 7) / 8);
     int rc = OJASX_OK;
     if (l.xs == XS_SWIGLU) {
