@@ -1006,7 +1006,11 @@ int moe_forward(MoE *m, const void *x, const int *idx, const float *w, void *y, 
         const bool ok = m->D == 16 && k <= 32 && aligned &&
                         (size_t)(kCB * 16 + (size_t)k * m->Si * 256) * 4 <= kMaxLds &&
                         (size_t)(kCB * 16 + m->Sin * 256) * 4 <= kMaxLds;
-        if (m->D == 16 && aligned && T_ >= kBankMinTokens && m->E <= 65535 && m->gub.ptr && (size_t)T_ * k <= kBankMaxPairs)
+        // grouped by expert: expert ids fit the work entries' 16 bits and the
+        // plan kernel's LDS holds 3 E + P ints
+        const size_t P = (size_t)T_ * k;
+        if (m->D == 16 && aligned && T_ >= kBankMinTokens && m->gub.ptr && P <= kBankMaxPairs &&
+            m->E <= 65535 && (3 * (size_t)m->E + P) * sizeof(int) <= kMaxLds)
             return dtype == OJASX_DTYPE_F32 ? moe_forward_bank<float>(m, x, idx, w, y, T_, k, st)
                                             : moe_forward_bank<__hip_bfloat16>(m, x, idx, w, y, T_, k, st);
         if (m->D == 16 && T_ >= kGroupMinTokens)
