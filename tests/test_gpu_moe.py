@@ -223,3 +223,21 @@ def test_moe_by_expert_many_pairs_per_expert(pkg, dev, dtype_tag):
         want = cpu.moe_forward(xr[t], m["cb_in"], m["cb_down"], m["gu_codes"], m["gu_scales"],
                                m["dn_codes"], m["dn_scales"], idx[t], w[t])
         assert rel_err(y[t], want) < (1e-5 if dtype_tag == 0 else 1e-2), t
+
+
+@pytest.mark.parametrize("E", [4096, 16384])   # by-expert path / its plan LDS too small: per slot
+def test_moe_many_experts(pkg, dev, E):
+    """Large expert counts at 16 tokens: 4096 experts run the plan kernel in
+    49 KB of LDS, 16384 would need 196 KB and take the per-slot path."""
+    import torch
+    H, I, k, T = 64, 32, 4, 16
+    m = gen.moe(E=E, H=H, I=I, T=T, seed=E % 97, scales="u")
+    nat = make_native(pkg, m, E, H, I, k)
+    idx, w = cpu.router_topk(m["logits"], k, renorm=True)
+    idx[2, 3] = idx[2, 0]                            # a repeated expert within a token
+    idx[5, 1] = idx[9, 2]                            # and across tokens
+    y = device_moe(pkg, dev, nat, torch.from_numpy(m["x"]).to(dev), idx, w, k)
+    for t in range(T):
+        want = cpu.moe_forward(m["x"][t], m["cb_in"], m["cb_down"], m["gu_codes"], m["gu_scales"],
+                               m["dn_codes"], m["dn_scales"], idx[t], w[t])
+        assert rel_err(y[t], want) < 1e-5, t
