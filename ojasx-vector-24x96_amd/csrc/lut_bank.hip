@@ -28,18 +28,19 @@
 // Its output lane (h, n) holds rows 8(r/4) + 4h + r%4 of column n, so the
 // stores of each half-wave hit 32 distinct banks.  Lane half h supplies input
 // dimensions 8h .. 8h + 7 of both operands: 8 contiguous floats of x and of
-// its codebook row.
+// its codebook row.  The codebook is split per wave once, x once per
+// workgroup when it is staged (its three pieces side by side in LDS, zero
+// rows up to the last slice's end, so groups past G give zero LUT columns).
 // Two LUT buffers in the 64-word rows: slice s + 1 is built while slice s is
 // gathered, one barrier per slice.
 //
 // Codes come from the handle's bank layout [row block of 64][slice][group]
 // [64 rows]: a lane's 32 codes of a slice are 32 contiguous bytes, a wave's
 // 2 KB contiguous; kBPF slices are in flight in a register ring.
-// x is staged in LDS once (rows of 20 words per group, so the B operand's
-// 16-byte reads are conflict-free).  Outliers: after the slice loop the
-// workgroup's CSR range (its rows are contiguous) is loaded coalesced, the
-// products val * x[col] staged in the then free LUT space, and each lane adds
-// its row's products in CSR order.
+// Outliers: the workgroup's CSR range (its rows are contiguous) is loaded
+// coalesced (most of it before the slice loop), the products val * x[col]
+// staged in the then free LUT space, and each lane adds its row's products in
+// CSR order.
 #include <algorithm>
 
 #include "common.h"
