@@ -264,6 +264,24 @@ def linear_leg(b, hs, base, wbytes, M, K, B, dt, steps, warmup):
     return out, y.float().cpu().numpy()
 
 
+def host_pointer_call(b, handles, base, n=200):
+    """The reference's own entry point, ojasx_linear_forward (host x and y,
+    synchronous: copy in, kernel, copy out), on the headline shape: the
+    PCIe-inclusive rate a host-pointer caller sees.  Never the headline value."""
+    L = b.L
+    x = np.ascontiguousarray(base["x"][:1], np.float32)
+    y = np.empty((1, M_GU), np.float32)
+    px, py = x.ctypes.data_as(VP), y.ctypes.data_as(VP)
+    for i in range(10):
+        assert L.ojasx_linear_forward(handles[i % len(handles)], px, py, 1, 1) == 0
+    t0 = time.perf_counter()
+    for i in range(n):
+        L.ojasx_linear_forward(handles[i % len(handles)], px, py, 1, 1)
+    us = (time.perf_counter() - t0) / n * 1e6
+    return {"us_per_call": round(us, 2), "calls": n,
+            "code_GBs": round(M_GU * (K_GU // 16) / (us * 1e-6) / 1e9, 2)}
+
+
 def bench_linear2560(b, args):
     """LUT linear 2560 -> 2560, batch 1, fp32, 0.38 %
     CSR, over 400 instances (268 MB), with the reference engine's CPU time."""
@@ -844,6 +862,7 @@ def main():
         "pmc_calibration_copy_bytes": CAL_COPY_BYTES,
         "wall_s_timed": round(t_wall, 3),
         "host": host_info(),
+        "host_pointer_call": host_pointer_call(b, handles, base),
     }
     if not args.no_cpu:
         c = cpu_linear(base, 1, args.cpu_seconds, y_bench, threads=(1,))
