@@ -9,6 +9,7 @@
 #include <cstddef>
 #include <cstdint>
 #include <cstdio>
+#include <cstring>
 #include <string>
 
 #include "ojasx_lut_c_api.h"
@@ -37,6 +38,20 @@ struct DevBuf {
 };
 
 int upload(DevBuf &buf, const void *host, size_t n);  // ensure + memcpy
+
+// The host-pointer entry points (the reference's synchronous C-ABI): a call
+// copies its host inputs into this thread's pinned buffer, uploads them with
+// one asynchronous copy on this thread's stream, runs its kernels there,
+// downloads into the pinned buffer and synchronises that stream once (a
+// pageable copy is a synchronous staging pass of its own).
+struct HostIO {
+    hipStream_t st = nullptr;
+    unsigned char *pin = nullptr;
+    size_t cap = 0;
+    int reserve(size_t bytes);   // creates the stream on first use
+    ~HostIO();
+};
+HostIO &host_io();   // the calling thread's
 
 // Small per-call argument arrays (work lists, descriptors) staged for a
 // launch: kSlots slots of pinned host memory and their device copies, so the

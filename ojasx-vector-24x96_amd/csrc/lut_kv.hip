@@ -964,13 +964,13 @@ struct KVHead {
 struct KVCache {
     int heads = 0, hd = 0, D = 0, G = 0, max_seq = 0;
     std::vector<KVHead> h;
-    DevBuf cb, bt, kstage, vstage, qstage, ostage;
+    DevBuf cb, bt, kstage, qstage, ostage;   // kstage holds k | v of one append
     int bt_pages = 0;
     KVWork work;
     ~KVCache() {
         for (auto &x : h)
             for (DevBuf *b : {&x.kc, &x.vc, &x.ks, &x.vs}) b->release();
-        for (DevBuf *b : {&cb, &bt, &kstage, &vstage, &qstage, &ostage}) b->release();
+        for (DevBuf *b : {&cb, &bt, &kstage, &qstage, &ostage}) b->release();
     }
 };
 
@@ -1032,8 +1032,7 @@ OJASX_API OjasxKVHandle ojasx_create_kv_cache(int num_heads, int head_dim, int m
         if (!rc) rc = grow(hh.vs, 0, (size_t)cap * 4);
         hh.cap = cap;
     }
-    if (!rc) rc = c->kstage.ensure((size_t)head_dim * 4);
-    if (!rc) rc = c->vstage.ensure((size_t)head_dim * 4);
+    if (!rc) rc = c->kstage.ensure((size_t)head_dim * 8);
     if (!rc) rc = c->qstage.ensure((size_t)head_dim * 4);
     if (!rc) rc = c->ostage.ensure((size_t)head_dim * 4);
     if (rc) {
@@ -1059,14 +1058,21 @@ OJASX_API int ojasx_kv_cache_append(OjasxKVHandle handle, int head_idx, const fl
         if (rc) return rc;
         hh.cap = nc;
     }
-    OJX_HIP(hipMemcpy(c->kstage.ptr, k, (size_t)c->hd * 4, hipMemcpyHostToDevice));
-    OJX_HIP(hipMemcpy(c->vstage.ptr, v, (size_t)c->hd * 4, hipMemcpyHostToDevice));
-    OJX_LAUNCH(kv_append_kernel, dim3(1), dim3(128), 0, nullptr, c->kstage.as<float>(),
-                       c->vstage.as<float>(), c->hd, c->D, hh.kc.as<uint8_t>() + (size_t)hh.len * c->G,
+    // one upload: k [hd] | v [hd]
+    const size_t hb = (size_t)c->hd * 4;
+    HostIO &io = host_io();
+    int rc = io.reserve(2 * hb);
+    if (rc) return rc;
+    memcpy(io.pin, k, hb);
+    memcpy(io.pin + hb, v, hb);
+    OJX_HIP(hipMemcpyAsync(c->kstage.ptr, io.pin, 2 * hb, hipMemcpyHostToDevice, io.st));
+    OJX_LAUNCH(kv_append_kernel, dim3(1), dim3(128), 0, io.st, c->kstage.as<float>(),
+                       c->kstage.as<float>() + c->hd, c->hd, c->D,
+                       hh.kc.as<uint8_t>() + (size_t)hh.len * c->G,
                        hh.vc.as<uint8_t>() + (size_t)hh.len * c->G, hh.ks.as<float>() + hh.len,
                        hh.vs.as<float>() + hh.len);
     OJX_HIP(hipGetLastError());
-    OJX_HIP(hipDeviceSynchronize());
+    OJX_HIP(hipStreamSynchronize(io.st));
     hh.len++;
     return OJASX_OK;
 }
@@ -1081,13 +1087,20 @@ OJASX_API int ojasx_kv_cache_attention(OjasxKVHandle handle, int head_idx, const
     if (hh.len == 0) return OJASX_OK;
     int rc = ensure_pages(c, hh.cap / 16);
     if (rc) return rc;
-    OJX_HIP(hipMemcpy(c->qstage.ptr, q, (size_t)c->hd * 4, hipMemcpyHostToDevice));
+    const size_t hb = (size_t)c->hd * 4, oo = round_up(hb, 256);
+    HostIO &io = host_io();
+    rc = io.reserve(oo + hb);
+    if (rc) return rc;
+    memcpy(io.pin, q, hb);
+    OJX_HIP(hipMemcpyAsync(c->qstage.ptr, io.pin, hb, hipMemcpyHostToDevice, io.st));
     rc = kv_decode(c->qstage.as<float>(), hh.kc.as<uint8_t>(), hh.ks.as<float>(),
                    hh.vc.as<uint8_t>(), hh.vs.as<float>(), c->cb.as<float>(), c->cb.as<float>(),
                    c->bt.as<int>(), hh.len, 16, 1, 1, c->hd, c->D, scale_factor,
-                   c->ostage.as<float>(), nullptr, c->work);
+                   c->ostage.as<float>(), io.st, c->work);
+    if (!rc) OJX_HIP(hipMemcpyAsync(io.pin + oo, c->ostage.ptr, hb, hipMemcpyDeviceToHost, io.st));
+    OJX_HIP(hipStreamSynchronize(io.st));
     if (rc) return rc;
-    OJX_HIP(hipMemcpy(out_context, c->ostage.ptr, (size_t)c->hd * 4, hipMemcpyDeviceToHost));
+    memcpy(out_context, io.pin + oo, hb);
     return OJASX_OK;
 }
 

@@ -1027,11 +1027,17 @@ OJASX_API int ojasx_linear_forward(OjasxLinearHandle handle, const float *x, flo
     const size_t yb = (size_t)batch_size * L->M * sizeof(float);
     int rc = L->xstage.ensure(xb);
     if (!rc) rc = L->ystage.ensure(yb);
+    HostIO &io = host_io();
+    const size_t yo = round_up(xb, 256);
+    if (!rc) rc = io.reserve(yo + yb);
     if (rc) return rc;
-    OJX_HIP(hipMemcpy(L->xstage.ptr, x, xb, hipMemcpyHostToDevice));
-    rc = forward(L, L->xstage.ptr, L->ystage.ptr, batch_size, OJASX_DTYPE_F32, nullptr);
+    memcpy(io.pin, x, xb);
+    OJX_HIP(hipMemcpyAsync(L->xstage.ptr, io.pin, xb, hipMemcpyHostToDevice, io.st));
+    rc = forward(L, L->xstage.ptr, L->ystage.ptr, batch_size, OJASX_DTYPE_F32, io.st);
+    if (!rc) OJX_HIP(hipMemcpyAsync(io.pin + yo, L->ystage.ptr, yb, hipMemcpyDeviceToHost, io.st));
+    OJX_HIP(hipStreamSynchronize(io.st));
     if (rc) return rc;
-    OJX_HIP(hipMemcpy(y, L->ystage.ptr, yb, hipMemcpyDeviceToHost));
+    memcpy(y, io.pin + yo, yb);
     return OJASX_OK;
 }
 

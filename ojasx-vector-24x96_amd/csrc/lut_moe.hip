@@ -55,12 +55,12 @@ struct MoE {
     DevBuf cb_in, cb_dn, gu, dn, gus, dns;
     DevBuf gub, dnb;                    // bank layouts per expert (block_dim 16)
     size_t gub_bytes = 0, dnb_bytes = 0;
-    DevBuf lut_in, lut_dn, dout, inter, gu_part, xstage, ystage, istage, wstage;
+    DevBuf lut_in, lut_dn, dout, inter, gu_part, xstage, ystage;
     DevBuf work, nwork, gu_out;         // bank path: plan output, gate/up rows per pair
     size_t lut_dn_pairs = 0;
     ~MoE() {
         for (DevBuf *b : {&cb_in, &cb_dn, &gu, &dn, &gus, &dns, &gub, &dnb, &lut_in, &lut_dn,
-                          &dout, &inter, &gu_part, &xstage, &ystage, &istage, &wstage, &work,
+                          &dout, &inter, &gu_part, &xstage, &ystage, &work,
                           &nwork, &gu_out})
             b->release();
     }
@@ -1175,18 +1175,27 @@ OJASX_API int ojasx_moe_forward(OjasxMoEHandle handle, const float *x, const int
     if (!handle || !x || !top_k_indices || !top_k_weights || !y_out) return OJASX_ERR_NULL;
     if (k_active <= 0) return OJASX_OK;
     MoE *m = static_cast<MoE *>(handle);
-    int rc = m->xstage.ensure((size_t)m->H * 4);
-    if (!rc) rc = m->ystage.ensure((size_t)m->H * 4);
-    if (!rc) rc = m->istage.ensure((size_t)k_active * 4);
-    if (!rc) rc = m->wstage.ensure((size_t)k_active * 4);
+    // one upload: x [H] | indices [k] | weights [k], 256-byte aligned parts
+    const size_t xb = (size_t)m->H * 4, kb = (size_t)k_active * 4;
+    const size_t io_i = round_up(xb, 256), io_w = io_i + round_up(kb, 256);
+    const size_t in_bytes = io_w + kb, yo = round_up(in_bytes, 256);
+    int rc = m->xstage.ensure(in_bytes);
+    if (!rc) rc = m->ystage.ensure(xb);
+    HostIO &io = host_io();
+    if (!rc) rc = io.reserve(yo + xb);
     if (rc) return rc;
-    OJX_HIP(hipMemcpy(m->xstage.ptr, x, (size_t)m->H * 4, hipMemcpyHostToDevice));
-    OJX_HIP(hipMemcpy(m->istage.ptr, top_k_indices, (size_t)k_active * 4, hipMemcpyHostToDevice));
-    OJX_HIP(hipMemcpy(m->wstage.ptr, top_k_weights, (size_t)k_active * 4, hipMemcpyHostToDevice));
-    rc = moe_forward(m, m->xstage.ptr, m->istage.as<int>(), m->wstage.as<float>(), m->ystage.ptr,
-                     1, k_active, OJASX_DTYPE_F32, nullptr);
+    memcpy(io.pin, x, xb);
+    memcpy(io.pin + io_i, top_k_indices, kb);
+    memcpy(io.pin + io_w, top_k_weights, kb);
+    unsigned char *d = m->xstage.as<unsigned char>();
+    OJX_HIP(hipMemcpyAsync(d, io.pin, in_bytes, hipMemcpyHostToDevice, io.st));
+    rc = moe_forward(m, d, reinterpret_cast<const int *>(d + io_i),
+                     reinterpret_cast<const float *>(d + io_w), m->ystage.ptr, 1, k_active,
+                     OJASX_DTYPE_F32, io.st);
+    if (!rc) OJX_HIP(hipMemcpyAsync(io.pin + yo, m->ystage.ptr, xb, hipMemcpyDeviceToHost, io.st));
+    OJX_HIP(hipStreamSynchronize(io.st));
     if (rc) return rc;
-    OJX_HIP(hipMemcpy(y_out, m->ystage.ptr, (size_t)m->H * 4, hipMemcpyDeviceToHost));
+    memcpy(y_out, io.pin + yo, xb);
     return OJASX_OK;
 }
 

@@ -54,6 +54,28 @@ int upload(DevBuf &buf, const void *host, size_t n) {
     return OJASX_OK;
 }
 
+int HostIO::reserve(size_t bytes) {
+    if (!st) OJX_HIP(hipStreamCreate(&st));   // blocking: ordered after null-stream work
+    if (bytes <= cap) return OJASX_OK;
+    if (pin) (void)hipHostFree(pin);
+    pin = nullptr;
+    cap = 0;
+    const size_t n = round_up(std::max<size_t>(bytes, 64 << 10), 4096);
+    OJX_HIP(hipHostMalloc(reinterpret_cast<void **>(&pin), n, hipHostMallocDefault));
+    cap = n;
+    return OJASX_OK;
+}
+
+HostIO::~HostIO() {
+    if (pin) (void)hipHostFree(pin);
+    if (st) (void)hipStreamDestroy(st);
+}
+
+HostIO &host_io() {
+    static thread_local HostIO io;
+    return io;
+}
+
 int StagingRing::reserve(size_t bytes) {
     if (bytes <= cap) return OJASX_OK;
     for (hipEvent_t &e : ev)

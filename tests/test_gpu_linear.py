@@ -205,6 +205,40 @@ def test_repeat_calls_deterministic_and_outlier_reset(pkg):
     assert rel_err(y0, want) < F32_TOL
 
 
+def test_host_calls_from_threads(pkg):
+    """Host-pointer calls stage through a per-thread pinned buffer and stream:
+    four threads, each with its own layer and batch sizes that grow and shrink
+    the buffer, give the same results as the oracle."""
+    import threading
+    cases = [gen.linear(256 + 64 * i, 512, B=1 + 7 * i, seed=90 + i, scales="u", bias=True)
+             for i in range(4)]
+    errs = [None] * 4
+
+    def run(i):
+        try:
+            d = cases[i]
+            M = d["codes"].shape[0]
+            nat = native_linear(pkg, d, M, 512)
+            want = cpu.linear_forward(d["x"], d["codebook"], d["codes"], d["scales"], d["bias"],
+                                      *d["csr"])
+            for rep in range(6):
+                b = d["x"].shape[0] if rep % 2 == 0 else 1
+                y = nat.forward(d["x"][:b])
+                y = y.reshape(b, M)
+                assert rel_err(y, want[:b]) < F32_TOL, (i, rep)
+        except BaseException as e:   # reported by the main thread
+            errs[i] = e
+
+    ts = [threading.Thread(target=run, args=(i,)) for i in range(4)]
+    for t in ts:
+        t.start()
+    for t in ts:
+        t.join()
+    for e in errs:
+        if e is not None:
+            raise e
+
+
 def test_invalid_outliers_rejected(pkg):
     d = gen.linear(64, 256, seed=3)
     nat = native_linear(pkg, dict(codebook=d["codebook"], codes=d["codes"]), 64, 256)
