@@ -299,6 +299,52 @@ __device__ __forceinline__ int wave_min_i(int v) {
     const int c = __builtin_amdgcn_readlane(v, 32), d = __builtin_amdgcn_readlane(v, 48);
     return min(min(a, b), min(c, d));
 }
+// Minima over the wave of N values per lane, the N reductions interleaved
+// (independent DPP chains in one straight-line block); every lane gets them.
+template <int N>
+__device__ __forceinline__ void wave_min_n(float (&v)[N]) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) v[i] = fminf(v[i], __int_as_float(dpp_i<0xB1>(__float_as_int(v[i]))));
+#pragma unroll
+    for (int i = 0; i < N; ++i) v[i] = fminf(v[i], __int_as_float(dpp_i<0x4E>(__float_as_int(v[i]))));
+#pragma unroll
+    for (int i = 0; i < N; ++i) v[i] = fminf(v[i], __int_as_float(dpp_i<0x141>(__float_as_int(v[i]))));
+#pragma unroll
+    for (int i = 0; i < N; ++i) v[i] = fminf(v[i], __int_as_float(dpp_i<0x140>(__float_as_int(v[i]))));
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+        const int iv = __float_as_int(v[i]);
+        const float a = __int_as_float(__builtin_amdgcn_readlane(iv, 0));
+        const float b = __int_as_float(__builtin_amdgcn_readlane(iv, 16));
+        const float c = __int_as_float(__builtin_amdgcn_readlane(iv, 32));
+        const float d = __int_as_float(__builtin_amdgcn_readlane(iv, 48));
+        v[i] = fminf(fminf(a, b), fminf(c, d));
+    }
+}
+template <int N>
+__device__ __forceinline__ void wave_min_n(int (&v)[N]) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) v[i] = min(v[i], dpp_i<0xB1>(v[i]));
+#pragma unroll
+    for (int i = 0; i < N; ++i) v[i] = min(v[i], dpp_i<0x4E>(v[i]));
+#pragma unroll
+    for (int i = 0; i < N; ++i) v[i] = min(v[i], dpp_i<0x141>(v[i]));
+#pragma unroll
+    for (int i = 0; i < N; ++i) v[i] = min(v[i], dpp_i<0x140>(v[i]));
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+        const int a = __builtin_amdgcn_readlane(v[i], 0), b = __builtin_amdgcn_readlane(v[i], 16);
+        const int c = __builtin_amdgcn_readlane(v[i], 32), d = __builtin_amdgcn_readlane(v[i], 48);
+        v[i] = min(min(a, b), min(c, d));
+    }
+}
+
+// A 256 x 16 fp32 codebook in LDS as 4 float4 per row, float4 w of row r at
+// slot r * 4 + (w ^ ((r >> 1) & 3)).  A row is 16 banks long, so without the
+// swizzle float4 w of every row falls in one of two 4-bank groups and lanes
+// reading rows at random collide; with it they spread over all eight.
+__device__ __forceinline__ int cb_slot(int r, int w) { return r * 4 + (w ^ ((r >> 1) & 3)); }
+
 __device__ __forceinline__ float wave_sum_f(float v) {
     v += __int_as_float(dpp_i<0xB1>(__float_as_int(v)));
     v += __int_as_float(dpp_i<0x4E>(__float_as_int(v)));

@@ -71,10 +71,10 @@ constexpr int kAttnC = 64;        // tokens per chunk, one per lane
 //     o = v_scale * Cv[code].  No workgroup reads the slot being written, and
 //     the encoder's chain runs beside the chunks' instead of inside one.
 __global__ __launch_bounds__(kAttnNT) void attn_decode_kernel(AttnParams p) {
-    __shared__ float4 ck4[256 * 4];      // K codebook [256][16]
+    __shared__ float4 ck4[256 * 4];      // K codebook [256][16], rows swizzled (cb_slot)
     __shared__ float4 cv4[256 * 4];      // V codebook [256][16]
     __shared__ float4 q4s[4 * 32];       // rotated q [4][128]
-    __shared__ float xs[2 * kHd];        // new token: k / s_k, v / s_v
+    __shared__ __align__(16) float xs[2 * kHd];   // new token: k / s_k, v / s_v
     __shared__ float nscale[2];          // its scales
     __shared__ float wd[2][kG][4];       // per-wave nearest distance
     __shared__ int wi[2][kG][4];         // and its lowest centroid
@@ -137,7 +137,8 @@ __global__ __launch_bounds__(kAttnNT) void attn_decode_kernel(AttnParams p) {
     const int npage = fresh ? p.bt[pos / p.P] : 0;
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-        ck4[tid + u * kAttnNT] = a[u];
+        const int i = tid + u * kAttnNT;
+        ck4[cb_slot(i >> 2, i & 3)] = a[u];
         cv4[tid + u * kAttnNT] = b[u];
     }
     if (j < nj) {
@@ -165,28 +166,48 @@ __global__ __launch_bounds__(kAttnNT) void attn_decode_kernel(AttnParams p) {
         float ck[kBd], cv[kBd];
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
-            const float4 ka = ck4[tid * 4 + u], va = cv4[tid * 4 + u];
+            const float4 ka = ck4[cb_slot(tid, u)], va = cv4[tid * 4 + u];
             ck[4 * u] = ka.x, ck[4 * u + 1] = ka.y, ck[4 * u + 2] = ka.z, ck[4 * u + 3] = ka.w;
             cv[4 * u] = va.x, cv[4 * u + 1] = va.y, cv[4 * u + 2] = va.z, cv[4 * u + 3] = va.w;
         }
+        // squared distances of centroid tid to the 8 K and 8 V groups, then
+        // the 16 wave minima and their lowest centroids, interleaved
+        float dd[2 * kG];
 #pragma unroll
         for (int g = 0; g < kG; ++g) {
+            const float4 *xk = reinterpret_cast<const float4 *>(xs + g * kBd);
+            const float4 *xv = reinterpret_cast<const float4 *>(xs + kHd + g * kBd);
             float dk = 0.f, dv = 0.f;
 #pragma unroll
-            for (int d = 0; d < kBd; ++d) {
-                const float fk = xs[g * kBd + d] - ck[d];
-                const float fv = xs[kHd + g * kBd + d] - cv[d];
-                dk = fmaf(fk, fk, dk);
-                dv = fmaf(fv, fv, dv);
+            for (int w = 0; w < 4; ++w) {
+                const float4 a4 = xk[w], b4 = xv[w];
+                const float ak[4] = {a4.x, a4.y, a4.z, a4.w}, bv[4] = {b4.x, b4.y, b4.z, b4.w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float fk = ak[e] - ck[4 * w + e];
+                    const float fv = bv[e] - cv[4 * w + e];
+                    dk = fmaf(fk, fk, dk);
+                    dv = fmaf(fv, fv, dv);
+                }
             }
-            const float mk = wave_min_f(dk), mv = wave_min_f(dv);
-            const int ik = wave_min_i(dk == mk ? tid : 0x7fffffff);
-            const int iv = wave_min_i(dv == mv ? tid : 0x7fffffff);
-            if (lane == 0) {
-                wd[0][g][j] = mk;
-                wi[0][g][j] = ik;
-                wd[1][g][j] = mv;
-                wi[1][g][j] = iv;
+            dd[g] = dk;
+            dd[kG + g] = dv;
+        }
+        float mn[2 * kG];
+        int id[2 * kG];
+#pragma unroll
+        for (int i = 0; i < 2 * kG; ++i) mn[i] = dd[i];
+        wave_min_n(mn);
+#pragma unroll
+        for (int i = 0; i < 2 * kG; ++i) id[i] = dd[i] == mn[i] ? tid : 0x7fffffff;
+        wave_min_n(id);
+        if (lane == 0) {
+#pragma unroll
+            for (int g = 0; g < kG; ++g) {
+                wd[0][g][j] = mn[g];
+                wi[0][g][j] = id[g];
+                wd[1][g][j] = mn[kG + g];
+                wi[1][g][j] = id[kG + g];
             }
         }
         __syncthreads();
@@ -217,12 +238,11 @@ __global__ __launch_bounds__(kAttnNT) void attn_decode_kernel(AttnParams p) {
 #pragma unroll
             for (int g = 0; g < kG; ++g) {
                 const uint32_t code = (kd[g >> 2] >> ((g & 3) * 8)) & 0xffu;
-                const float4 *cr = ck4 + code * 4;
                 const float4 *qr = q4s + j * 32 + g * 4;
                 float dot = 0.f;
 #pragma unroll
                 for (int w = 0; w < 4; ++w) {
-                    const float4 cq = cr[w], qq = qr[w];
+                    const float4 cq = ck4[cb_slot(code, w)], qq = qr[w];
                     dot = fmaf(qq.x, cq.x, dot);
                     dot = fmaf(qq.y, cq.y, dot);
                     dot = fmaf(qq.z, cq.z, dot);
@@ -269,12 +289,11 @@ __global__ __launch_bounds__(kAttnNT) void attn_decode_kernel(AttnParams p) {
 #pragma unroll
         for (int g = 0; g < kG; ++g) {
             const uint32_t code = (kd[g >> 2] >> ((g & 3) * 8)) & 0xffu;
-            const float4 *cr = ck4 + code * 4;
             const float4 *qr = q4s + j * 32 + g * 4;
             float dot = 0.f;
 #pragma unroll
             for (int w = 0; w < 4; ++w) {
-                const float4 cq = cr[w], qq = qr[w];
+                const float4 cq = ck4[cb_slot(code, w)], qq = qr[w];
                 dot = fmaf(qq.x, cq.x, dot);
                 dot = fmaf(qq.y, cq.y, dot);
                 dot = fmaf(qq.z, cq.z, dot);

@@ -110,17 +110,34 @@ __device__ void encode_kv_token(const float *kr, const float *vr, const float *k
     const int c = tid;
     const float *kcr = kcb + (size_t)c * D;
     const float *vcr = vcb + (size_t)c * D;
-    for (int g = 0; g < G; ++g) {
-        const float dk = centroid_dist<DT>(xs + g * D, kreg, kcr, D);
-        const float dv = centroid_dist<DT>(xs + hd + g * D, vreg, vcr, D);
-        const float mk2 = wave_min_f(dk), mv2 = wave_min_f(dv);
-        const int ik = wave_min_i(dk == mk2 ? c : 0x7fffffff);
-        const int iv = wave_min_i(dv == mv2 ? c : 0x7fffffff);
+    // 8 groups at a time: 16 distances per centroid, then their 16 wave
+    // minima and lowest centroids as interleaved reductions
+    for (int g0 = 0; g0 < G; g0 += 8) {
+        float dd[16];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int g = min(g0 + u, G - 1);
+            dd[u] = centroid_dist<DT>(xs + g * D, kreg, kcr, D);
+            dd[8 + u] = centroid_dist<DT>(xs + hd + g * D, vreg, vcr, D);
+        }
+        float mn[16];
+        int id[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) mn[i] = dd[i];
+        wave_min_n(mn);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) id[i] = dd[i] == mn[i] ? c : 0x7fffffff;
+        wave_min_n(id);
         if (lane == 0) {
-            wd[0][g][w] = mk2;
-            wi[0][g][w] = ik;
-            wd[1][g][w] = mv2;
-            wi[1][g][w] = iv;
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                if (g0 + u < G) {
+                    wd[0][g0 + u][w] = mn[u];
+                    wi[0][g0 + u][w] = id[u];
+                    wd[1][g0 + u][w] = mn[8 + u];
+                    wi[1][g0 + u][w] = id[8 + u];
+                }
+            }
         }
     }
     __syncthreads();

@@ -480,7 +480,7 @@ constexpr int kSmallMaxT = 4096;
 template <int TPL>
 __global__ __launch_bounds__(kNT) void kv_decode_small_kernel(KVParams p) {
     constexpr int C = kSmallC * TPL;     // tokens per chunk
-    __shared__ float4 ck4[256 * 4];      // K codebook [256][16]
+    __shared__ float4 ck4[256 * 4];      // K codebook [256][16], rows swizzled (cb_slot)
     __shared__ float4 cv4[256 * 4];      // V codebook [256][16]
     __shared__ float4 q4s[4 * 32];       // q [4][128]
     __shared__ uint2 kcw[C], vcw[C];
@@ -523,7 +523,8 @@ __global__ __launch_bounds__(kNT) void kv_decode_small_kernel(KVParams p) {
     }
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-        ck4[tid + u * kNT] = a[u];
+        const int i = tid + u * kNT;
+        ck4[cb_slot(i >> 2, i & 3)] = a[u];
         cv4[tid + u * kNT] = b[u];
     }
     if (tid < 128) q4s[tid] = qv;
@@ -556,12 +557,11 @@ __global__ __launch_bounds__(kNT) void kv_decode_small_kernel(KVParams p) {
 #pragma unroll
             for (int g = 0; g < 8; ++g) {
                 const uint32_t code = (kd[g >> 2] >> ((g & 3) * 8)) & 0xffu;
-                const float4 *cr = ck4 + code * 4;
                 const float4 *qr = q4s + j * 32 + g * 4;
                 float dot = 0.f;
 #pragma unroll
                 for (int w = 0; w < 4; ++w) {
-                    const float4 cq = cr[w], qq = qr[w];
+                    const float4 cq = ck4[cb_slot(code, w)], qq = qr[w];
                     dot = fmaf(qq.x, cq.x, dot);
                     dot = fmaf(qq.y, cq.y, dot);
                     dot = fmaf(qq.z, cq.z, dot);
