@@ -71,6 +71,7 @@ class LUTDecoder:
         if not h:
             raise RuntimeError("ojasx_create_decoder failed: "
                                + _lib.lib().ojasx_get_last_error().decode(errors="replace"))
+        self._destroy = _lib.lib().ojasx_destroy_decoder
         self._h = h
 
     @staticmethod
@@ -136,12 +137,15 @@ class LUTDecoder:
         return kc, ks, vc, vs
 
     def close(self):
-        if getattr(self, "_h", None):
-            _lib.lib().ojasx_destroy_decoder(self._h)
+        destroy = getattr(self, "_destroy", None)
+        if getattr(self, "_h", None) and destroy is not None:
+            destroy(self._h)
             self._h = None
         self._keep = []
 
     def __del__(self):
+        # close() calls the destroy entry point bound at creation: at
+        # interpreter exit the module's globals may already be gone
         self.close()
 
 

@@ -44,6 +44,7 @@ class NativeSplitManifoldLinear:
         bs = None if bias is None else np.ascontiguousarray(bias, np.float32)
         if self._handle:
             lib().ojasx_destroy_linear(self._handle)
+        self._destroy = lib().ojasx_destroy_linear
         self._handle = lib().ojasx_create_linear(
             self.in_features, self.out_features, self.block_dim, self.codebook_size,
             _p(cb), _p(cd), _p(sc), _p(bs))
@@ -81,8 +82,11 @@ class NativeSplitManifoldLinear:
         return self._handle
 
     def __del__(self):
-        if getattr(self, "_handle", None):
-            lib().ojasx_destroy_linear(self._handle)
+        # the destroy entry point is bound at creation: at interpreter exit the
+        # module's globals may already be gone
+        destroy = getattr(self, "_destroy", None)
+        if getattr(self, "_handle", None) and destroy is not None:
+            destroy(self._handle)
             self._handle = None
 
 
@@ -93,6 +97,7 @@ class NativeKVCache:
                  block_dim: int = 16):
         self.num_heads = num_heads
         self.head_dim = head_dim
+        self._destroy = lib().ojasx_destroy_kv_cache
         self._handle = lib().ojasx_create_kv_cache(num_heads, head_dim, max_seq_len, block_dim)
         if not self._handle:
             raise RuntimeError("ojasx_create_kv_cache failed: "
@@ -120,8 +125,11 @@ class NativeKVCache:
         return lib().ojasx_kv_cache_get_compression_ratio(self._handle)
 
     def __del__(self):
-        if getattr(self, "_handle", None):
-            lib().ojasx_destroy_kv_cache(self._handle)
+        # the destroy entry point is bound at creation: at interpreter exit the
+        # module's globals may already be gone
+        destroy = getattr(self, "_destroy", None)
+        if getattr(self, "_handle", None) and destroy is not None:
+            destroy(self._handle)
             self._handle = None
 
 
@@ -147,6 +155,7 @@ class NativeSplitManifoldMoE:
                 np.ascontiguousarray(down_scales, np.float32)]
         if self._handle:
             lib().ojasx_destroy_moe(self._handle)
+        self._destroy = lib().ojasx_destroy_moe
         self._handle = lib().ojasx_create_moe(
             self.num_experts, self.hidden_dim, self.intermediate_dim, self.top_k,
             self.block_dim, *[_p(a) for a in arrs])
@@ -175,6 +184,9 @@ class NativeSplitManifoldMoE:
         return self._handle
 
     def __del__(self):
-        if getattr(self, "_handle", None):
-            lib().ojasx_destroy_moe(self._handle)
+        # the destroy entry point is bound at creation: at interpreter exit the
+        # module's globals may already be gone
+        destroy = getattr(self, "_destroy", None)
+        if getattr(self, "_handle", None) and destroy is not None:
+            destroy(self._handle)
             self._handle = None
