@@ -339,6 +339,83 @@ __device__ __forceinline__ void wave_min_n(int (&v)[N]) {
     }
 }
 
+// Maxima / sums over the wave of N values per lane, interleaved as in
+// wave_min_n; every lane gets them.
+template <int N>
+__device__ __forceinline__ void wave_max_n(float (&v)[N]) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) v[i] = fmaxf(v[i], __int_as_float(dpp_i<0xB1>(__float_as_int(v[i]))));
+#pragma unroll
+    for (int i = 0; i < N; ++i) v[i] = fmaxf(v[i], __int_as_float(dpp_i<0x4E>(__float_as_int(v[i]))));
+#pragma unroll
+    for (int i = 0; i < N; ++i) v[i] = fmaxf(v[i], __int_as_float(dpp_i<0x141>(__float_as_int(v[i]))));
+#pragma unroll
+    for (int i = 0; i < N; ++i) v[i] = fmaxf(v[i], __int_as_float(dpp_i<0x140>(__float_as_int(v[i]))));
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+        const int iv = __float_as_int(v[i]);
+        const float a = __int_as_float(__builtin_amdgcn_readlane(iv, 0));
+        const float b = __int_as_float(__builtin_amdgcn_readlane(iv, 16));
+        const float c = __int_as_float(__builtin_amdgcn_readlane(iv, 32));
+        const float d = __int_as_float(__builtin_amdgcn_readlane(iv, 48));
+        v[i] = fmaxf(fmaxf(a, b), fmaxf(c, d));
+    }
+}
+template <int N>
+__device__ __forceinline__ void wave_sum_n(float (&v)[N]) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) v[i] += __int_as_float(dpp_i<0xB1>(__float_as_int(v[i])));
+#pragma unroll
+    for (int i = 0; i < N; ++i) v[i] += __int_as_float(dpp_i<0x4E>(__float_as_int(v[i])));
+#pragma unroll
+    for (int i = 0; i < N; ++i) v[i] += __int_as_float(dpp_i<0x141>(__float_as_int(v[i])));
+#pragma unroll
+    for (int i = 0; i < N; ++i) v[i] += __int_as_float(dpp_i<0x140>(__float_as_int(v[i])));
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+        const int iv = __float_as_int(v[i]);
+        const float a = __int_as_float(__builtin_amdgcn_readlane(iv, 0));
+        const float b = __int_as_float(__builtin_amdgcn_readlane(iv, 16));
+        const float c = __int_as_float(__builtin_amdgcn_readlane(iv, 32));
+        const float d = __int_as_float(__builtin_amdgcn_readlane(iv, 48));
+        v[i] = (a + b) + (c + d);
+    }
+}
+
+// Exact three-way bf16 split of fp32 values and the 32 x 32 x 16 MFMA tile
+// over it.  v = v1 + v2 + v3 exactly: v1 = bf16(v), v2 = bf16(v - v1),
+// v3 = v - v1 - v2 (an fp32 value has 24 significant bits, each bf16 piece
+// takes 8; the remainders are exact in fp32).
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+__device__ __forceinline__ void split3_bf16(const float (&v)[8], bf16x8_t (&p)[3]) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const __bf16 h1 = (__bf16)v[i];
+        const float r1 = v[i] - (float)h1;
+        const __bf16 h2 = (__bf16)r1;
+        p[0][i] = h1;
+        p[1][i] = h2;
+        p[2][i] = (__bf16)(r1 - (float)h2);
+    }
+}
+// A[32 x 16] . B[16 x 32] on v_mfma_f32_32x32x16_bf16 with A = a1 + a2 + a3
+// and B = b1 + b2 + b3: the six products a_i b_j with i + j <= 4 (each exact
+// in fp32) accumulated in fp32, smallest first; the three left out are below
+// 2^-24 of the result.  Lane (h = lane / 32, n = lane % 32) supplies row n of
+// A and column n of B, input dimensions 8h .. 8h + 7 of both; its result
+// value r is row 8 (r / 4) + 4 h + r % 4 of column n.
+__device__ __forceinline__ f32x16_t mfma32_bf16x3(const bf16x8_t (&a)[3], const bf16x8_t (&b)[3]) {
+    f32x16_t d = {};
+    d = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0], b[2], d, 0, 0, 0);
+    d = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[1], b[1], d, 0, 0, 0);
+    d = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[2], b[0], d, 0, 0, 0);
+    d = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0], b[1], d, 0, 0, 0);
+    d = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[1], b[0], d, 0, 0, 0);
+    d = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0], b[0], d, 0, 0, 0);
+    return d;
+}
+
 // A 256 x 16 fp32 codebook in LDS as 4 float4 per row, float4 w of row r at
 // slot r * 4 + (w ^ ((r >> 1) & 3)).  A row is 16 banks long, so without the
 // swizzle float4 w of every row falls in one of two 4-bank groups and lanes

@@ -56,7 +56,7 @@ constexpr int kLutRow = 64;             // words per code in the LUT: two buffer
 constexpr int kStagePT = 12;            // CSR entries staged per thread
 constexpr int kEarlyPT = 10;            // of which loaded before the slice loop
 constexpr int kStage = kStagePT * kBNT; // per workgroup (4 B each, in the 64 KB LUT space)
-typedef float v16f __attribute__((ext_vector_type(16)));
+typedef f32x16_t v16f;
 
 // Codes of slice s for lane (h, g) from the block's bank layout [G][64 rows]:
 // cp points at group g, rows 32h...  In a partial last slice the lanes past G
@@ -76,7 +76,7 @@ __device__ __forceinline__ void bank_codes(const uint8_t *cp, int s, uint4 (&c)[
 // itself is (x1 + x2) + x3 in fp32, exact (24 significant bits).
 constexpr int kXRow = 24;
 
-typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+typedef bf16x8_t v8bf;
 
 // MFMA B operand of slice s: the three pieces of x[16 (32 s + g) + 8 h .. + 8)
 // from the staged x (zero rows for the groups past G up to the slice's end,
@@ -94,35 +94,14 @@ __device__ __forceinline__ float xs_value(const float *xs, int k) {
     return ((float)r[0] + (float)r[16]) + (float)r[32];
 }
 
-// v = v1 + v2 + v3 exactly: v1 = bf16(v), v2 = bf16(v - v1), v3 = v - v1 - v2
-// (an fp32 value has 24 significant bits, each bf16 piece takes 8; the
-// remainders are exact in fp32).
-__device__ __forceinline__ void split3(const float (&v)[8], v8bf (&p)[3]) {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const __bf16 h1 = (__bf16)v[i];
-        const float r1 = v[i] - (float)h1;
-        const __bf16 h2 = (__bf16)r1;
-        p[0][i] = h1;
-        p[1][i] = h2;
-        p[2][i] = (__bf16)(r1 - (float)h2);
-    }
-}
+// v = v1 + v2 + v3 exactly (split3_bf16).
+__device__ __forceinline__ void split3(const float (&v)[8], v8bf (&p)[3]) { split3_bf16(v, p); }
 
 // LUT tile = C_tile . X_s^T on v_mfma_f32_32x32x16_bf16 (16 input dims in one
-// step): with C = c1 + c2 + c3 and x = x1 + x2 + x3 split exactly into bf16
-// pieces, the six products c_i x_j with i + j <= 4 (each exact in fp32) are
-// accumulated in fp32, smallest first; the three left out are below 2^-24 of
-// the result.  A lane's 8 values are dimensions 8h .. 8h + 7 in both operands.
+// step) over the exact bf16 splits of C and x (mfma32_bf16x3: fp32 accuracy).
+// A lane's 8 values are dimensions 8h .. 8h + 7 in both operands.
 __device__ __forceinline__ v16f bank_build(const v8bf (&a)[3], const v8bf (&b)[3]) {
-    v16f d = {};
-    d = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0], b[2], d, 0, 0, 0);
-    d = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[1], b[1], d, 0, 0, 0);
-    d = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[2], b[0], d, 0, 0, 0);
-    d = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0], b[1], d, 0, 0, 0);
-    d = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[1], b[0], d, 0, 0, 0);
-    d = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0], b[0], d, 0, 0, 0);
-    return d;
+    return mfma32_bf16x3(a, b);
 }
 
 // LUT[32 w + m][g] of buffer buf <- column g of the wave's tile.

@@ -288,29 +288,36 @@ __global__ __launch_bounds__(kNT) void kv_decode_chunk_kernel(KVParams p) {
 }
 
 // Fast path (G = 8 groups of D = 16, head_dim 128, up to 4 query heads per kv
-// head): 1024 threads, one token per thread, chunk of C <= 1024 tokens.  The
-// work of a chunk is spread over 16 waves so LDS latency is hidden:
-//  * round trip 1: the token's block-table entry, q, the K codebook row of
-//    centroid tid % 256 and one float4 of the V codebook; round trip 2: the
-//    token's K/V code words and scales;
-//  * LUT_q[j][g][c] by all threads (8 dots of 16 each);
+// head): 1024 threads, one token per thread, chunk of C <= 1024 tokens.
+//  * round trip 1: the token's block-table entry, q, one float4 of the V
+//    codebook and, for waves 0-7, their operand of the K codebook; round
+//    trip 2: the token's K/V code words and scales;
+//  * LUT_q^T[256 x 32] = Ck[256 x 16] . Q^T[16 x 32] (column n = (j, g):
+//    dims 16g .. 16g + 15 of query head j) on v_mfma_f32_32x32x16_bf16 over
+//    exact bf16 splits (fp32 accuracy), wave w < 8 taking centroids
+//    32w .. 32w + 31;
 //  * scores (8 LUT gathers per head), chunk max and sum of exp per head by
 //    DPP wave reductions and 16 per-wave values in LDS (fixed order);
 //  * V in the code domain: thread (token group tg of 32, group g, d-quad dq)
 //    adds p_jt * vs_t * Cv[code][4dq..4dq+3] for the 4 heads over tokens
-//    tg, tg+32, ...; the two token groups of a wave are added with one
-//    shuffle, the 16 waves' partials in LDS in a fixed order.
+//    tg, tg+32, ... (code rows addressed by byte offsets staged per token);
+//    the two token groups of a wave are added with one shuffle, the 16 waves'
+//    partials in LDS in a fixed order.  Measured and not kept: code
+//    histograms contracted on MFMA (3x slower: LDS float atomics on
+//    colliding bins serialise) and 8 dims per lane (the cross-lane sums cost
+//    more than the shared weight reads save).
 constexpr int kWideNT = 1024;
+constexpr int kLutP = 257;    // LUT_q row pitch (one row per (j, g)): conflict-free stores
 
 __global__ __launch_bounds__(kWideNT) void kv_decode_wide_kernel(KVParams p) {
     extern __shared__ float sm[];
-    float *qs = sm;                                             // [4][128]
-    float *cv = qs + 4 * 128;                                   // [256][16]
-    float *lutq = cv + 256 * 16;                                // [4][8][256]
-    float4 *pw = reinterpret_cast<float4 *>(lutq + 4 * 8 * 256);  // [C] weights of 4 heads
-    uint2 *vcw = reinterpret_cast<uint2 *>(pw + kWideNT);       // [C] V code words
-    float *part = reinterpret_cast<float *>(vcw + kWideNT);     // [16 waves][32][16]
-    __shared__ float wred[2][4][kWideNT / 64];
+    float *qs = sm;                                          // [4][128]
+    float *cv = qs + 4 * 128;                                // [256][16]
+    float *lutq = cv + 256 * 16;                             // [32][kLutP]
+    float4 *pw = reinterpret_cast<float4 *>(lutq + 32 * kLutP + 32);   // [C] weights of 4 heads
+    uint4 *vof = reinterpret_cast<uint4 *>(pw + kWideNT);   // [C][8] V codebook row offsets, u16
+    float *part = reinterpret_cast<float *>(vof + kWideNT); // [16 waves][32][16]
+    __shared__ __align__(16) float wred[2][4][kWideNT / 64];
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int R = p.Hq / p.Hkv;
     const int h = blockIdx.y;
@@ -324,18 +331,14 @@ __global__ __launch_bounds__(kWideNT) void kv_decode_wide_kernel(KVParams p) {
 
     // ---- round trip 1
     const int pg = p.bt[tc / p.P];
-    const int cc = tid & 255;
-    float ck[16];
+    float af[8];   // K codebook row 32 (wv % 8) + lane % 32, dims 8 (lane / 32) ..
     {
-        const float4 *kr = reinterpret_cast<const float4 *>(p.kcb + ((size_t)h * 256 + cc) * 16);
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const float4 f = kr[u];
-            ck[4 * u] = f.x;
-            ck[4 * u + 1] = f.y;
-            ck[4 * u + 2] = f.z;
-            ck[4 * u + 3] = f.w;
-        }
+        const int cr = (wv & 7) * 32 + (lane & 31);
+        const float4 *kr =
+            reinterpret_cast<const float4 *>(p.kcb + ((size_t)h * 256 + cr) * 16 + 8 * (lane >> 5));
+        const float4 u = kr[0], v = kr[1];
+        af[0] = u.x; af[1] = u.y; af[2] = u.z; af[3] = u.w;
+        af[4] = v.x; af[5] = v.y; af[6] = v.z; af[7] = v.w;
     }
     const float4 cvv = reinterpret_cast<const float4 *>(p.vcb + (size_t)h * 256 * 16)[tid];
     float4 qv = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -345,59 +348,81 @@ __global__ __launch_bounds__(kWideNT) void kv_decode_wide_kernel(KVParams p) {
     const uint2 kw = *reinterpret_cast<const uint2 *>(p.kc + slot * 8);
     const uint2 vw = *reinterpret_cast<const uint2 *>(p.vc + slot * 8);
     const float ksv = p.ks[slot], vsv = p.vs[slot];
-    if (tid < 128) reinterpret_cast<float4 *>(qs)[tid] = qv;
+    if (tid < 128) reinterpret_cast<float4 *>(qs)[tid] = qv;   // zero rows past nj
     reinterpret_cast<float4 *>(cv)[tid] = cvv;
     __syncthreads();
 
-    // ---- LUT_q[jg][cc] for jg = tid / 256 + 4k
-#pragma unroll 2
-    for (int k = 0; k < 8; ++k) {
-        const int jg = (tid >> 8) + 4 * k;
-        const float4 *q4 = reinterpret_cast<const float4 *>(qs + jg * 16);   // [j][g] rows of 16
-        const float4 a0 = q4[0], a1 = q4[1], a2 = q4[2], a3 = q4[3];
-        const float qd[16] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w,
-                              a2.x, a2.y, a2.z, a2.w, a3.x, a3.y, a3.z, a3.w};
-        float dot = 0.f;
+    // ---- LUT_q on MFMA: wave w < 8, centroids 32w .. 32w + 31
+    if (wv < 8) {
+        const int n = lane & 31, hh = lane >> 5;
+        const float4 *qp =
+            reinterpret_cast<const float4 *>(qs + (n >> 3) * 128 + 16 * (n & 7) + 8 * hh);
+        const float4 b0 = qp[0], b1 = qp[1];
+        const float bf[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+        bf16x8_t a[3], b[3];
+        split3_bf16(af, a);
+        split3_bf16(bf, b);
+        const f32x16_t d = mfma32_bf16x3(a, b);
+        float *L = lutq + n * kLutP + 32 * wv + 4 * hh;
 #pragma unroll
-        for (int d = 0; d < 16; ++d) dot = fmaf(qd[d], ck[d], dot);
-        lutq[jg * 256 + cc] = dot;
+        for (int r = 0; r < 16; ++r) L[8 * (r / 4) + (r % 4)] = d[r];
     }
     __syncthreads();
 
-    // ---- scores, chunk max and sum of exp per head
+    // ---- scores, chunk max and sum of exp per head (the 4 heads' wave
+    //      reductions interleaved)
     const uint32_t kwd[2] = {kw.x, kw.y};
-    float s[4];
+    float s[4], wm[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         s[j] = -INFINITY;
         if (live && j < nj) {
-            const float *L = lutq + j * 8 * 256;
+            const float *L = lutq + j * 8 * kLutP;
             float v[8];
 #pragma unroll
-            for (int g = 0; g < 8; ++g) v[g] = L[g * 256 + ((kwd[g >> 2] >> ((g & 3) * 8)) & 0xffu)];
+            for (int g = 0; g < 8; ++g)
+                v[g] = L[g * kLutP + ((kwd[g >> 2] >> ((g & 3) * 8)) & 0xffu)];
             float a = 0.f;
 #pragma unroll
             for (int g = 0; g < 8; ++g) a += v[g];
             s[j] = a * (ksv * p.sf);
         }
-        const float m = wave_max_f(s[j]);
-        if (lane == 0) wred[0][j][wv] = m;
+        wm[j] = s[j];
     }
+    wave_max_n(wm);
+    if (lane == 0)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) wred[0][j][wv] = wm[j];
     __syncthreads();
     float mx[4], e[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        float m = wred[0][j][0];
+        const float4 *w4 = reinterpret_cast<const float4 *>(wred[0][j]);
+        float m = -INFINITY;
 #pragma unroll
-        for (int q = 1; q < kWideNT / 64; ++q) m = fmaxf(m, wred[0][j][q]);
+        for (int q = 0; q < kWideNT / 256; ++q) {
+            const float4 u = w4[q];
+            m = fmaxf(m, fmaxf(fmaxf(u.x, u.y), fmaxf(u.z, u.w)));
+        }
         mx[j] = m;
         e[j] = s[j] == -INFINITY ? 0.f : expf(s[j] - m);
-        const float l = wave_sum_f(e[j]);
-        if (lane == 0) wred[1][j][wv] = l;
+        wm[j] = e[j];
     }
+    wave_sum_n(wm);
+    if (lane == 0)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) wred[1][j][wv] = wm[j];
     const float f = live ? vsv : 0.f;
     pw[tid] = make_float4(e[0] * f, e[1] * f, e[2] * f, e[3] * f);
-    vcw[tid] = vw;
+    // the token's V codes as byte offsets of their codebook rows (code * 64),
+    // 16 bits each, group g at element g
+    {
+        const uint32_t x = vw.x, y = vw.y;
+        auto pair = [](uint32_t wd, int sh) {
+            return (((wd >> sh) & 0xffu) << 6) | (((wd >> (sh + 8)) & 0xffu) << 22);
+        };
+        vof[tid] = make_uint4(pair(x, 0), pair(x, 16), pair(y, 0), pair(y, 16));
+    }
     __syncthreads();
 
     // ---- V in the code domain
@@ -408,12 +433,11 @@ __global__ __launch_bounds__(kWideNT) void kv_decode_wide_kernel(KVParams p) {
         for (int j = 0; j < 4; ++j)
 #pragma unroll
             for (int k = 0; k < 4; ++k) acc[j][k] = 0.f;
-        const float4 *cv4 = reinterpret_cast<const float4 *>(cv);
+        const char *cvq = reinterpret_cast<const char *>(cv) + 16 * dq;
+        const unsigned short *vo = reinterpret_cast<const unsigned short *>(vof) + g;
 #pragma unroll 4
         for (int tl = tg; tl < C; tl += 32) {
-            const uint2 cwv = vcw[tl];
-            const uint32_t code = ((g < 4 ? cwv.x : cwv.y) >> ((g & 3) * 8)) & 0xffu;
-            const float4 cq = cv4[code * 4 + dq];
+            const float4 cq = *reinterpret_cast<const float4 *>(cvq + vo[8 * tl]);
             const float4 wj = pw[tl];
             const float wa[4] = {wj.x, wj.y, wj.z, wj.w};
             const float ca[4] = {cq.x, cq.y, cq.z, cq.w};
@@ -894,8 +918,8 @@ int kv_decode(const float *q, const uint8_t *kc, const float *ks, const uint8_t 
         }
         KVParams p{q, kc, vc, ks, vs, kcb, vcb, bt, wk.po, wk.pml, out, T, P,
                    Hq, Hkv, hd, D, G, (int)C, 4, n_chunks, sf, nullptr, 0};
-        const size_t lds = (size_t)(4 * 128 + 256 * 16 + 4 * 8 * 256) * 4 + (size_t)kWideNT * 16 +
-                           (size_t)kWideNT * 8 + (size_t)16 * 32 * 16 * 4;
+        const size_t lds = (size_t)(4 * 128 + 256 * 16 + 32 * kLutP + 32) * 4 + (size_t)kWideNT * 16 +
+                           (size_t)kWideNT * 16 + (size_t)16 * 32 * 16 * 4;
         static size_t gw = 0;
         int rc = ensure_dyn_lds(reinterpret_cast<const void *>(&kv_decode_wide_kernel), lds, &gw);
         if (rc) return rc;
