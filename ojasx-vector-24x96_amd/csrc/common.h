@@ -104,6 +104,7 @@ struct GroupItem {
     const uint8_t *codes;     // [S][Mp][16]
     const uint8_t *codes_b;   // bank layout [ceil(M/64)][S32][32][64] (lut_bank.hip)
     const float *cb;          // [256][16]
+    const void *cb3;          // the codebook split for the bank kernel (split_codebook_bf16x3)
     const float *scales;      // [M]
     const float *bias;        // [M] or null
     const int *rowp;          // [M+1] or null
@@ -113,6 +114,12 @@ struct GroupItem {
     float *y;                 // [M]
     int K, M, Mp, S, S32;     // S32 = ceil(G / 32)
 };
+// A 256 x 16 fp32 codebook split exactly into three bf16 pieces per value
+// (v = v1 + v2 + v3, v1 = bf16(v), v2 = bf16(v - v1), v3 = v - v1 - v2, each
+// rounded to nearest even), laid out for the bank kernels' MFMA A operand:
+// [centroid][half h][piece][dims 8h .. 8h + 7], 96 bytes per centroid.
+constexpr size_t kCb3Bytes = 256 * 2 * 3 * 8 * 2;
+void split_codebook_bf16x3(const float *cb, uint16_t *out);
 int linear_items(const void *h, GroupItem *it);
 // Grouped batch-1 LUT-GEMV with bank-aligned gathers (lut_bank.hip): items
 // staged in device memory, work[t] = (item, first row of a 512-row block) in
@@ -134,7 +141,8 @@ int launch_moe_plan(const int *idx, const float *w, int P, int E, int nb_gu, int
 struct MoEBankLaunch {
     const uint8_t *codes_b;     // [E][bank layout]
     size_t expert_bytes;
-    const float *cb, *scales;   // [256][16], [E][M]
+    const void *cb3;            // the split codebook (split_codebook_bf16x3)
+    const float *scales;        // [E][M]
     const void *x;              // xs 0: [T][K] fp32, 1: bf16, 2: [P][2K] fp32 gate|up rows
     float *y;                   // [P][M]
     const int *idx;

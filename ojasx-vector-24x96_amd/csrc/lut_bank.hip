@@ -28,9 +28,10 @@
 // Its output lane (h, n) holds rows 8(r/4) + 4h + r%4 of column n, so the
 // stores of each half-wave hit 32 distinct banks.  Lane half h supplies input
 // dimensions 8h .. 8h + 7 of both operands: 8 contiguous floats of x and of
-// its codebook row.  The codebook is split per wave once, x once per
-// workgroup when it is staged (its three pieces side by side in LDS, zero
-// rows up to the last slice's end, so groups past G give zero LUT columns).
+// its codebook row.  The codebook is split once when the handle is made (its
+// pieces loaded as they are), x once per workgroup when it is staged (its
+// three pieces side by side in LDS, zero rows up to the last slice's end, so
+// groups past G give zero LUT columns).
 // Two LUT buffers in the 64-word rows: slice s + 1 is built while slice s is
 // gathered, one barrier per slice.
 //
@@ -70,7 +71,7 @@ __device__ __forceinline__ void bank_codes(const uint8_t *cp, int s, uint4 (&c)[
 }
 
 // x staged in LDS once per workgroup, already split into its three bf16
-// pieces (x = x1 + x2 + x3 exactly, see split3): a row of kXRow words per
+// pieces (x = x1 + x2 + x3 exactly, see split3_bf16): a row of kXRow words per
 // group, piece p in words 8p .. 8p + 7 (16 bf16), no padding (two
 // workgroups per CU up to K = 2560: 64 KB of LUT + 96 B per group each).  x
 // itself is (x1 + x2) + x3 in fp32, exact (24 significant bits).
@@ -93,9 +94,6 @@ __device__ __forceinline__ float xs_value(const float *xs, int k) {
     const __bf16 *r = reinterpret_cast<const __bf16 *>(xs + (k >> 4) * kXRow) + (k & 15);
     return ((float)r[0] + (float)r[16]) + (float)r[32];
 }
-
-// v = v1 + v2 + v3 exactly (split3_bf16).
-__device__ __forceinline__ void split3(const float (&v)[8], v8bf (&p)[3]) { split3_bf16(v, p); }
 
 // LUT tile = C_tile . X_s^T on v_mfma_f32_32x32x16_bf16 (16 input dims in one
 // step) over the exact bf16 splits of C and x (mfma32_bf16x3: fp32 accuracy).
@@ -178,7 +176,7 @@ __device__ __forceinline__ float bank_reduce(const float (&acc)[32], int lane) {
 // optional bias and CSR outliers, input and output.
 struct BankBlock {
     const uint8_t *codes_b;     // the matrix's bank layout [ceil(M/64)][G][64]
-    const float *cb;            // [256][16]
+    const v8bf *cb3;            // [256][2][3] the codebook's bf16 pieces (split_codebook_bf16x3)
     const float *scales;        // [M]
     const float *bias;          // [M] or null
     const int *rowp;            // [M + 1] or null
@@ -255,12 +253,13 @@ __device__ __forceinline__ void bank_block(const BankBlock &bb, float *L, float 
     const bool outl = bb.rowp != nullptr;
 
     // ---- round trip 1: L2-resident operands first, then the HBM codes
-    float af[8];
+    // MFMA A operand: centroid 32 w + g, dims 8 h .. 8 h + 7, three bf16 pieces
+    v8bf a[3];
     {
-        const float4 *p = reinterpret_cast<const float4 *>(bb.cb + (32 * w + g) * 16 + 8 * h);
-        const float4 u = gld(p), v = gld(p + 1);
-        af[0] = u.x; af[1] = u.y; af[2] = u.z; af[3] = u.w;
-        af[4] = v.x; af[5] = v.y; af[6] = v.z; af[7] = v.w;
+        const v8bf *p = bb.cb3 + ((32 * w + g) * 2 + h) * 3;
+        a[0] = gld(p);
+        a[1] = gld(p + 1);
+        a[2] = gld(p + 2);
     }
     const float sc = gld(bb.scales + mc);
     const float bs = bb.bias ? gld(bb.bias + mc) : 0.f;
@@ -279,8 +278,7 @@ __device__ __forceinline__ void bank_block(const BankBlock &bb, float *L, float 
     __syncthreads();
 
     // ---- slice 0 into buffer 0
-    v8bf a[3], b[3];
-    split3(af, a);
+    v8bf b[3];
     bank_xop(xs, 0, g, h, b);
     {
         const v16f d = bank_build(a, b);
@@ -381,7 +379,7 @@ __global__ __launch_bounds__(kBNT) void lut_bank_kernel(const GroupItem *__restr
     extern __shared__ float xs[];                    // [32 S][kXRow]: x pieces (B operands, outliers)
     const int2 wk = work[blockIdx.x];
     const GroupItem it = items[wk.x];
-    const BankBlock bb{it.codes_b, it.cb, it.scales, it.bias, it.rowp, it.col, it.val,
+    const BankBlock bb{it.codes_b, static_cast<const v8bf *>(it.cb3), it.scales, it.bias, it.rowp, it.col, it.val,
                        it.x, it.y, it.K, it.M, wk.y};
     bank_block<XS_F32>(bb, L, xs);
 }
@@ -396,7 +394,7 @@ __global__ __launch_bounds__(kBNT) void lut_bank_kernel(const GroupItem *__restr
 struct MoEBankParams {
     const uint8_t *codes_b;     // [E][bank layout of M x G]
     size_t expert_bytes;
-    const float *cb;            // [256][16]
+    const v8bf *cb3;            // [256][2][3] the codebook's bf16 pieces
     const float *scales;        // [E][M]
     const void *x;              // gate/up: [T][K]; down: [P][2K] fp32
     float *y;                   // [P][M]
@@ -423,7 +421,7 @@ __global__ __launch_bounds__(kBNT) void moe_bank_kernel(MoEBankParams p) {
         x = static_cast<const __hip_bfloat16 *>(p.x) + (size_t)(pr / p.k) * p.K;
     else
         x = static_cast<const float *>(p.x) + (size_t)(pr / p.k) * p.K;
-    const BankBlock bb{p.codes_b + (size_t)e * p.expert_bytes, p.cb,
+    const BankBlock bb{p.codes_b + (size_t)e * p.expert_bytes, p.cb3,
                        p.scales + (size_t)e * p.M, nullptr, nullptr, nullptr, nullptr,
                        x, p.y + (size_t)pr * p.M, p.K, p.M, (wk.y >> 16) * kBRows};
     bank_block<XS>(bb, L, xs);
@@ -538,7 +536,7 @@ int launch_moe_plan(const int *idx, const float *w, int P, int E, int nb_gu, int
 }
 
 int launch_moe_bank(const MoEBankLaunch &l, hipStream_t st) {
-    MoEBankParams p{l.codes_b, l.expert_bytes, l.cb, l.scales, l.x, l.y, l.idx, l.work,
+    MoEBankParams p{l.codes_b, l.expert_bytes, static_cast<const v8bf *>(l.cb3), l.scales, l.x, l.y, l.idx, l.work,
                     l.n_work, l.M, l.K, l.k};
     const size_t lds = round_up((size_t)(l.K / 16), 32) * kXRow * sizeof(float);
     const int grid = 8 * ((l.max_work + 7) / 8);

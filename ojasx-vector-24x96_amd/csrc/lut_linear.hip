@@ -539,10 +539,10 @@ struct Linear {
     int K = 0, M = 0, D = 0, Kcb = 0, G = 0, S = 0, Mp = 0;
     bool has_bias = false;
     size_t nnz = 0;
-    DevBuf codes, codes_b, codebook, scales, bias, rowp, col, val;
+    DevBuf codes, codes_b, codebook, cb3, scales, bias, rowp, col, val;
     DevBuf lut, xstage, ystage;
     ~Linear() {
-        for (DevBuf *b : {&codes, &codes_b, &codebook, &scales, &bias, &rowp, &col, &val, &lut,
+        for (DevBuf *b : {&codes, &codes_b, &codebook, &cb3, &scales, &bias, &rowp, &col, &val, &lut,
                           &xstage, &ystage})
             b->release();
     }
@@ -771,6 +771,7 @@ int linear_items(const void *h, GroupItem *it) {
     it->codes_b = L->codes_b.as<uint8_t>();
     it->S32 = (L->G + 31) / 32;
     it->cb = L->codebook.as<float>();
+    it->cb3 = L->cb3.ptr;
     it->scales = L->scales.as<float>();
     it->bias = L->has_bias ? L->bias.as<float>() : nullptr;
     it->rowp = L->nnz ? L->rowp.as<int>() : nullptr;
@@ -907,6 +908,11 @@ OJASX_API OjasxLinearHandle ojasx_create_linear(int in_features, int out_feature
         rc = upload(L->codes_b, bank.data(), bank.size());
     }
     if (!rc) rc = upload(L->codebook, cb.data(), cb.size() * sizeof(float));
+    if (!rc && L->D == 16) {   // the grouped kernel's MFMA operand
+        std::vector<uint16_t> cb3(kCb3Bytes / 2);
+        split_codebook_bf16x3(cb.data(), cb3.data());
+        rc = upload(L->cb3, cb3.data(), kCb3Bytes);
+    }
     if (!rc) rc = upload(L->scales, sc.data(), sc.size() * sizeof(float));
     if (!rc && bias_data) {
         L->has_bias = true;

@@ -53,13 +53,14 @@ struct MoE {
     int E = 0, H = 0, I = 0, top_k = 0, D = 0;
     int Gin = 0, Gi = 0, Sin = 0, Si = 0, Ip = 0, Hp = 0;
     DevBuf cb_in, cb_dn, gu, dn, gus, dns;
+    DevBuf cb3_in, cb3_dn;              // bank path: the codebooks' bf16 pieces
     DevBuf gub, dnb;                    // bank layouts per expert (block_dim 16)
     size_t gub_bytes = 0, dnb_bytes = 0;
     DevBuf lut_in, lut_dn, dout, inter, gu_part, xstage, ystage;
     DevBuf work, nwork, gu_out;         // bank path: plan output, gate/up rows per pair
     size_t lut_dn_pairs = 0;
     ~MoE() {
-        for (DevBuf *b : {&cb_in, &cb_dn, &gu, &dn, &gus, &dns, &gub, &dnb, &lut_in, &lut_dn,
+        for (DevBuf *b : {&cb_in, &cb_dn, &cb3_in, &cb3_dn, &gu, &dn, &gus, &dns, &gub, &dnb, &lut_in, &lut_dn,
                           &dout, &inter, &gu_part, &xstage, &ystage, &work,
                           &nwork, &gu_out})
             b->release();
@@ -944,7 +945,7 @@ int moe_forward_bank(MoE *m, const void *x, const int *idx, const float *w, void
     MoEBankLaunch l{};
     l.codes_b = m->gub.as<uint8_t>();
     l.expert_bytes = m->gub_bytes;
-    l.cb = m->cb_in.as<float>();
+    l.cb3 = m->cb3_in.ptr;
     l.scales = m->gus.as<float>();
     l.x = x;
     l.y = m->gu_out.as<float>();
@@ -960,7 +961,7 @@ int moe_forward_bank(MoE *m, const void *x, const int *idx, const float *w, void
     if (rc) return rc;
     l.codes_b = m->dnb.as<uint8_t>();
     l.expert_bytes = m->dnb_bytes;
-    l.cb = m->cb_dn.as<float>();
+    l.cb3 = m->cb3_dn.ptr;
     l.scales = m->dns.as<float>();
     l.x = m->gu_out.as<float>();
     l.y = m->dout.as<float>();
@@ -1149,6 +1150,11 @@ OJASX_API OjasxMoEHandle ojasx_create_moe(int num_experts, int hidden_dim, int i
                                 db.data() + e * m->dnb_bytes);
         rc = upload(m->gub, gb.data(), gb.size());
         if (!rc) rc = upload(m->dnb, db.data(), db.size());
+        std::vector<uint16_t> c3(kCb3Bytes / 2);
+        split_codebook_bf16x3(cbi.data(), c3.data());
+        if (!rc) rc = upload(m->cb3_in, c3.data(), kCb3Bytes);
+        split_codebook_bf16x3(cbd.data(), c3.data());
+        if (!rc) rc = upload(m->cb3_dn, c3.data(), kCb3Bytes);
     }
     if (!rc) rc = upload(m->cb_in, cbi.data(), cbi.size() * 4);
     if (!rc) rc = upload(m->cb_dn, cbd.data(), cbd.size() * 4);

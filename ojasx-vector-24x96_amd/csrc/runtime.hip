@@ -54,6 +54,39 @@ int upload(DevBuf &buf, const void *host, size_t n) {
     return OJASX_OK;
 }
 
+namespace {
+// fp32 -> bf16, round to nearest even (finite values; NaN stays NaN)
+uint16_t bf16_rne(float f) {
+    uint32_t u;
+    memcpy(&u, &f, 4);
+    if ((u & 0x7f800000u) == 0x7f800000u) return (uint16_t)((u >> 16) | ((u & 0xffffu) ? 0x40u : 0u));
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+float bf16_to_f(uint16_t h) {
+    const uint32_t u = (uint32_t)h << 16;
+    float f;
+    memcpy(&f, &u, 4);
+    return f;
+}
+}  // namespace
+
+void split_codebook_bf16x3(const float *cb, uint16_t *out) {
+    for (int c = 0; c < 256; ++c)
+        for (int h = 0; h < 2; ++h)
+            for (int i = 0; i < 8; ++i) {
+                const float v = cb[c * 16 + 8 * h + i];
+                const uint16_t h1 = bf16_rne(v);
+                const float r1 = v - bf16_to_f(h1);
+                const uint16_t h2 = bf16_rne(r1);
+                const uint16_t h3 = bf16_rne(r1 - bf16_to_f(h2));
+                uint16_t *o = out + ((c * 2 + h) * 3) * 8 + i;
+                o[0] = h1;
+                o[8] = h2;
+                o[16] = h3;
+            }
+}
+
 int HostIO::reserve(size_t bytes) {
     if (!st) OJX_HIP(hipStreamCreate(&st));   // blocking: ordered after null-stream work
     if (bytes <= cap) return OJASX_OK;
