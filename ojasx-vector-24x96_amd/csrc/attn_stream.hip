@@ -20,9 +20,10 @@
 //    query position, :133-139).  Chunk maximum m_c, p = exp(s - m_c) with
 //    p = 0 for -inf scores (the reference's guard, :144-156), l_c = sum p.
 //    Values: thread (4 dims, token phase) accumulates p * vscale_t * v_t of
-//    every row over its tokens (int8 v rows staged in LDS by coalesced loads
-//    issued before the scores); the chunk's (acc, m_c, l_c) go to a partial
-//    slot.
+//    every row over its tokens (int8 v: at head_dim 128 each thread's 32
+//    words loaded into registers at the start, otherwise the rows staged in
+//    LDS by coalesced loads issued before the scores); the chunk's
+//    (acc, m_c, l_c) go to a partial slot.
 //  * attn_merge_kernel -- per query row, the state and the partials in chunk
 //    order merged as the reference merges tiles (:141-163): m = max of all,
 //    each part scaled by exp(m_part - m) (0 for m_part = -inf), l and acc
@@ -160,7 +161,26 @@ __global__ __launch_bounds__(kANT) void attn_tile_kernel(AttnParams p) {
             if (i < n_pieces) vstage[i] = vr[u];
         }
     };
-    if constexpr (kI8) v_load(0);
+    // int8 with head_dim 128: each value thread (dims 4dq.., phase ts) loads
+    // its 32 v words (tokens ts + 8 i) into registers at the start instead --
+    // no LDS stage, so more workgroups fit a CU and every load of the chunk is
+    // in flight under the scores
+    constexpr int kVW = 32;
+    const bool vreg = kI8 && D == 128;
+    uint32_t vw[kI8 ? kVW : 1];
+    if constexpr (kI8) {
+        if (vreg) {
+            const int dq = tid & 31, ts = tid >> 5;
+#pragma unroll
+            for (int i = 0; i < kVW; ++i) {
+                const int tt = min(ts + 8 * i, wk.n - 1);
+                vw[i] = gld(reinterpret_cast<const uint32_t *>(
+                    reinterpret_cast<const int8_t *>(vbase) + tt * tl.st + 4 * dq));
+            }
+        } else {
+            v_load(0);
+        }
+    }
 
     // ---- scores of the thread's token against the block's rows: the row's
     //      16-byte pieces loaded 8 at a time (all of a 128-dim int8 row at
@@ -209,10 +229,12 @@ __global__ __launch_bounds__(kANT) void attn_tile_kernel(AttnParams p) {
         if (lane == 0) rm[w][r] = m;
     }
     if constexpr (kI8) {
-        v_store(0);
-        for (int round = 1; round * kVP * kANT < n_pieces; ++round) {
-            v_load(round);
-            v_store(round);
+        if (!vreg) {
+            v_store(0);
+            for (int round = 1; round * kVP * kANT < n_pieces; ++round) {
+                v_load(round);
+                v_store(round);
+            }
         }
     }
     __syncthreads();
@@ -237,7 +259,23 @@ __global__ __launch_bounds__(kANT) void attn_tile_kernel(AttnParams p) {
     for (int r = 0; r < RB; ++r)
 #pragma unroll
         for (int j = 0; j < 4; ++j) a4[r][j] = 0.0;
-    if (ts < TS) {
+    if (vreg) {
+        // tokens past n: p = 0 (their v words repeat token n - 1's)
+#pragma unroll
+        for (int i = 0; i < kVW; ++i) {
+            const int tt = ts + 8 * i;
+            const uint32_t u = vw[i];
+            double v4[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) v4[j] = (double)(int8_t)(u >> (8 * j));
+#pragma unroll
+            for (int r = 0; r < RB; ++r) {
+                const double wgt = pv[r][tt];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) a4[r][j] = fma(wgt, v4[j], a4[r][j]);
+            }
+        }
+    } else if (ts < TS) {
         const uint32_t *vs32 = reinterpret_cast<const uint32_t *>(vstage) + dq;
         const T *vp = vbase + 4 * dq;
         for (int tt = ts; tt < wk.n; tt += TS) {
@@ -409,7 +447,8 @@ int check_rows(int rows, int D) {
 template <int KT>
 int launch_tiles(const AttnParams &p, int n_work, int B, int RB, hipStream_t st) {
     const dim3 grid(n_work, B * p.Hkv, (p.R + RB - 1) / RB);
-    const size_t lds = KT == KV_INT8 ? (size_t)kACH * p.D : 0;   // v rows, at most 64 KB
+    // int8 v rows staged in LDS (at most 64 KB), except at head_dim 128 (registers)
+    const size_t lds = KT == KV_INT8 && p.D != 128 ? (size_t)kACH * p.D : 0;
     const void *fn = RB == 1   ? reinterpret_cast<const void *>(&attn_tile_kernel<KT, 1>)
                      : RB == 2 ? reinterpret_cast<const void *>(&attn_tile_kernel<KT, 2>)
                      : RB == 4 ? reinterpret_cast<const void *>(&attn_tile_kernel<KT, 4>)
