@@ -348,13 +348,27 @@ __global__ __launch_bounds__(kANT) void attn_merge_kernel(double *state, const d
     const int dq = tid % NQ, ph = tid / NQ;
     double a4[4] = {0.0, 0.0, 0.0, 0.0}, l = 0.0;
     if (ph < PH) {
-        for (int i = ph; i < n; i += PH) {
-            const double *pi = pp + i * stride;
-            const double mi = pi[D];
-            const double f = isinf(mi) ? 0.0 : exp(mi - safe);
-            l = fma(f, pi[D + 1], l);
+        // 4 partials per step, their loads issued together (clamped indices;
+        // the repeats past n are not added)
+        constexpr int kU = 4;
+        for (int i0 = ph; i0 < n; i0 += kU * PH) {
+            double mi[kU], li[kU], v[kU][4];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) a4[j] = fma(f, pi[4 * dq + j], a4[j]);
+            for (int u = 0; u < kU; ++u) {
+                const double *pi = pp + (size_t)min(i0 + u * PH, n - 1) * stride;
+                mi[u] = pi[D];
+                li[u] = pi[D + 1];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) v[u][j] = pi[4 * dq + j];
+            }
+#pragma unroll
+            for (int u = 0; u < kU; ++u) {
+                if (i0 + u * PH >= n) break;
+                const double f = isinf(mi[u]) ? 0.0 : exp(mi[u] - safe);
+                l = fma(f, li[u], l);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) a4[j] = fma(f, v[u][j], a4[j]);
+            }
         }
     }
 #pragma unroll
