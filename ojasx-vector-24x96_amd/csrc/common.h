@@ -286,18 +286,6 @@ __device__ __forceinline__ float wave_max_f(float v) {
     const float d = __int_as_float(__builtin_amdgcn_readlane(iv, 48));
     return fmaxf(fmaxf(a, b), fmaxf(c, d));
 }
-__device__ __forceinline__ float wave_min_f(float v) {
-    v = fminf(v, __int_as_float(dpp_i<0xB1>(__float_as_int(v))));
-    v = fminf(v, __int_as_float(dpp_i<0x4E>(__float_as_int(v))));
-    v = fminf(v, __int_as_float(dpp_i<0x141>(__float_as_int(v))));
-    v = fminf(v, __int_as_float(dpp_i<0x140>(__float_as_int(v))));
-    const int iv = __float_as_int(v);
-    const float a = __int_as_float(__builtin_amdgcn_readlane(iv, 0));
-    const float b = __int_as_float(__builtin_amdgcn_readlane(iv, 16));
-    const float c = __int_as_float(__builtin_amdgcn_readlane(iv, 32));
-    const float d = __int_as_float(__builtin_amdgcn_readlane(iv, 48));
-    return fminf(fminf(a, b), fminf(c, d));
-}
 __device__ __forceinline__ int wave_min_i(int v) {
     v = min(v, dpp_i<0xB1>(v));
     v = min(v, dpp_i<0x4E>(v));
