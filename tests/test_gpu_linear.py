@@ -112,7 +112,10 @@ def test_baseline_configs_fp32(pkg, dev, M, K, B):
     (70, 4096, 16, 1, 0.02),       # one row tile, 16 slices (no tail)
     (95, 2560, 14, 0, 0.05),       # one row tile, outliers past the LDS stage
     (2049, 768, 20, 0, 0.0038),    # two row tiles, 3 slices (main loop skipped)
-    (517, 3072, 31, 1, 0.0038)])   # two row tiles, 12 slices
+    (517, 3072, 31, 1, 0.0038),    # two row tiles, 12 slices
+    (257, 9728, 65, 0, 0.0038),    # 38 slices (a tail of 2); five 16-token tiles, the last of 1
+    (64, 176, 100, 0, 0.02),       # 11 groups in one slice; 100 tokens
+    (40, 2560, 128, 1, 0.0038)])   # eight full 16-token tiles
 def test_mfma_batched_shapes(pkg, dev, M, K, B, dt, density):
     """Many tokens (x . W^T on MFMA): ragged rows, tokens and slices, bias,
     outliers given with each row's columns shuffled (the handle sorts them),
