@@ -603,7 +603,7 @@ OJASX_API int ojasx_attention_stream_update_device(double *state, int batch, int
     memcpy(sg.host.data() + tile_bytes, wl.data(), sizeof(AttnWork) * wl.size());
     hipStream_t st = static_cast<hipStream_t>(stream);
     void *staged = nullptr;
-    rc = sg.ring.stage(sg.host.data(), bytes, false, st, &staged);
+    rc = sg.ring.stage(sg.host.data(), bytes, true, st, &staged);
     if (rc) return rc;
     const size_t per_work = (size_t)rows * (D + 2) * sizeof(double);
     const int n_work = (int)wl.size();

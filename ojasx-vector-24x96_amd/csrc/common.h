@@ -58,8 +58,10 @@ HostIO &host_io();   // the calling thread's
 // upload is an asynchronous copy (a pageable source would make every call wait
 // for it).  A slot is rewritten only after the event recorded behind the last
 // launch that read it has completed, whatever stream the calls run on.  With
-// reuse, a call whose bytes equal the last upload's launches on that device
-// copy without a new upload.  One ring per host thread (thread_local).
+// reuse, a call whose bytes equal those of a slot uploaded on the same stream
+// launches on that device copy without a new upload (callers that rotate over
+// a few argument sets keep them resident).  One ring per host thread
+// (thread_local).
 struct StagingRing {
     static constexpr int kSlots = 4;
     DevBuf dev;                         // [kSlots][cap] bytes
@@ -67,11 +69,13 @@ struct StagingRing {
     size_t cap = 0;
     hipEvent_t ev[kSlots] = {};
     int next = 0, cur = -1;             // the slot of the current call
-    int last = -1;                      // the slot holding the last upload
-    size_t last_bytes = 0;
+    size_t bytes_of[kSlots] = {};       // bytes of each slot's upload (0: none)
+    hipStream_t stream_of[kSlots] = {}; // the stream each slot was uploaded on
     int reserve(size_t bytes);
-    // Uploads bytes from host (or reuses the last upload) on st; *dev_out is
-    // the device copy, valid for launches on st until launched() is called.
+    // Uploads bytes from host on st, or with reuse launches on a slot that
+    // already holds them, uploaded on st (so the upload precedes the call's
+    // launches); *dev_out is the device copy, valid for launches on st until
+    // launched() is called.
     int stage(const void *host, size_t bytes, bool reuse, hipStream_t st, void **dev_out);
     // Records the current slot's event on st, behind the launches that read it.
     int launched(hipStream_t st);

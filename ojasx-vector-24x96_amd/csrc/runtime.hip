@@ -116,7 +116,7 @@ int StagingRing::reserve(size_t bytes) {
     if (pinned) (void)hipHostFree(pinned);
     pinned = nullptr;
     cap = 0;
-    last = -1;
+    for (size_t &b : bytes_of) b = 0;
     const size_t n = round_up(std::max<size_t>(bytes, 64 << 10), 256);
     OJX_HIP(hipHostMalloc(reinterpret_cast<void **>(&pinned), n * kSlots, hipHostMallocDefault));
     const int rc = dev.ensure(n * kSlots);
@@ -130,16 +130,24 @@ int StagingRing::reserve(size_t bytes) {
 int StagingRing::stage(const void *host, size_t bytes, bool reuse, hipStream_t st, void **dev_out) {
     int rc = reserve(bytes);
     if (rc) return rc;
-    int k = last;
-    if (!reuse || k < 0 || last_bytes != bytes || memcmp(pinned + (size_t)k * cap, host, bytes) != 0) {
+    int k = -1;
+    if (reuse) {
+        // the newest matching slot first (the one before next)
+        for (int i = 1; i <= kSlots && k < 0; ++i) {
+            const int s = (next - i + kSlots) % kSlots;
+            if (bytes_of[s] != bytes || memcmp(pinned + (size_t)s * cap, host, bytes) != 0) continue;
+            if (stream_of[s] == st) k = s;   // its upload precedes this call on st
+        }
+    }
+    if (k < 0) {
         k = next;
         next = (k + 1) % kSlots;
         OJX_HIP(hipEventSynchronize(ev[k]));             // slot k's last launch is done
         memcpy(pinned + (size_t)k * cap, host, bytes);
         OJX_HIP(hipMemcpyAsync(dev.as<unsigned char>() + (size_t)k * cap, pinned + (size_t)k * cap,
                                bytes, hipMemcpyHostToDevice, st));
-        last = k;
-        last_bytes = bytes;
+        bytes_of[k] = bytes;
+        stream_of[k] = st;
     }
     cur = k;
     *dev_out = dev.as<unsigned char>() + (size_t)k * cap;

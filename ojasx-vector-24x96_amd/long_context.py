@@ -380,7 +380,9 @@ class OnlineSoftmaxBlockAttention:
                 kv_offset += S_k
         lse = torch.empty(state.shape[0], dtype=torch.float64, device=query.device)
         out = self._finalize(state, query, lse)
-        max_lse = float(lse.max().item()) if kv_offset > 0 else 0.0
+        # the rows' log-sum-exps copied out and reduced on the host: one
+        # synchronising copy, no reduction kernel
+        max_lse = float(lse.cpu().max()) if kv_offset > 0 else 0.0
         return out, BlockAttentionReport(query_tokens=S_q, kv_tokens=kv_offset,
                                          num_kv_blocks=num_blocks, peak_tile_elements=peak,
                                          max_logsumexp=max_lse)
