@@ -59,10 +59,13 @@ constexpr int kAttnC = 64;        // tokens per chunk, one per lane
 // Workgroup (x, kv head h, slice z of up to 4 of its query heads); wave j < nj
 // owns query head h*R + 4z + j, whose q it normalises (RMSNorm by a wave sum)
 // and rotates itself: lane l holds dimensions l and l + 64, a RoPE pair.
-//   x < n_chunks: chunk x of the tokens before pos.  Lane l scores token
-//     64x + l for each query head from the K codebook in LDS, the chunk's
-//     softmax statistics are wave reductions, then lane l accumulates output
-//     dimensions 2l, 2l + 1 from the V codebook.
+//   x < n_chunks: chunk x of the tokens before pos.  Lane (token 16 j + l / 4,
+//     quarter l % 4) of wave j reads its token's K codebook quarter once per
+//     group for all the workgroup's query heads (a quad sum completes each
+//     score); wave j then takes head j's softmax over the chunk (wave
+//     reductions); for V, lane l of wave j accumulates output dimensions 2l,
+//     2l + 1 of every head over tokens 16 j .. 16 j + 15 (each V codebook row
+//     read once), and the four waves' sums are added in wave order.
 //   x = n_chunks: the new token.  Wave 2 normalises and rotates k, wave 3
 //     takes v as is, each scaled by max|.| / 127; thread t holds centroid t of
 //     the head's K and V codebooks for the nearest-centroid search of each
@@ -81,6 +84,8 @@ __global__ __launch_bounds__(kAttnNT) void attn_decode_kernel(AttnParams p) {
     __shared__ uint2 ncode[2];           // its K and V codes
     __shared__ uint2 kcw[kAttnC], vcw[kAttnC];
     __shared__ float wsc[4][kAttnC];     // K scale * sf and V scale, then p_jt * vs_t
+    __shared__ float ssc[4][kAttnC];     // scores of the chunk's tokens per head
+    __shared__ float2 ored[4][4][64];    // V sums per wave, head and dim pair
     const int tid = threadIdx.x, lane = tid & 63, j = tid >> 6;
     const int R = p.Hq / p.Hkv;
     const int h = blockIdx.y;
@@ -89,6 +94,9 @@ __global__ __launch_bounds__(kAttnNT) void attn_decode_kernel(AttnParams p) {
     const int c = blockIdx.x;
     const bool fresh = c == p.n_chunks;          // the new token's workgroup
     const int stride = p.n_chunks + 1;           // partial slots per query head
+    // the new token's workgroup has the longest chain (norms, RoPE, the
+    // nearest-centroid searches): its waves issue first on their SIMDs
+    if (fresh) __builtin_amdgcn_s_setprio(3);
     // ---- round trip 1: the position, codebooks, q rows and norm weights, the
     // new token's k / v rows (its workgroup), wave 0's block-table entry
     const int pos = min(p.state[0], p.max_ctx - 1);
@@ -277,55 +285,86 @@ __global__ __launch_bounds__(kAttnNT) void attn_decode_kernel(AttnParams p) {
         wsc[1][lane] = tw < T ? vsv : 0.f;
     }
     __syncthreads();
-    const float kf = wsc[0][lane], vf = wsc[1][lane];
-    const uint2 kwl = kcw[lane];
-    __syncthreads();   // wsc is rewritten with the weights below
 
-    // score of token tw for head j: sum_g <q_j,g, Ck[code_g]> * ks * sf
-    float sc = -INFINITY;
-    if (j < nj) {
-        const uint32_t kd[2] = {kwl.x, kwl.y};
-        float acc = 0.f;
+    // scores: lane (token tq = 16 j + lane / 4, quarter k4 = lane % 4) reads
+    // its token's codebook quarter once per group for every head; the quarters
+    // are summed across the lane quad
+    const int tq = 16 * j + (lane >> 2), k4 = lane & 3;
+    float pq[4] = {0.f, 0.f, 0.f, 0.f};
+    {
+        const uint2 kq = kcw[tq];
+        const uint32_t kd[2] = {kq.x, kq.y};
 #pragma unroll
         for (int g = 0; g < kG; ++g) {
             const uint32_t code = (kd[g >> 2] >> ((g & 3) * 8)) & 0xffu;
-            const float4 *qr = q4s + j * 32 + g * 4;
-            float dot = 0.f;
+            const float4 cq = ck4[cb_slot(code, k4)];
 #pragma unroll
-            for (int w = 0; w < 4; ++w) {
-                const float4 cq = ck4[cb_slot(code, w)], qq = qr[w];
+            for (int jj = 0; jj < 4; ++jj) {
+                if (jj >= nj) break;
+                const float4 qq = q4s[jj * 32 + g * 4 + k4];
+                float dot = pq[jj];
                 dot = fmaf(qq.x, cq.x, dot);
                 dot = fmaf(qq.y, cq.y, dot);
                 dot = fmaf(qq.z, cq.z, dot);
                 dot = fmaf(qq.w, cq.w, dot);
+                pq[jj] = dot;
             }
-            acc += dot;
         }
-        if (tw < T) sc = acc * kf;
     }
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {
+        pq[jj] += __shfl_xor(pq[jj], 1);
+        pq[jj] += __shfl_xor(pq[jj], 2);
+    }
+    const float kfq = wsc[0][tq], vf = wsc[1][lane];
+    if (k4 == 0) {
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj)
+            ssc[jj][tq] = c * kAttnC + tq < T ? pq[jj] * kfq : -INFINITY;
+    }
+    __syncthreads();   // the scores are in; wsc is rewritten with the weights below
+
+    // softmax of head j over the chunk (lane = token)
+    const float sc = j < nj ? ssc[j][lane] : -INFINITY;
     const float m = wave_max_f(sc);
     const float e = (sc == -INFINITY) ? 0.f : expf(sc - m);
     wsc[j][lane] = e * vf;
     const float l = wave_sum_f(e);
     __syncthreads();
 
-    // V: lane owns dims 2*lane, 2*lane+1 (group g = lane / 8)
-    if (j < nj) {
+    // V: lane owns dims 2 lane, 2 lane + 1 (group g = lane / 8) of every head;
+    // wave j takes tokens 16 j .. 16 j + 15; the waves' sums meet in LDS
+    {
         const int g = lane >> 3, d0 = (lane & 7) * 2;
         const float *cvf = reinterpret_cast<const float *>(cv4);
-        float o0 = 0.f, o1 = 0.f;
-#pragma unroll 8
-        for (int tl = 0; tl < kAttnC; ++tl) {
+        float o[4][2] = {{0.f, 0.f}, {0.f, 0.f}, {0.f, 0.f}, {0.f, 0.f}};
+#pragma unroll 4
+        for (int tl = 16 * j; tl < 16 * j + 16; ++tl) {
             const uint2 cw = vcw[tl];
             const uint32_t code = ((g < 4 ? cw.x : cw.y) >> ((g & 3) * 8)) & 0xffu;
             const float2 cvv = *reinterpret_cast<const float2 *>(cvf + code * 16 + d0);
-            const float w = wsc[j][tl];
-            o0 = fmaf(w, cvv.x, o0);
-            o1 = fmaf(w, cvv.y, o1);
+#pragma unroll
+            for (int jj = 0; jj < 4; ++jj) {
+                const float wgt = wsc[jj][tl];
+                o[jj][0] = fmaf(wgt, cvv.x, o[jj][0]);
+                o[jj][1] = fmaf(wgt, cvv.y, o[jj][1]);
+            }
+        }
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) ored[j][jj][lane] = make_float2(o[jj][0], o[jj][1]);
+    }
+    __syncthreads();
+    if (j < nj) {
+        float2 o = ored[0][j][lane];
+#pragma unroll
+        for (int u = 1; u < 4; ++u) {
+            const float2 t = ored[u][j][lane];
+            o.x += t.x;
+            o.y += t.y;
         }
         float *po = p.part_o + ((size_t)(j0 + j) * stride + c) * kHd + lane * 2;
-        po[0] = o0;
-        po[1] = o1;
+        po[0] = o.x;
+        po[1] = o.y;
         if (lane == 0) {
             float *ml = p.part_ml + ((size_t)(j0 + j) * stride + c) * 2;
             ml[0] = m;
