@@ -66,21 +66,23 @@ constexpr int kAttnC = 64;        // tokens per chunk, one per lane
 //     reductions); for V, lane l of wave j accumulates output dimensions 2l,
 //     2l + 1 of every head over tokens 16 j .. 16 j + 15 (each V codebook row
 //     read once), and the four waves' sums are added in wave order.
-//   x = n_chunks: the new token.  Wave 2 normalises and rotates k, wave 3
-//     takes v as is, each scaled by max|.| / 127; thread t holds centroid t of
-//     the head's K and V codebooks for the nearest-centroid search of each
-//     16-dimension group (ties to the lower index); slice z = 0 stores codes
-//     and scales into the cache.  Its partial: max = its score, sum = 1,
-//     o = v_scale * Cv[code].  No workgroup reads the slot being written, and
-//     the encoder's chain runs beside the chunks' instead of inside one.
+//   x = n_chunks, n_chunks + 1: the new token's K and V.  Wave 2 of the first
+//     normalises and rotates k, wave 3 of the second takes v as is, each
+//     scaled by max|.| / 127; thread t holds centroid t of the head's K (V)
+//     codebook for the nearest-centroid search of each 16-dimension group
+//     (ties to the lower index); slice z = 0 stores codes and scales into the
+//     cache.  Its partial (slot n_chunks): max = its score and sum = 1 from the
+//     K workgroup, o = v_scale * Cv[code] from the V workgroup.  No workgroup
+//     reads the slot being written, and the encoder's chains run beside the
+//     chunks' instead of inside one.
 __global__ __launch_bounds__(kAttnNT) void attn_decode_kernel(AttnParams p) {
     __shared__ float4 ck4[256 * 4];      // K codebook [256][16], rows swizzled (cb_slot)
     __shared__ float4 cv4[256 * 4];      // V codebook [256][16]
     __shared__ float4 q4s[4 * 32];       // rotated q [4][128]
-    __shared__ __align__(16) float xs[2 * kHd];   // new token: k / s_k, v / s_v
+    __shared__ __align__(16) float xs[kHd];       // new token: k / s_k or v / s_v
     __shared__ float nscale[2];          // its scales
-    __shared__ float wd[2][kG][4];       // per-wave nearest distance
-    __shared__ int wi[2][kG][4];         // and its lowest centroid
+    __shared__ float wd[1][kG][4];       // per-wave nearest distance
+    __shared__ int wi[1][kG][4];         // and its lowest centroid
     __shared__ uint2 ncode[2];           // its K and V codes
     __shared__ uint2 kcw[kAttnC], vcw[kAttnC];
     __shared__ float wsc[4][kAttnC];     // K scale * sf and V scale, then p_jt * vs_t
@@ -92,7 +94,8 @@ __global__ __launch_bounds__(kAttnNT) void attn_decode_kernel(AttnParams p) {
     const int j0 = h * R + blockIdx.z * 4;
     const int nj = min(4, R - (int)blockIdx.z * 4);
     const int c = blockIdx.x;
-    const bool fresh = c == p.n_chunks;          // the new token's workgroup
+    const bool fresh = c >= p.n_chunks;          // the new token's workgroups: K, then V
+    const int kvf = c - p.n_chunks;              // 0: K, 1: V (fresh)
     const int stride = p.n_chunks + 1;           // partial slots per query head
     // the new token's workgroup has the longest chain (norms, RoPE, the
     // nearest-centroid searches): its waves issue first on their SIMDs
@@ -117,7 +120,7 @@ __global__ __launch_bounds__(kAttnNT) void attn_decode_kernel(AttnParams p) {
         w1 = p.qn_w[lane + 64];
     }
     float e0 = 0.f, e1 = 0.f, u0 = 0.f, u1 = 0.f;   // k (wave 2, k_norm weights) / v (wave 3)
-    if (fresh && j >= 2) {
+    if (fresh && j == 2 + kvf) {
         const float *src = p.qkv + (size_t)(p.Hq + (j - 2) * p.Hkv + h) * kHd;
         e0 = src[lane];
         e1 = src[lane + 64];
@@ -158,89 +161,85 @@ __global__ __launch_bounds__(kAttnNT) void attn_decode_kernel(AttnParams p) {
     }
 
     if (fresh) {
-        if (j == 2) {
+        // kvf = 0: wave 2 normalises and rotates k; kvf = 1: wave 3 takes v
+        if (j == 2 && kvf == 0) {
             const float rn = 1.0f / sqrtf(wave_sum_f(e0 * e0 + e1 * e1) / (float)kHd + p.eps);
             const float x0 = (e0 * rn) * u0, x1 = (e1 * rn) * u1;
             e0 = x0 * cs - x1 * sn;
             e1 = x1 * cs + x0 * sn;
         }
-        if (j >= 2) {
+        if (j == 2 + kvf) {
             const float s = fmaxf(1e-8f, wave_max_f(fmaxf(fabsf(e0), fabsf(e1)))) / 127.0f;
-            xs[(j - 2) * kHd + lane] = e0 / s;
-            xs[(j - 2) * kHd + lane + 64] = e1 / s;
-            if (lane == 0) nscale[j - 2] = s;
+            xs[lane] = e0 / s;
+            xs[lane + 64] = e1 / s;
+            if (lane == 0) nscale[kvf] = s;
         }
         __syncthreads();
-        float ck[kBd], cv[kBd];
+        const float4 *cb4 = kvf ? cv4 : ck4;
+        float cc[kBd];
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
-            const float4 ka = ck4[cb_slot(tid, u)], va = cv4[tid * 4 + u];
-            ck[4 * u] = ka.x, ck[4 * u + 1] = ka.y, ck[4 * u + 2] = ka.z, ck[4 * u + 3] = ka.w;
-            cv[4 * u] = va.x, cv[4 * u + 1] = va.y, cv[4 * u + 2] = va.z, cv[4 * u + 3] = va.w;
+            const float4 ka = cb4[kvf ? tid * 4 + u : cb_slot(tid, u)];
+            cc[4 * u] = ka.x, cc[4 * u + 1] = ka.y, cc[4 * u + 2] = ka.z, cc[4 * u + 3] = ka.w;
         }
-        // squared distances of centroid tid to the 8 K and 8 V groups, then
-        // the 16 wave minima and their lowest centroids, interleaved
-        float dd[2 * kG];
+        // squared distances of centroid tid to the 8 groups, then the 8 wave
+        // minima and their lowest centroids, interleaved
+        float dd[kG];
 #pragma unroll
         for (int g = 0; g < kG; ++g) {
-            const float4 *xk = reinterpret_cast<const float4 *>(xs + g * kBd);
-            const float4 *xv = reinterpret_cast<const float4 *>(xs + kHd + g * kBd);
-            float dk = 0.f, dv = 0.f;
+            const float4 *xg = reinterpret_cast<const float4 *>(xs + g * kBd);
+            float dk = 0.f;
 #pragma unroll
             for (int w = 0; w < 4; ++w) {
-                const float4 a4 = xk[w], b4 = xv[w];
-                const float ak[4] = {a4.x, a4.y, a4.z, a4.w}, bv[4] = {b4.x, b4.y, b4.z, b4.w};
+                const float4 a4 = xg[w];
+                const float ak[4] = {a4.x, a4.y, a4.z, a4.w};
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    const float fk = ak[e] - ck[4 * w + e];
-                    const float fv = bv[e] - cv[4 * w + e];
+                    const float fk = ak[e] - cc[4 * w + e];
                     dk = fmaf(fk, fk, dk);
-                    dv = fmaf(fv, fv, dv);
                 }
             }
             dd[g] = dk;
-            dd[kG + g] = dv;
         }
-        float mn[2 * kG];
-        int id[2 * kG];
+        float mn[kG];
+        int id[kG];
 #pragma unroll
-        for (int i = 0; i < 2 * kG; ++i) mn[i] = dd[i];
+        for (int i = 0; i < kG; ++i) mn[i] = dd[i];
         wave_min_n(mn);
 #pragma unroll
-        for (int i = 0; i < 2 * kG; ++i) id[i] = dd[i] == mn[i] ? tid : 0x7fffffff;
+        for (int i = 0; i < kG; ++i) id[i] = dd[i] == mn[i] ? tid : 0x7fffffff;
         wave_min_n(id);
         if (lane == 0) {
 #pragma unroll
             for (int g = 0; g < kG; ++g) {
                 wd[0][g][j] = mn[g];
                 wi[0][g][j] = id[g];
-                wd[1][g][j] = mn[kG + g];
-                wi[1][g][j] = id[kG + g];
             }
         }
         __syncthreads();
-        if (tid < 2 * kG) {
-            const int kv = tid >= kG, g = tid - kv * kG;
-            float bm = wd[kv][g][0];
-            int bi = wi[kv][g][0];
+        if (tid < kG) {
+            const int g = tid;
+            float bm = wd[0][g][0];
+            int bi = wi[0][g][0];
 #pragma unroll
             for (int q = 1; q < 4; ++q)
-                if (wd[kv][g][q] < bm) {   // strictly smaller: earlier waves hold lower indices
-                    bm = wd[kv][g][q];
-                    bi = wi[kv][g][q];
+                if (wd[0][g][q] < bm) {   // strictly smaller: earlier waves hold lower indices
+                    bm = wd[0][g][q];
+                    bi = wi[0][g][q];
                 }
-            reinterpret_cast<uint8_t *>(ncode)[kv * kG + g] = (uint8_t)bi;
+            reinterpret_cast<uint8_t *>(ncode)[kvf * kG + g] = (uint8_t)bi;
             if (blockIdx.z == 0) {
                 const size_t row = ((size_t)npage * p.Hkv + h) * p.P + (pos % p.P);
-                (kv ? p.vc : p.kc)[row * kG + g] = (uint8_t)bi;
-                if (g == 0) (kv ? p.vs : p.ks)[row] = nscale[kv];
+                (kvf ? p.vc : p.kc)[row * kG + g] = (uint8_t)bi;
+                if (g == 0) (kvf ? p.vs : p.ks)[row] = nscale[kvf];
             }
         }
         __syncthreads();
-        // the new token's partial for head j: its score (the chunk arithmetic
-        // for one token), sum 1, o = v_scale * Cv[code]
-        if (j < nj) {
-            const uint2 kn = ncode[0], vn = ncode[1];
+        // the new token's partial for head j (slot n_chunks): the K workgroup
+        // writes its score (the chunk arithmetic for one token) as the max and
+        // 1 as the sum, the V workgroup o = v_scale * Cv[code]
+        if (j < nj && kvf == 0) {
+            const uint2 kn = ncode[0];
             const uint32_t kd[2] = {kn.x, kn.y};
             float acc = 0.f;
 #pragma unroll
@@ -258,7 +257,14 @@ __global__ __launch_bounds__(kAttnNT) void attn_decode_kernel(AttnParams p) {
                 }
                 acc += dot;
             }
-            const float sc = acc * (nscale[0] * p.sf);
+            if (lane == 0) {
+                float *ml = p.part_ml + ((size_t)(j0 + j) * stride + p.n_chunks) * 2;
+                ml[0] = acc * (nscale[0] * p.sf);
+                ml[1] = 1.0f;
+            }
+        }
+        if (j < nj && kvf == 1) {
+            const uint2 vn = ncode[1];
             const int g = lane >> 3, d0 = (lane & 7) * 2;
             const uint32_t code = ((g < 4 ? vn.x : vn.y) >> ((g & 3) * 8)) & 0xffu;
             const float2 cvv =
@@ -267,11 +273,6 @@ __global__ __launch_bounds__(kAttnNT) void attn_decode_kernel(AttnParams p) {
             float *po = p.part_o + ((size_t)(j0 + j) * stride + p.n_chunks) * kHd + lane * 2;
             po[0] = wv * cvv.x;
             po[1] = wv * cvv.y;
-            if (lane == 0) {
-                float *ml = p.part_ml + ((size_t)(j0 + j) * stride + p.n_chunks) * 2;
-                ml[0] = sc;
-                ml[1] = 1.0f;
-            }
         }
         return;
     }
@@ -507,7 +508,7 @@ struct Decoder {
                           ly.vc.as<uint8_t>(), ly.ks.as<float>(), ly.vs.as<float>(),
                           part_o.as<float>(), part_ml.as<float>(), Hq, Hkv, P, max_ctx,
                           n_chunks(), eps, sf};
-            OJX_LAUNCH(attn_decode_kernel, dim3(n_chunks() + 1, Hkv, (Hq / Hkv + 3) / 4),
+            OJX_LAUNCH(attn_decode_kernel, dim3(n_chunks() + 2, Hkv, (Hq / Hkv + 3) / 4),
                        dim3(kAttnNT), 0, st, ap);
             rc = kv_merge_device_len(part_o.as<float>(), part_ml.as<float>(), n_chunks() + 1,
                                      kAttnC, Hq, pos, 0, 1, attn.as<float>(), st);
