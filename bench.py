@@ -298,7 +298,7 @@ def bench_linear2560(b, args):
     return res
 
 
-def bench_sustained(b, handles, base, wbytes, steps):
+def bench_sustained(b, handles, base, wbytes):
     """The same LUT-GEMV on all N weight instances in one grouped launch
     (ojasx_linear_forward_grouped_device): the sustained rate over a working
     set above the Infinity Cache."""
@@ -313,7 +313,9 @@ def bench_sustained(b, handles, base, wbytes, steps):
     for _ in range(3):
         assert call(0) == 0, L.ojasx_get_last_error()
     torch.cuda.synchronize()
-    reps = max(10, min(steps, 200))
+    # each launch is a whole pass over the 262 MB of instances, so the count
+    # only sets how steady the average is: 100 launches whatever --steps is
+    reps = 100
     us = b.events_us(call, reps)
     kern = b.kernels(call, reps)
     kname = dominant(kern)
@@ -892,7 +894,7 @@ def main():
             out["lut_gemv_bf16_b1"], _ = linear_leg(b, handles, base, wbytes, M_GU, K_GU, 1, 1,
                                                     args.steps, args.warmup)
         if "sustained" in extra:
-            out["sustained"] = bench_sustained(b, handles, base, wbytes, args.steps)
+            out["sustained"] = bench_sustained(b, handles, base, wbytes)
         if "batched" in extra:
             out["lut_gemv_batched"] = bench_batched(b, handles, base, wbytes, args)
     finally:
