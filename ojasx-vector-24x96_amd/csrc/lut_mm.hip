@@ -55,8 +55,9 @@ struct MmShape {
     static constexpr int kNT = 64 * kQ * RT;        // threads
     static constexpr int kRows = 16 * RT;           // rows
     static constexpr int kXF = kMmTok * 256 / kNT;  // x floats staged per thread per slice
-    // slices of x and of codes in flight (kPX divides kPF): deeper where the
-    // registers allow, since few waves per SIMD leave a slice short
+    // slices of x and of codes in flight (kPX divides kPF and the kernel's
+    // reduced depth): deeper where the registers allow, since few waves per
+    // SIMD leave a slice short
     static constexpr int kPX = 2;
     static constexpr int kPF = 4;
     // CSR entries of the workgroup's rows staged in LDS (columns as 16-bit:
@@ -117,7 +118,10 @@ __device__ __forceinline__ uint32_t mm_codes(const MmParams &p, int s, int row, 
 template <typename T, int RT>
 __global__ __launch_bounds__(MmShape<RT>::kNT) __attribute__((amdgpu_waves_per_eu(MmShape<RT>::kWaves))) void lut_mm_kernel(MmParams p) {
     using Sh = MmShape<RT>;
-    constexpr int NT = Sh::kNT, XF = Sh::kXF, NC = Sh::kCsr, PX = Sh::kPX, PF = Sh::kPF;
+    // two code slices in flight where four spill at the register budget
+    // (fp32 at 4 row tiles, bf16 at 2 and 4): 2-2.5 % faster there
+    constexpr int PF = (RT == 4 || (RT == 2 && !std::is_same<T, float>::value)) ? 2 : Sh::kPF;
+    constexpr int NT = Sh::kNT, XF = Sh::kXF, NC = Sh::kCsr, PX = Sh::kPX;
     constexpr int kQ = Sh::kQ, GPW = Sh::kGPW;
     static_assert(PF % PX == 0, "the unrolled slice body covers both rings");
     __shared__ float4 cb4[256 * 4];                 // codebook [256][16]
