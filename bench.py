@@ -7,30 +7,41 @@ batch 1, fp32 activations, d = 16 / 256 centroids, 0.38 % CSR outliers.  A
 step is one call of the fused LUT-GEMV kernel on one of N distinct weight
 instances (round robin, 262 MB at N = 160, above the 256 MB Infinity Cache).
 
-HBM residency: before every timed pass (events, kernel timing, every extra
-leg) a 512 MiB buffer is read and written, which evicts the Infinity Cache
-and the L2s, so the first N calls of a pass read their codes from HBM
-whatever K is; longer passes cycle through a working set above 256 MB.
+HBM residency: before every timed pass a 512 MiB buffer is read (a sum, no
+writes), which evicts the Infinity Cache and the L2s without leaving dirty
+lines, so the first N calls of a pass read their codes from HBM whatever K
+is; longer passes cycle through a working set above 256 MB.
 
-Printed: one JSON line.  ``value`` is microseconds per call (lower is
-better), measured with HIP events on the launch stream over the K timed
-back-to-back steps (it includes the GPU's gap between dependent launches).
+Printed: one JSON line (kept under 8 KB).  ``value`` is microseconds per call
+(lower is better), measured with HIP events on the launch stream over the K
+timed back-to-back steps, enqueued behind a bounded spin kernel (the gate) so
+the events time the GPU running them, not the host issuing them.
 ``roofline`` relates the algorithmic code bytes of one launch to the
-kernel's own average duration, measured live over another K steps with the
-library's start/stop events (hipExtLaunchKernelGGL, the kernel's begin and
-end on the launch stream); ``traffic`` is the HBM bytes per launch from the
-rocprofv3 FETCH_SIZE/WRITE_SIZE summary under profiles/ when present.
-``cpu_baseline`` times the reference's own C++ engine (compiled from its
-sources into oracle/_ref when present, else the repo's C restatement) on the
-host, one thread, on the same inputs.  Extra fields (each with its own
-timing, roofline fraction and CPU figure where the reference has one): the
-2560 -> 2560 linear, bf16 at batch 1 and the batched linear
-(configs[1]), the grouped launch (the sustained form), the MoE layer
-(configs[2]), the KV decode and the 4B-shaped decoder
-(configs[4]), plus a measured device-to-device copy rate and the host CPU.
+kernel's own average duration, measured live with the library's start/stop
+events (hipExtLaunchKernelGGL: the kernel's begin and end on the launch
+stream) over max(K, 200) launches that also run back to back behind a gate;
+``gate_held`` says the host had enqueued every launch before the gate ended.
+``traffic`` is the HBM bytes per launch from the rocprofv3
+FETCH_SIZE / WRITE_SIZE summaries committed under profiles/ (lines
+``traffic_bytes_per_launch[<leg>]: <bytes>``).  ``cpu_baseline`` times the
+reference's own C++ engine (compiled from its sources into oracle/_ref when
+present, else the repo's C restatement) on the host, one thread.
+
+Legs beside the headline (``legs``; each with its call time, its dominant
+kernel's roofline and traffic, and a CPU figure where the reference has one):
+the 2560 -> 2560 linear, bf16 at batch 1 and the batched linear
+(configs[1]), the grouped launch (the sustained form), the MoE layer per
+call and as a 16-layer graph, the KV decode and append
+(configs[3]), the streamed attention over int8 pages, the 4B-shaped decoder
+(configs[4]) and a measured device-to-device copy rate.
+
+Profiling switches (not used by the driver): ``--skip-headline`` runs only
+the legs named by ``--extra``; ``--gate-us`` sets the gate's hold per
+enqueued call (raise it under a profiler, whose launches cost more host time).
 """
 import argparse
 import ctypes
+import glob
 import json
 import os
 import re
@@ -46,21 +57,29 @@ HBM_PEAK_GBS = 8000.0
 M_GU, K_GU = 6912, 2560
 CAL_COPY_BYTES = 64 << 20
 FLUSH_BYTES = 512 << 20
+MIN_KERNEL_LAUNCHES = 200
 PROFILES = os.path.join(ROOT, "profiles")
-TRAFFIC_SUMMARY = os.path.join(PROFILES, "lut_dec_kernel_2560x6912_b1_hbm_traffic.md")
-GROUP_TRAFFIC_SUMMARY = os.path.join(PROFILES, "lut_bank_kernel_160x2560x6912_hbm_traffic.md")
 VP = ctypes.c_void_p
+ALL_LEGS = ("copy,linear2560,bf16,batched,sustained,moe,moe_sustained,kv,kv_append,attn,"
+            "decoder")
 
 
-def measured_traffic(path=TRAFFIC_SUMMARY):
-    """HBM bytes per launch of the benchmarked kernel, from the committed
-    rocprofv3 PMC summary (None when absent)."""
-    try:
-        with open(path) as f:
-            m = re.search(r"traffic_bytes_per_launch:\s*(\d+)", f.read())
-        return int(m.group(1)) if m else None
-    except OSError:
-        return None
+def profile_traffic():
+    """{leg key: HBM bytes per launch} from every committed rocprofv3 PMC
+    summary under profiles/ (lines ``traffic_bytes_per_launch[key]: N``)."""
+    out = {}
+    for path in sorted(glob.glob(os.path.join(PROFILES, "*.md"))):
+        try:
+            with open(path) as f:
+                for key, val in re.findall(r"traffic_bytes_per_launch\[([\w.-]+)\]:\s*(\d+)",
+                                           f.read()):
+                    out[key] = int(val)
+        except OSError:
+            pass
+    return out
+
+
+TRAFFIC = profile_traffic()
 
 
 def host_info():
@@ -98,10 +117,15 @@ def timed_cpu(call, seconds, max_calls, warm=3):
             return el / n, n
 
 
-class Bench:
-    """Device, stream, library and the cache flush shared by every leg."""
+def short(name):
+    """Kernel name as recorded by the library, without a long template list."""
+    return name if len(name) <= 26 else name.split("<")[0]
 
-    def __init__(self, torch, pkg):
+
+class Bench:
+    """Device, stream, library, the cache flush and the gate shared by every leg."""
+
+    def __init__(self, torch, pkg, gate_us):
         self.torch = torch
         self.pkg = pkg
         self.L = pkg.lib()
@@ -109,65 +133,109 @@ class Bench:
         self.stream = torch.cuda.current_stream()
         self.sp = VP(self.stream.cuda_stream)
         self.fbuf = torch.zeros(FLUSH_BYTES // 4, device=self.dev)
+        self.gate_us = gate_us
 
     def flush(self):
         """Read 512 MiB (a sum): evicts the Infinity Cache and every L2 without
         leaving dirty lines, whose write-back would otherwise land in the timed
-        calls (0.3-0.4 µs per call over a 20-call headline pass)."""
+        calls (0.3-0.4 us per call over a 20-call headline pass)."""
         self.fbuf.sum()
         self.torch.cuda.synchronize()
 
-    def gate(self, n):
-        """Hold the stream with a bounded spin kernel (about 15 µs per call to
-        come) while the host enqueues the timed calls, so the timed region
-        measures the GPU running them back to back, not the host issuing the
-        first ones."""
-        if hasattr(self.torch.cuda, "_sleep"):
-            self.torch.cuda._sleep(int(min(n * 15, 200000) * 2400))
+    def gate(self, n, per_call_us):
+        """Hold the stream with a bounded spin kernel (per_call_us for each of
+        the n calls to come, at least 50 ms, at most 0.2 s) while the host
+        enqueues the timed calls.  Returns an event recorded behind it: still
+        pending once the calls are enqueued means the gate held."""
+        torch = self.torch
+        torch.cuda._sleep(int(min(max(n * per_call_us, 50000), 200000) * 2400))
+        ev = torch.cuda.Event()
+        ev.record(self.stream)
+        return ev
 
-    def events_us(self, fn, n):
-        """Average µs per call of fn(i), i < n, from HIP events on the launch
-        stream, after a flush, the calls enqueued behind a gate."""
+    def events_us(self, fn, n, gate=True):
+        """Average us per call of fn(i), i < n, from HIP events on the launch
+        stream, after a flush, the calls enqueued behind a gate.  Returns
+        (us, gate held)."""
         torch = self.torch
         self.flush()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        self.gate(n)
+        g = self.gate(n, self.gate_us) if gate else None
         e0.record(self.stream)
         for i in range(n):
             fn(i)
         e1.record(self.stream)
+        held = (not g.query()) if g is not None else None
         torch.cuda.synchronize()
-        return e0.elapsed_time(e1) * 1e3 / n
+        return e0.elapsed_time(e1) * 1e3 / n, held
 
-    def kernels(self, fn, n):
-        """{kernel: {"calls", "avg_us"}} of fn(i), i < n, from the library's
-        start/stop events, after a flush."""
-        self.flush()
+    def kernels(self, fn, n, gate=True):
+        """({kernel: {"calls", "avg_us"}}, gate held) of fn(i) over
+        max(n, 200) calls from the library's start/stop events, after a flush,
+        enqueued behind a gate so the kernels run back to back as in the
+        events pass.  A first untimed pass sizes the library's event pool."""
+        n = max(n, MIN_KERNEL_LAUNCHES)
         lib = self.pkg._lib
         lib.kernel_timing_enable(True)
         try:
             for i in range(n):
                 fn(i)
+            lib.kernel_timing_report()
+            self.flush()
+            lib.kernel_timing_enable(True)
+            g = self.gate(n, self.gate_us * 6) if gate else None
+            for i in range(n):
+                fn(i)
+            held = (not g.query()) if g is not None else None
             rep = lib.kernel_timing_report()
         finally:
             lib.kernel_timing_enable(False)
         rep.pop("_dropped", None)
-        return rep
+        return rep, held
+
+
+def frac(nbytes, us):
+    return round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 5)
 
 
 def roofline(code_bytes, all_bytes, kernel_us, kernel, calls, traffic=None):
+    """The contract's roofline object for the headline kernel."""
     ach = code_bytes / (kernel_us * 1e-6) / 1e9
     return {"bound": "hbm", "achieved": round(ach, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(ach / HBM_PEAK_GBS, 5), "traffic": traffic, "kernel": kernel,
+            "frac": round(ach / HBM_PEAK_GBS, 5), "traffic": traffic, "kernel": short(kernel),
             "kernel_avg_us": round(kernel_us, 4), "kernel_launches_timed": calls,
             "algorithmic_bytes_per_launch": int(code_bytes),
             "all_compulsory_bytes_per_launch": int(all_bytes),
-            "achieved_all_bytes_GBs": round(all_bytes / (kernel_us * 1e-6) / 1e9, 2),
-            "frac_all_bytes": round(all_bytes / (kernel_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 5)}
+            "frac_all_bytes": frac(all_bytes, kernel_us)}
+
+
+def leg(us, kern, name, code_bytes, all_bytes, key, held=None, per_call=1):
+    """Compact record of one leg: call period, the dominant kernel's average
+    (``kus``, over ``n`` launches), its fractions of 8 TB/s on code bytes and
+    on all compulsory bytes per launch, and its measured traffic per launch.
+    ``per_call`` is the dominant kernel's launches per call."""
+    kus = kern[name]["avg_us"]
+    out = {"us": round(us, 3), "kernel": short(name), "kus": round(kus, 3),
+           "n": kern[name]["calls"], "code_B": int(code_bytes), "frac": frac(code_bytes, kus),
+           "frac_all": frac(all_bytes, kus), "traffic": TRAFFIC.get(key)}
+    if per_call != 1:
+        out["per_call"] = per_call
+    if held is False:
+        out["gate_held"] = False
+    return out
+
+
+def sizes(args, default):
+    """The sizes a leg runs: its defaults, or --sizes (profiling runs)."""
+    return tuple(int(v) for v in args.sizes.split(",")) if args.sizes else default
 
 
 def dominant(kern):
     return max(kern, key=lambda k: kern[k]["calls"] * kern[k]["avg_us"])
+
+
+def per_call_us(kern, calls):
+    return {short(k): round(v["avg_us"] * v["calls"] / calls, 3) for k, v in kern.items()}
 
 
 def parse():
@@ -180,8 +248,14 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true",
                     help="skip every extra figure (headline only)")
-    ap.add_argument("--extra", default="copy,linear2560,bf16,batched,sustained,moe,kv,attn,decoder",
-                    help="comma-separated extra figures to run")
+    ap.add_argument("--extra", default=ALL_LEGS, help="comma-separated legs to run")
+    ap.add_argument("--skip-headline", action="store_true",
+                    help="profiling runs only: run just the legs named by --extra")
+    ap.add_argument("--gate-us", type=float, default=15.0,
+                    help="gate hold per enqueued call, us (raise it under a profiler)")
+    ap.add_argument("--sizes", default=None,
+                    help="profiling runs only: the batch / token counts of the batched, MoE, "
+                         "KV and append legs to run (comma-separated), instead of their defaults")
     return ap.parse_args()
 
 
@@ -210,7 +284,7 @@ def make_instances(b, M, K, n, seed):
 
 def cpu_linear(base, B, seconds, y_gpu=None, threads=(1,)):
     """Reference C++ engine (or the C restatement) on the host for one call of
-    B tokens: µs per call per thread count; its output on instance 0 is the
+    B tokens: us per call per thread count; its output on instance 0 is the
     parity check of the GPU result (max |GPU - CPU| / max |CPU|)."""
     from oracle import ref, cpu
     x = base["x"][:B]
@@ -223,21 +297,21 @@ def cpu_linear(base, B, seconds, y_gpu=None, threads=(1,)):
                                                     base["scales"], None, *base["csr"]))
         kind = "port"
         threads = (1,)
-    out = {"kind": kind, "unit": "us/call", "batch": B}
+    out = {"kind": kind, "batch": B}
     if y_gpu is not None:
         y_cpu = np.asarray(mk(1)(), np.float64).reshape(-1)
-        out["parity_rel_err"] = float(np.abs(np.asarray(y_gpu, np.float64).reshape(-1) - y_cpu).max()
-                                      / np.abs(y_cpu).max())
+        out["rel_err"] = float("%.3g" % (np.abs(np.asarray(y_gpu, np.float64).reshape(-1) - y_cpu)
+                                         .max() / np.abs(y_cpu).max()))
     for nt in threads:
         s, n = timed_cpu(mk(nt), seconds, 1000)
-        out[f"us_{nt}t"] = round(s * 1e6, 2)
+        out[f"us_{nt}t"] = round(s * 1e6, 1)
         out[f"calls_{nt}t"] = n
     return out
 
 
-def linear_leg(b, hs, base, wbytes, M, K, B, dt, steps, warmup):
-    """µs per call (events) and kernel roofline of ``B``-token calls over the
-    instances in round robin (flushed before each pass)."""
+def linear_leg(b, hs, base, wbytes, M, K, B, dt, steps, warmup, key):
+    """us per call (events) and the kernel roofline of ``B``-token calls over
+    the instances in round robin (flushed before each pass)."""
     torch, L = b.torch, b.L
     n = len(hs)
     x = torch.from_numpy(base["x"][:B]).to(b.dev)
@@ -250,17 +324,13 @@ def linear_leg(b, hs, base, wbytes, M, K, B, dt, steps, warmup):
     for i in range(max(warmup, n)):   # every instance once: workspaces sized outside the timing
         call(i)
     torch.cuda.synchronize()
-    us = b.events_us(call, steps)
-    kern = b.kernels(call, steps)
+    us, held = b.events_us(call, steps)
+    kern, kheld = b.kernels(call, steps)
     name = dominant(kern)
     code_bytes = M * (K // 16)
     all_bytes = wbytes + B * K * x.element_size() + B * M * x.element_size()
-    out = {"us_per_call": round(us, 4), "us_per_token": round(us / B, 4), "instances": n,
-           "working_set_MB": round(n * wbytes / 2**20, 1),
-           "timed_pass_bytes_touched_MB": round(min(steps, n) * wbytes / 2**20, 1),
-           "roofline": roofline(code_bytes, all_bytes, kern[name]["avg_us"], name,
-                                kern[name]["calls"])}
-    out["useful_TFLOPs"] = round(2.0 * M * K * B / (kern[name]["avg_us"] * 1e-6) / 1e12, 3)
+    out = leg(us, kern, name, code_bytes, all_bytes, key, held and kheld)
+    out["TFLOPs"] = round(2.0 * M * K * B / (kern[name]["avg_us"] * 1e-6) / 1e12, 2)
     assert L.ojasx_linear_forward_device(hs[0], xp, yp, B, dt, b.sp) == 0
     torch.cuda.synchronize()
     return out, y.float().cpu().numpy()
@@ -280,8 +350,8 @@ def host_pointer_call(b, handles, base, n=200):
     for i in range(n):
         L.ojasx_linear_forward(handles[i % len(handles)], px, py, 1, 1)
     us = (time.perf_counter() - t0) / n * 1e6
-    return {"us_per_call": round(us, 2), "calls": n,
-            "code_GBs": round(M_GU * (K_GU // 16) / (us * 1e-6) / 1e9, 2)}
+    return {"us": round(us, 2), "calls": n,
+            "code_GBs": round(M_GU * (K_GU // 16) / (us * 1e-6) / 1e9, 1)}
 
 
 def bench_linear2560(b, args):
@@ -289,11 +359,13 @@ def bench_linear2560(b, args):
     CSR, over 400 instances (268 MB), with the reference engine's CPU time."""
     M = K = 2560
     hs, base, wbytes = make_instances(b, M, K, 400, 2040)
+    n = max(MIN_KERNEL_LAUNCHES, min(args.steps, 400))
     try:
-        res, y0 = linear_leg(b, hs, base, wbytes, M, K, 1, 0, args.steps, args.warmup)
+        res, y0 = linear_leg(b, hs, base, wbytes, M, K, 1, 0, n, args.warmup, "linear2560")
         if not args.no_cpu:
-            res["cpu_baseline"] = cpu_linear(base, 1, min(2.0, args.cpu_seconds), y0,
-                                             threads=(1, cpu_threads()))
+            c = cpu_linear(base, 1, min(2.0, args.cpu_seconds), y0, threads=(1, cpu_threads()))
+            res["cpu"] = {"us": c["us_1t"], "cores": 1, "kind": c["kind"], "rel_err": c["rel_err"],
+                          f"us_{cpu_threads()}t": c.get(f"us_{cpu_threads()}t")}
     finally:
         for h in hs:
             b.L.ojasx_destroy_linear(h)
@@ -303,7 +375,9 @@ def bench_linear2560(b, args):
 def bench_sustained(b, handles, base, wbytes):
     """The same LUT-GEMV on all N weight instances in one grouped launch
     (ojasx_linear_forward_grouped_device): the sustained rate over a working
-    set above the Infinity Cache."""
+    set above the Infinity Cache.  Each launch is a whole pass over the 262 MB
+    of instances, so the count only sets how steady the average is: 200
+    launches whatever --steps is."""
     torch, L = b.torch, b.L
     n = len(handles)
     x = torch.from_numpy(base["x"][:1]).to(b.dev)
@@ -315,19 +389,16 @@ def bench_sustained(b, handles, base, wbytes):
     for _ in range(3):
         assert call(0) == 0, L.ojasx_get_last_error()
     torch.cuda.synchronize()
-    # each launch is a whole pass over the 262 MB of instances, so the count
-    # only sets how steady the average is: 100 launches whatever --steps is
-    reps = 100
-    us = b.events_us(call, reps)
-    kern = b.kernels(call, reps)
+    reps = MIN_KERNEL_LAUNCHES
+    us, held = b.events_us(call, reps)
+    kern, kheld = b.kernels(call, reps)
     kname = dominant(kern)
-    kus = kern[kname]["avg_us"]
-    code_bytes = M_GU * (K_GU // 16)
-    all_bytes = wbytes + K_GU * 4 + M_GU * 4
-    rf = roofline(n * code_bytes, n * all_bytes, kus, kname, kern[kname]["calls"],
-                  measured_traffic(GROUP_TRAFFIC_SUMMARY) if n == 160 else None)
-    return {"instances": n, "us_per_launch": round(us, 3), "us_per_linear": round(kus / n, 4),
-            "roofline": rf}
+    code_bytes = n * M_GU * (K_GU // 16)
+    all_bytes = n * (wbytes + K_GU * 4 + M_GU * 4)
+    out = leg(us, kern, kname, code_bytes, all_bytes, "sustained" if n == 160 else None,
+              held and kheld)
+    out.update({"instances": n, "us_per_linear": round(kern[kname]["avg_us"] / n, 4)})
+    return out
 
 
 def bench_batched(b, handles, base, wbytes, args):
@@ -337,48 +408,132 @@ def bench_batched(b, handles, base, wbytes, args):
     (lut_mm_kernel), below that the in-place LUT kernel (lut_dec_kernel).
     CPU: the reference engine at 8 and 64 tokens (it loops tokens)."""
     res = {}
-    n = max(50, min(args.steps, 400))
+    n = max(MIN_KERNEL_LAUNCHES, min(args.steps, 400))
     y8 = {}
     for dt, tag in ((0, "fp32"), (1, "bf16")):
-        for B in (8, 16, 32, 64):
-            r, y0 = linear_leg(b, handles, base, wbytes, M_GU, K_GU, B, dt, n, min(args.warmup, 20))
+        for B in sizes(args, (8, 16, 32, 64)):
+            r, y0 = linear_leg(b, handles, base, wbytes, M_GU, K_GU, B, dt, n,
+                               min(args.warmup, 20), f"{tag}_B{B}")
             res[f"{tag}_B{B}"] = r
             if dt == 0:
                 y8[B] = y0
     if not args.no_cpu:
-        for B in (8, 64):
-            res[f"cpu_baseline_fp32_B{B}"] = cpu_linear(base, B, min(1.5, args.cpu_seconds),
-                                                        y8[B], threads=(1, cpu_threads()))
+        for B in (B for B in (8, 64) if B in y8):
+            c = cpu_linear(base, B, min(1.5, args.cpu_seconds), y8[B], threads=(1,))
+            res[f"fp32_B{B}"]["cpu"] = {"us": c["us_1t"], "cores": 1, "kind": c["kind"],
+                                        "rel_err": c["rel_err"]}
     return res
 
 
 # --- MoE ----------------------------------------------------------------------------
 
-def moe_sustained(b, banks, E, K, per_expert, T, n_layers=16, replays=5):
+E_MOE, H_MOE, I_MOE, K_MOE = 512, 2048, 768, 10
+GU_BYTES = 2 * I_MOE * (H_MOE // 16)      # gate/up code bytes per expert
+DN_BYTES = H_MOE * (I_MOE // 16)          # down code bytes per expert
+SC_BYTES = (2 * I_MOE + H_MOE) * 4        # scales per expert
+
+
+def moe_banks(b):
+    L = b.L
+    gen = b.pkg.synthetic
+    p = lambda a: a.ctypes.data_as(VP)
+    banks = []
+    for seed in (11, 12):
+        m = gen.moe(E=E_MOE, H=H_MOE, I=I_MOE, T=256, seed=seed)
+        h = L.ojasx_create_moe(E_MOE, H_MOE, I_MOE, K_MOE, 16, p(m["cb_in"]), p(m["cb_down"]),
+                               p(m["gu_codes"]), p(m["gu_scales"]), p(m["dn_codes"]),
+                               p(m["dn_scales"]))
+        assert h, L.ojasx_get_last_error()
+        banks.append((h, m))
+    return banks
+
+
+def moe_route(b, T, n, seed):
+    torch, L = b.torch, b.L
+    r = np.random.default_rng(seed)
+    logits = torch.from_numpy(r.normal(size=(n, T, E_MOE)).astype(np.float32)).to(b.dev)
+    idx = torch.empty(n, T, K_MOE, dtype=torch.int32, device=b.dev)
+    w = torch.empty(n, T, K_MOE, dtype=torch.float32, device=b.dev)
+    for i in range(n):
+        assert L.ojasx_moe_route_device(VP(logits[i].data_ptr()), T, E_MOE, K_MOE, 0,
+                                        VP(idx[i].data_ptr()), VP(w[i].data_ptr()), b.sp) == 0
+    torch.cuda.synchronize()
+    distinct = np.array([len(np.unique(a)) for a in idx.cpu().numpy().reshape(n, -1)])
+    return idx, w, distinct
+
+
+def moe_dominant_bytes(name, experts):
+    """Algorithmic code bytes per launch of an MoE kernel: the gate/up or down
+    codes of the distinct routed experts (the kernels reading codes)."""
+    if "SWIGLU" in name or "down" in name:
+        return experts * DN_BYTES
+    return experts * GU_BYTES
+
+
+def bench_moe(b, args):
+    """512-expert top-10 MoE layer (H 2048, I 768), T = 1 and 16 tokens.  Two
+    expert banks (2 x 151 MB, above the 256 MB Infinity Cache) alternate and
+    every step has its own routing (routed on the device); code bytes count
+    the distinct experts a call reads.  CPU: the reference engine, whose API
+    is one token per call (16 calls for T = 16)."""
+    from oracle import ref
+    torch, L = b.torch, b.L
+    banks = moe_banks(b)
+    res = {}
+    nsteps = max(MIN_KERNEL_LAUNCHES, min(args.steps, 400))
+    try:
+        for T in sizes(args, (1, 16)):
+            idx, w, distinct = moe_route(b, T, nsteps, T)
+            x = torch.from_numpy(banks[0][1]["x"][:T]).to(b.dev)
+            y = torch.empty(T, H_MOE, device=b.dev)
+            fwd = lambda i: L.ojasx_moe_forward_device(banks[i % 2][0], VP(x.data_ptr()),
+                                                       VP(idx[i].data_ptr()), VP(w[i].data_ptr()),
+                                                       VP(y.data_ptr()), T, K_MOE, 0, b.sp)
+            for i in range(min(args.warmup, nsteps)):
+                fwd(i)
+            torch.cuda.synchronize()
+            us, held = b.events_us(fwd, nsteps)
+            kern, kheld = b.kernels(fwd, nsteps)
+            U = float(distinct.mean())
+            name = dominant(kern)
+            code = U * (GU_BYTES + DN_BYTES)
+            kb = moe_dominant_bytes(name, U)
+            r = leg(us, kern, name, kb, kb + U * SC_BYTES / 2, f"moe_T{T}", held and kheld)
+            r.update({"experts": U, "code_B_call": int(code), "frac_call": frac(code, us),
+                      "kernels_us": per_call_us(kern, kern[name]["calls"])})
+            res[f"T{T}"] = r
+            if not args.no_cpu and ref.available():
+                m = banks[0][1]
+                R = ref.RefMoE(m["cb_in"], m["cb_down"], m["gu_codes"], m["gu_scales"],
+                               m["dn_codes"], m["dn_scales"])
+                ii = idx[0].cpu().numpy()
+                ww = w[0].cpu().numpy()
+                call = lambda: [R.forward(m["x"][t], ii[t], ww[t]) for t in range(T)]
+                s, n = timed_cpu(call, min(2.0, args.cpu_seconds), 100, warm=1)
+                r["cpu"] = {"us": round(s * 1e6, 1), "cores": 1, "kind": "reference",
+                            "sample": f"{n} calls x {T} token(s)"}
+    finally:
+        for h, _ in banks:
+            L.ojasx_destroy_moe(h)
+    return res
+
+
+def moe_sustained_one(b, banks, T, n_layers=16, replays=5):
     """n_layers MoE layers, each on the next of the two alternating expert
     banks with its own device routing, layer i's output the input of layer
     i + 1, captured as one HIP graph and replayed after a flush: the steady
     state of a deep MoE stack (302 MB of banks per pair of layers).  The
     replay's output is compared with an eager run of the same layers."""
     torch, L = b.torch, b.L
-    H = banks[0][1]["x"].shape[1]
-    r = np.random.default_rng(1000 + T)
-    logits = torch.from_numpy(r.normal(size=(n_layers, T, E)).astype(np.float32)).to(b.dev)
-    idx = torch.empty(n_layers, T, K, dtype=torch.int32, device=b.dev)
-    w = torch.empty(n_layers, T, K, dtype=torch.float32, device=b.dev)
-    for i in range(n_layers):
-        assert L.ojasx_moe_route_device(VP(logits[i].data_ptr()), T, E, K, 0, VP(idx[i].data_ptr()),
-                                        VP(w[i].data_ptr()), b.sp) == 0
-    torch.cuda.synchronize()
-    distinct = np.array([len(np.unique(a)) for a in idx.cpu().numpy().reshape(n_layers, -1)])
-    xs = [torch.zeros(T, H, device=b.dev) for _ in range(n_layers + 1)]
+    idx, w, distinct = moe_route(b, T, n_layers, 1000 + T)
+    xs = [torch.zeros(T, H_MOE, device=b.dev) for _ in range(n_layers + 1)]
     xs[0].copy_(torch.from_numpy(banks[0][1]["x"][:T]))
 
     def layers(sp):
         for i in range(n_layers):
             rc = L.ojasx_moe_forward_device(banks[i % 2][0], VP(xs[i].data_ptr()),
                                             VP(idx[i].data_ptr()), VP(w[i].data_ptr()),
-                                            VP(xs[i + 1].data_ptr()), T, K, 0, sp)
+                                            VP(xs[i + 1].data_ptr()), T, K_MOE, 0, sp)
             assert rc == 0, L.ojasx_get_last_error()
 
     layers(b.sp)                                     # eager: sizes every workspace
@@ -401,87 +556,30 @@ def moe_sustained(b, banks, E, K, per_expert, T, n_layers=16, replays=5):
     e1.record(b.stream)
     torch.cuda.synchronize()
     us = e0.elapsed_time(e1) * 1e3 / (replays * n_layers)
-    code = float(distinct.mean()) * per_expert
+    # the eager layers' kernels, timed back to back, for the per-kernel split
+    kern, held = b.kernels(lambda i: layers(b.sp) if i % n_layers == 0 else None,
+                           n_layers * 4, gate=True)
     del g
-    return {"us_per_layer": round(us, 3), "layers": n_layers, "replays": replays,
-            "distinct_experts_mean": float(distinct.mean()), "code_bytes_per_layer": int(code),
-            "achieved_code_GBs": round(code / (us * 1e-6) / 1e9, 2),
-            "frac_code": round(code / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 5),
-            "graph_equals_eager": same}
+    U = float(distinct.mean())
+    code = U * (GU_BYTES + DN_BYTES)
+    name = dominant(kern)
+    calls = kern[name]["calls"]
+    kb = moe_dominant_bytes(name, U)
+    return {"us": round(us, 3), "experts": U, "code_B": int(code), "frac_call": frac(code, us),
+            "kernel": short(name), "kus": round(kern[name]["avg_us"], 3), "n": calls,
+            "frac": frac(kb, kern[name]["avg_us"]), "traffic": TRAFFIC.get(f"moe_sus_T{T}"),
+            "kernels_us": per_call_us(kern, calls), "graph_equals_eager": same}
 
 
-def bench_moe(b, args):
-    """512-expert top-10 MoE layer (H 2048, I 768), T = 1 and 16 tokens.  Two
-    expert banks (2 x 151 MB, above the 256 MB Infinity Cache) alternate and
-    every step has its own routing (routed on the device); code bytes count
-    the distinct experts a call reads.  CPU: the reference engine, whose API
-    is one token per call (16 calls for T = 16).  "sustained": 16 layers of
-    T = 16, 64 and 256 tokens in one HIP graph."""
-    from oracle import ref
-    torch, L = b.torch, b.L
-    gen = b.pkg.synthetic
-    p = lambda a: a.ctypes.data_as(VP)
-    E, H, I, K = 512, 2048, 768, 10
-    banks = []
-    for seed in (11, 12):
-        m = gen.moe(E=E, H=H, I=I, T=256, seed=seed)
-        h = L.ojasx_create_moe(E, H, I, K, 16, p(m["cb_in"]), p(m["cb_down"]), p(m["gu_codes"]),
-                               p(m["gu_scales"]), p(m["dn_codes"]), p(m["dn_scales"]))
-        assert h, L.ojasx_get_last_error()
-        banks.append((h, m))
-    res = {}
-    per_expert = 2 * I * (H // 16) + H * (I // 16)
-    per_expert_scales = (2 * I + H) * 4
-    nsteps = max(50, min(args.steps, 400))
+def bench_moe_sustained(b, args):
+    """16 layers of T = 16, 64 and 256 tokens in one HIP graph (see
+    moe_sustained_one)."""
+    banks = moe_banks(b)
     try:
-        for T in (1, 16):
-            r = np.random.default_rng(T)
-            logits = torch.from_numpy(r.normal(size=(nsteps, T, E)).astype(np.float32)).to(b.dev)
-            idx = torch.empty(nsteps, T, K, dtype=torch.int32, device=b.dev)
-            w = torch.empty(nsteps, T, K, dtype=torch.float32, device=b.dev)
-            for i in range(nsteps):
-                assert L.ojasx_moe_route_device(VP(logits[i].data_ptr()), T, E, K, 0,
-                                                VP(idx[i].data_ptr()), VP(w[i].data_ptr()),
-                                                b.sp) == 0
-            torch.cuda.synchronize()
-            distinct = np.array([len(np.unique(a))
-                                 for a in idx.cpu().numpy().reshape(nsteps, -1)])
-            x = torch.from_numpy(banks[0][1]["x"][:T]).to(b.dev)
-            y = torch.empty(T, H, device=b.dev)
-            fwd = lambda i: L.ojasx_moe_forward_device(banks[i % 2][0], VP(x.data_ptr()),
-                                                       VP(idx[i].data_ptr()), VP(w[i].data_ptr()),
-                                                       VP(y.data_ptr()), T, K, 0, b.sp)
-            for i in range(min(args.warmup, nsteps)):
-                fwd(i)
-            torch.cuda.synchronize()
-            us = b.events_us(fwd, nsteps)
-            kern = b.kernels(fwd, nsteps)
-            code_bytes = float(distinct.mean()) * per_expert
-            all_bytes = float(distinct.mean()) * (per_expert + per_expert_scales) + 2 * T * H * 4
-            res[f"T{T}"] = {"us_per_call": round(us, 3),
-                            "distinct_experts_mean": float(distinct.mean()),
-                            "code_bytes_per_call": int(code_bytes),
-                            "achieved_code_GBs": round(code_bytes / (us * 1e-6) / 1e9, 2),
-                            "frac_code": round(code_bytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 5),
-                            "achieved_all_bytes_GBs": round(all_bytes / (us * 1e-6) / 1e9, 2),
-                            "kernels_avg_us": {k: v["avg_us"] for k, v in kern.items()}}
-            if not args.no_cpu and ref.available():
-                m = banks[0][1]
-                R = ref.RefMoE(m["cb_in"], m["cb_down"], m["gu_codes"], m["gu_scales"],
-                               m["dn_codes"], m["dn_scales"])
-                ii = idx[0].cpu().numpy()
-                ww = w[0].cpu().numpy()
-                call = lambda: [R.forward(m["x"][t], ii[t], ww[t]) for t in range(T)]
-                s, n = timed_cpu(call, min(2.0, args.cpu_seconds), 100, warm=1)
-                res[f"T{T}"]["cpu_baseline"] = {
-                    "value": round(s * 1e6, 1), "unit": "us/call", "cores": 1, "kind": "reference",
-                    "sample": f"{n} calls of {T} token(s) (one reference call per token), 1 thread"}
-        res["sustained"] = {f"T{T}": moe_sustained(b, banks, E, K, per_expert, T)
-                            for T in (16, 64, 256)}
+        return {f"T{T}": moe_sustained_one(b, banks, T) for T in sizes(args, (16, 64, 256))}
     finally:
         for h, _ in banks:
-            L.ojasx_destroy_moe(h)
-    return res
+            b.L.ojasx_destroy_moe(h)
 
 
 # --- KV decode ----------------------------------------------------------------------
@@ -499,7 +597,7 @@ def bench_kv(b, args):
     res = {}
     Hkv, Hq, hd, P = 8, 32, 128, 16
     g = torch.Generator(device=b.dev).manual_seed(5)
-    for T in (2048, 32768):
+    for T in sizes(args, (2048, 32768)):
         pages = T // P
         per_layer = 2 * pages * Hkv * P * 8 + 2 * pages * Hkv * P * 4 + 2 * Hkv * 256 * 16 * 4
         layers = max(2, -(-(300 << 20) // per_layer))
@@ -523,45 +621,35 @@ def bench_kv(b, args):
         for i in range(min(args.warmup, 20)):
             call(i)
         torch.cuda.synchronize()
-        n = max(50, min(args.steps, 400))
-        us = b.events_us(call, n)
-        kern = b.kernels(call, n)
+        n = max(MIN_KERNEL_LAUNCHES, min(args.steps, 400))
+        us, held = b.events_us(call, n)
+        kern, kheld = b.kernels(call, n)
         code_bytes = 2 * T * Hkv * 8
         all_bytes = code_bytes + 2 * T * Hkv * 4 + 2 * Hkv * 256 * 16 * 4
         name = dominant(kern)
-        res[f"T{T}"] = {"us_per_call": round(us, 3), "layers_rotated": layers,
-                        "working_set_MB": round(layers * per_layer / 2**20, 1),
-                        "code_bytes": code_bytes, "all_compulsory_bytes": all_bytes,
-                        "achieved_code_GBs": round(code_bytes / (us * 1e-6) / 1e9, 2),
-                        "achieved_all_GBs": round(all_bytes / (us * 1e-6) / 1e9, 2),
-                        "frac_all_bytes_per_call": round(all_bytes / (us * 1e-6) / 1e9
-                                                         / HBM_PEAK_GBS, 5),
-                        "kernels_avg_us": {k: v["avg_us"] for k, v in kern.items()},
-                        "dominant_kernel_roofline": roofline(
-                            code_bytes, all_bytes, kern[name]["avg_us"], name,
-                            kern[name]["calls"])}
+        r = leg(us, kern, name, code_bytes, all_bytes, f"kv_T{T}", held and kheld)
+        r.update({"layers_rotated": layers, "frac_all_call": frac(all_bytes, us),
+                  "kernels_us": per_call_us(kern, kern[name]["calls"])})
+        res[f"T{T}"] = r
         del kc, vc, ks, vs, kcb, vcb
         if not args.no_cpu and ref.available():
             R = ref.RefKV(Hkv, hd, T, 16)
-            r = np.random.default_rng(T)
-            kv = r.normal(size=(T, 2, Hkv, hd)).astype(np.float32)
+            rg = np.random.default_rng(T)
+            kv = rg.normal(size=(T, 2, Hkv, hd)).astype(np.float32)
             for t in range(T):
                 for h in range(Hkv):
                     R.append(h, kv[t, 0, h], kv[t, 1, h])
-            qh = r.normal(size=(Hq, hd)).astype(np.float32)
+            qh = rg.normal(size=(Hq, hd)).astype(np.float32)
             outh = np.zeros(hd, np.float32)
             pq = [qh[j].ctypes.data_as(VP) for j in range(Hq)]
             po = outh.ctypes.data_as(VP)
             RL = ref.lib()
             call_cpu = lambda: [RL.ojasx_kv_cache_attention(R.h, j // (Hq // Hkv), pq[j], po, -1.0)
                                 for j in range(Hq)]
-            s, n = timed_cpu(call_cpu, min(2.0, args.cpu_seconds), 1000)
-            res[f"T{T}"]["cpu_baseline"] = {
-                "value": round(s * 1e6, 1), "unit": "us/call", "cores": 1, "kind": "reference",
-                "sample": f"{n} decodes of 32 query heads over {T} tokens x 8 kv heads "
-                          "(reference scalar-quantised cache), 1 thread"}
+            s, m = timed_cpu(call_cpu, min(2.0, args.cpu_seconds), 1000)
+            r["cpu"] = {"us": round(s * 1e6, 1), "cores": 1, "kind": "reference",
+                        "sample": f"{m} decodes x 32 q heads"}
             del R
-    res["append"] = bench_kv_append(b, args)
     return res
 
 
@@ -571,8 +659,8 @@ def bench_attn_pages(b, args, T=32768, page=256, n_caches=4):
     one decode query, T tokens in pages of 256, fp64 state.  Calls rotate over
     n_caches caches (more than 256 MB) after a flush; each call is the whole
     Python face (init, update, merge, finalize and the report's max_logsumexp,
-    which synchronises).  CPU: the fp64 NumPy restatement of forward_stream
-    over the same cache's dequantised pages, 1 thread."""
+    which synchronises, so no gate).  CPU: the fp64 NumPy restatement of
+    forward_stream over the same cache's dequantised pages, 1 thread."""
     from oracle import numpy_oracle as no
     torch = b.torch
     lc = b.pkg.long_context
@@ -593,20 +681,15 @@ def bench_attn_pages(b, args, T=32768, page=256, n_caches=4):
         call(i)
     torch.cuda.synchronize()
     n = max(40, min(args.steps, 200))
-    us = b.events_us(call, n)
-    kern = b.kernels(call, n)
+    us, _ = b.events_us(call, n, gate=False)
+    kern, _ = b.kernels(call, n, gate=False)
     code = T * Hkv * 2 * D
     all_bytes = code + T * Hkv * 2 * 2
     tile = [k for k in kern if k.startswith("attn_tile_kernel")][0]
-    res = {"tokens": T, "page_size": page, "caches_rotated": n_caches,
-           "working_set_MB": round(n_caches * all_bytes / 2**20, 1),
-           "us_per_call": round(us, 3), "int8_bytes": code, "all_compulsory_bytes": all_bytes,
-           "achieved_all_GBs_per_call": round(all_bytes / (us * 1e-6) / 1e9, 2),
-           "kernels_avg_us": {k: v["avg_us"] for k, v in kern.items()},
-           "tile_kernel_roofline": roofline(code, all_bytes, kern[tile]["avg_us"], tile,
-                                            kern[tile]["calls"]),
-           "tile_kernel_fp64_TFLOPs": round(4 * T * Hq * D / (kern[tile]["avg_us"] * 1e-6)
-                                            / 1e12, 3)}
+    res = leg(us, kern, tile, code, all_bytes, "attn_tile")
+    res.update({"tokens": T, "page": page, "caches_rotated": n_caches,
+                "kernels_us": {short(k): round(v["avg_us"], 3) for k, v in kern.items()},
+                "fp64_TFLOPs": round(4 * T * Hq * D / (kern[tile]["avg_us"] * 1e-6) / 1e12, 2)})
     if not args.no_cpu:
         from threadpoolctl import threadpool_limits
         c = caches[0]
@@ -619,12 +702,10 @@ def bench_attn_pages(b, args, T=32768, page=256, n_caches=4):
                              min(10.0, args.cpu_seconds), 5, warm=1)
         want = no.block_attention_stream(qn, pages, False)[0]
         got = attn.forward_stream(q.double(), c)[0].cpu().numpy()
-        res["cpu_baseline"] = {"value": round(s * 1e6, 1), "unit": "us/call", "cores": 1,
-                               "kind": "port",
-                               "sample": f"{m} calls over the first cache's {T} tokens "
-                                         "(NumPy fp64 forward_stream over its dequantised pages)",
-                               "parity_rel_err_fp64_query": float(np.abs(got - want).max()
-                                                                  / np.abs(want).max())}
+        res["cpu"] = {"us": round(s * 1e6, 1), "cores": 1, "kind": "port",
+                      "sample": f"{m} calls, NumPy fp64 forward_stream",
+                      "rel_err_fp64": float("%.3g" % (np.abs(got - want).max()
+                                                      / np.abs(want).max()))}
     return res
 
 
@@ -644,8 +725,8 @@ def bench_kv_append(b, args, cpu_seconds=2.0):
     vs = torch.zeros_like(ks)
     cb = torch.from_numpy(r.normal(0, 30, size=(2, Hkv, 256, D)).astype(np.float32)).to(b.dev)
     res = {}
-    n = max(50, min(args.steps, 400))
-    for tokens in (1, 16):
+    n = max(MIN_KERNEL_LAUNCHES, min(args.steps, 400))
+    for tokens in sizes(args, (1, 16)):
         kv = torch.from_numpy(r.normal(size=(2, n, tokens, Hkv, hd)).astype(np.float32)).to(b.dev)
         slots = torch.arange(n * tokens, dtype=torch.int32, device=b.dev).view(n, tokens)
         for mode in ("codebook", "scalar"):
@@ -658,11 +739,13 @@ def bench_kv_append(b, args, cpu_seconds=2.0):
             for i in range(min(n, 20)):
                 call(i)
             torch.cuda.synchronize()
-            us = b.events_us(call, n)
-            kern = b.kernels(call, n)
-            res[f"{mode}_{tokens}tok"] = {
-                "us_per_call": round(us, 3), "us_per_token": round(us / tokens, 3),
-                "kernels_avg_us": {k: v["avg_us"] for k, v in kern.items()}}
+            us, held = b.events_us(call, n)
+            kern, kheld = b.kernels(lambda i: call(i % n), n)
+            name = dominant(kern)
+            in_bytes = 2 * tokens * Hkv * hd * 4
+            out_bytes = 2 * tokens * Hkv * (hd // D + 4)
+            res[f"{mode}_{tokens}tok"] = leg(us, kern, name, in_bytes, in_bytes + out_bytes,
+                                             f"kv_append_{mode}_{tokens}tok", held and kheld)
     if not args.no_cpu and ref.available():
         R = ref.lib()
         h = R.ojasx_create_kv_cache(Hkv, hd, 1 << 17, D)
@@ -673,9 +756,9 @@ def bench_kv_append(b, args, cpu_seconds=2.0):
             for head in range(Hkv):
                 R.ojasx_kv_cache_append(h, head, p(k[head]), p(k[head]))
             count += 1
-        res["cpu_reference_us_per_token"] = round((time.perf_counter() - t0) / count * 1e6, 3)
-        res["cpu_reference_sample"] = (f"{count} tokens x {Hkv} heads of ojasx_kv_cache_append, "
-                                       "1 thread (reference engine, scalar quantiser)")
+        res["cpu"] = {"us_per_token": round((time.perf_counter() - t0) / count * 1e6, 2),
+                      "cores": 1, "kind": "reference",
+                      "sample": f"{count} tokens x {Hkv} heads, scalar quantiser"}
         R.ojasx_destroy_kv_cache(h)
     return res
 
@@ -708,15 +791,10 @@ def bench_decoder(b, args, n_tokens=128, context=4096):
     from oracle import numpy_oracle as no
     decm = b.pkg.decoder
     cfg = decm.DecoderConfig(max_steps=n_tokens, max_context=context + n_tokens)
-    t0 = time.perf_counter()
     keep = not args.no_cpu
     d, weights = decm.synthetic_decoder(cfg, context=context, seed=3, device="cuda:0",
                                         keep_weights=keep)
-    t_build = time.perf_counter() - t0
-    res = {"config": "hidden 2560, 36 layers, 32 q / 8 kv heads, head_dim 128, MLP 9728, "
-                     f"vocab {cfg.vocab}, all linears LUT d=16/256 + 0.38% CSR, "
-                     f"{context}-token 8-bit code KV context, page 16",
-           "tokens": n_tokens, "build_s": round(t_build, 1)}
+    res = {"tokens": n_tokens, "context": context}
     runs = {}
     for mode, graph in (("graph", True), ("eager", False)):
         d.reset(context)
@@ -727,8 +805,8 @@ def bench_decoder(b, args, n_tokens=128, context=4096):
         toks = d.generate(1, n_tokens, use_graph=graph)
         el = time.perf_counter() - t0
         runs[mode] = toks
-        res[mode] = {"tokens_per_s": round(n_tokens / el, 2),
-                     "ms_per_token": round(el / n_tokens * 1e3, 4)}
+        res[f"ms_per_token_{mode}"] = round(el / n_tokens * 1e3, 4)
+    res["tokens_per_s"] = round(1e3 / res["ms_per_token_graph"], 1)
     res["graph_equals_eager"] = bool(np.array_equal(runs["graph"], runs["eager"]))
     d.reset(context)
     b.flush()
@@ -739,9 +817,10 @@ def bench_decoder(b, args, n_tokens=128, context=4096):
     finally:
         b.pkg._lib.kernel_timing_enable(False)
     kern.pop("_dropped", None)
-    res["kernels_per_token_us"] = {
-        k: round(v["avg_us"] * v["calls"] / 8, 2)
+    res["kernels_us_per_token"] = {
+        short(k): round(v["avg_us"] * v["calls"] / 8, 1)
         for k, v in sorted(kern.items(), key=lambda kv: -kv[1]["avg_us"] * kv[1]["calls"])}
+    res["launches_per_token"] = sum(v["calls"] for v in kern.values()) // 8
     qkv, o, gu, dn = 6144, 2560, 19456, 2560
     shapes = [(qkv, 2560), (o, 4096), (gu, 2560), (dn, 9728)]
     dens = 0.0038
@@ -752,22 +831,18 @@ def bench_decoder(b, args, n_tokens=128, context=4096):
     kv_bytes = 36 * 8 * (context + n_tokens // 2) * (2 * 8 + 2 * 4)
     code_bytes = 36 * per_layer_codes + lm_codes
     all_bytes = code_bytes + 36 * per_layer_csr + lm_csr + kv_bytes
-    ms = res["graph"]["ms_per_token"]
-    res.update({"code_bytes_per_token": code_bytes, "all_bytes_per_token": int(all_bytes),
-                "achieved_code_GBs": round(code_bytes / (ms * 1e-3) / 1e9, 2),
-                "achieved_all_GBs": round(all_bytes / (ms * 1e-3) / 1e9, 2),
-                "frac_all_bytes": round(all_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 5)})
+    ms = res["ms_per_token_graph"]
+    res.update({"code_B_token": code_bytes, "all_B_token": int(all_bytes),
+                "frac_code": frac(code_bytes, ms * 1e3), "frac_all": frac(all_bytes, ms * 1e3),
+                "traffic_per_token": TRAFFIC.get("decoder_token")})
     if keep:
         emb = weights["embedding"]
         caches = [d.read_kv(l, 0, context + 1) for l in range(cfg.layers)]
         t0 = time.perf_counter()
         no.decoder_step(emb[1], weights, cfg, context, caches, {}, linear=_CpuLinear)
         el = time.perf_counter() - t0
-        res["cpu_baseline"] = {"value": round(el * 1e3, 1), "unit": "ms/token", "cores": 1,
-                               "kind": "port",
-                               "sample": "one greedy token at 4096 context: every linear on the "
-                                         "C restatement of the reference engine (1 thread), "
-                                         "norms / RoPE / attention in NumPy fp64"}
+        res["cpu"] = {"ms_per_token": round(el * 1e3, 1), "cores": 1, "kind": "port",
+                      "sample": "one token: linears on the C restatement, rest NumPy fp64"}
     d.close()
     return res
 
@@ -790,31 +865,17 @@ def copy_peak(b):
     torch.cuda.synchronize()
     s = e0.elapsed_time(e1) * 1e-3 / 10
     del src, dst
-    return {"bytes_moved": 2 << 30, "GBs": round((2 << 30) / s / 1e9, 1),
-            "frac_of_8TBs": round((2 << 30) / s / 1e9 / HBM_PEAK_GBS, 4)}
+    return {"GBs": round((2 << 30) / s / 1e9, 1), "frac": round((2 << 30) / s / 1e9 / HBM_PEAK_GBS, 4)}
 
 
-def main():
-    args = parse()
-    if args.gpus != 1:
-        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported "
-              "(the path would shard by output rows / experts / kv heads, see DESIGN.md)",
-              file=sys.stderr)
-        sys.exit(2)
-    import torch
-    import __graft_entry__
-
-    pkg = __graft_entry__.load_package()
-    dev = torch.device("cuda:0")
-    torch.cuda.set_device(dev)
-    b = Bench(torch, pkg)
-    L = b.L
-
-    # --- headline: N distinct 2560 -> 6912 instances, shared x --------------------
-    handles, base, wbytes = make_instances(b, M_GU, K_GU, args.instances, 2026)
+def headline(b, args, handles, base, wbytes):
+    """The headline: K back-to-back calls of the 2560 -> 6912 B = 1 fp32
+    LUT-GEMV over the instances, with the kernel's roofline and the CPU
+    baseline."""
+    torch, L = b.torch, b.L
     n = len(handles)
-    x = torch.from_numpy(base["x"][:1]).to(dev)
-    y = torch.empty(1, M_GU, device=dev)
+    x = torch.from_numpy(base["x"][:1]).to(b.dev)
+    y = torch.empty(1, M_GU, device=b.dev)
     xp, yp = VP(x.data_ptr()), VP(y.data_ptr())
     fwd = L.ojasx_linear_forward_device
     call = lambda i: fwd(handles[i % n], xp, yp, 1, 0, b.sp)
@@ -822,26 +883,20 @@ def main():
     torch.cuda.synchronize()
     y_bench = y.cpu().numpy()
 
-    # PMC calibration: one device-to-device copy of known size (read and write)
-    cal_src = torch.ones(CAL_COPY_BYTES // 4, device=dev)
-    cal_dst = torch.empty_like(cal_src)
-    cal_dst.copy_(cal_src)
-    torch.cuda.synchronize()
-    del cal_src, cal_dst
-
     for i in range(args.warmup):
         call(i)
     torch.cuda.synchronize()
     t_wall = time.perf_counter()
-    us_call = b.events_us(call, args.steps)
+    us_call, held = b.events_us(call, args.steps)
     t_wall = time.perf_counter() - t_wall
     code_bytes = M_GU * (K_GU // 16)
     all_bytes = wbytes + K_GU * 4 + M_GU * 4
-    kern = b.kernels(call, args.steps)
+    kern, kheld = b.kernels(call, args.steps)
     kname = dominant(kern)
     rf = roofline(code_bytes, all_bytes, kern[kname]["avg_us"], kname, kern[kname]["calls"],
-                  measured_traffic())
-    rf["call_period_GBs"] = round(code_bytes / (us_call * 1e-6) / 1e9, 2)
+                  TRAFFIC.get("headline"))
+    rf["call_period_frac"] = frac(code_bytes, us_call)
+    rf["gate_held"] = bool(held and kheld)
 
     out = {
         "metric": "LUT-GEMV 2560->6912 us/call (HBM GB/s on code bytes alongside)",
@@ -859,13 +914,9 @@ def main():
         "config": {"workload": "LUT-GEMV 2560->6912 gate/up, B=1, fp32, d=16/256 centroids, "
                                "0.38% CSR outliers", "batch": 1, "in_features": K_GU,
                    "out_features": M_GU, "weight_instances": n,
-                   "working_set_MB": round(n * wbytes / 2**20, 1),
-                   "timed_pass_bytes_touched_MB": round(min(args.steps, n) * wbytes / 2**20, 1),
-                   "cache_flush_before_each_pass_MiB": FLUSH_BYTES >> 20},
+                   "working_set_MB": round(n * wbytes / 2**20, 1)},
         "roofline": rf,
-        "pmc_calibration_copy_bytes": CAL_COPY_BYTES,
         "wall_s_timed": round(t_wall, 3),
-        "host": host_info(),
         "host_pointer_call": host_pointer_call(b, handles, base),
     }
     if not args.no_cpu:
@@ -874,7 +925,7 @@ def main():
                                "kind": c["kind"],
                                "sample": f"{c['calls_1t']} calls of LUT-GEMV 2560->6912 B=1 fp32 "
                                          "with CSR, 1 thread, after 3 warm-up calls",
-                               "parity_rel_err": c["parity_rel_err"]}
+                               "rel_err": c["rel_err"]}
         if c["kind"] == "reference":
             from oracle import ref
             var = {}
@@ -886,33 +937,71 @@ def main():
                 for nt in sorted({1, cpu_threads()}):
                     s, _ = timed_cpu(lambda: R.forward(base["x"][:1], nt),
                                      min(2.0, args.cpu_seconds), 1000)
-                    var[f"{tag}_{nt}t"] = round(s * 1e6, 2)
-            out["cpu_baseline"]["variants_us_per_call"] = var
+                    var[f"{tag}_{nt}t"] = round(s * 1e6, 1)
+            out["cpu_baseline"]["variants_us"] = var
+    out["host"] = host_info()
+    return out
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported "
+              "(the path would shard by output rows / experts / kv heads, see DESIGN.md)",
+              file=sys.stderr)
+        sys.exit(2)
+    import torch
+    import __graft_entry__
+
+    pkg = __graft_entry__.load_package()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    b = Bench(torch, pkg, args.gate_us)
+    L = b.L
     extra = set() if args.no_extra else set(args.extra.split(","))
+
+    # PMC calibration: one device-to-device copy of known size (read and write)
+    cal_src = torch.ones(CAL_COPY_BYTES // 4, device=dev)
+    cal_dst = torch.empty_like(cal_src)
+    cal_dst.copy_(cal_src)
+    torch.cuda.synchronize()
+    del cal_src, cal_dst
+
+    out = {}
+    legs = {}
+    handles, base, wbytes = make_instances(b, M_GU, K_GU, args.instances, 2026)
     try:
+        if not args.skip_headline:
+            out = headline(b, args, handles, base, wbytes)
         if "copy" in extra:
-            out["hbm_copy_peak"] = copy_peak(b)
+            legs["hbm_copy"] = copy_peak(b)
         if "bf16" in extra:
-            out["lut_gemv_bf16_b1"], _ = linear_leg(b, handles, base, wbytes, M_GU, K_GU, 1, 1,
-                                                    args.steps, args.warmup)
+            legs["bf16_b1"], _ = linear_leg(b, handles, base, wbytes, M_GU, K_GU, 1, 1,
+                                            max(MIN_KERNEL_LAUNCHES, args.steps), args.warmup,
+                                            "bf16_b1")
         if "sustained" in extra:
-            out["sustained"] = bench_sustained(b, handles, base, wbytes)
+            legs["sustained"] = bench_sustained(b, handles, base, wbytes)
         if "batched" in extra:
-            out["lut_gemv_batched"] = bench_batched(b, handles, base, wbytes, args)
+            legs["batched"] = bench_batched(b, handles, base, wbytes, args)
     finally:
         for h in handles:
             L.ojasx_destroy_linear(h)
     if "linear2560" in extra:
-        out["lut_linear_2560x2560_b1"] = bench_linear2560(b, args)
+        legs["linear2560_b1"] = bench_linear2560(b, args)
     if "moe" in extra:
-        out["moe_512x_top10"] = bench_moe(b, args)
+        legs["moe"] = bench_moe(b, args)
+    if "moe_sustained" in extra:
+        legs["moe_graph16"] = bench_moe_sustained(b, args)
     if "kv" in extra:
-        out["kv_decode_gqa4"] = bench_kv(b, args)
+        legs["kv_decode"] = bench_kv(b, args)
+    if "kv_append" in extra:
+        legs["kv_append"] = bench_kv_append(b, args)
     if "attn" in extra:
-        out["attn_stream_int8_pages"] = bench_attn_pages(b, args)
+        legs["attn_stream"] = bench_attn_pages(b, args)
     if "decoder" in extra:
-        out["decoder_4b_shaped"] = bench_decoder(b, args)
-    print(json.dumps(out))
+        legs["decoder"] = bench_decoder(b, args)
+    out["legs"] = legs
+    print(json.dumps(out, separators=(",", ":")))
 
 
 if __name__ == "__main__":
