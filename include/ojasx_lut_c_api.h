@@ -172,11 +172,17 @@ OJASX_API int ojasx_kv_decode_paged_device(const float *q, const uint8_t *k_code
  * serving loops, harnesses that forbid hipMalloc).  Same arguments, kernels
  * and results; the decode partials live in a fixed library scratch of
  * 4 MiB + 64 KiB per GPU (held until the process ends) instead of a growable
- * workspace, so num_q_heads x chunks (chunks = ceil(seq_len / 64) up to 4096
- * tokens, at most 256 beyond) is limited to 4 MiB / (head_dim * 4 bytes):
- * 8192 at head_dim 128.  Larger calls return OJASX_ERR_INVALID with a
- * message.  All calls on one GPU share the scratch: calls that overlap in
- * time on one GPU (other streams, other host threads) race. */
+ * workspace: partial outputs (num_q_heads x chunks x head_dim fp32) in the
+ * 4 MiB, partial maxima and sums (num_q_heads x chunks x 2 fp32) in the
+ * 64 KiB, so num_q_heads x chunks <= min(4 MiB / (head_dim * 4), 8192):
+ * 8192 at head_dim 128 and at 64.  Chunks per call: the GQA-4, head_dim 128,
+ * block_dim 16 path takes ceil(seq_len / 64) up to 4096 tokens, then
+ * ceil(seq_len / C) with C = 64 .. 1024 tokens (about one workgroup per CU;
+ * 1024 from 65536 tokens at 8 kv heads); other shapes take
+ * ceil(seq_len / 256).  A single chunk needs no scratch.  Larger calls return
+ * OJASX_ERR_INVALID with a message.  All calls on one GPU share the scratch:
+ * calls that overlap in time on one GPU (other streams, other host threads)
+ * race. */
 OJASX_API int ojasx_kv_decode_paged_device_noalloc(const float *q, const uint8_t *k_codes,
                                                    const float *k_scales, const uint8_t *v_codes,
                                                    const float *v_scales, const float *k_cb,
@@ -206,17 +212,18 @@ OJASX_API int ojasx_kv_encode_append_device(const float *k, const float *v, int 
                                             uint8_t *v_codes, float *v_scales, void *stream);
 
 /* PagedCompressedKVCache._quantize_int8 (ojasx_24x96/long_context.py:234-240)
- * on device: rows of dim elements of x (dtype F32, BF16 or F16), row r of
+ * on device: rows of dim elements of x (dtype F32, BF16, F16 or F64), row r of
  * group g at x + g*x_group_stride + r*dim (elements), int8 codes to
  * q + g*q_group_stride + r*dim and the fp16 scale to scale + g*scale_group_stride + r.
  * Arithmetic as torch on a tensor of x's dtype: s = T(max(max|x|, T(1e-8)) / 127),
- * q = clamp(round_half_even(T(x / s)), -127, 127). */
+ * q = clamp(round_half_even(T(x / s)), -127, 127); an F64 scale is stored as
+ * torch casts float64 to float16 (through float32). */
 OJASX_API int ojasx_quantize_int8_device(const void *x, long groups, int rows, int dim,
                                          long x_group_stride, int dtype, int8_t *q,
                                          long q_group_stride, void *scale_f16,
                                          long scale_group_stride, void *stream);
 /* long_context.py:242-244 _dequantize_int8: out[g][r][d] = dtype(float(q) * float(s))
- * into a contiguous [groups][rows][dim] out (F32, BF16 or F16); q and scale
+ * into a contiguous [groups][rows][dim] out (F32, BF16, F16 or F64); q and scale
  * addressed as in ojasx_quantize_int8_device. */
 OJASX_API int ojasx_dequantize_int8_device(const int8_t *q, const void *scale_f16, long groups,
                                            int rows, int dim, long q_group_stride,

@@ -131,6 +131,9 @@ int linear_items(const void *h, GroupItem *it);
 constexpr int kBankRows = 512;
 int launch_bank(const GroupItem *items_dev, const int2 *work_dev, int n_work, int max_K,
                 hipStream_t st);
+// Whether the bank kernels' LDS (64 KB of LUT plus the staged input pieces of
+// K / 16 groups) fits a workgroup for input length K: K <= 16384.
+bool bank_fits(int K);
 // Bank layout of [M][G] codes: [row block of 64 rows][group][64 rows], 0 past M.
 void pack_bank_codes(const uint8_t *codes, int M, int G, uint8_t *out);
 inline size_t bank_codes_bytes(int M, int G) { return (size_t)((M + 63) / 64) * G * 64; }
@@ -174,6 +177,8 @@ struct MmParams {
     int K, M, Mp, S, B;
 };
 int launch_mm(const MmParams &p, int dtype, hipStream_t st);
+// One linear handle's forward of B tokens (dtype F32 or BF16) on st.
+int linear_forward(void *h, const void *x, void *y, int B, int dtype, hipStream_t st);
 int linear_forward_fused(void *h, const float *x, float *y, int pro, const float *w, float eps,
                          const float *res, hipStream_t st);
 
@@ -243,6 +248,27 @@ __device__ __forceinline__ float load_act(const __hip_bfloat16 *p, size_t i) {
     return __bfloat162float(p[i]);
 }
 __device__ __forceinline__ float load_act(const __half *p, size_t i) { return __half2float(p[i]); }
+
+// One LUT entry for any group width D: sum_{d < D} v[d] * row[d] in d order
+// (the reference's scalar LUT loop), for the calling thread's codebook row.
+// v (a group of D activations, zeros when !v_ok) is staged through xs, an
+// LDS buffer of blockDim.x floats, blockDim.x values at a time; every thread
+// of the workgroup must call it (it synchronises).
+template <typename T>
+__device__ __forceinline__ float staged_group_dot(const T *__restrict__ v, bool v_ok,
+                                                  const float *__restrict__ row, int D,
+                                                  float *xs) {
+    const int nt = blockDim.x, tid = threadIdx.x;
+    float dot = 0.f;
+    for (int d0 = 0; d0 < D; d0 += nt) {
+        const int n = min(nt, D - d0);
+        __syncthreads();
+        if (tid < n) xs[tid] = v_ok ? load_act(v, (size_t)d0 + tid) : 0.f;
+        __syncthreads();
+        for (int d = 0; d < n; ++d) dot = fmaf(xs[d], row[d0 + d], dot);
+    }
+    return dot;
+}
 
 // v rounded (to nearest even) to the element type of p and back to fp32:
 // the result of a torch elementwise op on tensors of that type.
@@ -440,6 +466,7 @@ __device__ __forceinline__ void store_act(__hip_bfloat16 *p, size_t i, float v) 
     p[i] = __float2bfloat16(v);
 }
 __device__ __forceinline__ void store_act(__half *p, size_t i, float v) { p[i] = __float2half_rn(v); }
+__device__ __forceinline__ void store_act(double *p, size_t i, float v) { p[i] = (double)v; }
 
 // Copy n activations (converted to fp32) from global memory to LDS with all
 // of a thread's loads in flight before the first LDS store: loads and stores

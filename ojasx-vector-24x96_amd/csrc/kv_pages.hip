@@ -7,7 +7,8 @@
 //    (every elementwise result rounded to that type):
 //      a = max(max_d |t_d|, T(1e-8)),  s = T(a / 127),
 //      q_d = clamp(round_half_even(T(t_d / s)), -127, 127) as int8,
-//    s stored as fp16.  For fp32 input every T() is the identity.  One wave
+//    s stored as fp16.  For fp32 input every T() is the identity; fp64 rows
+//    run the same steps in fp64 (quantize_int8_f64_kernel).  One wave
 //    per row: abs-max by DPP wave reduction, then each lane writes its
 //    elements.  Rows are addressed as (group, row) with strides, so a slice
 //    of a [B, H, S, D] tensor quantises straight into a page buffer.
@@ -69,6 +70,55 @@ __global__ __launch_bounds__(kNT) void quantize_int8_kernel(QuantParams p) {
         qr[d] = (v != v) ? (int8_t)0 : (int8_t)fminf(127.f, fmaxf(-127.f, v));
     }
     if (lane == 0) p.scale[g * p.s_gs + row] = __float2half_rn(s);
+}
+
+// fp32 -> fp16 bits, round to nearest even, in integer steps: the compiler
+// otherwise merges (half)(float)d into one fp64 -> fp16 rounding, while torch
+// rounds a float64 scale to float32 first and then to float16.
+__device__ __forceinline__ unsigned short f32_to_f16_bits_rne(float f) {
+    const unsigned int b = __float_as_uint(f);
+    const unsigned int sign = (b >> 16) & 0x8000u;
+    const int e = (int)((b >> 23) & 0xffu);
+    unsigned int m = b & 0x7fffffu;
+    if (e == 0xff) return (unsigned short)(sign | 0x7c00u | (m ? 0x200u : 0u));
+    const int he = e - 127 + 15;                 // biased half exponent
+    if (he >= 31) return (unsigned short)(sign | 0x7c00u);
+    if (he >= 1) {                               // normal half: 10 of 23 mantissa bits
+        const unsigned int hm = m >> 13, rem = m & 0x1fffu;
+        unsigned int v = ((unsigned int)he << 10) | hm;
+        if (rem > 0x1000u || (rem == 0x1000u && (hm & 1u))) ++v;   // a carry may reach inf
+        return (unsigned short)(sign | v);
+    }
+    if (he < -10) return (unsigned short)sign;   // below half the smallest subnormal
+    m |= 0x800000u;                              // subnormal half: units of 2^-24
+    const int shift = 14 - he;                   // 14 .. 24
+    unsigned int hm = m >> shift;
+    const unsigned int rem = m & ((1u << shift) - 1u), half = 1u << (shift - 1);
+    if (rem > half || (rem == half && (hm & 1u))) ++hm;
+    return (unsigned short)(sign | hm);
+}
+
+// fp64 rows: the same steps in fp64 (torch's arithmetic on a float64 tensor),
+// the scale stored as torch casts float64 to float16 (through fp32: two
+// roundings to nearest even).
+__global__ __launch_bounds__(kNT) void quantize_int8_f64_kernel(QuantParams p) {
+    const int lane = threadIdx.x & 63;
+    const long r = (long)blockIdx.x * kNW + (threadIdx.x >> 6);
+    if (r >= p.groups * p.rows) return;          // wave-uniform
+    const long g = r / p.rows;
+    const int row = (int)(r - g * p.rows);
+    const double *xr = static_cast<const double *>(p.x) + g * p.x_gs + (long)row * p.dim;
+    double am = 0.0;
+    for (int d = lane; d < p.dim; d += 64) am = fmax(am, fabs(xr[d]));
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) am = fmax(am, __shfl_xor(am, o, 64));
+    const double s = fmax(am, 1e-8) / 127.0;
+    int8_t *qr = p.q + g * p.q_gs + (long)row * p.dim;
+    for (int d = lane; d < p.dim; d += 64)
+        qr[d] = (int8_t)fmin(127.0, fmax(-127.0, rint(xr[d] / s)));
+    if (lane == 0)
+        reinterpret_cast<unsigned short *>(p.scale)[g * p.s_gs + row] =
+            f32_to_f16_bits_rne((float)s);
 }
 
 template <typename T>
@@ -143,6 +193,8 @@ OJASX_API int ojasx_quantize_int8_device(const void *x, long groups, int rows, i
         OJX_LAUNCH(quantize_int8_kernel<__hip_bfloat16>, grid, dim3(kNT), 0, st, p);
     else if (dtype == OJASX_DTYPE_F16)
         OJX_LAUNCH(quantize_int8_kernel<__half>, grid, dim3(kNT), 0, st, p);
+    else if (dtype == OJASX_DTYPE_F64)
+        OJX_LAUNCH(quantize_int8_f64_kernel, grid, dim3(kNT), 0, st, p);
     else {
         set_error("unsupported dtype %d", dtype);
         return OJASX_ERR_INVALID;
@@ -180,6 +232,9 @@ OJASX_API int ojasx_dequantize_int8_device(const int8_t *q, const void *scale_f1
     else if (dtype == OJASX_DTYPE_F16)
         OJX_LAUNCH(dequantize_int8_kernel<__half>, grid, dim3(kNT), 0, st, q, s, groups, rows, dim,
                    q_group_stride, scale_group_stride, static_cast<__half *>(out));
+    else if (dtype == OJASX_DTYPE_F64)
+        OJX_LAUNCH(dequantize_int8_kernel<double>, grid, dim3(kNT), 0, st, q, s, groups, rows, dim,
+                   q_group_stride, scale_group_stride, static_cast<double *>(out));
     else {
         set_error("unsupported dtype %d", dtype);
         return OJASX_ERR_INVALID;

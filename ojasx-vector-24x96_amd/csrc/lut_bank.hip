@@ -509,6 +509,10 @@ int set_dyn_lds(F *fn, size_t lds, size_t *granted) {
 }
 }  // namespace
 
+bool bank_fits(int K) {
+    return 64 * 1024 + round_up((size_t)(K / 16), 32) * kXRow * sizeof(float) <= 160 * 1024;
+}
+
 int launch_bank(const GroupItem *items_dev, const int2 *work_dev, int n_work, int max_K,
                 hipStream_t st) {
     const size_t lds = round_up((size_t)(max_K / 16), 32) * kXRow * sizeof(float);

@@ -153,6 +153,7 @@ OJASX_API int ojasx_linear_forward_grouped_device(const OjasxLinearHandle *handl
     GroupItem *host = reinterpret_cast<GroupItem *>(gw.host.data());
     int rc = OJASX_OK;
     int max_K = 0;
+    std::vector<int> wide;                           // items whose K exceeds the bank kernel's LDS
     for (int i = 0; i < count; ++i) {
         if (!handles[i] || !xs[i] || !ys[i]) return OJASX_ERR_NULL;
         GroupItem &it = host[i];
@@ -164,18 +165,28 @@ OJASX_API int ojasx_linear_forward_grouped_device(const OjasxLinearHandle *handl
         }
         it.x = xs[i];
         it.y = ys[i];
-        max_K = std::max(max_K, it.K);
+        if (bank_fits(it.K)) max_K = std::max(max_K, it.K);
+        else wide.push_back(i);
     }
-    // the bank kernel's work list: every 512-row block of every item, item-major
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    // wide items run one by one on the single-linear path (in-place LUT
+    // kernel, or the L2-LUT kernels beyond its LDS), on the same stream
+    for (int i : wide) {
+        rc = linear_forward(handles[i], xs[i], ys[i], 1, OJASX_DTYPE_F32, st);
+        if (rc) return rc;
+    }
+    if (wide.size() == (size_t)count) return OJASX_OK;
+    // the bank kernel's work list: every 512-row block of every other item, item-major
     int n_work = 0;
-    for (int i = 0; i < count; ++i) n_work += (host[i].M + kBankRows - 1) / kBankRows;
+    for (int i = 0; i < count; ++i)
+        if (bank_fits(host[i].K)) n_work += (host[i].M + kBankRows - 1) / kBankRows;
     const size_t bytes = item_bytes + sizeof(int2) * (size_t)n_work;
     gw.host.resize(bytes);
     host = reinterpret_cast<GroupItem *>(gw.host.data());
     int2 *wl = reinterpret_cast<int2 *>(gw.host.data() + item_bytes);
     for (int i = 0, t = 0; i < count; ++i)
-        for (int b = 0; b < host[i].M; b += kBankRows) wl[t++] = make_int2(i, b);
-    hipStream_t st = static_cast<hipStream_t>(stream);
+        if (bank_fits(host[i].K))
+            for (int b = 0; b < host[i].M; b += kBankRows) wl[t++] = make_int2(i, b);
     void *staged = nullptr;
     rc = gw.ring.stage(gw.host.data(), bytes, true, st, &staged);
     if (rc) return rc;

@@ -74,23 +74,27 @@ struct GatherParams {
 };
 
 // K1: LUT of token b for group blockIdx.x (zero for padded groups >= G).
+// DT = 16 holds the codebook row in registers; DT = 0 takes any group width
+// D, staging the group 256 values at a time.
 template <int DT, typename T>
 __global__ __launch_bounds__(kCB) void lut_build_kernel(const T *__restrict__ x,
                                                       const float *__restrict__ cb, int K, int D,
                                                       int G, int Gp, float *__restrict__ lut) {
-    constexpr int DMAX = DT > 0 ? DT : 32;
-    const int Dr = DT > 0 ? DT : D;
-    __shared__ float xs[32];
+    __shared__ float xs[kCB];
     const int b = blockIdx.y, g = blockIdx.x, k = threadIdx.x;
-    float c[DMAX];
-#pragma unroll
-    for (int d = 0; d < DMAX; ++d) c[d] = d < Dr ? cb[k * Dr + d] : 0.f;
-    if (k < Dr) xs[k] = g < G ? load_act(x, (size_t)b * K + (size_t)g * Dr + k) : 0.f;
-    __syncthreads();
     float dot = 0.f;
+    if constexpr (DT > 0) {
+        float c[DT];
 #pragma unroll
-    for (int d = 0; d < DMAX; ++d)
-        if (d < Dr) dot = fmaf(xs[d], c[d], dot);
+        for (int d = 0; d < DT; ++d) c[d] = cb[k * DT + d];
+        if (k < DT) xs[k] = g < G ? load_act(x, (size_t)b * K + (size_t)g * DT + k) : 0.f;
+        __syncthreads();
+#pragma unroll
+        for (int d = 0; d < DT; ++d) dot = fmaf(xs[d], c[d], dot);
+    } else {
+        dot = staged_group_dot(x + (size_t)b * K + (size_t)min(g, G - 1) * D, g < G,
+                               cb + (size_t)k * D, D, xs);
+    }
     lut[((size_t)b * Gp + g) * kCB + k] = dot;
 }
 
@@ -525,13 +529,10 @@ __global__ __launch_bounds__(kCB) void build_lut_kernel(const T *__restrict__ x,
                                                       const float *__restrict__ cb, int G, int D,
                                                       int Kcb, float *__restrict__ lut) {
     const int g = blockIdx.x, b = blockIdx.y, k = threadIdx.x;
-    __shared__ float xs[32];
-    if (k < D) xs[k] = load_act(x, (size_t)b * G * D + (size_t)g * D + k);
-    __syncthreads();
-    if (k >= Kcb) return;
-    float dot = 0.f;
-    for (int d = 0; d < D; ++d) dot = fmaf(xs[d], cb[(size_t)k * D + d], dot);
-    lut[((size_t)b * G + g) * Kcb + k] = dot;
+    __shared__ float xs[kCB];
+    const float dot = staged_group_dot(x + (size_t)b * G * D + (size_t)g * D, true,
+                                       cb + (size_t)min(k, Kcb - 1) * D, D, xs);
+    if (k < Kcb) lut[((size_t)b * G + g) * Kcb + k] = dot;
 }
 
 // ---------------------------------------------------------------------------
@@ -871,8 +872,8 @@ OJASX_API OjasxLinearHandle ojasx_create_linear(int in_features, int out_feature
                                                 const uint8_t *codes_data,
                                                 const float *scales_data, const float *bias_data) {
     using namespace ojx;
-    if (in_features <= 0 || out_features <= 0 || block_dim <= 0 || block_dim > 32 ||
-        codebook_size <= 0 || codebook_size > 256 || in_features % block_dim) {
+    if (in_features <= 0 || out_features <= 0 || block_dim <= 0 || codebook_size <= 0 ||
+        codebook_size > 256 || in_features % block_dim) {
         set_error("invalid linear shape in=%d out=%d block=%d codebook=%d", in_features,
                   out_features, block_dim, codebook_size);
         return nullptr;
@@ -999,8 +1000,8 @@ OJASX_API int ojasx_build_lut_device(const void *x, const float *codebook, int b
     using namespace ojx;
     if (!x || !codebook || !lut) return OJASX_ERR_NULL;
     if (batch_size <= 0 || groups <= 0) return OJASX_OK;
-    if (block_dim <= 0 || block_dim > 32 || codebook_size <= 0 || codebook_size > 256 ||
-        groups > 65535 || batch_size > 65535) {
+    if (block_dim <= 0 || codebook_size <= 0 || codebook_size > 256 || groups > 65535 ||
+        batch_size > 65535) {
         set_error("invalid LUT build shape");
         return OJASX_ERR_INVALID;
     }

@@ -26,8 +26,9 @@
 //    expert (moe_plan, a counting sort) on the bank-layout LUT-GEMV of
 //    lut_bank.hip -- moe_bank (gate/up), moe_bank (SwiGLU input, down),
 //    moe_combine -- so each distinct expert's codes stream from HBM once.
-//  * other block sizes: LUT_in build, moe_gateup (gathers from the L2-resident
-//    LUT, SwiGLU, LUT_down rows), moe_down, moe_combine.
+//  * other block sizes (any divisor of H and I): LUT_in build, moe_gateup
+//    (gathers from the L2-resident LUT, SwiGLU), moe_lut_down (the pair's
+//    LUT_down rows), moe_down, moe_combine.
 // Every path sums slots in slot order, so results are deterministic.
 //  Router: moe_route, one workgroup per token.
 #include <algorithm>
@@ -58,7 +59,6 @@ struct MoE {
     size_t gub_bytes = 0, dnb_bytes = 0;
     DevBuf lut_in, lut_dn, dout, inter, gu_part, xstage, ystage;
     DevBuf work, nwork, gu_out;         // bank path: plan output, gate/up rows per pair
-    size_t lut_dn_pairs = 0;
     ~MoE() {
         for (DevBuf *b : {&cb_in, &cb_dn, &cb3_in, &cb3_dn, &gu, &dn, &gus, &dns, &gub, &dnb, &lut_in, &lut_dn,
                           &dout, &inter, &gu_part, &xstage, &ystage, &work,
@@ -76,6 +76,7 @@ struct MoEParams {
     const float *lut_in;    // [T][Sin*16][256]
     float *lut_dn;          // [P][Si*16][256]
     float *dout;            // [P][H]
+    float *inter;           // [P][I]: silu(gate) * up
     const int *idx;         // [T][k]
     const float *w;         // [T][k]
     void *y;                // [T][H]
@@ -105,11 +106,9 @@ __device__ __forceinline__ float gather16(const float *__restrict__ L, uint4 c) 
     return a;
 }
 
-template <int DT>
 __global__ __launch_bounds__(kNT) void moe_gateup_kernel(MoEParams p) {
     constexpr int QG = kNT / kRG;  // 8 slice groups
     __shared__ float red[2][QG][kRG];
-    __shared__ float inter_s[kRG];
     const int tid = threadIdx.x;
     const int r = tid % kRG, q = tid / kRG;
     const int nrb = (p.I + kRG - 1) / kRG;
@@ -132,40 +131,32 @@ __global__ __launch_bounds__(kNT) void moe_gateup_kernel(MoEParams p) {
     red[0][q][r] = ag;
     red[1][q][r] = au;
     __syncthreads();
-    if (q == 0) {
-        float g = red[0][0][r], u = red[1][0][r];
+    if (q != 0 || i >= p.I) return;
+    float g = red[0][0][r], u = red[1][0][r];
 #pragma unroll
-        for (int k = 1; k < QG; ++k) {
-            g += red[0][k][r];
-            u += red[1][k][r];
-        }
-        float v = 0.f;
-        if (i < p.I) {
-            g *= p.gus[(size_t)e * 2 * p.I + i];
-            u *= p.gus[(size_t)e * 2 * p.I + p.I + i];
-            v = g / (1.f + expf(-g)) * u;
-        }
-        inter_s[r] = v;
+    for (int k = 1; k < QG; ++k) {
+        g += red[0][k][r];
+        u += red[1][k][r];
     }
-    __syncthreads();
-    // LUT_down rows of the kRG / D groups this workgroup produced.
-    constexpr int DMAX = DT > 0 ? DT : 32;
-    const int D = DT > 0 ? DT : p.D;
-    const int ng = kRG / D;
-    const int g0 = rb * ng;
-    float c[DMAX];
-#pragma unroll
-    for (int d = 0; d < DMAX; ++d) c[d] = d < D ? p.cb_dn[tid * D + d] : 0.f;
-    float *Ld = p.lut_dn + (size_t)pr * p.Si * kGS * kCB;
-    for (int gl = 0; gl < ng; ++gl) {
-        const int g = g0 + gl;
-        if (g * D >= p.I) break;
-        float dot = 0.f;
-#pragma unroll
-        for (int d = 0; d < DMAX; ++d)
-            if (d < D) dot = fmaf(inter_s[gl * D + d], c[d], dot);
-        Ld[(size_t)g * kCB + tid] = dot;
-    }
+    g *= p.gus[(size_t)e * 2 * p.I + i];
+    u *= p.gus[(size_t)e * 2 * p.I + p.I + i];
+    p.inter[(size_t)pr * p.I + i] = g / (1.f + expf(-g)) * u;
+}
+
+// LUT_down of one active pair: row g (blockIdx.y, all Si * 16 rows of the
+// slices, zero past Gi) = <inter[pair][gD : gD + D], C_down[k]> for thread
+// k, any block size D (the group is staged 256 values at a time).  Every
+// row the down gathers can read is written here, so the workspace needs no
+// clearing.
+__global__ __launch_bounds__(kNT) void moe_lut_down_kernel(MoEParams p) {
+    __shared__ float xs[kNT];
+    const int pr = blockIdx.x, g = blockIdx.y, k = threadIdx.x;
+    int e;
+    if (!pair_active(p, pr, &e)) return;
+    const int Gi = p.I / p.D;
+    const float dot = staged_group_dot(p.inter + (size_t)pr * p.I + (size_t)min(g, Gi - 1) * p.D,
+                                       g < Gi, p.cb_dn + (size_t)k * p.D, p.D, xs);
+    p.lut_dn[((size_t)pr * p.Si * kGS + g) * kCB + k] = dot;
 }
 
 __global__ __launch_bounds__(kNT) void moe_down_kernel(MoEParams p) {
@@ -1004,17 +995,24 @@ int moe_forward(MoE *m, const void *x, const int *idx, const float *w, void *y, 
         const size_t align = dtype == OJASX_DTYPE_F32 ? 16 : 8;
         const bool aligned = m->H % 4 == 0 && m->I % 4 == 0 &&
                              reinterpret_cast<uintptr_t>(x) % align == 0;
+        // (the dynamic LDS plus the kernels' static partial sums, <= 4.3 KB)
+        constexpr size_t kDecStatic = 8 * 1024;
         const bool ok = m->D == 16 && k <= 32 && aligned &&
-                        (size_t)(kCB * 16 + (size_t)k * m->Si * 256) * 4 <= kMaxLds &&
-                        (size_t)(kCB * 16 + m->Sin * 256) * 4 <= kMaxLds;
+                        (size_t)(kCB * 16 + (size_t)k * m->Si * 256) * 4 + kDecStatic <= kMaxLds &&
+                        (size_t)(kCB * 16 + m->Sin * 256) * 4 + kDecStatic <= kMaxLds;
         // grouped by expert: expert ids fit the work entries' 16 bits and the
         // plan kernel's LDS holds 3 E + P ints
         const size_t P = (size_t)T_ * k;
         if (m->D == 16 && aligned && T_ >= kBankMinTokens && m->gub.ptr && P <= kBankMaxPairs &&
-            m->E <= 65535 && (3 * (size_t)m->E + P) * sizeof(int) <= kMaxLds)
+            m->E <= 65535 && (3 * (size_t)m->E + P) * sizeof(int) <= kMaxLds &&
+            bank_fits(m->H) && bank_fits(m->I))
             return dtype == OJASX_DTYPE_F32 ? moe_forward_bank<float>(m, x, idx, w, y, T_, k, st)
                                             : moe_forward_bank<__hip_bfloat16>(m, x, idx, w, y, T_, k, st);
-        if (m->D == 16 && T_ >= kGroupMinTokens)
+        // grouped per slot: the staged input and two LUT buffers fit the LDS
+        const bool group_fits =
+            (size_t)std::max(m->Sin, m->Si) * 256 * sizeof(float) + slices::lut_bytes(kGroupDB) <=
+            kMaxLds;
+        if (m->D == 16 && T_ >= kGroupMinTokens && group_fits)
             return dtype == OJASX_DTYPE_F32 ? moe_forward_group<float>(m, x, idx, w, y, T_, k, st)
                                             : moe_forward_group<__hip_bfloat16>(m, x, idx, w, y, T_, k, st);
         if (ok)
@@ -1025,15 +1023,9 @@ int moe_forward(MoE *m, const void *x, const int *idx, const float *w, void *y, 
     const int Gp_in = m->Sin * kGS;
     int rc = m->lut_in.ensure((size_t)T_ * Gp_in * kCB * sizeof(float));
     if (!rc) rc = m->dout.ensure(P * m->H * sizeof(float));
+    if (!rc) rc = m->inter.ensure(P * m->I * sizeof(float));
+    if (!rc) rc = m->lut_dn.ensure(P * m->Si * kGS * kCB * sizeof(float));
     if (rc) return rc;
-    const size_t ldn = (size_t)m->Si * kGS * kCB * sizeof(float);
-    if (P > m->lut_dn_pairs) {
-        // LUT_down rows of padded groups (>= Gi) stay zero: written only here.
-        rc = m->lut_dn.ensure(P * ldn);
-        if (rc) return rc;
-        OJX_HIP(hipMemsetAsync(m->lut_dn.ptr, 0, P * ldn, st));
-        m->lut_dn_pairs = P;
-    }
     rc = launch_lut_build(x, m->cb_in.as<float>(), T_, m->H, m->D, m->Gin, Gp_in,
                           m->lut_in.as<float>(), dtype, st);
     if (rc) return rc;
@@ -1046,6 +1038,7 @@ int moe_forward(MoE *m, const void *x, const int *idx, const float *w, void *y, 
     p.lut_in = m->lut_in.as<float>();
     p.lut_dn = m->lut_dn.as<float>();
     p.dout = m->dout.as<float>();
+    p.inter = m->inter.as<float>();
     p.idx = idx;
     p.w = w;
     p.y = y;
@@ -1061,10 +1054,8 @@ int moe_forward(MoE *m, const void *x, const int *idx, const float *w, void *y, 
     p.k = k;
     const int nrb_g = (m->I + kRG - 1) / kRG;
     const int nrb_d = (m->H + kRD - 1) / kRD;
-    if (m->D == 16)
-        OJX_LAUNCH(moe_gateup_kernel<16>, dim3(P * nrb_g), dim3(kNT), 0, st, p);
-    else
-        OJX_LAUNCH(moe_gateup_kernel<0>, dim3(P * nrb_g), dim3(kNT), 0, st, p);
+    OJX_LAUNCH(moe_gateup_kernel, dim3(P * nrb_g), dim3(kNT), 0, st, p);
+    OJX_LAUNCH(moe_lut_down_kernel, dim3(P, m->Si * kGS), dim3(kNT), 0, st, p);
     OJX_LAUNCH(moe_down_kernel, dim3(P * nrb_d), dim3(kNT), 0, st, p);
     dim3 gc((m->H + kNT - 1) / kNT, T_);
     if (dtype == OJASX_DTYPE_F32)
@@ -1090,8 +1081,7 @@ OJASX_API OjasxMoEHandle ojasx_create_moe(int num_experts, int hidden_dim, int i
                                           const float *down_scales) {
     using namespace ojx;
     if (num_experts <= 0 || hidden_dim <= 0 || intermediate_dim <= 0 || block_dim <= 0 ||
-        block_dim > 32 || hidden_dim % block_dim || intermediate_dim % block_dim ||
-        kRG % block_dim) {
+        hidden_dim % block_dim || intermediate_dim % block_dim) {
         set_error("invalid MoE shape E=%d H=%d I=%d block=%d (block must divide 32)", num_experts, hidden_dim,
                   intermediate_dim, block_dim);
         return nullptr;

@@ -4,12 +4,11 @@ csrc/lut_kv.hip.
 * ``PagedCompressedKVCache`` mirrors ojasx_24x96/long_context.py:212-279: the
   int8 cache with per-token fp16 scales and sink + sliding-window eviction.
   Names, argument meaning, validation, the page list ``_pages`` of
-  ``(qk, sk, qv, sv)`` and ``storage_bytes`` match the reference.  Pages live
-  in a pool of at most ``max_resident_pages`` page buffers that is allocated as
-  pages are first needed and recycled on eviction, so a long stream allocates
-  nothing in steady state.  Each entry of ``_pages`` is a view of its buffer
-  trimmed to the page's length; an evicted page's buffer is rewritten by a
-  later page.
+  ``(qk, sk, qv, sv)`` and ``storage_bytes`` match the reference.  Each page
+  gets tensors of its own length, so an evicted page keeps its values for a
+  caller that still holds it, as the reference's popped page does; the memory
+  of an evicted page nobody holds returns to torch's caching allocator and is
+  reused by a later page without a device allocation.
 * ``PagedCodeKVCache`` is the code-domain counterpart for decode: per token
   and kv head, 8-bit codes into a 256-centroid codebook (or the reference's
   scalar quantiser, ojasx_lut_kv_cache.cpp:16-65) and an fp32 scale, in the
@@ -61,9 +60,9 @@ def _require_gpu(t, what):
 
 def _dtype_tag(dtype):
     torch = _torch()
-    tags = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
+    tags = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2, torch.float64: 3}
     if dtype not in tags:
-        raise TypeError(f"unsupported KV dtype {dtype}: float32, bfloat16 or float16")
+        raise TypeError(f"unsupported KV dtype {dtype}: float32, bfloat16, float16 or float64")
     return tags[dtype]
 
 
@@ -98,9 +97,6 @@ class PagedCompressedKVCache:
         self.sink_pages = int(sink_pages)
         self.total_tokens_seen: int = 0
         self._pages: List[Tuple] = []
-        self._slots: List[int] = []      # page buffer of each resident page
-        self._buffers: List[Tuple] = []  # (qk, sk, qv, sv) page buffers
-        self._free: List[int] = []
         self._layout = None              # (B, H, D, device) of the first append
         self._version = 0                # bumped by every append
         self._tiles = None               # (version, attention tile array, tokens, max page)
@@ -108,7 +104,7 @@ class PagedCompressedKVCache:
     @staticmethod
     def _quantize_int8(t):
         """long_context.py:234-240 on the GPU: t [..., D] float32/bfloat16/
-        float16 -> (q int8 [..., D], scale float16 [..., 1])."""
+        float16/float64 -> (q int8 [..., D], scale float16 [..., 1])."""
         torch = _torch()
         _require_gpu(t, "PagedCompressedKVCache._quantize_int8")
         t = t.contiguous()
@@ -140,17 +136,12 @@ class PagedCompressedKVCache:
             _lib.check(rc, "ojasx_dequantize_int8_device")
         return out
 
-    def _take_buffer(self, B, H, D, device) -> int:
+    @staticmethod
+    def _new_page(B, H, n, D, device):
         torch = _torch()
-        if self._free:
-            return self._free.pop()
-        P = self.page_size
-        qk = torch.empty(B, H, P, D, dtype=torch.int8, device=device)
-        sk = torch.empty(B, H, P, 1, dtype=torch.float16, device=device)
-        qv = torch.empty_like(qk)
-        sv = torch.empty_like(sk)
-        self._buffers.append((qk, sk, qv, sv))
-        return len(self._buffers) - 1
+        qk = torch.empty(B, H, n, D, dtype=torch.int8, device=device)
+        sk = torch.empty(B, H, n, 1, dtype=torch.float16, device=device)
+        return qk, sk, torch.empty_like(qk), torch.empty_like(sk)
 
     def append(self, key, value) -> None:
         """Quantise and append a K/V chunk ``[B, H, S, D]`` into bounded pages
@@ -172,16 +163,13 @@ class PagedCompressedKVCache:
             n = min(start + self.page_size, S) - start
             if len(self._pages) == self.max_resident_pages:
                 # Evicting before the append leaves the same pages as the
-                # reference's append-then-pop(sink_pages), with one page
-                # buffer fewer.
+                # reference's append-then-pop(sink_pages); the popped page's
+                # memory can then serve the new page when nobody holds it.
                 self._pages.pop(self.sink_pages)
-                self._free.append(self._slots.pop(self.sink_pages))
-            slot = self._take_buffer(B, H, D, key.device)
-            qk, sk, qv, sv = self._buffers[slot]
+            qk, sk, qv, sv = self._new_page(B, H, n, D, key.device)
             _quantize_into(key[:, :, start:start + n], qk, sk)
             _quantize_into(value[:, :, start:start + n], qv, sv)
-            self._pages.append((qk[:, :, :n], sk[:, :, :n], qv[:, :, :n], sv[:, :, :n]))
-            self._slots.append(slot)
+            self._pages.append((qk, sk, qv, sv))
 
     def iter_dequantized_pages(self, dtype=None) -> Iterator[Tuple]:
         """Lazily dequantise resident pages one by one (long_context.py:259-267)."""
@@ -265,6 +253,14 @@ class OnlineSoftmaxBlockAttention:
         self.kv_block_size = int(kv_block_size)
         self.causal = bool(causal)
         self.scale = 1.0 / math.sqrt(self.head_dim)
+        # the kernels take head dims in multiples of 8: others run zero-padded
+        # to the next one (exact: the added products are fp64 zeros; the
+        # scale stays 1/sqrt(head_dim)) and the output is cut back
+        self._dpad = -(-self.head_dim // 8) * 8
+
+    def _pad_d(self, t):
+        extra = self._dpad - t.shape[-1]
+        return t if extra == 0 else _torch().nn.functional.pad(t, (0, extra))
 
     def _expand_kv_heads(self, tensor):
         """[B, H_kv, S, D] -> [B, H_q, S, D], each kv head repeated for its
@@ -349,7 +345,8 @@ class OnlineSoftmaxBlockAttention:
         torch = _torch()
         self._check_query(query)
         B, H_q, S_q, D = query.shape
-        state = self._init(query)
+        qp = self._pad_d(query)
+        state = self._init(qp)
         kv_offset = num_blocks = peak = 0
         if isinstance(kv_stream, PagedCompressedKVCache) and kv_stream._pages and \
                 kv_stream._pages[0][0].shape[3] % 16 == 0:
@@ -357,7 +354,7 @@ class OnlineSoftmaxBlockAttention:
             arr, kv_offset, max_n = self._page_tiles(kv_stream, query)
             num_blocks = len(arr)
             peak = B * H_q * S_q * max_n
-            self._update(state, query, arr, _lib.DTYPE_INT8, query_start_pos, 0)
+            self._update(state, qp, arr, _lib.DTYPE_INT8, query_start_pos, 0)
         else:
             if isinstance(kv_stream, PagedCompressedKVCache):
                 kv_stream = kv_stream.iter_dequantized_pages()   # head_dim not a multiple of 16
@@ -373,13 +370,15 @@ class OnlineSoftmaxBlockAttention:
                 if S_k == 0:
                     continue
                 keep = []
-                tile, tag = _float_tile(k_blk, v_blk, keep)
-                self._update(state, query, [tile], tag, query_start_pos, kv_offset)
+                tile, tag = _float_tile(self._pad_d(k_blk), self._pad_d(v_blk), keep)
+                self._update(state, qp, [tile], tag, query_start_pos, kv_offset)
                 num_blocks += 1
                 peak = max(peak, B * H_q * S_q * S_k)
                 kv_offset += S_k
         lse = torch.empty(state.shape[0], dtype=torch.float64, device=query.device)
-        out = self._finalize(state, query, lse)
+        out = self._finalize(state, qp, lse)
+        if qp is not query:
+            out = out[..., :D].contiguous()
         # the rows' log-sum-exps copied out and reduced on the host: one
         # synchronising copy, no reduction kernel
         max_lse = float(lse.cpu().max()) if kv_offset > 0 else 0.0
@@ -399,11 +398,12 @@ class OnlineSoftmaxBlockAttention:
         value = value.to(device=query.device)
         self._check_block(key, B, "key")
         self._check_block(value, B, "value")
+        key, value, qp = self._pad_d(key), self._pad_d(value), self._pad_d(query)
         S_k = key.shape[2]
         outs = []
         for q_start in range(0, S_q, self.q_block_size):
             q_stop = min(q_start + self.q_block_size, S_q)
-            q_chunk = query[:, :, q_start:q_stop, :]
+            q_chunk = qp[:, :, q_start:q_stop, :]
             eff_k = min(S_k, query_start_pos + q_stop) if self.causal else S_k
             state = self._init(q_chunk)
             keep, tiles, tag = [], [], None
@@ -415,7 +415,8 @@ class OnlineSoftmaxBlockAttention:
             if tiles:
                 self._update(state, q_chunk, tiles, tag, query_start_pos + q_start, 0)
             outs.append(self._finalize(state, q_chunk))
-        return torch.cat(outs, dim=2)
+        out = torch.cat(outs, dim=2)
+        return out if qp is query else out[..., :D].contiguous()
 
     __call__ = forward
 

@@ -242,7 +242,13 @@ def paged_quantize_int8(t, kind="float32"):
     a = max(|t|_D, T(1e-8)), s = T(a / 127), q = clamp(round_half_even(T(t / s)),
     -127, 127) int8 with every elementwise result T() rounded to the type as
     torch does; s returned as float16.  An all-zero float16 row gives s = 0
-    and 0/0 in the reference; q is 0 there."""
+    and 0/0 in the reference; q is 0 there.  For "float64" every step is
+    float64 and s reaches float16 as torch casts it: through float32."""
+    if kind == "float64":
+        t = np.asarray(t, np.float64)
+        s = np.maximum(np.abs(t).max(axis=-1, keepdims=True), 1e-8) / 127.0
+        q = np.clip(np.rint(t / s), -127, 127).astype(np.int8)
+        return q, s.astype(np.float32).astype(np.float16)
     t = round_to(t, kind)
     amax = np.maximum(np.abs(t).max(axis=-1, keepdims=True), round_to(np.float32(1e-8), kind))
     s = round_to(amax / np.float32(127.0), kind)
@@ -257,7 +263,7 @@ def paged_dequantize_int8(q, s, kind="float32"):
     """PagedCompressedKVCache._dequantize_int8 (long_context.py:242-244):
     float(q) * float(s) in fp32, then rounded to ``kind``."""
     v = np.asarray(q, np.float32) * np.asarray(s, np.float16).astype(np.float32)
-    return round_to(v, kind)
+    return v.astype(np.float64) if kind == "float64" else round_to(v, kind)
 
 
 def code_domain_kv_decode(q_heads, kv_group, k_cb, v_cb, k_codes, k_scales, v_codes, v_scales,

@@ -9,7 +9,8 @@ input/output vectors.  Inputs come from the repo's seeded generators
 own tests (NAT/tests/test_native_lut.cpp T2, T3, T6), which are regenerated
 from their formulas at test time, so only their outputs are stored.
 
-Run from the repository root:  python tests/golden/make_golden.py
+Run from the repository root:  python tests/golden/make_golden.py [block_sizes]
+(``block_sizes`` writes only the block-size fixtures.)
 """
 import os
 import sys
@@ -38,8 +39,32 @@ def linear_case(name, M, K, B, D, Kcb, seed, density, bias):
          row_ptrs=rp, cols=cl, vals=vl, x=d["x"], y=y)
 
 
-def main():
+def moe_case(name, E, H, I, D, seed, idx, w):
+    m = gen.moe(E=E, H=H, I=I, T=1, D=D, seed=seed, scales="u")
+    idx = np.array(idx, np.int32)
+    w = np.array(w, np.float32)
+    M = ref.RefMoE(m["cb_in"], m["cb_down"], m["gu_codes"], m["gu_scales"], m["dn_codes"],
+                   m["dn_scales"], top_k=idx.size)
+    y = M.forward(m["x"][0], idx, w)
+    save(name, cb_in=m["cb_in"], cb_down=m["cb_down"], gu_codes=m["gu_codes"],
+         gu_scales=m["gu_scales"], dn_codes=m["dn_codes"], dn_scales=m["dn_scales"],
+         x=m["x"][0], idx=idx, w=w, y=y)
+
+
+def block_size_cases():
+    """Block sizes beyond the configured 16: wider than 32 and not dividing 32."""
+    linear_case("linear_d64_k512_m72_b3", 72, 512, 3, 64, 256, 14, 0.02, True)
+    linear_case("linear_d48_k480_m40_b2_cb100", 40, 480, 2, 48, 100, 15, 0.03, False)
+    moe_case("moe_d24_e16_h96_i72", 16, 96, 72, 24, 22,
+             [5, 11, 5, 0, 15, 99], [0.3, 0.2, 0.15, 0.15, 0.2, 0.5])
+    moe_case("moe_d64_e8_h256_i128", 8, 256, 128, 64, 23, [7, 2, 4], [0.5, 0.3, 0.2])
+
+
+def main(only=None):
     assert ref.available(), "build the reference engine first: make -C oracle ref"
+    if only == "block_sizes":
+        block_size_cases()
+        return
     linear_case("linear_k256_m200_b3", 200, 256, 3, 16, 256, 11, 0.02, True)
     linear_case("linear_d8_k128_m96_b2_cb64", 96, 128, 2, 8, 64, 12, 0.03, False)
     linear_case("linear_k2560_m64_b1", 64, 2560, 1, 16, 256, 13, 0.0038, False)
@@ -78,7 +103,8 @@ def main():
     rc2, out_sf = kv.attention(1, q, 0.05)
     assert rc == 0 and rc2 == 0
     save("kv_ref_head_t150", K=K, V=V, q=q, out=out, out_sf005=out_sf)
+    block_size_cases()
 
 
 if __name__ == "__main__":
-    main()
+    main(sys.argv[1] if len(sys.argv) > 1 else None)

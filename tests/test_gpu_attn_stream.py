@@ -196,3 +196,57 @@ def test_fully_masked_rows_and_errors(pkg, dev):
         lc.OnlineSoftmaxBlockAttention(3, 2, 8)
     with pytest.raises(RuntimeError, match="GPU only"):
         attn.forward_stream(q.cpu(), [(k, v)])
+
+
+@pytest.mark.parametrize("causal,qsp", [(False, 0), (True, 700)])
+def test_paged_int8_in_place_head_dim_128(pkg, dev, causal, qsp):
+    """The int8 head_dim-128 path (value words held in registers): GQA 32/8,
+    partial pages (appends that end inside a page), a decode row and a short
+    prefill, causal with a query offset and non-causal, against the fp64
+    stream oracle over the dequantised pages."""
+    import torch
+    B, Hq, Hkv, D = 1, 32, 8, 128
+    cache = make_cache(pkg, dev, torch, B, Hkv, D, page=256, pages=6, sink=1,
+                       chunks=[300, 100, 250, 7, 400], seed=50)
+    assert any(p[0].shape[2] < 256 for p in cache._pages)
+    q = randn(torch, B, Hq, 3, D, seed=51).to(dev)
+    attn = pkg.long_context.OnlineSoftmaxBlockAttention(Hq, Hkv, D, causal=causal)
+    for qq in (q.double(), q[:, :, :1].double()):
+        out, rep = attn.forward_stream(qq, cache, query_start_pos=qsp)
+        pages = [(no.paged_dequantize_int8(qk.cpu().numpy(), sk.cpu().numpy()),
+                  no.paged_dequantize_int8(qv.cpu().numpy(), sv.cpu().numpy()))
+                 for qk, sk, qv, sv in cache._pages]
+        want, lse, n, nt = no.block_attention_stream(qq.cpu().numpy(), pages, causal, qsp)
+        print(f"int8 hd128: rel {rel_err(out.cpu().numpy(), want):.3e}")
+        assert rel_err(out.cpu().numpy(), want) < 1e-12
+        assert rep.kv_tokens == n and rep.num_kv_blocks == nt
+        assert abs(rep.max_logsumexp - float(lse.max())) < 1e-10
+
+
+@pytest.mark.parametrize("D", [12, 20, 3])
+def test_head_dim_not_multiple_of_8(pkg, dev, D):
+    """Any positive head_dim, as the reference accepts: forward, forward_stream
+    over tiles and over an int8 paged cache, against fp64 full attention."""
+    import torch
+    B, Hq, Hkv, S = 1, 4, 2, 150
+    q = randn(torch, B, Hq, S, D, seed=60 + D)
+    k, v = randn(torch, B, Hkv, S, D, seed=61 + D), randn(torch, B, Hkv, S, D, seed=62 + D)
+    attn = pkg.long_context.OnlineSoftmaxBlockAttention(Hq, Hkv, D, q_block_size=64,
+                                                        kv_block_size=48, causal=True)
+    out = attn.forward(q.to(dev), k.to(dev), v.to(dev))
+    assert out.shape == (B, Hq, S, D) and out.is_contiguous()
+    check(out, q, k, v, True, 0)
+    out, rep = attn.forward_stream(q.to(dev), [(k[:, :, :70].to(dev), v[:, :, :70].to(dev)),
+                                               (k[:, :, 70:].to(dev), v[:, :, 70:].to(dev))])
+    assert out.shape == (B, Hq, S, D) and rep.kv_tokens == S
+    check(out, q, k, v, True, 0)
+    cache = make_cache(pkg, dev, torch, B, Hkv, D, page=64, pages=8, sink=1,
+                       chunks=[90, 60], seed=63 + D)
+    qd = q[:, :, -2:].double().to(dev)
+    out, rep = attn.forward_stream(qd, cache, query_start_pos=148)
+    pages = [(no.paged_dequantize_int8(qk.cpu().numpy(), sk.cpu().numpy()),
+              no.paged_dequantize_int8(qv.cpu().numpy(), sv.cpu().numpy()))
+             for qk, sk, qv, sv in cache._pages]
+    want, _, _, _ = no.block_attention_stream(qd.cpu().numpy(), pages, True, 148)
+    assert out.shape == (B, Hq, 2, D)
+    assert rel_err(out.cpu().numpy(), want) < 1e-12

@@ -1,5 +1,5 @@
 """GPU parity of the KV write path against the CPU oracle: the int8 page
-quantiser and dequantiser bit-exact for float32, bfloat16 and float16 input,
+quantiser and dequantiser bit-exact for float32, bfloat16, float16 and float64 input,
 the PagedCompressedKVCache face (the reference's own M13 checks, including the
 eviction known answer), the codebook encode-append codes and scales bit-exact
 through a slot mapping, and PagedCodeKVCache append -> decode end to end."""
@@ -27,7 +27,7 @@ def edge_rows(torch, dtype, B, H, S, D, seed):
     return t.to(dtype)
 
 
-@pytest.mark.parametrize("kind", ["float32", "bfloat16", "float16"])
+@pytest.mark.parametrize("kind", ["float32", "bfloat16", "float16", "float64"])
 @pytest.mark.parametrize("shape", [(1, 4, 300, 64), (2, 3, 17, 130), (1, 1, 5, 8)])
 def test_quantize_dequantize_int8(pkg, dev, kind, shape):
     import torch
@@ -35,14 +35,29 @@ def test_quantize_dequantize_int8(pkg, dev, kind, shape):
     t = edge_rows(torch, dtype, *shape, seed=shape[2])
     lc = pkg.long_context
     q, s = lc.PagedCompressedKVCache._quantize_int8(t.to(dev))
-    qn, sn = no.paged_quantize_int8(t.float().numpy(), kind)
+    qn, sn = no.paged_quantize_int8(t.double().numpy() if kind == "float64" else
+                                    t.float().numpy(), kind)
     assert q.dtype == torch.int8 and s.dtype == torch.float16 and s.shape == (*shape[:3], 1)
     assert np.array_equal(q.cpu().numpy(), qn)
     assert np.array_equal(s.cpu().numpy().view(np.uint16), sn.view(np.uint16))
-    for out_kind in ("float32", "bfloat16", "float16"):
+    for out_kind in ("float32", "bfloat16", "float16", "float64"):
         d = lc.PagedCompressedKVCache._dequantize_int8(q, s, getattr(torch, out_kind))
         dn = no.paged_dequantize_int8(qn, sn, out_kind)
-        assert np.array_equal(d.float().cpu().numpy().view(np.uint32), dn.view(np.uint32))
+        assert d.dtype == getattr(torch, out_kind)
+        assert np.array_equal(d.double().cpu().numpy(), dn.astype(np.float64))
+
+
+def test_quantize_int8_float64_scale_tie(pkg, dev):
+    """A float64 row whose scale sits just above a float16 tie once rounded to
+    float32: the stored scale follows torch's cast through float32."""
+    import torch
+    s_want = 1 + 2 ** -11 + 2 ** -40
+    t = torch.tensor([[[[127.0 * s_want, 63.0, -1.0, 0.25]]]], dtype=torch.float64)
+    q, s = pkg.long_context.PagedCompressedKVCache._quantize_int8(t.to(dev))
+    qn, sn = no.paged_quantize_int8(t.numpy(), "float64")
+    assert float(s.cpu()[0, 0, 0, 0]) == 1.0
+    assert np.array_equal(s.cpu().numpy().view(np.uint16), sn.view(np.uint16))
+    assert np.array_equal(q.cpu().numpy(), qn)
 
 
 def test_paged_cache_compression_and_accuracy(pkg, dev):
@@ -95,7 +110,30 @@ def test_paged_cache_eviction_known_answer(pkg, dev):
     assert len(cache._pages) == 5 and cache.resident_tokens == 5 * 16
     means = [round(p[0].mean().item(), 1) for p in cache.iter_dequantized_pages()]
     assert means == [1.0, 2.0, 10.0, 11.0, 12.0]
-    assert len(cache._buffers) == 5                 # page buffers recycled, not reallocated
+
+
+def test_paged_cache_evicted_page_kept_for_its_holder(pkg, dev):
+    """The reference's pop (long_context.py:255-257) leaves a page that a
+    caller still holds intact: later appends must not write into it.  Chunks
+    in float64 (the reference accepts any float tensor)."""
+    import torch
+    lc = pkg.long_context
+    cache = lc.PagedCompressedKVCache(page_size=16, max_resident_pages=3, sink_pages=1)
+    held = None
+    for i in range(8):
+        k = torch.full((1, 2, 16, 8), float(i + 1), dtype=torch.float64, device=dev)
+        cache.append(k, -k)
+        if i == 1:
+            held = cache._pages[1]                   # page 2, evicted at i == 3
+            snap = [t.clone() for t in held]
+    assert cache.total_tokens_seen == 8 * 16
+    assert all(torch.equal(a, b) for a, b in zip(held, snap))
+    assert all(p is not held for p in cache._pages)
+    kd = lc.PagedCompressedKVCache._dequantize_int8(held[0], held[1], torch.float64)
+    qn, sn = no.paged_quantize_int8(np.full((1, 2, 16, 8), 2.0), "float64")
+    assert np.array_equal(kd.cpu().numpy(), no.paged_dequantize_int8(qn, sn, "float64"))
+    means = [round(p[0].mean().item(), 1) for p in cache.iter_dequantized_pages(torch.float64)]
+    assert means == [1.0, 7.0, 8.0]
 
 
 def test_paged_cache_ragged_chunks_match_reference_pages(pkg, dev):

@@ -45,7 +45,8 @@ def dev_forward(pkg, nat, x_t, dtype_tag, out_dtype):
 
 
 @pytest.mark.parametrize("name", ["linear_k256_m200_b3", "linear_d8_k128_m96_b2_cb64",
-                                  "linear_k2560_m64_b1"])
+                                  "linear_k2560_m64_b1", "linear_d64_k512_m72_b3",
+                                  "linear_d48_k480_m40_b2_cb100"])
 def test_host_api_golden(pkg, name):
     g = np.load(os.path.join(GOLDEN, name + ".npz"))
     M, G = g["codes"].shape
@@ -152,9 +153,13 @@ def test_baseline_gate_up_bf16(pkg, dev, B):
 
 
 @pytest.mark.parametrize("M,K,D,Kcb,bias", [(300, 200, 8, 256, True), (513, 384, 24, 100, False),
-                                            (64, 32, 32, 256, True), (1, 16, 16, 256, False)])
+                                            (64, 32, 32, 256, True), (1, 16, 16, 256, False),
+                                            (200, 768, 64, 256, True), (96, 1536, 512, 64, False),
+                                            (40, 300, 300, 256, True)])
 def test_odd_shapes(pkg, dev, M, K, D, Kcb, bias):
-    """Groups not a multiple of 16, block_dim != 16, small codebooks, one row."""
+    """Groups not a multiple of 16, block_dim != 16 (up to groups wider than
+    the 256-thread LUT-build workgroup and a single group), small codebooks,
+    one row."""
     d = gen.linear(M, K, B=5, D=D, Kcb=Kcb, seed=M + K, scales="u", bias=bias, density=0.02)
     nat = native_linear(pkg, d, M, K, D, Kcb)
     y = nat.forward(d["x"])
@@ -386,6 +391,38 @@ def test_grouped_linears(pkg, dev):
                                      np.zeros(0, np.float32))
         want = cpu.linear_forward(d["x"], d["codebook"], d["codes"], d["scales"], d["bias"], *csr)
         assert rel_err(y.cpu().numpy()[None], want) < F32_TOL, (M, K)
+
+
+def test_grouped_linears_wide_inputs(pkg, dev):
+    """Items whose input exceeds the bank kernel's LDS (K > 16384, e.g. an
+    18944-wide down projection) run on the single-linear path inside the same
+    grouped call; the others stay on the bank kernel.  Also a call of wide
+    items only."""
+    import torch
+    shapes = [(300, 18944, True), (700, 2560, True), (96, 20480, False), (64, 16384, True)]
+    nats, xs, ys, ds = [], [], [], []
+    for i, (M, K, outl) in enumerate(shapes):
+        d = gen.linear(M, K, B=1, seed=150 + i, scales="u", bias=True, outliers=outl)
+        nats.append(native_linear(pkg, d, M, K))
+        xs.append(torch.from_numpy(d["x"][0]).to(dev))
+        ys.append(torch.full((M,), 7.0, device=dev))
+        ds.append(d)
+    for sel in ([0, 1, 2, 3], [2, 0]):
+        n = len(sel)
+        H = (ctypes.c_void_p * n)(*[nats[i].handle for i in sel])
+        X = (ctypes.c_void_p * n)(*[xs[i].data_ptr() for i in sel])
+        Y = (ctypes.c_void_p * n)(*[ys[i].data_ptr() for i in sel])
+        rc = pkg.lib().ojasx_linear_forward_grouped_device(H, n, X, Y, None)
+        assert rc == 0, pkg.lib().ojasx_get_last_error()
+        torch.cuda.synchronize()
+        for i in sel:
+            M, K, outl = shapes[i]
+            d = ds[i]
+            csr = d["csr"] if outl else (np.zeros(M + 1, np.int32), np.zeros(0, np.int32),
+                                         np.zeros(0, np.float32))
+            want = cpu.linear_forward(d["x"], d["codebook"], d["codes"], d["scales"], d["bias"],
+                                      *csr)
+            assert rel_err(ys[i].cpu().numpy()[None], want) < F32_TOL, (M, K)
 
 
 def test_grouped_linears_repeat_and_errors(pkg, dev):

@@ -34,6 +34,17 @@ def test_host_api_golden_skip_rules(pkg):
     assert rel_err(y, g["y"]) < 1e-5
 
 
+@pytest.mark.parametrize("name", ["moe_d24_e16_h96_i72", "moe_d64_e8_h256_i128"])
+def test_host_api_golden_block_sizes(pkg, name):
+    """block_dim 24 (not dividing 32) and 64 against the compiled reference."""
+    g = np.load(os.path.join(GOLDEN, name + ".npz"))
+    E, two_i, _ = g["gu_codes"].shape
+    H = g["dn_codes"].shape[1]
+    nat = make_native(pkg, g, E, H, two_i // 2, g["idx"].size)
+    y = nat.forward(g["x"], g["idx"], g["w"])
+    assert rel_err(y, g["y"]) < 1e-5
+
+
 def test_host_api_reference_t6(pkg):
     t6 = gen.reference_t6()
     nat = make_native(pkg, t6, 512, 256, 64)
@@ -170,6 +181,8 @@ def device_moe(pkg, dev, nat, x_t, idx, w, k, dtype_tag=0):
     (40, 480, 208, 20, 16),    # partial input/intermediate slices; 20 slots > 16 waves
     (64, 512, 256, 32, 16),    # the largest k of the single-kernel stages
     (48, 256, 96, 6, 8),       # block_dim 8: LUT-build + gather path
+    (16, 96, 72, 6, 24),       # block_dim 24 (does not divide 32)
+    (12, 640, 384, 4, 128),    # block_dim 128
     (24, 4352, 1152, 4, 16),   # 17 input slices, 5 intermediate slices
 ])
 def test_moe_shapes(pkg, dev, E, H, I, k, D, T):
@@ -223,6 +236,23 @@ def test_moe_by_expert_many_pairs_per_expert(pkg, dev, dtype_tag):
         want = cpu.moe_forward(xr[t], m["cb_in"], m["cb_down"], m["gu_codes"], m["gu_scales"],
                                m["dn_codes"], m["dn_scales"], idx[t], w[t])
         assert rel_err(y[t], want) < (1e-5 if dtype_tag == 0 else 1e-2), t
+
+
+@pytest.mark.parametrize("H,I", [(18432, 64), (256, 17408), (36864, 48)])
+def test_moe_wide_hidden_or_intermediate(pkg, dev, H, I):
+    """16 tokens with a hidden (or intermediate) size beyond the by-expert
+    kernel's LDS: the call takes a path that fits (the per-slot kernels, or
+    the L2-LUT kernels where even their staged input does not fit)."""
+    import torch
+    E, k, T = 6, 2, 16
+    m = gen.moe(E=E, H=H, I=I, T=T, seed=H % 89, scales="u")
+    nat = make_native(pkg, m, E, H, I, k)
+    idx, w = cpu.router_topk(m["logits"], k, renorm=True)
+    y = device_moe(pkg, dev, nat, torch.from_numpy(m["x"]).to(dev), idx, w, k)
+    for t in range(T):
+        want = cpu.moe_forward(m["x"][t], m["cb_in"], m["cb_down"], m["gu_codes"], m["gu_scales"],
+                               m["dn_codes"], m["dn_scales"], idx[t], w[t])
+        assert rel_err(y[t], want) < 1e-5, t
 
 
 @pytest.mark.parametrize("E", [4096, 16384])   # by-expert path / its plan LDS too small: per slot

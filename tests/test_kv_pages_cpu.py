@@ -31,7 +31,7 @@ def rows_with_edges(torch, dtype, n=512, d=40, seed=0):
     return t.to(dtype)
 
 
-@pytest.mark.parametrize("kind", ["float32", "bfloat16", "float16"])
+@pytest.mark.parametrize("kind", ["float32", "bfloat16", "float16", "float64"])
 def test_int8_oracle_matches_torch_expression(kind):
     """Bit-exact codes and scales, and the dequantised values, against the
     reference expressions evaluated by torch on rows that include zero rows,
@@ -43,12 +43,29 @@ def test_int8_oracle_matches_torch_expression(kind):
     if kind == "float16":
         t = t[1:]
     q, s = torch_reference_quantise(t)
-    qn, sn = no.paged_quantize_int8(t.float().numpy(), kind)
+    qn, sn = no.paged_quantize_int8(t.double().numpy() if kind == "float64" else
+                                    t.float().numpy(), kind)
     assert np.array_equal(qn, q.numpy())
     assert np.array_equal(sn.view(np.uint16), s.numpy().view(np.uint16))
     d = (q.to(torch.float32) * s.to(torch.float32)).to(dtype)
     dn = no.paged_dequantize_int8(qn, sn, kind)
-    assert np.array_equal(dn.view(np.uint32), d.float().numpy().view(np.uint32))
+    assert np.array_equal(dn, d.double().numpy() if kind == "float64" else d.float().numpy())
+    assert dn.dtype == (np.float64 if kind == "float64" else np.float32)
+
+
+def test_int8_oracle_float64_scale_rounds_through_float32():
+    """torch casts a float64 scale to float16 through float32; a direct cast
+    rounds differently when the float32 value is a float16 tie.  A row whose
+    scale is just above such a tie (1 + 2^-11 + 2^-40 in units of 2^k) pins
+    the double rounding, and its codes pin the float64 division."""
+    import torch
+    s_want = 1 + 2 ** -11 + 2 ** -40
+    t = torch.tensor([[127.0 * s_want, 63.0, -1.0]], dtype=torch.float64)
+    q, s = torch_reference_quantise(t)
+    qn, sn = no.paged_quantize_int8(t.numpy(), "float64")
+    assert float(s[0, 0]) == 1.0 and float(np.float16(s_want)) != 1.0
+    assert np.array_equal(sn.view(np.uint16), s.numpy().view(np.uint16))
+    assert np.array_equal(qn, q.numpy())
 
 
 def test_int8_oracle_rounding_steps():

@@ -45,7 +45,8 @@ def test_lut_matches_fp64_dot():
 # ------------------------------------------------------------------- linear --
 
 @pytest.mark.parametrize("name", ["linear_k256_m200_b3", "linear_d8_k128_m96_b2_cb64",
-                                  "linear_k2560_m64_b1"])
+                                  "linear_k2560_m64_b1", "linear_d64_k512_m72_b3",
+                                  "linear_d48_k480_m40_b2_cb100"])
 def test_linear_golden_bit_exact(name):
     g = golden(name)
     y = cpu.linear_forward(g["x"], g["codebook"], g["codes"], g["scales"],
@@ -148,6 +149,18 @@ def test_moe_reference_t6():
 
 def test_moe_golden_skip_rules():
     g = golden("moe_e32_h128_i64")
+    y = cpu.moe_forward(g["x"], g["cb_in"], g["cb_down"], g["gu_codes"], g["gu_scales"],
+                        g["dn_codes"], g["dn_scales"], g["idx"], g["w"])
+    assert np.array_equal(y, g["y"])
+    y64 = no.moe_fp64(g["x"], g["cb_in"], g["cb_down"], g["gu_codes"], g["gu_scales"],
+                      g["dn_codes"], g["dn_scales"], g["idx"], g["w"])
+    assert rel_err(y, y64) < 1e-5
+
+
+@pytest.mark.parametrize("name", ["moe_d24_e16_h96_i72", "moe_d64_e8_h256_i128"])
+def test_moe_golden_block_sizes(name):
+    """block_dim 24 (not dividing 32) and 64, written by the compiled reference."""
+    g = golden(name)
     y = cpu.moe_forward(g["x"], g["cb_in"], g["cb_down"], g["gu_codes"], g["gu_scales"],
                         g["dn_codes"], g["dn_scales"], g["idx"], g["w"])
     assert np.array_equal(y, g["y"])
