@@ -153,9 +153,10 @@ struct MoEBankLaunch {
     const void *x;              // xs 0: [T][K] fp32, 1: bf16, 2: [P][2K] fp32 gate|up rows
     float *y;                   // [P][M]
     const int *idx;
-    const int2 *work;
+    const float *w;             // slot weights (read by the direct mapping)
+    const int2 *work;           // the plan's work list, or null: workgroup = (pair, row block)
     const int *n_work;          // device count of work entries
-    int M, K, k, max_work, xs;
+    int M, K, k, E, max_work, xs;   // direct mapping: max_work = pairs x row blocks
 };
 int launch_moe_bank(const MoEBankLaunch &l, hipStream_t st);
 // One tall batch-1 fp32 linear with the RMSNorm prologue (lut_group.hip):

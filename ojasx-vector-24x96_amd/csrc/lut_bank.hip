@@ -399,21 +399,34 @@ struct MoEBankParams {
     const void *x;              // gate/up: [T][K]; down: [P][2K] fp32
     float *y;                   // [P][M]
     const int *idx;             // [P] expert of each pair
-    const int2 *work;           // [n] (pair, block << 16 | expert)
+    const float *w;             // [P] slot weights (direct mapping: the skip rule)
+    const int2 *work;           // [n] (pair, block << 16 | expert), or null: direct mapping
     const int *n_work;          // n
-    int M, K, k;                // rows, inputs, slots per token
+    int M, K, k, E, nb;         // rows, inputs, slots per token, experts, row blocks per pair
 };
 
 template <int XS>
 __global__ __launch_bounds__(kBNT) void moe_bank_kernel(MoEBankParams p) {
     __shared__ float L[256 * kLutRow];
     extern __shared__ float xs[];
-    const int n = *p.n_work;
-    const int q = (n + 7) >> 3;
-    const int pos = (int)(blockIdx.x & 7) * q + (int)(blockIdx.x >> 3);
-    if (pos >= n || (int)(blockIdx.x >> 3) >= q) return;
-    const int2 wk = p.work[pos];
-    const int pr = wk.x, e = wk.y & 0xffff;          // the expert travels with the entry
+    int pr, e, blk;
+    if (p.work) {
+        const int n = *p.n_work;
+        const int q = (n + 7) >> 3;
+        const int pos = (int)(blockIdx.x & 7) * q + (int)(blockIdx.x >> 3);
+        if (pos >= n || (int)(blockIdx.x >> 3) >= q) return;
+        const int2 wk = p.work[pos];
+        pr = wk.x;
+        e = wk.y & 0xffff;                            // the expert travels with the entry
+        blk = wk.y >> 16;
+    } else {
+        // direct mapping, no plan: workgroup = (pair, row block) in pair
+        // order; skipped pairs (ojasx_lut_cpu.cpp:284-286) exit at once
+        pr = (int)blockIdx.x / p.nb;
+        blk = (int)blockIdx.x - pr * p.nb;
+        e = p.idx[pr];
+        if (e < 0 || e >= p.E || fabsf(p.w[pr]) < 1e-8f) return;
+    }
     const void *x;
     if constexpr (XS == XS_SWIGLU)
         x = static_cast<const float *>(p.x) + (size_t)pr * 2 * p.K;
@@ -423,7 +436,7 @@ __global__ __launch_bounds__(kBNT) void moe_bank_kernel(MoEBankParams p) {
         x = static_cast<const float *>(p.x) + (size_t)(pr / p.k) * p.K;
     const BankBlock bb{p.codes_b + (size_t)e * p.expert_bytes, p.cb3,
                        p.scales + (size_t)e * p.M, nullptr, nullptr, nullptr, nullptr,
-                       x, p.y + (size_t)pr * p.M, p.K, p.M, (wk.y >> 16) * kBRows};
+                       x, p.y + (size_t)pr * p.M, p.K, p.M, blk * kBRows};
     bank_block<XS>(bb, L, xs);
 }
 
@@ -540,10 +553,11 @@ int launch_moe_plan(const int *idx, const float *w, int P, int E, int nb_gu, int
 }
 
 int launch_moe_bank(const MoEBankLaunch &l, hipStream_t st) {
-    MoEBankParams p{l.codes_b, l.expert_bytes, static_cast<const v8bf *>(l.cb3), l.scales, l.x, l.y, l.idx, l.work,
-                    l.n_work, l.M, l.K, l.k};
+    const int nb = (l.M + kBRows - 1) / kBRows;
+    MoEBankParams p{l.codes_b, l.expert_bytes, static_cast<const v8bf *>(l.cb3), l.scales, l.x, l.y, l.idx,
+                    l.w, l.work, l.n_work, l.M, l.K, l.k, l.E, nb};
     const size_t lds = round_up((size_t)(l.K / 16), 32) * kXRow * sizeof(float);
-    const int grid = 8 * ((l.max_work + 7) / 8);
+    const int grid = l.work ? 8 * ((l.max_work + 7) / 8) : l.max_work;
     int rc = OJASX_OK;
     if (l.xs == XS_SWIGLU) {
         static size_t gr = 0;

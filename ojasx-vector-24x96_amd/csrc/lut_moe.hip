@@ -22,10 +22,11 @@
 //    grouped LUT GEMVs in slot order, each workgroup building its 16-group
 //    LUT slices with MFMA -- moe_gu_group (gate/up + SwiGLU), moe_dn_group
 //    (down, scaled), moe_combine.
-//  * block_dim 16, more tokens, aligned activations: the pairs grouped by
-//    expert (moe_plan, a counting sort) on the bank-layout LUT-GEMV of
-//    lut_bank.hip -- moe_bank (gate/up), moe_bank (SwiGLU input, down),
-//    moe_combine -- so each distinct expert's codes stream from HBM once.
+//  * block_dim 16, more tokens, aligned activations: the pairs on the
+//    bank-layout LUT-GEMV of lut_bank.hip -- moe_bank (gate/up), moe_bank
+//    (SwiGLU input, down), moe_combine -- from 128 tokens grouped by expert
+//    first (moe_plan, a counting sort), so each distinct expert's codes
+//    stream from HBM once.
 //  * other block sizes (any divisor of H and I): LUT_in build, moe_gateup
 //    (gathers from the L2-resident LUT, SwiGLU), moe_lut_down (the pair's
 //    LUT_down rows), moe_down, moe_combine.
@@ -766,7 +767,16 @@ constexpr int kGroupMinTokens = 3;
 // 151 MB banks: 33.4 vs 34.2 us at 16 tokens, 48.2 vs 51.9 at 32, 85.4 vs
 // 87.1 at 64, 264 vs 286 at 256 (bank vs grouped per slot); 27.1 vs 26.7 at 8.
 constexpr int kBankMinTokens = 16;
-constexpr size_t kBankMaxPairs = 16384;
+constexpr size_t kBankMaxPairs = 16384;   // sorted by expert: the plan's LDS
+// From this many tokens a plan launch sorts the pairs by expert first; below
+// it workgroups map straight to (pair, row block): a repeated expert's codes
+// are read once per pair (about 15 % more code bytes at 16 tokens) but the
+// plan's dependent launch leaves the chain.  Measured per call (same box,
+// sorted vs direct): 29.6 vs 26.5 us at 16 tokens, 44.0 vs 41.6 at 32, 75.3
+// vs 72.9 at 64, 104.7 vs 104.0 at 96, 132.5 vs 131.4 at 128, 237.3 vs
+// 240.3 at 256: the gathers and LUT builds per pair, not the code stream,
+// set the time.
+constexpr int kBankSortMinTokens = 128;
 
 template <typename T>
 int moe_forward_dec(MoE *m, const void *x, const int *idx, const float *w, void *y, int T_, int k,
@@ -914,25 +924,31 @@ int moe_forward_group(MoE *m, const void *x, const int *idx, const float *w, voi
     return OJASX_OK;
 }
 
-// Routed pairs grouped by expert on the bank kernel (lut_bank.hip): a plan
-// launch sorts the valid pairs by expert into work lists of (pair, 512-row
-// block); gate/up then writes s_m * (gate | up) rows per pair, down stages
-// silu(gate) * up as its input and writes s_dn * down per pair, and the
-// ordered combine sums w_j * down_j over the slots.  The pairs of one expert
-// run back to back on one XCD, so its codes stream through one L2.
+// Routed pairs on the bank kernel (lut_bank.hip): from kBankSortMinTokens
+// tokens a plan launch sorts the valid pairs by expert into work lists of
+// (pair, 512-row block), so the pairs of one expert run back to back on one
+// XCD and its codes stream through one L2; below it workgroups map straight
+// to (pair, row block).  Gate/up writes s_m * (gate | up) rows per pair, down
+// stages silu(gate) * up as its input and writes s_dn * down per pair, and
+// the ordered combine sums w_j * down_j over the slots.
 template <typename T>
 int moe_forward_bank(MoE *m, const void *x, const int *idx, const float *w, void *y, int T_, int k,
-                     hipStream_t st) {
+                     bool sorted, hipStream_t st) {
     const size_t P = (size_t)T_ * k;
     const int nb_gu = (2 * m->I + kBankRows - 1) / kBankRows, nb_dn = (m->H + kBankRows - 1) / kBankRows;
-    int rc = m->work.ensure(P * (nb_gu + nb_dn) * sizeof(int2));
-    if (!rc) rc = m->nwork.ensure(2 * sizeof(int));
-    if (!rc) rc = m->gu_out.ensure(P * 2 * m->I * sizeof(float));
+    int rc = m->gu_out.ensure(P * 2 * m->I * sizeof(float));
     if (!rc) rc = m->dout.ensure(P * m->H * sizeof(float));
+    if (!rc && sorted) rc = m->work.ensure(P * (nb_gu + nb_dn) * sizeof(int2));
+    if (!rc && sorted) rc = m->nwork.ensure(2 * sizeof(int));
     if (rc) return rc;
-    int2 *work_gu = m->work.as<int2>(), *work_dn = work_gu + P * nb_gu;
-    rc = launch_moe_plan(idx, w, (int)P, m->E, nb_gu, nb_dn, work_gu, work_dn, m->nwork.as<int>(), st);
-    if (rc) return rc;
+    int2 *work_gu = nullptr, *work_dn = nullptr;
+    if (sorted) {
+        work_gu = m->work.as<int2>();
+        work_dn = work_gu + P * nb_gu;
+        rc = launch_moe_plan(idx, w, (int)P, m->E, nb_gu, nb_dn, work_gu, work_dn,
+                             m->nwork.as<int>(), st);
+        if (rc) return rc;
+    }
     MoEBankLaunch l{};
     l.codes_b = m->gub.as<uint8_t>();
     l.expert_bytes = m->gub_bytes;
@@ -941,11 +957,13 @@ int moe_forward_bank(MoE *m, const void *x, const int *idx, const float *w, void
     l.x = x;
     l.y = m->gu_out.as<float>();
     l.idx = idx;
+    l.w = w;
     l.work = work_gu;
     l.n_work = m->nwork.as<int>();
     l.M = 2 * m->I;
     l.K = m->H;
     l.k = k;
+    l.E = m->E;
     l.max_work = (int)(P * nb_gu);
     l.xs = std::is_same<T, float>::value ? 0 : 1;
     rc = launch_moe_bank(l, st);
@@ -957,7 +975,7 @@ int moe_forward_bank(MoE *m, const void *x, const int *idx, const float *w, void
     l.x = m->gu_out.as<float>();
     l.y = m->dout.as<float>();
     l.work = work_dn;
-    l.n_work = m->nwork.as<int>() + 1;
+    l.n_work = sorted ? m->nwork.as<int>() + 1 : nullptr;
     l.M = m->H;
     l.K = m->I;
     l.max_work = (int)(P * nb_dn);
@@ -1000,14 +1018,18 @@ int moe_forward(MoE *m, const void *x, const int *idx, const float *w, void *y, 
         const bool ok = m->D == 16 && k <= 32 && aligned &&
                         (size_t)(kCB * 16 + (size_t)k * m->Si * 256) * 4 + kDecStatic <= kMaxLds &&
                         (size_t)(kCB * 16 + m->Sin * 256) * 4 + kDecStatic <= kMaxLds;
-        // grouped by expert: expert ids fit the work entries' 16 bits and the
-        // plan kernel's LDS holds 3 E + P ints
+        // on the bank kernel; sorted by expert, the expert ids must fit the
+        // work entries' 16 bits and the plan kernel's LDS hold 3 E + P ints
         const size_t P = (size_t)T_ * k;
-        if (m->D == 16 && aligned && T_ >= kBankMinTokens && m->gub.ptr && P <= kBankMaxPairs &&
-            m->E <= 65535 && (3 * (size_t)m->E + P) * sizeof(int) <= kMaxLds &&
-            bank_fits(m->H) && bank_fits(m->I))
-            return dtype == OJASX_DTYPE_F32 ? moe_forward_bank<float>(m, x, idx, w, y, T_, k, st)
-                                            : moe_forward_bank<__hip_bfloat16>(m, x, idx, w, y, T_, k, st);
+        const bool sorted = T_ >= kBankSortMinTokens;
+        const bool plan_fits = P <= kBankMaxPairs && m->E <= 65535 &&
+                               (3 * (size_t)m->E + P) * sizeof(int) <= kMaxLds;
+        const int nb = (std::max(2 * m->I, m->H) + kBankRows - 1) / kBankRows;
+        if (m->D == 16 && aligned && T_ >= kBankMinTokens && m->gub.ptr && bank_fits(m->H) &&
+            bank_fits(m->I) && (sorted ? plan_fits : P * nb <= 0x7fffffff))
+            return dtype == OJASX_DTYPE_F32
+                       ? moe_forward_bank<float>(m, x, idx, w, y, T_, k, sorted, st)
+                       : moe_forward_bank<__hip_bfloat16>(m, x, idx, w, y, T_, k, sorted, st);
         // grouped per slot: the staged input and two LUT buffers fit the LDS
         const bool group_fits =
             (size_t)std::max(m->Sin, m->Si) * 256 * sizeof(float) + slices::lut_bytes(kGroupDB) <=

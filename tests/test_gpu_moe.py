@@ -217,12 +217,14 @@ def test_moe_unaligned_activations(pkg, dev, baseline_moe, dtype_tag):
         assert rel_err(y[t], want) < (1e-5 if dtype_tag == 0 else 1e-2)
 
 
+@pytest.mark.parametrize("T", [64, 160])
 @pytest.mark.parametrize("dtype_tag", [0, 1])
-def test_moe_by_expert_many_pairs_per_expert(pkg, dev, dtype_tag):
-    """256 routed pairs over 8 experts (32 pairs each on average, the plan's
-    expert-sorted work lists), with skipped slots, fp32 and bf16 inputs."""
+def test_moe_by_expert_many_pairs_per_expert(pkg, dev, dtype_tag, T):
+    """256 and 640 routed pairs over 8 experts (32 and 80 per expert on
+    average): mapped straight to (pair, row block) at 64 tokens, through the
+    plan's expert-sorted work lists at 160; skipped slots, fp32 and bf16."""
     import torch
-    E, H, I, k, T = 8, 256, 96, 4, 64
+    E, H, I, k = 8, 256, 96, 4
     m = gen.moe(E=E, H=H, I=I, T=T, seed=77, scales="u")
     nat = make_native(pkg, m, E, H, I, k)
     idx, w = cpu.router_topk(m["logits"], k, renorm=True)
@@ -255,12 +257,14 @@ def test_moe_wide_hidden_or_intermediate(pkg, dev, H, I):
         assert rel_err(y[t], want) < 1e-5, t
 
 
-@pytest.mark.parametrize("E", [4096, 16384])   # by-expert path / its plan LDS too small: per slot
-def test_moe_many_experts(pkg, dev, E):
-    """Large expert counts at 16 tokens: 4096 experts run the plan kernel in
-    49 KB of LDS, 16384 would need 196 KB and take the per-slot path."""
+@pytest.mark.parametrize("E,T", [(4096, 16), (16384, 16), (4096, 128), (16384, 128)])
+def test_moe_many_experts(pkg, dev, E, T):
+    """Large expert counts: at 16 tokens the bank kernel maps workgroups to
+    (pair, row block) directly; at 128 tokens 4096 experts run the plan
+    kernel (sorted by expert) in 50 KB of LDS, 16384 would need 198 KB and
+    take the per-slot path."""
     import torch
-    H, I, k, T = 64, 32, 4, 16
+    H, I, k = 64, 32, 4
     m = gen.moe(E=E, H=H, I=I, T=T, seed=E % 97, scales="u")
     nat = make_native(pkg, m, E, H, I, k)
     idx, w = cpu.router_topk(m["logits"], k, renorm=True)
