@@ -19,8 +19,10 @@ the events time the GPU running them, not the host issuing them.
 ``roofline`` relates the algorithmic code bytes of one launch to the
 kernel's own average duration, measured live with the library's start/stop
 events (hipExtLaunchKernelGGL: the kernel's begin and end on the launch
-stream) over max(K, 200) launches that also run back to back behind a gate;
-``gate_held`` says the host had enqueued every launch before the gate ended.
+stream) over max(K, 200) launches that also run back to back behind a gate
+(``gate_held``: the host had enqueued every launch before the gate ended);
+for a call that launches one kernel the call period bounds it too, and the
+smaller bound is used (kernel_us).
 ``traffic`` is the HBM bytes per launch from the rocprofv3
 FETCH_SIZE / WRITE_SIZE summaries committed under profiles/ (lines
 ``traffic_bytes_per_launch[<leg>]: <bytes>``).  ``cpu_baseline`` times the
@@ -209,17 +211,29 @@ def roofline(code_bytes, all_bytes, kernel_us, kernel, calls, traffic=None):
             "frac_all_bytes": frac(all_bytes, kernel_us)}
 
 
-def leg(us, kern, name, code_bytes, all_bytes, key, held=None, per_call=1):
-    """Compact record of one leg: call period, the dominant kernel's average
-    (``kus``, over ``n`` launches), its fractions of 8 TB/s on code bytes and
-    on all compulsory bytes per launch, and its measured traffic per launch.
-    ``per_call`` is the dominant kernel's launches per call."""
-    kus = kern[name]["avg_us"]
+def kernel_us(kern, name, us):
+    """(kernel duration, library-event average) in us.  The duration is the
+    event average, or, when each call launches this one kernel and nothing
+    else, the call period if that is smaller: those calls run back to back,
+    so a kernel lasts at most one period, while the events' own overhead
+    (about 0.2 us on long kernels, up to 1.2 us on 3 us ones) can lift their
+    average above it.  Both are upper bounds of the kernel's duration."""
+    ev = kern[name]["avg_us"]
+    single = len(kern) == 1
+    return (min(ev, us) if single else ev), ev
+
+
+def leg(us, kern, name, code_bytes, all_bytes, key, held=None):
+    """Compact record of one leg: call period, the dominant kernel's duration
+    (``kus``, see kernel_us; ``kus_events`` when the event average is larger;
+    ``n`` launches timed), its fractions of 8 TB/s on code bytes and on all
+    compulsory bytes per launch, and its measured traffic per launch."""
+    kus, ev = kernel_us(kern, name, us)
     out = {"us": round(us, 3), "kernel": short(name), "kus": round(kus, 3),
            "n": kern[name]["calls"], "code_B": int(code_bytes), "frac": frac(code_bytes, kus),
            "frac_all": frac(all_bytes, kus), "traffic": TRAFFIC.get(key)}
-    if per_call != 1:
-        out["per_call"] = per_call
+    if ev > kus:
+        out["kus_events"] = round(ev, 3)
     if held is False:
         out["gate_held"] = False
     return out
@@ -330,7 +344,7 @@ def linear_leg(b, hs, base, wbytes, M, K, B, dt, steps, warmup, key):
     code_bytes = M * (K // 16)
     all_bytes = wbytes + B * K * x.element_size() + B * M * x.element_size()
     out = leg(us, kern, name, code_bytes, all_bytes, key, held and kheld)
-    out["TFLOPs"] = round(2.0 * M * K * B / (kern[name]["avg_us"] * 1e-6) / 1e12, 2)
+    out["TFLOPs"] = round(2.0 * M * K * B / (out["kus"] * 1e-6) / 1e12, 2)
     assert L.ojasx_linear_forward_device(hs[0], xp, yp, B, dt, b.sp) == 0
     torch.cuda.synchronize()
     return out, y.float().cpu().numpy()
@@ -397,7 +411,7 @@ def bench_sustained(b, handles, base, wbytes):
     all_bytes = n * (wbytes + K_GU * 4 + M_GU * 4)
     out = leg(us, kern, kname, code_bytes, all_bytes, "sustained" if n == 160 else None,
               held and kheld)
-    out.update({"instances": n, "us_per_linear": round(kern[kname]["avg_us"] / n, 4)})
+    out.update({"instances": n, "us_per_linear": round(out["kus"] / n, 4)})
     return out
 
 
@@ -893,8 +907,10 @@ def headline(b, args, handles, base, wbytes):
     all_bytes = wbytes + K_GU * 4 + M_GU * 4
     kern, kheld = b.kernels(call, args.steps)
     kname = dominant(kern)
-    rf = roofline(code_bytes, all_bytes, kern[kname]["avg_us"], kname, kern[kname]["calls"],
-                  TRAFFIC.get("headline"))
+    kus, ev = kernel_us(kern, kname, us_call)
+    rf = roofline(code_bytes, all_bytes, kus, kname, kern[kname]["calls"], TRAFFIC.get("headline"))
+    if ev > kus:
+        rf["kernel_events_us"] = round(ev, 4)
     rf["call_period_frac"] = frac(code_bytes, us_call)
     rf["gate_held"] = bool(held and kheld)
 
