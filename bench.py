@@ -581,7 +581,8 @@ def moe_sustained_one(b, banks, T, n_layers=16, replays=5):
     kb = moe_dominant_bytes(name, U)
     return {"us": round(us, 3), "experts": U, "code_B": int(code), "frac_call": frac(code, us),
             "kernel": short(name), "kus": round(kern[name]["avg_us"], 3), "n": calls,
-            "frac": frac(kb, kern[name]["avg_us"]), "traffic": TRAFFIC.get(f"moe_sus_T{T}"),
+            "frac": frac(kb, kern[name]["avg_us"]),
+            "traffic": TRAFFIC.get(f"moe_sus_T{T}", TRAFFIC.get(f"moe_T{T}")),
             "kernels_us": per_call_us(kern, calls), "graph_equals_eager": same}
 
 
