@@ -440,6 +440,129 @@ __global__ __launch_bounds__(kBNT) void moe_bank_kernel(MoEBankParams p) {
     bank_block<XS>(bb, L, xs);
 }
 
+// MoE gate/up, token-major, for inputs of at most 4 slices (K <= 2048).  The
+// input codebook is shared by all experts, so a token's LUT serves every slot
+// the token is routed to.  Workgroup = (token t, up to R consecutive units),
+// unit u = (slot u / nb, 512-row block u % nb) of the token: all slices of
+// LUT_t are built once (the two [256][64]-word buffer pairs of bank_block,
+// slices 0-1 and 2-3, 128 KB), one barrier, then the units' codes stream
+// through the gathers with no barrier at all, unit i + 1's codes and scales
+// in flight while unit i gathers.  Skipped slots (expert outside [0, E) or
+// |w| < 1e-8, ojasx_lut_cpu.cpp:284-286) are passed over.  Each row sees the
+// same LUT entries in the same order as in moe_bank_kernel: identical results.
+struct MoEGuTokenParams {
+    const uint8_t *codes_b;     // [E][bank layout of M x G]
+    size_t expert_bytes;
+    const v8bf *cb3;            // [256][2][3] the codebook's bf16 pieces
+    const float *scales;        // [E][M]
+    const void *x;              // [T][K] fp32 or bf16
+    float *y;                   // [P][M]
+    const int *idx;             // [P]
+    const float *w;             // [P]
+    int M, K, k, E, nb, R, cpt; // rows, inputs, slots per token, experts, blocks per pair, units per workgroup, workgroups per token
+};
+constexpr int kTokMaxUnits = 8;
+
+// 16 waves in two teams of 8: both teams share the LUT, team 0 builds slices
+// 0-1 and team 1 slices 2-3, and team q runs the units i = q, q + 2, ... of
+// the workgroup's list (one team of 8 waves measured 6-7 % slower: two waves
+// per SIMD leave the gathers' LDS latency exposed).
+constexpr int kTokThreads = 2 * kBNT;
+template <int XS>
+__global__ __launch_bounds__(kTokThreads) void moe_gu_token_kernel(MoEGuTokenParams p) {
+    extern __shared__ float sm[];
+    float *const Lq[2] = {sm, sm + 256 * kLutRow};   // slices 0-1, slices 2-3
+    float *xs = sm + 2 * 256 * kLutRow;
+    const int tid = threadIdx.x, lane = tid & 63, wt_ = tid >> 6, h = lane >> 5, g = lane & 31;
+    const int w = wt_ & 7, team = wt_ >> 3;
+    const int t = (int)blockIdx.x / p.cpt, c = (int)blockIdx.x - t * p.cpt;
+    const int K = p.K, G = K >> 4, S = (G + 31) >> 5, M = p.M;
+    const int u0 = c * p.R, u1 = min(u0 + p.R, p.k * p.nb);
+    const int rb_last = ((M + 63) >> 6) - 1;
+
+    // ---- the units' slots (L2), then the first valid unit's codes (HBM)
+    unsigned mask = 0;
+#pragma unroll
+    for (int i = 0; i < kTokMaxUnits; ++i) {
+        const int u = min(u0 + i, u1 - 1);
+        const int pr = t * p.k + u / p.nb;
+        const int e = gld(p.idx + pr);
+        const float wt = gld(p.w + pr);
+        if (u0 + i < u1 && e >= 0 && e < p.E && fabsf(wt) >= 1e-8f) mask |= 1u << i;
+    }
+    mask &= team ? 0xaaaaaaaau : 0x55555555u;   // this team's units
+    // codes of unit i (all slices, clamped to the last) and its rows' scale;
+    // the unit's expert id is read again here (a cached load) rather than kept
+    // in an array indexed at run time, which would live in scratch
+    auto load_unit = [&](int i, uint4 (&cc)[4][2], float &sc) {
+        const int u = u0 + i, b = u % p.nb;
+        const int e = gld(p.idx + t * p.k + u / p.nb);
+        const int rb = min(b * (kBRows / 64) + w, rb_last);
+        const uint8_t *cp = p.codes_b + (size_t)e * p.expert_bytes + ((size_t)rb * G + g) * 64 + 32 * h;
+#pragma unroll
+        for (int s4 = 0; s4 < 4; ++s4) bank_codes(cp, min(s4, S - 1), cc[s4]);
+        const int m = b * kBRows + 64 * w + 32 * h + g;
+        sc = gld(p.scales + (size_t)e * M + min(m, M - 1));
+    };
+    v8bf a[3];
+    {
+        const v8bf *ap = p.cb3 + ((32 * w + g) * 2 + h) * 3;
+        a[0] = gld(ap);
+        a[1] = gld(ap + 1);
+        a[2] = gld(ap + 2);
+    }
+    uint4 cA[4][2], cB[4][2];
+    float sA = 0.f, sB = 0.f;
+    int iA = mask ? __builtin_ctz(mask) : kTokMaxUnits;
+    if (mask) load_unit(iA, cA, sA);
+    mask &= mask - 1;
+
+    // ---- x_t staged as bf16 pieces, then every slice of LUT_t
+    const void *x;
+    if constexpr (XS == XS_BF16)
+        x = static_cast<const __hip_bfloat16 *>(p.x) + (size_t)t * K;
+    else
+        x = static_cast<const float *>(p.x) + (size_t)t * K;
+    if (tid < kBNT) bank_stage_x<XS>(x, K, xs, tid);
+    __syncthreads();
+#pragma unroll
+    for (int s4 = 0; s4 < 4; ++s4) {
+        if (s4 < S && (s4 >> 1) == team) {
+            v8bf b[3];
+            bank_xop(xs, s4, g, h, b);
+            const v16f d = bank_build(a, b);
+            bank_store(Lq[s4 >> 1], s4 & 1, w, g, h, d);
+        }
+    }
+    __syncthreads();
+
+    // ---- the units: gathers from the resident LUT, the next unit's loads in flight
+    const uint32_t gsel[2] = {4u * g, 4u * g + 128u};
+    auto run = [&](int i, const uint4 (&cc)[4][2], float sc) __attribute__((always_inline)) {
+        float acc[32];
+#pragma unroll
+        for (int j = 0; j < 32; ++j) acc[j] = 0.f;
+#pragma unroll
+        for (int s4 = 0; s4 < 4; ++s4)
+            if (s4 < S) bank_gather(Lq[s4 >> 1], gsel[s4 & 1], cc[s4], acc);
+        const float tot = bank_reduce(acc, lane);
+        const int u = u0 + i, b = u % p.nb;
+        const int m = b * kBRows + 64 * w + 32 * h + g;
+        if (m < M) p.y[(size_t)(t * p.k + u / p.nb) * M + m] = tot * sc;
+    };
+    while (iA < kTokMaxUnits) {
+        const int iB = mask ? __builtin_ctz(mask) : kTokMaxUnits;
+        mask &= mask - 1;
+        if (iB < kTokMaxUnits) load_unit(iB, cB, sB);
+        run(iA, cA, sA);
+        if (iB >= kTokMaxUnits) break;
+        iA = mask ? __builtin_ctz(mask) : kTokMaxUnits;
+        mask &= mask - 1;
+        if (iA < kTokMaxUnits) load_unit(iA, cA, sA);
+        run(iB, cB, sB);
+    }
+}
+
 // The MoE plan, one workgroup: the valid routed pairs (expert id in [0, E),
 // |w| >= 1e-8) sorted by expert (counting sort; the order within an expert
 // does not change any result), expanded into the gate/up and down work lists
@@ -571,6 +694,43 @@ int launch_moe_bank(const MoEBankLaunch &l, hipStream_t st) {
         static size_t gr = 0;
         rc = set_dyn_lds(&moe_bank_kernel<XS_F32>, lds, &gr);
         if (!rc) OJX_LAUNCH(moe_bank_kernel<XS_F32>, dim3(grid), dim3(kBNT), lds, st, p);
+    }
+    if (rc) return rc;
+    OJX_HIP(hipGetLastError());
+    return OJASX_OK;
+}
+
+bool moe_gu_token_fits(int K) { return K % 16 == 0 && K / 16 <= 4 * 32; }
+
+int launch_moe_gu_token(const MoEBankLaunch &l, int T, hipStream_t st) {
+    if (!moe_gu_token_fits(l.K)) {
+        set_error("token-major gate/up: at most 2048 inputs (got %d)", l.K);
+        return OJASX_ERR_INVALID;
+    }
+    const int nb = (l.M + kBRows - 1) / kBRows;
+    const int units = l.k * nb;
+    // about one round of workgroups (one per CU: 128 KB of LUT each), at
+    // least one unit per team and at most kTokMaxUnits units per workgroup
+    const long total = (long)T * units;
+    const int R = (int)std::min<long>(kTokMaxUnits, std::max<long>(2, (total + 255) / 256));
+    const int cpt = (units + R - 1) / R;
+    MoEGuTokenParams p{l.codes_b, l.expert_bytes, static_cast<const v8bf *>(l.cb3), l.scales, l.x, l.y,
+                       l.idx, l.w, l.M, l.K, l.k, l.E, nb, R, cpt};
+    const size_t lds = (size_t)2 * 256 * kLutRow * sizeof(float) +
+                       round_up((size_t)(l.K / 16), 32) * kXRow * sizeof(float);
+    if ((long)T * cpt > 0x7fffffffL) {
+        set_error("token-major gate/up: too many workgroups");
+        return OJASX_ERR_INVALID;
+    }
+    int rc = OJASX_OK;
+    if (l.xs == XS_BF16) {
+        static size_t gr = 0;
+        rc = set_dyn_lds(&moe_gu_token_kernel<XS_BF16>, lds, &gr);
+        if (!rc) OJX_LAUNCH(moe_gu_token_kernel<XS_BF16>, dim3(T * cpt), dim3(kTokThreads), lds, st, p);
+    } else {
+        static size_t gr = 0;
+        rc = set_dyn_lds(&moe_gu_token_kernel<XS_F32>, lds, &gr);
+        if (!rc) OJX_LAUNCH(moe_gu_token_kernel<XS_F32>, dim3(T * cpt), dim3(kTokThreads), lds, st, p);
     }
     if (rc) return rc;
     OJX_HIP(hipGetLastError());

@@ -135,7 +135,7 @@ def test_baseline_moe_bf16(pkg, dev, baseline_moe):
         assert rel_err(y[t].float().cpu().numpy(), want) < 1e-2
 
 
-@pytest.mark.parametrize("T", [1, 4, 20])   # in-place, grouped-per-slot and by-expert paths
+@pytest.mark.parametrize("T", [1, 4, 20, 28])   # in-place, grouped-per-slot, by-expert, token-major
 def test_repeat_deterministic_and_skips(pkg, dev, baseline_moe, T):
     """Skipped slots (id out of range, |w| < 1e-8) and repeated experts within a
     token; repeated calls return identical bits."""
@@ -176,7 +176,7 @@ def device_moe(pkg, dev, nat, x_t, idx, w, k, dtype_tag=0):
 
 # below / from the token count that selects the grouped path; from the one
 # that groups the routed pairs by expert (bank kernel: partial slices, rows)
-@pytest.mark.parametrize("T", [2, 6, 20])
+@pytest.mark.parametrize("T", [2, 6, 20, 28])
 @pytest.mark.parametrize("E,H,I,k,D", [
     (40, 480, 208, 20, 16),    # partial input/intermediate slices; 20 slots > 16 waves
     (64, 512, 256, 32, 16),    # the largest k of the single-kernel stages
@@ -230,6 +230,42 @@ def test_moe_by_expert_many_pairs_per_expert(pkg, dev, dtype_tag, T):
     idx, w = cpu.router_topk(m["logits"], k, renorm=True)
     idx[3, 2] = E + 5                                # out of range: skipped
     w[7, 1] = 0.0                                    # below 1e-8: skipped
+    tdt = torch.float32 if dtype_tag == 0 else torch.bfloat16
+    xt = torch.from_numpy(m["x"]).to(dev).to(tdt)
+    y = device_moe(pkg, dev, nat, xt, idx, w, k, dtype_tag)
+    xr = xt.float().cpu().numpy()
+    for t in range(T):
+        want = cpu.moe_forward(xr[t], m["cb_in"], m["cb_down"], m["gu_codes"], m["gu_scales"],
+                               m["dn_codes"], m["dn_scales"], idx[t], w[t])
+        assert rel_err(y[t], want) < (1e-5 if dtype_tag == 0 else 1e-2), t
+
+
+def test_token_major_rows_equal_bank_rows(pkg, dev, baseline_moe):
+    """Gate/up runs per (pair, row block) below 24 tokens and token-major from
+    24: a token's output row is the same bits either way."""
+    import torch
+    m, nat = baseline_moe
+    idx, w = cpu.router_topk(m["logits"], 10)
+    x = torch.from_numpy(m["x"]).to(dev)
+    y16 = device_moe(pkg, dev, nat, x[:16].contiguous(), idx[:16], w[:16], 10)
+    y32 = device_moe(pkg, dev, nat, x, idx, w, 10)
+    assert np.array_equal(y16, y32[:16])
+
+
+@pytest.mark.parametrize("dtype_tag", [0, 1])
+def test_moe_token_major_full_workgroups(pkg, dev, dtype_tag):
+    """72 tokens x 8 slots x 4 row blocks (the last one partial): eight units
+    per token-major workgroup, the last workgroup of each token short, with
+    skipped and repeated slots."""
+    import torch
+    E, H, I, k, T = 32, 512, 1008, 8, 72
+    m = gen.moe(E=E, H=H, I=I, T=T, seed=4321, scales="u")
+    nat = make_native(pkg, m, E, H, I, k)
+    idx, w = cpu.router_topk(m["logits"], k, renorm=True)
+    idx[4, 3] = -1                                   # out of range: skipped
+    idx[10, 0] = E                                   # out of range: skipped
+    w[20, 7] = 5e-9                                  # below 1e-8: skipped
+    idx[30, 2] = idx[30, 5]                          # repeated expert within a token
     tdt = torch.float32 if dtype_tag == 0 else torch.bfloat16
     xt = torch.from_numpy(m["x"]).to(dev).to(tdt)
     y = device_moe(pkg, dev, nat, xt, idx, w, k, dtype_tag)
