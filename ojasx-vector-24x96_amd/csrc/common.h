@@ -159,10 +159,12 @@ struct MoEBankLaunch {
     int M, K, k, E, max_work, xs;   // direct mapping: max_work = pairs x row blocks
 };
 int launch_moe_bank(const MoEBankLaunch &l, hipStream_t st);
-// The gate/up stage token-major (lut_bank.hip, moe_gu_token_kernel): each
-// token's LUT built once for all its routed slots; inputs of at most 2048.
-bool moe_gu_token_fits(int K);
-int launch_moe_gu_token(const MoEBankLaunch &l, int T, hipStream_t st);
+// A MoE stage with each group's input LUT built once for all its row blocks
+// (lut_bank.hip, moe_resident_kernel): gate/up with groups = tokens and slots
+// = k (inputs of at most 2048), down (xs 2) with groups = pairs and slots = 1
+// (inputs of at most 1024).
+bool moe_resident_fits(int K, int xs);
+int launch_moe_resident(const MoEBankLaunch &l, int groups, int slots, hipStream_t st);
 // One tall batch-1 fp32 linear with the RMSNorm prologue (lut_group.hip):
 // it.x / it.y set, w the norm weight; both 16-byte aligned.
 int launch_tall_rms(const GroupItem &it, const float *w, float eps, hipStream_t st);

@@ -109,7 +109,9 @@ __device__ __forceinline__ void bank_store(float *L, int buf, int w, int g, int 
     for (int r = 0; r < 16; ++r) p[(8 * (r / 4) + (r % 4)) * kLutRow] = d[r];
 }
 
-// acc[j] += LUT[code of row j][g] for the 32 rows of the lane's half.
+// acc[j] += LUT[code of row j][g] for the 32 rows of the lane's half.  gsel
+// byte 0 = 4 g + 128 buffer, byte 2 = bits 16-23 of the LUT's byte offset
+// from L (so a LUT 64 KB above L costs no address add per read).
 __device__ __forceinline__ void bank_gather(const float *L, uint32_t gsel, const uint4 (&c)[2],
                                             float (&acc)[32]) {
     const uint32_t wd[8] = {c[0].x, c[0].y, c[0].z, c[0].w, c[1].x, c[1].y, c[1].z, c[1].w};
@@ -120,9 +122,9 @@ __device__ __forceinline__ void bank_gather(const float *L, uint32_t gsel, const
         float v[8];
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            // byte 1 <- the code (byte i % 4 of its word), byte 0 <- 4 g + 128 buffer
+            // byte 1 <- the code (byte i % 4 of its word), bytes 0 and 2 <- gsel's
             const uint32_t a = __builtin_amdgcn_perm(wd[2 * q2 + i / 4], gsel,
-                                                     0x0c0c0400u + ((i % 4) << 8));
+                                                     0x0c020400u + ((i % 4) << 8));
             v[i] = *reinterpret_cast<const float *>(Lb + a);
         }
 #pragma unroll
@@ -440,67 +442,74 @@ __global__ __launch_bounds__(kBNT) void moe_bank_kernel(MoEBankParams p) {
     bank_block<XS>(bb, L, xs);
 }
 
-// MoE gate/up, token-major, for inputs of at most 4 slices (K <= 2048).  The
-// input codebook is shared by all experts, so a token's LUT serves every slot
-// the token is routed to.  Workgroup = (token t, up to R consecutive units),
-// unit u = (slot u / nb, 512-row block u % nb) of the token: all slices of
-// LUT_t are built once (the two [256][64]-word buffer pairs of bank_block,
-// slices 0-1 and 2-3, 128 KB), one barrier, then the units' codes stream
-// through the gathers with no barrier at all, unit i + 1's codes and scales
-// in flight while unit i gathers.  Skipped slots (expert outside [0, E) or
-// |w| < 1e-8, ojasx_lut_cpu.cpp:284-286) are passed over.  Each row sees the
-// same LUT entries in the same order as in moe_bank_kernel: identical results.
-struct MoEGuTokenParams {
+// MoE stages with a group's input LUT resident over many row blocks.  Gate/up
+// (XS_F32, XS_BF16; inputs of at most 4 slices, K <= 2048) runs token-major:
+// the input codebook is shared by all experts, so a token's LUT serves every
+// slot the token is routed to (group = token, k slots).  Down (XS_SWIGLU;
+// at most 2 slices, K <= 1024) runs pair-major: group = one routed pair, its
+// input silu(gate) * up of the pair's gate/up row, one slot.  Workgroup =
+// (group, up to R consecutive units), unit u = (slot u / nb, 512-row block
+// u % nb) of the group: all slices of the group's LUT are built once (the
+// [256][64]-word buffer pairs of bank_block: slices 0-1, and 2-3 above them),
+// one barrier, then the units' codes stream through the gathers with no
+// barrier at all, unit i + 1's codes and scales in flight while unit i
+// gathers.  Skipped slots (expert outside [0, E) or |w| < 1e-8,
+// ojasx_lut_cpu.cpp:284-286) are passed over.  Each row sees the same LUT
+// entries in the same order as in moe_bank_kernel: identical results.
+struct MoEResParams {
     const uint8_t *codes_b;     // [E][bank layout of M x G]
     size_t expert_bytes;
     const v8bf *cb3;            // [256][2][3] the codebook's bf16 pieces
     const float *scales;        // [E][M]
-    const void *x;              // [T][K] fp32 or bf16
+    const void *x;              // gate/up: [T][K] fp32 or bf16; down: [P][2K] fp32
     float *y;                   // [P][M]
     const int *idx;             // [P]
     const float *w;             // [P]
-    int M, K, k, E, nb, R, cpt; // rows, inputs, slots per token, experts, blocks per pair, units per workgroup, workgroups per token
+    int M, K, k, E, nb, R, cpt; // rows, inputs, slots per group, experts, blocks per pair, units per workgroup, workgroups per group
 };
-constexpr int kTokMaxUnits = 8;
+constexpr int kResMaxUnits = 8;
 
-// 16 waves in two teams of 8: both teams share the LUT, team 0 builds slices
-// 0-1 and team 1 slices 2-3, and team q runs the units i = q, q + 2, ... of
-// the workgroup's list (one team of 8 waves measured 6-7 % slower: two waves
-// per SIMD leave the gathers' LDS latency exposed).
-constexpr int kTokThreads = 2 * kBNT;
-template <int XS>
-__global__ __launch_bounds__(kTokThreads) void moe_gu_token_kernel(MoEGuTokenParams p) {
-    extern __shared__ float sm[];
-    float *const Lq[2] = {sm, sm + 256 * kLutRow};   // slices 0-1, slices 2-3
-    float *xs = sm + 2 * 256 * kLutRow;
-    const int tid = threadIdx.x, lane = tid & 63, wt_ = tid >> 6, h = lane >> 5, g = lane & 31;
-    const int w = wt_ & 7, team = wt_ >> 3;
-    const int t = (int)blockIdx.x / p.cpt, c = (int)blockIdx.x - t * p.cpt;
+// TEAMS teams of 8 waves share the LUT.  Gate/up: two teams (16 waves, 128 KB
+// of LUT, one workgroup per CU); team q builds the slices q, q + 2 and runs
+// the units i = q, q + 2, ... of the workgroup's list (one team measured
+// 6-7 % slower there: two waves per SIMD leave the gathers' LDS latency
+// exposed).  Down: one team, 64 KB of LUT, two workgroups per CU.
+template <int XS, int TEAMS>
+__global__ __launch_bounds__(TEAMS * kBNT) void moe_resident_kernel(MoEResParams p) {
+    constexpr int NSL = 2 * TEAMS;                   // slices the LUT holds
+    // the LUT at a fixed LDS address (static), so the gathers' addresses need
+    // no base add; the staged x (dynamic) after it
+    __shared__ float Ls[TEAMS * 256 * kLutRow];
+    extern __shared__ float xs[];
     const int K = p.K, G = K >> 4, S = (G + 31) >> 5, M = p.M;
+    const int tid = threadIdx.x, lane = tid & 63, wt_ = tid >> 6, h = lane >> 5, g = lane & 31;
+    const int w = wt_ & 7, team = TEAMS == 2 ? wt_ >> 3 : 0;
+    const int t = (int)blockIdx.x / p.cpt, c = (int)blockIdx.x - t * p.cpt;
     const int u0 = c * p.R, u1 = min(u0 + p.R, p.k * p.nb);
     const int rb_last = ((M + 63) >> 6) - 1;
 
     // ---- the units' slots (L2), then the first valid unit's codes (HBM)
     unsigned mask = 0;
 #pragma unroll
-    for (int i = 0; i < kTokMaxUnits; ++i) {
+    for (int i = 0; i < kResMaxUnits; ++i) {
         const int u = min(u0 + i, u1 - 1);
         const int pr = t * p.k + u / p.nb;
         const int e = gld(p.idx + pr);
         const float wt = gld(p.w + pr);
         if (u0 + i < u1 && e >= 0 && e < p.E && fabsf(wt) >= 1e-8f) mask |= 1u << i;
     }
-    mask &= team ? 0xaaaaaaaau : 0x55555555u;   // this team's units
+    if (!mask) return;                               // the same for every wave
+    if (TEAMS == 2) mask &= team ? 0xaaaaaaaau : 0x55555555u;   // this team's units
     // codes of unit i (all slices, clamped to the last) and its rows' scale;
     // the unit's expert id is read again here (a cached load) rather than kept
     // in an array indexed at run time, which would live in scratch
-    auto load_unit = [&](int i, uint4 (&cc)[4][2], float &sc) {
+    auto load_unit = [&](int i, uint4 (&cc)[NSL][2], float &sc) {
         const int u = u0 + i, b = u % p.nb;
         const int e = gld(p.idx + t * p.k + u / p.nb);
         const int rb = min(b * (kBRows / 64) + w, rb_last);
         const uint8_t *cp = p.codes_b + (size_t)e * p.expert_bytes + ((size_t)rb * G + g) * 64 + 32 * h;
 #pragma unroll
-        for (int s4 = 0; s4 < 4; ++s4) bank_codes(cp, min(s4, S - 1), cc[s4]);
+        for (int s4 = 0; s4 < NSL; ++s4) bank_codes(cp, min(s4, S - 1), cc[s4]);
         const int m = b * kBRows + 64 * w + 32 * h + g;
         sc = gld(p.scales + (size_t)e * M + min(m, M - 1));
     };
@@ -511,54 +520,57 @@ __global__ __launch_bounds__(kTokThreads) void moe_gu_token_kernel(MoEGuTokenPar
         a[1] = gld(ap + 1);
         a[2] = gld(ap + 2);
     }
-    uint4 cA[4][2], cB[4][2];
+    uint4 cA[NSL][2], cB[NSL][2];
     float sA = 0.f, sB = 0.f;
-    int iA = mask ? __builtin_ctz(mask) : kTokMaxUnits;
+    int iA = mask ? __builtin_ctz(mask) : kResMaxUnits;
     if (mask) load_unit(iA, cA, sA);
     mask &= mask - 1;
 
-    // ---- x_t staged as bf16 pieces, then every slice of LUT_t
+    // ---- the group's input staged as bf16 pieces, then every slice of its LUT
     const void *x;
-    if constexpr (XS == XS_BF16)
+    if constexpr (XS == XS_SWIGLU)
+        x = static_cast<const float *>(p.x) + (size_t)t * 2 * K;
+    else if constexpr (XS == XS_BF16)
         x = static_cast<const __hip_bfloat16 *>(p.x) + (size_t)t * K;
     else
         x = static_cast<const float *>(p.x) + (size_t)t * K;
     if (tid < kBNT) bank_stage_x<XS>(x, K, xs, tid);
     __syncthreads();
 #pragma unroll
-    for (int s4 = 0; s4 < 4; ++s4) {
-        if (s4 < S && (s4 >> 1) == team) {
+    for (int s4 = 0; s4 < NSL; ++s4) {
+        if (s4 < S && (TEAMS == 1 || (s4 & 1) == team)) {
             v8bf b[3];
             bank_xop(xs, s4, g, h, b);
             const v16f d = bank_build(a, b);
-            bank_store(Lq[s4 >> 1], s4 & 1, w, g, h, d);
+            bank_store(Ls + (s4 >> 1) * 256 * kLutRow, s4 & 1, w, g, h, d);
         }
     }
     __syncthreads();
 
     // ---- the units: gathers from the resident LUT, the next unit's loads in flight
-    const uint32_t gsel[2] = {4u * g, 4u * g + 128u};
-    auto run = [&](int i, const uint4 (&cc)[4][2], float sc) __attribute__((always_inline)) {
+    // slice s4 at byte 65536 (s4 >> 1) + 128 (s4 & 1) + 4 g + 256 code of Ls
+    static_assert(256 * kLutRow * sizeof(float) == 65536, "slices 2-3 start 64 KB above Ls");
+    auto run = [&](int i, const uint4 (&cc)[NSL][2], float sc) __attribute__((always_inline)) {
         float acc[32];
 #pragma unroll
         for (int j = 0; j < 32; ++j) acc[j] = 0.f;
 #pragma unroll
-        for (int s4 = 0; s4 < 4; ++s4)
-            if (s4 < S) bank_gather(Lq[s4 >> 1], gsel[s4 & 1], cc[s4], acc);
+        for (int s4 = 0; s4 < NSL; ++s4)
+            if (s4 < S) bank_gather(Ls, 4u * g + 128u * (s4 & 1) + ((uint32_t)(s4 >> 1) << 16), cc[s4], acc);
         const float tot = bank_reduce(acc, lane);
         const int u = u0 + i, b = u % p.nb;
         const int m = b * kBRows + 64 * w + 32 * h + g;
         if (m < M) p.y[(size_t)(t * p.k + u / p.nb) * M + m] = tot * sc;
     };
-    while (iA < kTokMaxUnits) {
-        const int iB = mask ? __builtin_ctz(mask) : kTokMaxUnits;
+    while (iA < kResMaxUnits) {
+        const int iB = mask ? __builtin_ctz(mask) : kResMaxUnits;
         mask &= mask - 1;
-        if (iB < kTokMaxUnits) load_unit(iB, cB, sB);
+        if (iB < kResMaxUnits) load_unit(iB, cB, sB);
         run(iA, cA, sA);
-        if (iB >= kTokMaxUnits) break;
-        iA = mask ? __builtin_ctz(mask) : kTokMaxUnits;
+        if (iB >= kResMaxUnits) break;
+        iA = mask ? __builtin_ctz(mask) : kResMaxUnits;
         mask &= mask - 1;
-        if (iA < kTokMaxUnits) load_unit(iA, cA, sA);
+        if (iA < kResMaxUnits) load_unit(iA, cA, sA);
         run(iB, cB, sB);
     }
 }
@@ -700,37 +712,45 @@ int launch_moe_bank(const MoEBankLaunch &l, hipStream_t st) {
     return OJASX_OK;
 }
 
-bool moe_gu_token_fits(int K) { return K % 16 == 0 && K / 16 <= 4 * 32; }
+bool moe_resident_fits(int K, int xs) {
+    return K % 16 == 0 && K / 16 <= (xs == XS_SWIGLU ? 2 : 4) * 32;
+}
 
-int launch_moe_gu_token(const MoEBankLaunch &l, int T, hipStream_t st) {
-    if (!moe_gu_token_fits(l.K)) {
-        set_error("token-major gate/up: at most 2048 inputs (got %d)", l.K);
+int launch_moe_resident(const MoEBankLaunch &l, int groups, int slots, hipStream_t st) {
+    if (!moe_resident_fits(l.K, l.xs)) {
+        set_error("resident-LUT MoE stage: too many inputs (%d)", l.K);
         return OJASX_ERR_INVALID;
     }
+    const int teams = l.xs == XS_SWIGLU ? 1 : 2;
     const int nb = (l.M + kBRows - 1) / kBRows;
-    const int units = l.k * nb;
-    // about one round of workgroups (one per CU: 128 KB of LUT each), at
-    // least one unit per team and at most kTokMaxUnits units per workgroup
-    const long total = (long)T * units;
-    const int R = (int)std::min<long>(kTokMaxUnits, std::max<long>(2, (total + 255) / 256));
+    const int units = slots * nb;
+    // about one round of workgroups (2 / teams per CU), at least one unit
+    // per team and at most kResMaxUnits units per workgroup
+    const long total = (long)groups * units, round = 512 / teams;
+    const int R = (int)std::min<long>({(long)kResMaxUnits, (long)std::max(units, teams),
+                                       std::max<long>(teams, (total + round - 1) / round)});
     const int cpt = (units + R - 1) / R;
-    MoEGuTokenParams p{l.codes_b, l.expert_bytes, static_cast<const v8bf *>(l.cb3), l.scales, l.x, l.y,
-                       l.idx, l.w, l.M, l.K, l.k, l.E, nb, R, cpt};
-    const size_t lds = (size_t)2 * 256 * kLutRow * sizeof(float) +
-                       round_up((size_t)(l.K / 16), 32) * kXRow * sizeof(float);
-    if ((long)T * cpt > 0x7fffffffL) {
-        set_error("token-major gate/up: too many workgroups");
+    if ((long)groups * cpt > 0x7fffffffL) {
+        set_error("resident-LUT MoE stage: too many workgroups");
         return OJASX_ERR_INVALID;
     }
+    MoEResParams p{l.codes_b, l.expert_bytes, static_cast<const v8bf *>(l.cb3), l.scales, l.x, l.y,
+                   l.idx, l.w, l.M, l.K, slots, l.E, nb, R, cpt};
+    const size_t lds = round_up((size_t)(l.K / 16), 32) * kXRow * sizeof(float);   // + the static LUT
+    const dim3 grid(groups * cpt), block(teams * kBNT);
     int rc = OJASX_OK;
-    if (l.xs == XS_BF16) {
+    if (l.xs == XS_SWIGLU) {
         static size_t gr = 0;
-        rc = set_dyn_lds(&moe_gu_token_kernel<XS_BF16>, lds, &gr);
-        if (!rc) OJX_LAUNCH(moe_gu_token_kernel<XS_BF16>, dim3(T * cpt), dim3(kTokThreads), lds, st, p);
+        rc = set_dyn_lds(&moe_resident_kernel<XS_SWIGLU, 1>, lds, &gr);
+        if (!rc) OJX_LAUNCH((moe_resident_kernel<XS_SWIGLU, 1>), grid, block, lds, st, p);
+    } else if (l.xs == XS_BF16) {
+        static size_t gr = 0;
+        rc = set_dyn_lds(&moe_resident_kernel<XS_BF16, 2>, lds, &gr);
+        if (!rc) OJX_LAUNCH((moe_resident_kernel<XS_BF16, 2>), grid, block, lds, st, p);
     } else {
         static size_t gr = 0;
-        rc = set_dyn_lds(&moe_gu_token_kernel<XS_F32>, lds, &gr);
-        if (!rc) OJX_LAUNCH(moe_gu_token_kernel<XS_F32>, dim3(T * cpt), dim3(kTokThreads), lds, st, p);
+        rc = set_dyn_lds(&moe_resident_kernel<XS_F32, 2>, lds, &gr);
+        if (!rc) OJX_LAUNCH((moe_resident_kernel<XS_F32, 2>), grid, block, lds, st, p);
     }
     if (rc) return rc;
     OJX_HIP(hipGetLastError());

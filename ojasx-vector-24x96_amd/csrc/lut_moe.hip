@@ -782,7 +782,11 @@ constexpr int kBankSortMinTokens = 128;
 // (pair, row block).  Measured gate/up kernel per call (same box, bank vs
 // token-major, 512 experts, H 2048, I 768, top-10): 11.4 vs 12.6 us at 16
 // tokens, 15.8 vs 15.2 at 24, 19.7 vs 18.7 at 32, 27.2 vs 23.0 at 48, 35.3
-// vs 27.8 at 64, 111.5 vs 94.3 at 256.
+// vs 27.8 at 64, 111.5 vs 94.3 at 256.  Down (at most 1024 intermediate
+// values) always runs pair-major, each pair's LUT built once for all its row
+// blocks: per call 26.3 vs 25.3 us at 16 tokens, 32.8 vs 29.6 at 24, 63.0 vs
+// 55.0 at 64, 213.6 vs 175 at 256 (bank vs pair-major down).  With both
+// stages resident no work list is read, so no plan runs.
 constexpr int kTokGateUpMinTokens = 24;
 
 template <typename T>
@@ -936,7 +940,8 @@ int moe_forward_group(MoE *m, const void *x, const int *idx, const float *w, voi
 // (pair, 512-row block), so the pairs of one expert run back to back on one
 // XCD and its codes stream through one L2; below it workgroups map straight
 // to (pair, row block).  From kTokGateUpMinTokens tokens gate/up runs on the
-// token-major kernel instead (its rows are the same sums in the same order).
+// token-major resident-LUT kernel instead, and down on the pair-major one
+// whenever its input fits (their rows are the same sums in the same order).
 // Gate/up writes s_m * (gate | up) rows per pair, down
 // stages silu(gate) * up as its input and writes s_dn * down per pair, and
 // the ordered combine sums w_j * down_j over the slots.
@@ -975,8 +980,8 @@ int moe_forward_bank(MoE *m, const void *x, const int *idx, const float *w, void
     l.E = m->E;
     l.max_work = (int)(P * nb_gu);
     l.xs = std::is_same<T, float>::value ? 0 : 1;
-    rc = T_ >= kTokGateUpMinTokens && moe_gu_token_fits(m->H) ? launch_moe_gu_token(l, T_, st)
-                                                              : launch_moe_bank(l, st);
+    rc = T_ >= kTokGateUpMinTokens && moe_resident_fits(m->H, l.xs) ? launch_moe_resident(l, T_, k, st)
+                                                                     : launch_moe_bank(l, st);
     if (rc) return rc;
     l.codes_b = m->dnb.as<uint8_t>();
     l.expert_bytes = m->dnb_bytes;
@@ -990,7 +995,7 @@ int moe_forward_bank(MoE *m, const void *x, const int *idx, const float *w, void
     l.K = m->I;
     l.max_work = (int)(P * nb_dn);
     l.xs = 2;
-    rc = launch_moe_bank(l, st);
+    rc = moe_resident_fits(m->I, l.xs) ? launch_moe_resident(l, (int)P, 1, st) : launch_moe_bank(l, st);
     if (rc) return rc;
     MoEParams cp{};
     cp.dout = m->dout.as<float>();
@@ -1031,7 +1036,9 @@ int moe_forward(MoE *m, const void *x, const int *idx, const float *w, void *y, 
         // on the bank kernel; sorted by expert, the expert ids must fit the
         // work entries' 16 bits and the plan kernel's LDS hold 3 E + P ints
         const size_t P = (size_t)T_ * k;
-        const bool sorted = T_ >= kBankSortMinTokens;
+        const bool resident = T_ >= kTokGateUpMinTokens && moe_resident_fits(m->H, 0) &&
+                              moe_resident_fits(m->I, 2);
+        const bool sorted = T_ >= kBankSortMinTokens && !resident;
         const bool plan_fits = P <= kBankMaxPairs && m->E <= 65535 &&
                                (3 * (size_t)m->E + P) * sizeof(int) <= kMaxLds;
         const int nb = (std::max(2 * m->I, m->H) + kBankRows - 1) / kBankRows;

@@ -221,8 +221,8 @@ def test_moe_unaligned_activations(pkg, dev, baseline_moe, dtype_tag):
 @pytest.mark.parametrize("dtype_tag", [0, 1])
 def test_moe_by_expert_many_pairs_per_expert(pkg, dev, dtype_tag, T):
     """256 and 640 routed pairs over 8 experts (32 and 80 per expert on
-    average): mapped straight to (pair, row block) at 64 tokens, through the
-    plan's expert-sorted work lists at 160; skipped slots, fp32 and bf16."""
+    average) on the token-major gate/up and pair-major down kernels; skipped
+    slots, fp32 and bf16."""
     import torch
     E, H, I, k = 8, 256, 96, 4
     m = gen.moe(E=E, H=H, I=I, T=T, seed=77, scales="u")
@@ -254,11 +254,12 @@ def test_token_major_rows_equal_bank_rows(pkg, dev, baseline_moe):
 
 @pytest.mark.parametrize("dtype_tag", [0, 1])
 def test_moe_token_major_full_workgroups(pkg, dev, dtype_tag):
-    """72 tokens x 8 slots x 4 row blocks (the last one partial): eight units
-    per token-major workgroup, the last workgroup of each token short, with
-    skipped and repeated slots."""
+    """72 tokens x 8 slots x 4 gate/up row blocks (the last one partial):
+    eight units per token-major workgroup, the last workgroup of each token
+    short; down over 3 row blocks (the last partial) and a partial second
+    slice; skipped and repeated slots."""
     import torch
-    E, H, I, k, T = 32, 512, 1008, 8, 72
+    E, H, I, k, T = 32, 1200, 1008, 8, 72
     m = gen.moe(E=E, H=H, I=I, T=T, seed=4321, scales="u")
     nat = make_native(pkg, m, E, H, I, k)
     idx, w = cpu.router_topk(m["logits"], k, renorm=True)
@@ -274,6 +275,23 @@ def test_moe_token_major_full_workgroups(pkg, dev, dtype_tag):
         want = cpu.moe_forward(xr[t], m["cb_in"], m["cb_down"], m["gu_codes"], m["gu_scales"],
                                m["dn_codes"], m["dn_scales"], idx[t], w[t])
         assert rel_err(y[t], want) < (1e-5 if dtype_tag == 0 else 1e-2), t
+
+
+def test_moe_plan_sorted_down(pkg, dev):
+    """160 tokens with 1152 intermediate values (beyond the pair-major down
+    kernel's two slices): the plan sorts the pairs by expert and down runs on
+    the bank kernel's work list, gate/up token-major."""
+    import torch
+    E, H, I, k, T = 8, 256, 1152, 4, 160
+    m = gen.moe(E=E, H=H, I=I, T=T, seed=99, scales="u")
+    nat = make_native(pkg, m, E, H, I, k)
+    idx, w = cpu.router_topk(m["logits"], k, renorm=True)
+    idx[11, 0] = -2                                  # out of range: skipped
+    y = device_moe(pkg, dev, nat, torch.from_numpy(m["x"]).to(dev), idx, w, k)
+    for t in range(T):
+        want = cpu.moe_forward(m["x"][t], m["cb_in"], m["cb_down"], m["gu_codes"], m["gu_scales"],
+                               m["dn_codes"], m["dn_scales"], idx[t], w[t])
+        assert rel_err(y[t], want) < 1e-5, t
 
 
 @pytest.mark.parametrize("H,I", [(18432, 64), (256, 17408), (36864, 48)])
@@ -295,10 +313,9 @@ def test_moe_wide_hidden_or_intermediate(pkg, dev, H, I):
 
 @pytest.mark.parametrize("E,T", [(4096, 16), (16384, 16), (4096, 128), (16384, 128)])
 def test_moe_many_experts(pkg, dev, E, T):
-    """Large expert counts: at 16 tokens the bank kernel maps workgroups to
-    (pair, row block) directly; at 128 tokens 4096 experts run the plan
-    kernel (sorted by expert) in 50 KB of LDS, 16384 would need 198 KB and
-    take the per-slot path."""
+    """Large expert counts: at 16 tokens the gate/up bank kernel maps
+    workgroups to (pair, row block) directly; at 128 tokens both stages run
+    the resident-LUT kernels, which need no plan (no per-expert LDS)."""
     import torch
     H, I, k = 64, 32, 4
     m = gen.moe(E=E, H=H, I=I, T=T, seed=E % 97, scales="u")
