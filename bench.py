@@ -120,8 +120,13 @@ def timed_cpu(call, seconds, max_calls, warm=3):
 
 
 def short(name):
-    """Kernel name as recorded by the library, without a long template list."""
-    return name if len(name) <= 26 else name.split("<")[0]
+    """Kernel name as recorded by the library, compacted: "XS_" and the spaces
+    dropped from a long template list, the list dropped if still long (the
+    library records a template launch's parameter names there, not values)."""
+    if len(name) <= 26:
+        return name
+    c = name.replace("XS_", "").replace(", ", ",")
+    return c if len(c) <= 30 else name.split("<")[0]
 
 
 class Bench:
