@@ -116,10 +116,10 @@ def test_baseline_moe_fp32(pkg, dev, baseline_moe, T):
         assert rel_err(y[t].cpu().numpy(), want) < 1e-5, t
 
 
-def test_baseline_moe_bf16(pkg, dev, baseline_moe):
+@pytest.mark.parametrize("T", [4, 32])   # grouped-per-slot path; token-major + pair-major kernels
+def test_baseline_moe_bf16(pkg, dev, baseline_moe, T):
     import torch
     m, nat = baseline_moe
-    T = 4
     idx, w = route(pkg, torch.from_numpy(m["logits"][:T]).to(dev), 10, True)
     x = torch.from_numpy(m["x"][:T]).to(dev).to(torch.bfloat16)
     y = torch.empty(T, 2048, device=dev, dtype=torch.bfloat16)
@@ -292,6 +292,52 @@ def test_moe_plan_sorted_down(pkg, dev):
         want = cpu.moe_forward(m["x"][t], m["cb_in"], m["cb_down"], m["gu_codes"], m["gu_scales"],
                                m["dn_codes"], m["dn_scales"], idx[t], w[t])
         assert rel_err(y[t], want) < 1e-5, t
+
+
+@pytest.mark.parametrize("T", [16, 64])
+def test_moe_graph_replay_matches_eager(pkg, dev, T):
+    """The T >= 16 launch sequence (bank or token-major gate/up, pair-major
+    down, combine) captured in a HIP graph: every replay, with eager calls
+    and synchronisations between replays, returns the eager bits."""
+    import torch
+    E, H, I, k = 64, 512, 256, 8
+    m = gen.moe(E=E, H=H, I=I, T=T, seed=321 + T, scales="u")
+    nat = make_native(pkg, m, E, H, I, k)
+    idx, w = cpu.router_topk(m["logits"], k, renorm=True)
+    x = torch.from_numpy(m["x"]).to(dev)
+    it = torch.from_numpy(np.ascontiguousarray(idx, np.int32)).to(dev)
+    wt = torch.from_numpy(np.ascontiguousarray(w, np.float32)).to(dev)
+    y = torch.empty(T, H, device=dev)
+    L = pkg.lib()
+
+    def call(stream):
+        return L.ojasx_moe_forward_device(nat.handle, vp(x), vp(it), vp(wt), vp(y), T, k, 0, stream)
+
+    assert call(None) == 0                          # eager: sizes the workspaces
+    torch.cuda.synchronize()
+    eager = y.clone()
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s), torch.cuda.graph(g, stream=s):
+        assert call(ctypes.c_void_p(s.cuda_stream)) == 0
+    torch.cuda.synchronize()
+    other = torch.empty_like(y)
+    for rep in range(3):
+        y.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y, eager), rep
+        # eager work between replays (a call into another buffer)
+        assert L.ojasx_moe_forward_device(nat.handle, vp(x), vp(it), vp(wt), vp(other), T, k, 0,
+                                          None) == 0
+        torch.cuda.synchronize()
+        assert torch.equal(other, eager), rep
+    for t in range(T):
+        want = cpu.moe_forward(m["x"][t], m["cb_in"], m["cb_down"], m["gu_codes"], m["gu_scales"],
+                               m["dn_codes"], m["dn_scales"], idx[t], w[t])
+        assert rel_err(eager[t].cpu().numpy(), want) < 1e-5, t
+    del g
 
 
 @pytest.mark.parametrize("H,I", [(18432, 64), (256, 17408), (36864, 48)])
