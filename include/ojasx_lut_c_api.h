@@ -77,8 +77,9 @@ OJASX_API int ojasx_kernel_timing_report(char *buf, size_t buf_size);
 
 /* ---- linear (ref.h:46-91) --------------------------------------------- */
 /* ref.h:46-55.  codes_data is [out_features][in_features/block_dim] uint8,
- * codebook_data [codebook_size][block_dim] fp32.  block_dim <= 32,
- * codebook_size <= 256, in_features % block_dim == 0. */
+ * codebook_data [codebook_size][block_dim] fp32.  Any block_dim dividing
+ * in_features, codebook_size <= 256 (block_dim 16 runs the single-kernel and
+ * MFMA paths, other sizes the LUT-build + gather path). */
 OJASX_API OjasxLinearHandle ojasx_create_linear(int in_features, int out_features,
                                                 int block_dim, int codebook_size,
                                                 const float *codebook_data,
