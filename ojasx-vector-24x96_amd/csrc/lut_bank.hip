@@ -471,9 +471,9 @@ constexpr int kResMaxUnits = 8;
 
 // TEAMS teams of 8 waves share the LUT.  Gate/up: two teams (16 waves, 128 KB
 // of LUT, one workgroup per CU); team q builds the slices q, q + 2 and runs
-// the units i = q, q + 2, ... of the workgroup's list (one team measured
-// 6-7 % slower there: two waves per SIMD leave the gathers' LDS latency
-// exposed).  Down: one team, 64 KB of LUT, two workgroups per CU.
+// the units i = q, q + 2, ... of the workgroup's list (one team of 8 waves,
+// two per SIMD, measured 6-7 % slower there).  Down: one team, 64 KB of LUT,
+// two workgroups per CU (two teams in one workgroup per CU measured slower).
 template <int XS, int TEAMS>
 __global__ __launch_bounds__(TEAMS * kBNT) void moe_resident_kernel(MoEResParams p) {
     constexpr int NSL = 2 * TEAMS;                   // slices the LUT holds
