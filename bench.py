@@ -280,9 +280,10 @@ def parse():
 
 # --- linear legs ------------------------------------------------------------------
 
-def make_instances(b, M, K, n, seed):
-    """n LUT-GEMV handles M x K: one seeded codebook, scales, CSR and x, codes
-    drawn per instance.  Returns (handles, base inputs, device bytes per handle)."""
+def make_instances(b, M, K, n, seed, csr=True):
+    """n LUT-GEMV handles M x K: one seeded codebook, scales, CSR (unless csr
+    is False) and x, codes drawn per instance.  Returns (handles, base inputs,
+    device bytes per handle)."""
     L = b.L
     base = b.pkg.synthetic.linear(M, K, B=64, seed=seed)
     r = np.random.default_rng(seed + 1)
@@ -295,7 +296,8 @@ def make_instances(b, M, K, n, seed):
         h = L.ojasx_create_linear(K, M, 16, 256, p(base["codebook"]), p(codes),
                                   p(base["scales"]), None)
         assert h, L.ojasx_get_last_error()
-        assert L.ojasx_set_linear_outliers(h, vl.size, p(rp), p(cl), p(vl)) == 0
+        if csr:
+            assert L.ojasx_set_linear_outliers(h, vl.size, p(rp), p(cl), p(vl)) == 0
         hs.append(h)
         wbytes = L.ojasx_linear_device_weight_bytes(h)
     return hs, base, wbytes
@@ -385,6 +387,19 @@ def bench_linear2560(b, args):
             c = cpu_linear(base, 1, min(2.0, args.cpu_seconds), y0, threads=(1, cpu_threads()))
             res["cpu"] = {"us": c["us_1t"], "cores": 1, "kind": c["kind"], "rel_err": c["rel_err"],
                           f"us_{cpu_threads()}t": c.get(f"us_{cpu_threads()}t")}
+    finally:
+        for h in hs:
+            b.L.ojasx_destroy_linear(h)
+    return res
+
+
+def bench_nocsr(b, args):
+    """Profiling leg (only with --extra nocsr): the headline shape with no
+    outliers, for the traffic attribution of the CSR stream."""
+    hs, base, wbytes = make_instances(b, M_GU, K_GU, args.instances, 2026, csr=False)
+    try:
+        res, _ = linear_leg(b, hs, base, wbytes, M_GU, K_GU, 1, 0,
+                            max(MIN_KERNEL_LAUNCHES, args.steps), args.warmup, "nocsr_b1")
     finally:
         for h in hs:
             b.L.ojasx_destroy_linear(h)
@@ -1010,6 +1025,8 @@ def main():
             L.ojasx_destroy_linear(h)
     if "linear2560" in extra:
         legs["linear2560_b1"] = bench_linear2560(b, args)
+    if "nocsr" in extra:
+        legs["nocsr_b1"] = bench_nocsr(b, args)
     if "moe" in extra:
         legs["moe"] = bench_moe(b, args)
     if "moe_sustained" in extra:
