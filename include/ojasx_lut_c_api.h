@@ -308,9 +308,9 @@ OJASX_API void ojasx_destroy_moe(OjasxMoEHandle handle);
  * counterpart): x [num_tokens][hidden], idx/w [num_tokens][k_active],
  * y [num_tokens][hidden] fully overwritten (k_active <= 0: untouched).
  * Calls on one handle share its workspaces, grown as larger batches arrive:
- * serialise them per handle.  Once a call with a given num_tokens has run,
- * later calls with that num_tokens neither allocate nor record a memset, so
- * they can be captured in a HIP graph and replayed. */
+ * serialise them per handle.  Once a call with a given (num_tokens,
+ * k_active) has run, later calls with those values neither allocate nor
+ * record a memset, so they can be captured in a HIP graph and replayed. */
 OJASX_API int ojasx_moe_forward_device(OjasxMoEHandle handle, const void *x, const int *idx,
                                        const float *w, void *y, int num_tokens, int k_active,
                                        int dtype, void *stream);
