@@ -17,7 +17,13 @@ EXE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "host_asan", "_bu
 
 
 def _run():
-    assert os.path.exists(EXE), "host sanitizer check not built: run __graft_entry__.build()"
+    if not os.path.exists(EXE):                     # built by __graft_entry__.build(); else here
+        import importlib.util
+        spec = importlib.util.spec_from_file_location(
+            "_host_asan_build", os.path.join(os.path.dirname(EXE), "..", "build.py"))
+        mod = importlib.util.module_from_spec(spec)
+        spec.loader.exec_module(mod)
+        mod.build(verbose=False)
     env = dict(os.environ)
     env["ASAN_OPTIONS"] = "detect_leaks=1:abort_on_error=0:halt_on_error=1"
     env["LSAN_OPTIONS"] = "suppressions=" + os.path.join(os.path.dirname(EXE), "..", "lsan.supp")
