@@ -20,7 +20,8 @@ def _run():
     if not os.path.exists(EXE):                     # built by __graft_entry__.build(); else here
         import importlib.util
         spec = importlib.util.spec_from_file_location(
-            "_host_asan_build", os.path.join(os.path.dirname(EXE), "..", "build.py"))
+            "_host_asan_build",
+            os.path.join(os.path.dirname(os.path.abspath(__file__)), "host_asan", "build.py"))
         mod = importlib.util.module_from_spec(spec)
         spec.loader.exec_module(mod)
         mod.build(verbose=False)
