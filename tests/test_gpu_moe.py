@@ -294,6 +294,32 @@ def test_moe_plan_sorted_down(pkg, dev):
         assert rel_err(y[t], want) < 1e-5, t
 
 
+@pytest.mark.parametrize("case", range(8))
+def test_moe_seeded_shapes_around_thresholds(pkg, dev, case):
+    """Seeded shapes around the path thresholds (16, 24, 128 tokens) with
+    hidden and intermediate sizes any multiple of 16 (partial slices, partial
+    64- and 512-row blocks), on the bank, token-major and pair-major kernels."""
+    import torch
+    r = np.random.default_rng(900 + case)
+    T = (16, 23, 24, 25, 47, 130, 24, 130)[case]
+    E = int(r.integers(3, 40))
+    k = int(r.integers(1, min(E, 8) + 1))
+    H = 16 * int(r.integers(1, 129))                 # up to 2048
+    I = 16 * int(r.integers(1, 65))                  # up to 1024
+    m = gen.moe(E=E, H=H, I=I, T=T, seed=1000 + case, scales="u")
+    nat = make_native(pkg, m, E, H, I, k)
+    idx, w = cpu.router_topk(m["logits"], k, renorm=True)
+    tdt = torch.bfloat16 if case % 3 == 2 else torch.float32
+    xt = torch.from_numpy(m["x"]).to(dev).to(tdt)
+    y = device_moe(pkg, dev, nat, xt, idx, w, k, 1 if tdt == torch.bfloat16 else 0)
+    xr = xt.float().cpu().numpy()
+    for t in range(T):
+        want = cpu.moe_forward(xr[t], m["cb_in"], m["cb_down"], m["gu_codes"], m["gu_scales"],
+                               m["dn_codes"], m["dn_scales"], idx[t], w[t])
+        tol = 1e-2 if tdt == torch.bfloat16 else 1e-5
+        assert rel_err(y[t], want) < tol, (case, T, E, k, H, I, t)
+
+
 @pytest.mark.parametrize("T", [16, 64])
 def test_moe_graph_replay_matches_eager(pkg, dev, T):
     """The T >= 16 launch sequence (bank or token-major gate/up, pair-major
