@@ -397,7 +397,10 @@ OJASX_API int ojasx_decoder_read_kv(OjasxDecoderHandle handle, int layer, int fi
                                     uint8_t *v_codes, float *v_scales);
 /* Fused fp32 batch-1 LUT linear of the decoder: prologue 0 = none, 1 =
  * RMSNorm(x; norm_weight, eps), 2 = silu(x[:K]) * x[K:] from a 2K row; y =
- * residual + (...) when residual != NULL (residual may equal y). */
+ * residual + (...) when residual != NULL (residual may equal y).  Prologue 3
+ * = RMSNorm as 1 with a SwiGLU epilogue: out_features = 2I (gate rows, then up
+ * rows) and y [I] = silu(z[:I]) * z[I:] of the linear's output z, the input
+ * prologue 2 computes from z; no residual. */
 OJASX_API int ojasx_linear_forward_fused_device(OjasxLinearHandle handle, const float *x,
                                                 float *y, int prologue, const float *norm_weight,
                                                 float eps, const float *residual, void *stream);

@@ -11,8 +11,10 @@
 //        attn = softmax(q K^T / sqrt(hd)) V over pos + 1 tokens  attn_decode_kernel + merge
 //        (partials per 64-token chunk of the cached tokens and one for the new token)
 //     3. x   += LUT(Wo, attn)                          residual epilogue
-//     4. gu   = LUT(Wgu, RMSNorm(x, w_post))           RMSNorm prologue (gate rows, then up rows)
-//     5. x   += LUT(Wdown, silu(gate) * up)            SwiGLU prologue, residual epilogue
+//     4. h    = silu(gate) * up, [gate; up] = LUT(Wgu, RMSNorm(x, w_post))
+//                                                     RMSNorm prologue, SwiGLU epilogue (a
+//                                                     workgroup owns gate rows and their up rows)
+//     5. x   += LUT(Wdown, h)                          residual epilogue
 //   head: logits = LUT(Wlm, RMSNorm(x, w_final)); argmax_embed_kernel picks the
 //   token (ties to the lower id), stores it, loads its embedding row into x
 //   and advances the position.
@@ -516,10 +518,11 @@ struct Decoder {
             rc = linear_forward_fused(ly.o, attn.as<float>(), x.as<float>(), 0, nullptr, 0.f,
                                       x.as<float>(), st);
             if (rc) return rc;
-            rc = linear_forward_fused(ly.gu, x.as<float>(), gu.as<float>(), 1,
+            // gate/up with the SwiGLU epilogue: gu holds silu(gate) * up (I floats)
+            rc = linear_forward_fused(ly.gu, x.as<float>(), gu.as<float>(), 3,
                                       ly.post_norm.as<float>(), eps, nullptr, st);
             if (rc) return rc;
-            rc = linear_forward_fused(ly.down, gu.as<float>(), x.as<float>(), 2, nullptr, 0.f,
+            rc = linear_forward_fused(ly.down, gu.as<float>(), x.as<float>(), 0, nullptr, 0.f,
                                       x.as<float>(), st);
             if (rc) return rc;
         }

@@ -57,6 +57,9 @@ constexpr int kRows = 32;       // rows per gather workgroup
 constexpr int kOB = 32;         // outlier entries loaded per batch
 constexpr size_t kXLdsBytes = 48 * 1024;  // x staged in LDS up to this size
 constexpr int kMaxDecWaves = 16;          // waves (slice owners) per decode workgroup
+constexpr int kTallRowsPerTile = 16 * 256;  // batch-1 rows per row tile per workgroup: one per CU
+constexpr int kMaxTallTiles = 5;          // row tiles of 16 per batch-1 workgroup, at most
+                                          // (6 spills at the 128-VGPR limit)
 constexpr size_t kMaxLds = 160 * 1024;    // LDS per workgroup on gfx950
 }  // namespace
 
@@ -263,8 +266,12 @@ struct DecParams {
 //               multiplies the manifold and outlier sums in the epilogue (r is a
 //               per-token scalar, so it factors out of the linear map);
 //   kProSwiglu  x[i] = silu(a[i]) * a[K + i] from a row a of 2K elements
-//               (gate half, then up half), silu(v) = v / (1 + exp(-v)).
-enum { kProNone = 0, kProRms = 1, kProSwiglu = 2 };
+//               (gate half, then up half), silu(v) = v / (1 + exp(-v));
+//   kProRmsGlu  the RMSNorm prologue and a SwiGLU epilogue: of the M = 2I
+//               outputs (gate rows, then up rows) y holds silu(y[i]) * y[I + i],
+//               i < I, the kProSwiglu input of the next linear computed once.
+//               A workgroup owns 8 RPL gate rows and their up rows.
+enum { kProNone = 0, kProRms = 1, kProSwiglu = 2, kProRmsGlu = 3 };
 
 __device__ __forceinline__ float silu_f(float v) { return v / (1.0f + expf(-v)); }
 __device__ __forceinline__ float4 swiglu4(float4 g, float4 u) {
@@ -287,6 +294,12 @@ __device__ __forceinline__ float sumsq4(float4 a) {
 template <typename T, int BT, int RPL, int PRO = kProNone, bool RES = false, bool HO = false>
 __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(HO ? 8 : 1))) void lut_dec_kernel(DecParams p) {
     constexpr int R = 16 * RPL;            // rows per workgroup
+    constexpr bool RMS = PRO == kProRms || PRO == kProRmsGlu;
+    constexpr bool GLU = PRO == kProRmsGlu;
+    static_assert(!GLU || (BT == 1 && !RES), "SwiGLU epilogue: batch 1, no residual");
+    constexpr int RH = R / 2;              // GLU: gate rows per workgroup
+    // code rows past Mp only where R does not divide the row padding, or GLU
+    constexpr bool CLAMP = GLU || (kRowAlign % R) != 0;
     extern __shared__ float sm[];
     float *cbs = sm;                       // [256][16]
     float *xs = sm + kCB * 16;             // [BT][S*256]
@@ -296,7 +309,13 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(HO ? 8 : 1
     const int lane = tid & 63, w = tid >> 6;
     const int r = lane >> 2, j = lane & 3;
     const int NW = p.NW, S = p.S, KS = S * 256;
-    const int base = (int)blockIdx.x * R;  // base + R <= Mp: code loads need no clamp
+    const int base = (int)blockIdx.x * (GLU ? RH : R);
+    const int I = p.M / 2;                 // GLU: gate rows [0, I), up rows [I, M)
+    // output row of the workgroup's row rr: GLU takes gate rows base + rr and,
+    // from rr = RH on, their up rows I + base + rr - RH
+    auto grow = [&](int rr) { return GLU ? (rr < RH ? base + rr : I + base + rr - RH) : base + rr; };
+    // code row of the lane's row i, < Mp
+    auto crow = [&](int i) { return CLAMP ? min(grow(r + 16 * i), p.Mp - 1) : base + r + 16 * i; };
     const int t0 = (int)blockIdx.y * BT;
     const int nt = min(BT, p.B - t0);
     const bool outl = p.rowp != nullptr;
@@ -318,7 +337,7 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(HO ? 8 : 1
             const int e = min(tid + u * nthr, nx4 - 1) * 4;
             const int ec = min(e, p.K - 4);
             xv4[t][u] = load4_act(x, (size_t)(t0 + tt) * p.xrow + ec);
-            if constexpr (PRO == kProRms)
+            if constexpr (RMS)
                 av4[t][u] = *reinterpret_cast<const float4 *>(p.pro_w + ec);
             if constexpr (PRO == kProSwiglu)
                 av4[t][u] = load4_act(x, (size_t)(t0 + tt) * p.xrow + p.K + ec);
@@ -328,13 +347,19 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(HO ? 8 : 1
     uint4 cw[RPL];
 #pragma unroll
     for (int i = 0; i < RPL; ++i)
-        cw[i] = *reinterpret_cast<const uint4 *>(p.codes + ((size_t)w * p.Mp + base + r + 16 * i) * kGS);
+        cw[i] = *reinterpret_cast<const uint4 *>(p.codes + ((size_t)w * p.Mp + crow(i)) * kGS);
     // the epilogue thread of (row tid % R, token tid / R) when tid < R * BT
-    float sc = 0.f, bs = 0.f;
+    // (GLU: thread tid < RH also takes the scale and bias of its up row)
+    float sc = 0.f, bs = 0.f, sc2 = 0.f, bs2 = 0.f;
     if (tid < R * BT) {
-        const int mm = min(base + tid % R, p.M - 1);
+        const int mm = min(grow(tid % R), p.M - 1);
         sc = p.scales[mm];
         bs = p.bias ? p.bias[mm] : 0.f;
+    }
+    if (GLU && tid < RH) {
+        const int mm = min(grow(tid + RH), p.M - 1);
+        sc2 = p.scales[mm];
+        bs2 = p.bias ? p.bias[mm] : 0.f;
     }
     int j0[RPL], j1[RPL];
 #pragma unroll
@@ -342,7 +367,7 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(HO ? 8 : 1
     if (outl) {
 #pragma unroll
         for (int i = 0; i < RPL; ++i) {
-            const int mm = min(base + r + 16 * i, p.M - 1);
+            const int mm = min(grow(r + 16 * i), p.M - 1);
             j0[i] = p.rowp[mm];
             j1[i] = p.rowp[mm + 1];
         }
@@ -366,7 +391,7 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(HO ? 8 : 1
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
             float4 v = xv4[t][u];
-            if constexpr (PRO == kProRms) {
+            if constexpr (RMS) {
                 // x^2 once per element: the clamped duplicate indices past nx4 count 0
                 if (tid + u * nthr < nx4) ssq[t] += sumsq4(v);
                 v = mul4(v, av4[t][u]);
@@ -384,7 +409,7 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(HO ? 8 : 1
                 float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
                 if (e < p.K) {
                     v = load4_act(x, (size_t)(t0 + t) * p.xrow + e);
-                    if constexpr (PRO == kProRms) {
+                    if constexpr (RMS) {
                         ssq[t] += sumsq4(v);
                         v = mul4(v, *reinterpret_cast<const float4 *>(p.pro_w + e));
                     }
@@ -394,7 +419,7 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(HO ? 8 : 1
                 reinterpret_cast<float4 *>(xs + t * KS)[i] = v;
             }
     }
-    if constexpr (PRO == kProRms) {
+    if constexpr (RMS) {
 #pragma unroll
         for (int t = 0; t < BT; ++t) {
             const float v = wave_sum_f(ssq[t]);
@@ -435,7 +460,7 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(HO ? 8 : 1
 #pragma unroll
             for (int i = 0; i < RPL; ++i)
                 cw[i] = *reinterpret_cast<const uint4 *>(
-                    p.codes + ((size_t)(s + NW) * p.Mp + base + r + 16 * i) * kGS);
+                    p.codes + ((size_t)(s + NW) * p.Mp + crow(i)) * kGS);
         }
         const float *xsj = xs + s * 256 + 4 * j;
 #pragma unroll
@@ -496,6 +521,29 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(HO ? 8 : 1
     // ---- epilogue: one thread per (row, token), the waves' partials summed in
     // wave order (a launch has at least 64 threads; R * BT may be more)
     T *y = static_cast<T *>(p.y);
+    if constexpr (GLU) {
+        // thread tid < RH: gate row base + tid and its up row, each finished as
+        // below, then silu(gate) * up (the kProSwiglu prologue's expression)
+        if (tid >= RH || base + tid >= I) return;
+        float a = 0.f, o = 0.f, a2 = 0.f, o2 = 0.f, q = 0.f;
+        for (int k = 0; k < NW; ++k) {
+            a += part[0][k][tid][0];
+            o += part[1][k][tid][0];
+            a2 += part[0][k][tid + RH][0];
+            o2 += part[1][k][tid + RH][0];
+            q += ssq_part[k][0];
+        }
+        const float rn = 1.0f / sqrtf(q / (float)p.K + p.eps);
+        float g = (a * rn) * sc, u = (a2 * rn) * sc2;
+        if (p.bias) {
+            g += bs;
+            u += bs2;
+        }
+        g += o * rn;
+        u += o2 * rn;
+        store_act(y, (size_t)(base + tid), silu_f(g) * u);
+        return;
+    }
     for (int e = tid; e < R * BT; e += nthr) {
         const int rr = e % R, t = e / R;
         const int m = base + rr;
@@ -505,7 +553,7 @@ __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(HO ? 8 : 1
             a += part[0][k][rr][t];
             o += part[1][k][rr][t];
         }
-        if constexpr (PRO == kProRms) {
+        if constexpr (RMS) {
             float q = 0.f;
             for (int k = 0; k < NW; ++k) q += ssq_part[k][t];
             const float rn = 1.0f / sqrtf(q / (float)p.K + p.eps);
@@ -589,8 +637,10 @@ constexpr long kHighOccWorkgroups = 512;
 
 template <typename T, int BT, int RPL, int PRO, bool RES>
 int launch_dec_v(const DecParams &dp, int M, int B, size_t lds, hipStream_t st) {
-    dim3 grid((M + 16 * RPL - 1) / (16 * RPL), (B + BT - 1) / BT);
-    if constexpr (BT == 1) {
+    // rows per workgroup 16 RPL (SwiGLU epilogue: 8 RPL gate rows and their up rows)
+    const int rows = PRO == kProRmsGlu ? 8 * RPL : 16 * RPL;
+    dim3 grid(((PRO == kProRmsGlu ? M / 2 : M) + rows - 1) / rows, (B + BT - 1) / BT);
+    if constexpr (BT == 1 && RPL <= 2) {
         if ((long)grid.x * grid.y > kHighOccWorkgroups)
             return launch_dec_g<T, BT, RPL, PRO, RES, true>(dp, grid, lds, st);
     }
@@ -631,6 +681,8 @@ int launch_dec(Linear *L, const void *x, void *y, int B, size_t lds, hipStream_t
             if (f.pro == kProSwiglu)
                 return r ? launch_dec_v<T, 1, RPL, kProSwiglu, true>(dp, L->M, B, lds, st)
                          : launch_dec_v<T, 1, RPL, kProSwiglu, false>(dp, L->M, B, lds, st);
+            if (f.pro == kProRmsGlu)
+                return launch_dec_v<T, 1, RPL, kProRmsGlu, false>(dp, L->M, B, lds, st);
             return launch_dec_v<T, 1, RPL, kProNone, true>(dp, L->M, B, lds, st);
         }
     }
@@ -661,9 +713,26 @@ int try_dec(Linear *L, const void *x, void *y, int B, hipStream_t st, const Fuse
     // 32-row workgroups when that still gives about one workgroup per CU
     const long wg32 = (long)((L->M + 31) / 32) * ((B + bt - 1) / bt);
     const bool r2 = wg32 >= 192;
+    if (bt == 1) {
+        // Batch 1 with 8193 .. 20480 rows: ceil(M / 4096) row tiles of 16 per
+        // workgroup, one workgroup per CU of the 256 with the rows spread
+        // evenly (the LDS gathers of a CU's rows set the time): 19456 rows run
+        // as 244 workgroups of 80 rows in 8.7 us, against 9.9 us for 608 of 32
+        // (up to three on a CU) and 12.8 us for 304 of 64 (two on 48 CUs).
+        int rpl = r2 ? 2 : 1;
+        const int tall = (L->M + kTallRowsPerTile - 1) / kTallRowsPerTile;
+        if (L->M > 2 * kTallRowsPerTile && tall <= kMaxTallTiles &&
+            kCB * 16 * sizeof(float) + xrow + (size_t)(2 * 16 * 16 * tall + 16) * sizeof(float) <= kMaxLds)
+            rpl = tall;
+        switch (rpl) {
+            case 1: return launch_dec<T, 1, 1>(L, x, y, B, lds, st, f);
+            case 2: return launch_dec<T, 1, 2>(L, x, y, B, lds, st, f);
+            case 3: return launch_dec<T, 1, 3>(L, x, y, B, lds, st, f);
+            case 4: return launch_dec<T, 1, 4>(L, x, y, B, lds, st, f);
+            default: return launch_dec<T, 1, 5>(L, x, y, B, lds, st, f);
+        }
+    }
     switch (bt * 2 + (r2 ? 1 : 0)) {
-        case 2: return launch_dec<T, 1, 1>(L, x, y, B, lds, st, f);
-        case 3: return launch_dec<T, 1, 2>(L, x, y, B, lds, st, f);
         case 4: return launch_dec<T, 2, 1>(L, x, y, B, lds, st, f);
         case 5: return launch_dec<T, 2, 2>(L, x, y, B, lds, st, f);
         case 8: return launch_dec<T, 4, 1>(L, x, y, B, lds, st, f);
@@ -803,13 +872,18 @@ constexpr int kTallMinRows = 65536;
 int linear_forward_fused(void *h, const float *x, float *y, int pro, const float *w, float eps,
                          const float *res, hipStream_t st) {
     Linear *L = static_cast<Linear *>(h);
-    if (pro < kProNone || pro > kProSwiglu) {
+    if (pro < kProNone || pro > kProRmsGlu) {
         set_error("unknown prologue %d", pro);
         return OJASX_ERR_INVALID;
     }
-    if (pro == kProRms && !w) return OJASX_ERR_NULL;
-    if (L->K % 4 || (pro == kProRms && (reinterpret_cast<uintptr_t>(w) & 15))) {
+    const bool rms = pro == kProRms || pro == kProRmsGlu;
+    if (rms && !w) return OJASX_ERR_NULL;
+    if (L->K % 4 || (rms && (reinterpret_cast<uintptr_t>(w) & 15))) {
         set_error("fused linear: in_features %% 4 == 0 and a 16-byte aligned norm weight needed");
+        return OJASX_ERR_INVALID;
+    }
+    if (pro == kProRmsGlu && (L->M % 2 || res)) {
+        set_error("fused linear: the SwiGLU epilogue needs an even out_features and no residual");
         return OJASX_ERR_INVALID;
     }
     // (the tall kernel stages x * w beside two LUT buffers: it fits the LDS up

@@ -37,30 +37,75 @@ def make_linear(pkg, r, M, K, density=0.0038, scales="u"):
                                          # tall RMSNorm linears (MFMA-built LUT slices):
                                          # ragged rows; x longer than the first staging pass
                                          (65600, 2560, 1, False), (65536, 5120, 1, False),
-                                         (65600, 512, 1, True)])   # with a residual: in place
+                                         (65600, 512, 1, True),    # with a residual: in place
+                                         # batch-1 workgroups of 3 - 5 row tiles
+                                         (19456, 2560, 1, False), (9000, 9728, 2, True),
+                                         (12289, 512, 0, True),
+                                         # RMSNorm + SwiGLU epilogue (gate rows, then up rows):
+                                         # the decoder's 2 x 9728; 1 - 4 tiles; a ragged last
+                                         # workgroup; the 64-VGPR build (641 workgroups)
+                                         (19456, 2560, 3, False), (700, 2560, 3, False),
+                                         (9002, 1024, 3, False), (16384, 256, 3, False),
+                                         (20482, 64, 3, False), (12290, 9728, 3, False)])
 def test_fused_linear(pkg, dev, M, K, pro, res):
     import torch
     r = np.random.default_rng(M + K + pro)
     lin, W = make_linear(pkg, r, M, K)
     xin = r.normal(size=(2 * K if pro == 2 else K)).astype(np.float32) * 3.0
     w = r.uniform(0.5, 1.5, size=K).astype(np.float32)
-    resid = r.normal(size=M).astype(np.float32)
+    n_out = M // 2 if pro == 3 else M
+    resid = r.normal(size=n_out).astype(np.float32)
     x_t = torch.from_numpy(xin).to(dev)
     w_t = torch.from_numpy(w).to(dev)
     y_t = torch.from_numpy(resid.copy()).to(dev)      # residual in place (y == residual)
-    out = y_t if res else torch.empty(M, device=dev)
+    out = y_t if res else torch.empty(n_out, device=dev)
     rc = pkg.lib().ojasx_linear_forward_fused_device(
-        lin.handle, vp(x_t), vp(out), pro, vp(w_t) if pro == 1 else None, 1e-6,
+        lin.handle, vp(x_t), vp(out), pro, vp(w_t) if pro in (1, 3) else None, 1e-6,
         vp(y_t) if res else None, None)
     assert rc == 0, pkg.lib().ojasx_get_last_error()
     torch.cuda.synchronize()
     x64 = xin.astype(np.float64)
-    if pro == 1:
+    if pro in (1, 3):
         x64 = no.rmsnorm(x64, w, 1e-6)
     elif pro == 2:
         x64 = no.silu(x64[:K]) * x64[K:]
     want = W @ x64 + (resid if res else 0.0)
+    if pro == 3:
+        want = no.silu(want[:n_out]) * want[n_out:]
     assert rel_err(out.cpu().numpy(), want) < 1e-5
+
+
+def test_swiglu_epilogue_equals_two_step(pkg, dev):
+    """The SwiGLU epilogue (prologue 3) gives the bits of the two-step form it
+    replaces in the decoder: the RMSNorm linear's 2I outputs (prologue 1),
+    then silu(gate) * up as the SwiGLU prologue computes it, fed to a down
+    linear (prologue 2) against that linear on the epilogue's output
+    (prologue 0): equal outputs, bit for bit, at the decoder's 2560 -> 2 x 9728."""
+    import torch
+    r = np.random.default_rng(97)
+    I, H = 9728, 2560
+    gu, _ = make_linear(pkg, r, 2 * I, H)
+    dn, _ = make_linear(pkg, r, H, I)
+    x_t = torch.from_numpy(r.normal(size=H).astype(np.float32)).to(dev)
+    w_t = torch.from_numpy(r.uniform(0.5, 1.5, size=H).astype(np.float32)).to(dev)
+    L = pkg.lib()
+    z = torch.empty(2 * I, device=dev)
+    h = torch.empty(I, device=dev)
+    y2, y1 = torch.zeros(H, device=dev), torch.zeros(H, device=dev)
+    assert L.ojasx_linear_forward_fused_device(gu.handle, vp(x_t), vp(z), 1, vp(w_t), 1e-6,
+                                               None, None) == 0
+    assert L.ojasx_linear_forward_fused_device(dn.handle, vp(z), vp(y2), 2, None, 0.0, None,
+                                               None) == 0
+    assert L.ojasx_linear_forward_fused_device(gu.handle, vp(x_t), vp(h), 3, vp(w_t), 1e-6,
+                                               None, None) == 0
+    assert L.ojasx_linear_forward_fused_device(dn.handle, vp(h), vp(y1), 0, None, 0.0, None,
+                                               None) == 0
+    torch.cuda.synchronize()
+    zz = z.cpu().numpy()
+    g, u = zz[:I], zz[I:]
+    h_two_step = (g / (np.float32(1) + np.exp(-g))) * u      # float32 throughout
+    assert np.abs(h.cpu().numpy() - h_two_step).max() <= 2e-6 * np.abs(h_two_step).max()
+    assert torch.equal(y1, y2)
 
 
 def test_fused_linear_tall_beyond_tall_kernel_lds(pkg, dev):
@@ -107,8 +152,16 @@ def test_fused_linear_errors(pkg, dev):
     x = torch.zeros(64, device=dev)
     y = torch.zeros(32, device=dev)
     L = pkg.lib()
+    w = torch.ones(64, device=dev)
     assert L.ojasx_linear_forward_fused_device(lin.handle, vp(x), vp(y), 1, None, 1e-6, None, None) == -1
-    assert L.ojasx_linear_forward_fused_device(lin.handle, vp(x), vp(y), 3, None, 1e-6, None, None) == -3
+    assert L.ojasx_linear_forward_fused_device(lin.handle, vp(x), vp(y), 3, None, 1e-6, None, None) == -1
+    assert L.ojasx_linear_forward_fused_device(lin.handle, vp(x), vp(y), 4, vp(w), 1e-6, None, None) == -3
+    # the SwiGLU epilogue takes no residual and an even out_features
+    assert L.ojasx_linear_forward_fused_device(lin.handle, vp(x), vp(y), 3, vp(w), 1e-6, vp(y),
+                                               None) == -3
+    odd, _ = make_linear(pkg, r, 33, 64)
+    assert L.ojasx_linear_forward_fused_device(odd.handle, vp(x), vp(y), 3, vp(w), 1e-6, None,
+                                               None) == -3
     assert L.ojasx_linear_forward_fused_device(None, vp(x), vp(y), 0, None, 1e-6, None, None) == -1
 
 

@@ -83,7 +83,11 @@ def test_reference_t2(pkg):
                                    (333, 2000, 35),   # MFMA path: ragged rows, tokens, slices
                                    (70, 464, 33),
                                    (333, 2000, 9),    # MFMA, one row tile per workgroup
-                                   (517, 1040, 27)])  # MFMA, two row tiles per workgroup
+                                   (517, 1040, 27),   # MFMA, two row tiles per workgroup
+                                   # batch 1, tall: 3 / 4 / 5 row tiles per workgroup
+                                   # (48- and 80-row workgroups end past the padded rows)
+                                   (9000, 1024, 1), (12289, 256, 1), (19456, 2560, 1),
+                                   (20481, 64, 1)])   # past 5 tiles: 32-row workgroups
 def test_integer_inputs_bit_exact(pkg, dev, M, K, B):
     import torch
     c = integer_case(M * 7 + B, M=M, K=K, B=B)
@@ -140,11 +144,11 @@ def test_mfma_batched_shapes(pkg, dev, M, K, B, dt, density):
     assert rel_err(y, y_ref) < (BF16_TOL if dt else F32_TOL)
 
 
-@pytest.mark.parametrize("B", [1, 8, 64])
-def test_baseline_gate_up_bf16(pkg, dev, B):
+@pytest.mark.parametrize("B,M", [(1, 6912), (8, 6912), (64, 6912), (1, 19456)])
+def test_baseline_gate_up_bf16(pkg, dev, B, M):
     import torch
-    d = gen.linear(6912, 2560, B=B, seed=50 + B)
-    nat = native_linear(pkg, d, 6912, 2560)
+    d = gen.linear(M, 2560, B=B, seed=50 + B)
+    nat = native_linear(pkg, d, M, 2560)
     xb = torch.from_numpy(d["x"]).to(dev).to(torch.bfloat16)
     y = dev_forward(pkg, nat, xb, 1, torch.bfloat16).float().cpu().numpy()
     x_rounded = xb.float().cpu().numpy()
