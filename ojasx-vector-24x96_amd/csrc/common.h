@@ -166,8 +166,13 @@ int launch_moe_bank(const MoEBankLaunch &l, hipStream_t st);
 bool moe_resident_fits(int K, int xs);
 int launch_moe_resident(const MoEBankLaunch &l, int groups, int slots, hipStream_t st);
 // One tall batch-1 fp32 linear with the RMSNorm prologue (lut_group.hip):
-// it.x / it.y set, w the norm weight; both 16-byte aligned.
-int launch_tall_rms(const GroupItem &it, const float *w, float eps, hipStream_t st);
+// it.x / it.y set, w the norm weight; both 16-byte aligned.  With arg_part
+// set, workgroup b also writes arg_part[b] = (max, first row of it as the
+// float's bits) over its 256 rows' outputs above -inf (NaN skipped; none: -inf
+// and row INT_MAX): tall_rows_per_part() rows per partial.
+int launch_tall_rms(const GroupItem &it, const float *w, float eps, hipStream_t st,
+                    float2 *arg_part = nullptr);
+constexpr int tall_rows_per_part() { return 256; }
 
 // The block_dim-16 linear for many tokens on MFMA (lut_mm.hip): x [B][K] in
 // dtype (fp32 16-byte aligned, or bf16), y [B][M] in dtype.
@@ -188,6 +193,12 @@ int launch_mm(const MmParams &p, int dtype, hipStream_t st);
 int linear_forward(void *h, const void *x, void *y, int B, int dtype, hipStream_t st);
 int linear_forward_fused(void *h, const float *x, float *y, int pro, const float *w, float eps,
                          const float *res, hipStream_t st);
+// The RMSNorm linear (prologue 1, no residual) of a decoder's LM head with the
+// greedy pick's first stage: when it runs on the tall kernel, arg_part
+// [ceil(M / tall_rows_per_part())] receives the per-workgroup maxima and
+// *n_part their count; otherwise *n_part = 0 and the pick scans y.
+int linear_forward_lm_head(void *h, const float *x, float *y, const float *w, float eps,
+                           float2 *arg_part, int *n_part, hipStream_t st);
 
 // Paged code-domain decode (lut_kv.hip) with the context length read on the
 // device, *len_dev + len_add <= T_max; head dim 128, block dim 16; chunks of

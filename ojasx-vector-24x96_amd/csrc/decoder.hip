@@ -35,6 +35,7 @@ constexpr int kHd = 128;          // head dim of the decode kernels
 constexpr int kBd = 16;           // block dim of every LUT linear and of the KV codebooks
 constexpr int kG = kHd / kBd;     // KV code groups per head
 constexpr int kArgNT = 1024;
+constexpr int kArgBatch = 8;      // float4 loads in flight per thread in the logit scan
 }  // namespace
 
 struct AttnParams {
@@ -376,10 +377,12 @@ __global__ __launch_bounds__(kAttnNT) void attn_decode_kernel(AttnParams p) {
     }
 }
 
-// Greedy pick over V logits (first maximum), then the picked token's
-// embedding row into x; thread 0 records the token and advances
-// state = {position, step, token}.
+// Greedy pick over V logits (first maximum above -inf; none: token 0), from
+// the n_part per-workgroup maxima of the LM head when n_part > 0, else from
+// the logits; then the picked token's embedding row into x; thread 0 records
+// the token and advances state = {position, step, token}.
 __global__ __launch_bounds__(kArgNT) void argmax_embed_kernel(const float *logits, int V,
+                                                             const float2 *part, int n_part,
                                                              const float *emb, int hidden,
                                                              float *x, int *state, int *tokens,
                                                              int max_steps) {
@@ -387,21 +390,32 @@ __global__ __launch_bounds__(kArgNT) void argmax_embed_kernel(const float *logit
     __shared__ int wi[kArgNT / 64];
     __shared__ int pick;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    // each thread visits its indices in increasing order, 8 float4 loads in
-    // flight per batch; strict > keeps the first maximum
     float best = -INFINITY;
     int bi = 0x7fffffff;
-    const int n4 = V / 4;
+    // partials of the LM head's workgroups (first maximum of each, in row
+    // order): strict > keeps the first, equal maxima go to the lower row below
+    for (int i = tid; i < n_part; i += kArgNT) {
+        const float2 c = part[i];
+        if (c.x > best || (c.x == best && __float_as_int(c.y) < bi)) {
+            best = c.x;
+            bi = __float_as_int(c.y);
+        }
+    }
+    // no partials: each thread visits its logits in increasing order,
+    // kArgBatch float4 loads in flight per batch; strict > keeps the first
+    // maximum
+    const int n4 = n_part ? 0 : V / 4;
     const float4 *l4 = reinterpret_cast<const float4 *>(logits);
-    for (int b = tid; b < n4; b += kArgNT * 8) {
-        float4 v[8];
+    for (int b = tid; b < n4; b += kArgNT * kArgBatch) {
+        float4 v[kArgBatch];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
-            const int i4 = b + u * kArgNT;
-            v[u] = i4 < n4 ? l4[i4] : make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
+        for (int u = 0; u < kArgBatch; ++u) {
+            const int i4 = min(b + u * kArgNT, n4 - 1);
+            v[u] = l4[i4];
+            if (b + u * kArgNT >= n4) v[u] = make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
         }
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
+        for (int u = 0; u < kArgBatch; ++u) {
             const int i = (b + u * kArgNT) * 4;
             if (v[u].x > best) { best = v[u].x; bi = i; }
             if (v[u].y > best) { best = v[u].y; bi = i + 1; }
@@ -409,7 +423,7 @@ __global__ __launch_bounds__(kArgNT) void argmax_embed_kernel(const float *logit
             if (v[u].w > best) { best = v[u].w; bi = i + 3; }
         }
     }
-    for (int i = n4 * 4 + tid; i < V; i += kArgNT) {
+    for (int i = n4 * 4 + tid; i < (n_part ? 0 : V); i += kArgNT) {
         const float v = logits[i];
         if (v > best) {
             best = v;
@@ -431,7 +445,7 @@ __global__ __launch_bounds__(kArgNT) void argmax_embed_kernel(const float *logit
                 bm = wm[q];
                 b = wi[q];
             }
-        pick = min(max(b, 0), V - 1);            // all-NaN logits: token 0
+        pick = b < V ? b : 0;                     // no logit above -inf (all NaN): token 0
     }
     __syncthreads();
     const int tok = pick;
@@ -463,8 +477,8 @@ struct Decoder {
     float eps = 0.f, theta = 0.f;
     std::vector<DecoderLayer> L;
     void *lm = nullptr;
-    DevBuf final_norm, emb, cos_t, sin_t, bt, x, qkv, attn, gu, logits, part_o, part_ml, state,
-        tokens;
+    DevBuf final_norm, emb, cos_t, sin_t, bt, x, qkv, attn, gu, logits, arg_part, part_o, part_ml,
+        state, tokens;
     hipStream_t stream = nullptr;
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
@@ -526,12 +540,13 @@ struct Decoder {
                                       x.as<float>(), st);
             if (rc) return rc;
         }
-        rc = linear_forward_fused(lm, x.as<float>(), logits.as<float>(), 1, final_norm.as<float>(),
-                                  eps, nullptr, st);
+        int n_part = 0;
+        rc = linear_forward_lm_head(lm, x.as<float>(), logits.as<float>(), final_norm.as<float>(),
+                                    eps, arg_part.as<float2>(), &n_part, st);
         if (rc) return rc;
         OJX_LAUNCH(argmax_embed_kernel, dim3(1), dim3(kArgNT), 0, st, logits.as<float>(), vocab,
-                   emb.as<float>(), hidden, x.as<float>(), state.as<int>(), tokens.as<int>(),
-                   max_steps);
+                   arg_part.as<float2>(), n_part, emb.as<float>(), hidden, x.as<float>(),
+                   state.as<int>(), tokens.as<int>(), max_steps);
         OJX_HIP(hipGetLastError());
         return OJASX_OK;
     }
@@ -625,6 +640,9 @@ OJASX_API OjasxDecoderHandle ojasx_create_decoder(int hidden, int layers, int q_
     if (!rc) rc = d->attn.ensure((size_t)q_heads * kHd * 4);
     if (!rc) rc = d->gu.ensure((size_t)2 * intermediate * 4);
     if (!rc) rc = d->logits.ensure((size_t)vocab * 4);
+    if (!rc)   // the LM head's per-workgroup argmax partials
+        rc = d->arg_part.ensure((size_t)(vocab + tall_rows_per_part() - 1) / tall_rows_per_part() *
+                                sizeof(float2));
     if (!rc) rc = d->part_o.ensure((size_t)q_heads * (d->n_chunks() + 1) * kHd * 4);
     if (!rc) rc = d->part_ml.ensure((size_t)q_heads * (d->n_chunks() + 1) * 2 * 4);
     const int st0[4] = {0, 0, 0, 0};

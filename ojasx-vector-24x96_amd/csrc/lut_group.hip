@@ -23,7 +23,8 @@ constexpr int kTNT = 256;               // threads, one row each
 constexpr int kTPF = 2;                 // slices of codes in flight
 }  // namespace
 
-__global__ __launch_bounds__(kTNT) void lut_tall_rms_kernel(GroupItem it, const float *w, float eps) {
+__global__ __launch_bounds__(kTNT) void lut_tall_rms_kernel(GroupItem it, const float *w, float eps,
+                                                          float2 *arg_part) {
     __shared__ float L[slices::lut_bytes(true) / sizeof(float)];
     extern __shared__ float xs[];                     // [S * 256]: x * w, zero past K
     __shared__ float red[kTNT / 64];
@@ -86,9 +87,8 @@ __global__ __launch_bounds__(kTNT) void lut_tall_rms_kernel(GroupItem it, const 
     slices::slice_loop<4, 1, true, kTPF>(xs, L, bop, it.codes, row, it.Mp, 0, S, wv, lane, ring, acc);
 
     // ---- epilogue: ((r * sum) * s_m + bias) + r * outliers (4 loads in flight)
-    if (m >= it.M) return;
     float o = 0.f;
-    if (outl) {
+    if (outl && m < it.M) {
         int j = j0;
         for (; j + 4 <= j1; j += 4) {
             int c[4];
@@ -105,10 +105,30 @@ __global__ __launch_bounds__(kTNT) void lut_tall_rms_kernel(GroupItem it, const 
     }
     float y = (acc[0] * rn) * sc;
     if (it.bias) y += bs;
-    it.y[m] = y + o * rn;
+    y += o * rn;
+    if (m < it.M) it.y[m] = y;
+    if (arg_part) {
+        // the workgroup's first maximum: strict > over rows in order, NaN and
+        // -inf never taken
+        const float v = (m < it.M && y > -INFINITY) ? y : -INFINITY;
+        const float wm = wave_max_f(v);
+        const int wi = wave_min_i(v > -INFINITY && v == wm ? m : 0x7fffffff);
+        __shared__ float2 wpart[kTNT / 64];
+        if (lane == 0) wpart[wv] = make_float2(wm, __int_as_float(wi));
+        __syncthreads();
+        if (tid == 0) {
+            float2 b = wpart[0];
+            for (int q = 1; q < kTNT / 64; ++q) {
+                const float2 c = wpart[q];
+                if (c.x > b.x) b = c;   // equal maxima: the lower wave holds the lower row
+            }
+            arg_part[blockIdx.x] = b;
+        }
+    }
 }
 
-int launch_tall_rms(const GroupItem &it, const float *w, float eps, hipStream_t st) {
+int launch_tall_rms(const GroupItem &it, const float *w, float eps, hipStream_t st,
+                    float2 *arg_part) {
     if ((reinterpret_cast<uintptr_t>(it.x) | reinterpret_cast<uintptr_t>(w)) & 15) {
         set_error("tall linear: 16-byte aligned x and norm weight needed");
         return OJASX_ERR_INVALID;
@@ -118,7 +138,9 @@ int launch_tall_rms(const GroupItem &it, const float *w, float eps, hipStream_t 
     int rc = ensure_dyn_lds(reinterpret_cast<const void *>(&lut_tall_rms_kernel),
                             lds + slices::lut_bytes(true), &granted);
     if (rc) return rc;
-    OJX_LAUNCH(lut_tall_rms_kernel, dim3((it.M + kTNT - 1) / kTNT), dim3(kTNT), lds, st, it, w, eps);
+    static_assert(kTNT == tall_rows_per_part(), "one argmax partial per workgroup");
+    OJX_LAUNCH(lut_tall_rms_kernel, dim3((it.M + kTNT - 1) / kTNT), dim3(kTNT), lds, st, it, w, eps,
+               arg_part);
     OJX_HIP(hipGetLastError());
     return OJASX_OK;
 }

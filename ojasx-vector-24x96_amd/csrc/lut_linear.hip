@@ -869,9 +869,12 @@ int linear_shape(const void *h, int *K, int *M, int *D) {
 // rows (76 workgroups) took 11.8 vs 11.3 us.
 constexpr int kTallMinRows = 65536;
 
-int linear_forward_fused(void *h, const float *x, float *y, int pro, const float *w, float eps,
-                         const float *res, hipStream_t st) {
+// The fused forward; with n_part set, a tall launch also writes the argmax
+// partials arg_part and their count (0 on the in-place path).
+static int fused_forward(void *h, const float *x, float *y, int pro, const float *w, float eps,
+                         const float *res, hipStream_t st, float2 *arg_part, int *n_part) {
     Linear *L = static_cast<Linear *>(h);
+    if (n_part) *n_part = 0;
     if (pro < kProNone || pro > kProRmsGlu) {
         set_error("unknown prologue %d", pro);
         return OJASX_ERR_INVALID;
@@ -897,7 +900,8 @@ int linear_forward_fused(void *h, const float *x, float *y, int pro, const float
         if (rc) return rc;
         it.x = x;
         it.y = y;
-        return launch_tall_rms(it, w, eps, st);
+        if (n_part) *n_part = (L->M + tall_rows_per_part() - 1) / tall_rows_per_part();
+        return launch_tall_rms(it, w, eps, st, n_part ? arg_part : nullptr);
     }
     Fuse f;
     f.pro = pro;
@@ -917,6 +921,16 @@ int linear_forward_fused(void *h, const float *x, float *y, int pro, const float
         return OJASX_ERR_INVALID;
     }
     return rc;
+}
+
+int linear_forward_fused(void *h, const float *x, float *y, int pro, const float *w, float eps,
+                         const float *res, hipStream_t st) {
+    return fused_forward(h, x, y, pro, w, eps, res, st, nullptr, nullptr);
+}
+
+int linear_forward_lm_head(void *h, const float *x, float *y, const float *w, float eps,
+                           float2 *arg_part, int *n_part, hipStream_t st) {
+    return fused_forward(h, x, y, kProRms, w, eps, nullptr, st, arg_part, n_part);
 }
 
 int launch_lut_build(const void *x, const float *cb, int B, int K, int D, int G, int Gp,
