@@ -187,6 +187,7 @@ struct MmParams {
     const void *x;
     void *y;
     int K, M, Mp, S, B;
+    const void *cb3;        // the codebook's exact bf16 pieces (split_codebook_bf16x3)
 };
 int launch_mm(const MmParams &p, int dtype, hipStream_t st);
 // One linear handle's forward of B tokens (dtype F32 or BF16) on st.

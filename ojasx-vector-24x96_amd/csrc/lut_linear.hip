@@ -809,7 +809,7 @@ int forward(Linear *L, const void *x, void *y, int B, int dtype, hipStream_t st)
         MmParams mp{L->codes.as<uint8_t>(), L->codebook.as<float>(), L->scales.as<float>(),
                     L->has_bias ? L->bias.as<float>() : nullptr,
                     L->nnz ? L->rowp.as<int>() : nullptr, L->col.as<int>(), L->val.as<float>(),
-                    x, y, L->K, L->M, L->Mp, L->S, B};
+                    x, y, L->K, L->M, L->Mp, L->S, B, L->cb3.ptr};
         return launch_mm(mp, dtype, st);
     }
     int rc = dtype == OJASX_DTYPE_F32 ? try_dec<float>(L, x, y, B, st)

@@ -291,6 +291,297 @@ __global__ __launch_bounds__(MmShape<RT>::kNT) __attribute__((amdgpu_waves_per_e
     }
 }
 
+// ---- 32-row x 32-token tiles on bf16 MFMA
+//
+// lut_mm32_kernel: workgroup = 32 rows x 32 TT tokens, 8 waves: wave q
+// computes the 32 x 32 tiles of the TT token tiles over groups 2q, 2q + 1 of
+// every 16-group input slice (each A operand serves every token tile), on
+// v_mfma_f32_32x32x16_bf16 (one 16-dimension group per MFMA):
+//   A[m][k] = C[code(m, g)][k]  (the codebook's exact bf16 pieces, staged in LDS),
+//   B[k][n] = x_n[16 g + k]     (x staged per slice in LDS as fp32, split into
+//                                exact bf16 pieces at use; bf16 activations are
+//                                one piece already),
+// with the six products a_i b_j, i + j <= 4, of fp32 inputs (x split by
+// truncation, split3_trunc: the three left out are below 2^-22 of |a b|) or
+// the three a_i b of bf16 inputs, all accumulated in fp32 (mfma32_bf16x3's
+// operand layout).  A 32 x 32 tile reads 3 KB of A and 1-3 KB
+// of B per group for 16384 multiply-adds, against 2 KB per 4096 for the 16 x 16
+// fp32 tiles of lut_mm_kernel.  The x slices are staged through a register ring
+// one slice ahead; codes kPF slices ahead.
+//
+// The input parts' partial tiles meet in LDS at the end, added in part order;
+// wave q then finishes the RV = 16 / KP values r = RV q .. RV q + RV - 1 of its
+// lanes (rows 8 (r / 4) + 4 h + r % 4 of token n, h = lane / 32, n = lane %
+// 32).  The CSR outliers are added slice by slice from the staged x (entries
+// in LDS, sorted by column; thread tid takes row tid / 16 for tokens tid % 16
+// + 16 k), or from memory when the workgroup's rows hold more than kM32Csr
+// entries; their sums reach the epilogue through LDS.  Epilogue
+// (s_m * sum + bias) + outliers.
+namespace {
+constexpr int kM32XS = 260;      // floats per staged x row (256 + pad: conflict-free b128 reads)
+constexpr int kM32Csr = 512;     // CSR entries staged per workgroup
+constexpr int kM32PF = 4;        // slices of codes in flight
+constexpr int kM32NT = 512;      // threads: 8 waves
+}  // namespace
+
+// Exact three-way bf16 split of 8 fp32 values by truncation: v = p0 + p1 + p2,
+// p0 = v with its low 16 bits cleared, p1 the same of v - p0, p2 = v - p0 - p1
+// (the remainders are exact in fp32; p2 has at most 8 significant bits, a
+// bf16 value).  |p1| < 2^-7 |v|, |p2| < 2^-15 |v|.  Five operations per value
+// (two of them packing): the operand split that every workgroup repeats for
+// its x slices.
+__device__ __forceinline__ void split3_trunc(const float (&v)[8], bf16x8_t (&p)[3]) {
+    uint32_t w[3][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t ua = __float_as_uint(v[2 * i]), ub = __float_as_uint(v[2 * i + 1]);
+        const float ra = v[2 * i] - __uint_as_float(ua & 0xffff0000u);
+        const float rb = v[2 * i + 1] - __uint_as_float(ub & 0xffff0000u);
+        const uint32_t ura = __float_as_uint(ra), urb = __float_as_uint(rb);
+        const float sa = ra - __uint_as_float(ura & 0xffff0000u);
+        const float sb = rb - __uint_as_float(urb & 0xffff0000u);
+        // high halves of (a, b) into one word, element 2i in its low half
+        w[0][i] = __builtin_amdgcn_perm(ub, ua, 0x07060302u);
+        w[1][i] = __builtin_amdgcn_perm(urb, ura, 0x07060302u);
+        w[2][i] = __builtin_amdgcn_perm(__float_as_uint(sb), __float_as_uint(sa), 0x07060302u);
+    }
+#pragma unroll
+    for (int k = 0; k < 3; ++k) __builtin_memcpy(&p[k], w[k], sizeof(bf16x8_t));
+}
+
+template <typename T, int TT>
+__global__ __launch_bounds__(kM32NT) void lut_mm32_kernel(MmParams p) {
+    constexpr int KP = 8;                         // input parts, one wave each
+    constexpr int GPS = 16 / KP;                  // groups per slice per wave
+    constexpr int RV = 16 / KP;                   // tile values a wave finishes
+    constexpr int NTOK = 32 * TT;
+    constexpr int XU = NTOK * 64 / kM32NT;        // float4 of a slice's x per thread
+    constexpr bool BF = !std::is_same<T, float>::value;
+    __shared__ bf16x8_t cb3s[256 * 2 * 3];        // [centroid][half][piece]
+    __shared__ __align__(16) float xs[2][NTOK * kM32XS];   // x slices; the partial tiles at the end
+    __shared__ unsigned short lcol[kM32Csr];
+    __shared__ float lval[kM32Csr];
+    static_assert(TT * KP * 16 * 64 <= NTOK * kM32XS && 32 * NTOK <= NTOK * kM32XS,
+                  "partial tiles and outlier sums fit the x buffers");
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int q = w;
+    const int h = lane >> 5, n = lane & 31;
+    const int m0 = blockIdx.x * 32;
+    const int n0 = blockIdx.y * NTOK;
+    const int row = min(m0 + n, p.Mp - 1);        // the lane's A row (rows past M: never stored)
+    auto row_of = [&](int r) { return 8 * (r >> 2) + 4 * h + (r & 3); };   // tile row of value r
+
+    // ---- round trip 1: the codebook pieces, x slices 0 and 1, the CSR ranges, codes
+    constexpr int CBU = 256 * 2 * 3 / kM32NT;
+    const bf16x8_t *gcb = static_cast<const bf16x8_t *>(p.cb3);
+    bf16x8_t c3[CBU];
+#pragma unroll
+    for (int u = 0; u < CBU; ++u) c3[u] = gcb[tid + u * kM32NT];
+    auto load_x = [&](int s, float4 (&r)[XU]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int u = 0; u < XU; ++u) {
+            const int i = tid + u * kM32NT;       // float4 i of the slice: token i / 64, dims 4 (i % 64)
+            const int nn = min(n0 + (i >> 6), p.B - 1);
+            const int k = min(s * 256 + 4 * (i & 63), p.K - 4);
+            r[u] = load4_act(static_cast<const T *>(p.x), (size_t)nn * p.K + k);
+        }
+    };
+    auto store_x = [&](int s, float *dst, const float4 (&r)[XU]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int u = 0; u < XU; ++u) {
+            const int i = tid + u * kM32NT;
+            const bool ok = n0 + (i >> 6) < p.B && s * 256 + 4 * (i & 63) < p.K;   // K % 16 == 0
+            reinterpret_cast<float4 *>(dst + (i >> 6) * kM32XS)[i & 63] =
+                ok ? r[u] : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+    };
+    float4 x0[XU], xr[XU];
+    load_x(0, x0);
+    load_x(min(1, p.S - 1), xr);
+    // outliers: thread tid adds those of row ro = tid / 16 for tokens
+    // tid % 16 + 16 k, k < NOT
+    constexpr int NOT = NTOK / 16;
+    const int ro = tid >> 4, to = tid & 15;
+    int e_lo = 0, e_hi = 0, j = 0, je = 0;
+    if (p.rowp) {
+        e_lo = gld(p.rowp + m0);
+        e_hi = gld(p.rowp + min(m0 + 32, p.M));
+        j = gld(p.rowp + min(m0 + ro, p.M - 1));
+        je = m0 + ro < p.M ? gld(p.rowp + m0 + ro + 1) : j;
+    }
+    uint32_t cr[kM32PF];   // codes of slices s .. s + kM32PF - 1, slot s % kM32PF
+    auto load_codes = [&](int s) __attribute__((always_inline)) {
+        const uint8_t *src = p.codes + ((size_t)s * p.Mp + row) * 16 + GPS * q;
+        if constexpr (GPS == 4) return gld(reinterpret_cast<const uint32_t *>(src));
+        else return (uint32_t)gld(reinterpret_cast<const unsigned short *>(src));
+    };
+#pragma unroll
+    for (int u = 0; u < kM32PF; ++u) cr[u] = load_codes(min(u, p.S - 1));
+    // ---- round trip 2: the CSR entries of the workgroup's rows into LDS when they fit
+    const bool staged = e_hi - e_lo <= kM32Csr;
+    if (p.rowp && staged && e_hi > e_lo) {
+        const int e = min(e_lo + tid, e_hi - 1);
+        const int c = gld(p.col + e);
+        const float v = gld(p.val + e);
+        if (e_lo + tid < e_hi) {
+            lcol[tid] = (unsigned short)c;
+            lval[tid] = v;
+        }
+    }
+    static_assert(kM32Csr == kM32NT, "one staged entry per thread");
+#pragma unroll
+    for (int u = 0; u < CBU; ++u) cb3s[tid + u * kM32NT] = c3[u];
+    store_x(0, xs[0], x0);
+    __syncthreads();
+
+    f32x16_t acc[TT];
+#pragma unroll
+    for (int t = 0; t < TT; ++t) acc[t] = f32x16_t{};
+    float o[NOT];
+#pragma unroll
+    for (int k = 0; k < NOT; ++k) o[k] = 0.f;
+    j -= e_lo;
+    je -= e_lo;
+    const bool outl = p.rowp && staged;
+    // Slice s: code slot s % kM32PF, a constant in the unrolled body; the
+    // slot is refilled with slice s + kM32PF, and the x ring with slice s + 2,
+    // unconditionally (clamped to the last slice), so the loop body has one
+    // path and the wait counts of the rings stay exact across its back edge.
+    auto slice = [&](const int s, const int u) __attribute__((always_inline)) {
+        const uint32_t cw = cr[u];
+#pragma unroll
+        for (int i = 0; i < GPS; ++i) {
+            const int g = GPS * q + i;
+            const uint32_t code = (cw >> (8 * i)) & 0xffu;
+            const bf16x8_t *ap = cb3s + (code * 2 + h) * 3;
+            const bf16x8_t a0 = ap[0], a1 = ap[1], a2 = ap[2];
+#pragma unroll
+            for (int t = 0; t < TT; ++t) {            // each A operand serves every token tile
+                const float *xt = xs[s & 1] + (32 * t + n) * kM32XS + 16 * g + 8 * h;
+                const float4 xa = *reinterpret_cast<const float4 *>(xt);
+                const float4 xb = *reinterpret_cast<const float4 *>(xt + 4);
+                const float xv[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+                if constexpr (BF) {
+                    bf16x8_t b;
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) b[e] = (__bf16)xv[e];   // exact: bf16 values
+                    acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a2, b, acc[t], 0, 0, 0);
+                    acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, b, acc[t], 0, 0, 0);
+                    acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, b, acc[t], 0, 0, 0);
+                } else {
+                    bf16x8_t b[3];
+                    split3_trunc(xv, b);
+                    acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, b[2], acc[t], 0, 0, 0);
+                    acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, b[1], acc[t], 0, 0, 0);
+                    acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a2, b[0], acc[t], 0, 0, 0);
+                    acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, b[1], acc[t], 0, 0, 0);
+                    acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, b[0], acc[t], 0, 0, 0);
+                    acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, b[0], acc[t], 0, 0, 0);
+                }
+            }
+        }
+        // the thread's outliers whose columns fall in this slice, in column
+        // order (a row's entries are sorted by column): kOutPass candidates
+        // per pass, the reads of a pass in flight together (one pass covers a
+        // slice unless the row has more entries in it)
+        if (outl) {
+            const float *xsl = xs[s & 1] + to * kM32XS - s * 256;
+            const int lim = (s + 1) * 256;
+            bool more = true;
+            while (more) {
+                int c[kOutPass];
+                float vv[kOutPass];
+#pragma unroll
+                for (int k = 0; k < kOutPass; ++k) {
+                    const int e = min(j + k, kM32Csr - 1);
+                    c[k] = lcol[e];
+                    vv[k] = lval[e];
+                }
+                bool in = true;
+                int took = 0;
+#pragma unroll
+                for (int k = 0; k < kOutPass; ++k) {
+                    in = in && j + k < je && c[k] < lim;
+                    const int cc = in ? c[k] : s * 256;
+#pragma unroll
+                    for (int u = 0; u < NOT; ++u) {
+                        const float xv = xsl[16 * u * kM32XS + cc];
+                        if (in) o[u] += vv[k] * xv;
+                    }
+                    took += in ? 1 : 0;
+                }
+                j += took;
+                more = took == kOutPass;
+            }
+        }
+        // slice s + 1 into the other buffer (past the last slice: a clamped
+        // reload, never read), then the rings refilled
+        store_x(min(s + 1, p.S - 1), xs[(s + 1) & 1], xr);
+        load_x(min(s + 2, p.S - 1), xr);
+        cr[u] = load_codes(min(s + kM32PF, p.S - 1));
+        __syncthreads();   // slice s + 1 staged; slice s's reads done before it is overwritten
+    };
+    int s0 = 0;
+    for (; s0 + kM32PF <= p.S; s0 += kM32PF) {
+#pragma unroll
+        for (int u = 0; u < kM32PF; ++u) slice(s0 + u, u);
+    }
+#pragma unroll
+    for (int u = 0; u < kM32PF - 1; ++u)
+        if (s0 + u < p.S) slice(s0 + u, u);
+
+    // ---- a dense-outlier block: the row's entries and x from memory
+    if (p.rowp && !staged && m0 + ro < p.M)
+#pragma unroll
+        for (int u = 0; u < NOT; ++u) {
+            const int nn = n0 + to + 16 * u;
+            if (nn >= p.B) continue;
+            const T *xn = static_cast<const T *>(p.x) + (size_t)nn * p.K;
+            for (int e = j; e < je; ++e) o[u] += gld(p.val + e_lo + e) * load_act(xn, gld(p.col + e_lo + e));
+        }
+    // ---- the input parts' partial tiles and the outlier sums through LDS
+    // (the x buffers are free: the last slice ended with a barrier); the
+    // partial tiles are summed in part order
+    float *red = &xs[0][0];                       // [TT][KP][16][64]
+    float *osum = &xs[1][0];                      // [32 rows][NTOK tokens]
+#pragma unroll
+    for (int t = 0; t < TT; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) red[((t * KP + q) * 16 + r) * 64 + lane] = acc[t][r];
+#pragma unroll
+    for (int u = 0; u < NOT; ++u) osum[ro * NTOK + to + 16 * u] = o[u];
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < RV; ++i) {
+        const int r = RV * q + i;
+        const int m = m0 + row_of(r);
+        if (m >= p.M) continue;
+        const float sc = gld(p.scales + m);
+        const float bs = p.bias ? gld(p.bias + m) : 0.f;
+#pragma unroll
+        for (int t = 0; t < TT; ++t) {
+            const int nn = n0 + 32 * t + n;
+            if (nn >= p.B) continue;
+            float sum = red[((t * KP) * 16 + r) * 64 + lane];
+#pragma unroll
+            for (int qq = 1; qq < KP; ++qq) sum += red[((t * KP + qq) * 16 + r) * 64 + lane];
+            float yv = sum * sc;
+            if (p.bias) yv += bs;
+            store_act(static_cast<T *>(p.y) + (size_t)nn * p.M, (size_t)m, yv + osum[row_of(r) * NTOK + 32 * t + n]);
+        }
+    }
+}
+
+template <typename T>
+static void launch_mm32_t(const MmParams &p, int tt, hipStream_t st) {
+    if (tt == 1)
+        OJX_LAUNCH((lut_mm32_kernel<T, 1>), dim3((p.M + 31) / 32, (p.B + 31) / 32), dim3(kM32NT), 0,
+                   st, p);
+    else
+        OJX_LAUNCH((lut_mm32_kernel<T, 2>), dim3((p.M + 31) / 32, (p.B + 63) / 64), dim3(kM32NT), 0,
+                   st, p);
+}
+
 // Row tiles per workgroup by batch: small batches take one tile per
 // workgroup for the most workgroups, larger ones share the staged x among
 // more tiles.
@@ -306,11 +597,24 @@ static void launch_mm_t(const MmParams &p, int rt, int gy, hipStream_t st) {
         OJX_LAUNCH((lut_mm_kernel<T, 4>), dim3((p.M + 63) / 64, gy), dim3(MmShape<4>::kNT), 0, st, p);
 }
 
+// From this many tokens the 32 x 32 bf16-MFMA tiles run (lut_mm32_kernel).
+constexpr int kMm32MinBatch = 17;
+
 int launch_mm(const MmParams &p, int dtype, hipStream_t st) {
     const int gy = (p.B + kMmTok - 1) / kMmTok;
     if (gy > 65535) {
         set_error("batch %d too large for the MFMA path", p.B);
         return OJASX_ERR_INVALID;
+    }
+    if (p.B >= kMm32MinBatch && p.cb3 &&
+        (dtype == OJASX_DTYPE_F32 || reinterpret_cast<uintptr_t>(p.x) % 8 == 0)) {
+        const int tt = p.B > 32 ? 2 : 1;
+        if (dtype == OJASX_DTYPE_F32)
+            launch_mm32_t<float>(p, tt, st);
+        else
+            launch_mm32_t<__hip_bfloat16>(p, tt, st);
+        OJX_HIP(hipGetLastError());
+        return OJASX_OK;
     }
     const int rt = mm_row_tiles(p.B);
     if (dtype == OJASX_DTYPE_F32)
