@@ -377,23 +377,26 @@ __global__ __launch_bounds__(kM32NT) void lut_mm32_kernel(MmParams p) {
     bf16x8_t c3[CBU];
 #pragma unroll
     for (int u = 0; u < CBU; ++u) c3[u] = gcb[tid + u * kM32NT];
+    // x staging: thread tid holds float4 tid % 64 (dims 4 (tid % 64) ..) of
+    // tokens tid / 64 + 8 u, u < XU.  Tokens past B read the last token and
+    // feed only outputs that are never stored; dims past K (a last partial
+    // slice) are clamped on load and zeroed before the store.
+    const int xd = 4 * (tid & 63);
+    size_t xrow[XU];
+#pragma unroll
+    for (int u = 0; u < XU; ++u) xrow[u] = (size_t)min(n0 + (tid >> 6) + 8 * u, p.B - 1) * p.K;
     auto load_x = [&](int s, float4 (&r)[XU]) __attribute__((always_inline)) {
+        const T *xs0 = static_cast<const T *>(p.x) + min(s * 256 + xd, p.K - 4);
 #pragma unroll
-        for (int u = 0; u < XU; ++u) {
-            const int i = tid + u * kM32NT;       // float4 i of the slice: token i / 64, dims 4 (i % 64)
-            const int nn = min(n0 + (i >> 6), p.B - 1);
-            const int k = min(s * 256 + 4 * (i & 63), p.K - 4);
-            r[u] = load4_act(static_cast<const T *>(p.x), (size_t)nn * p.K + k);
-        }
+        for (int u = 0; u < XU; ++u) r[u] = load4_act(xs0, xrow[u]);
     };
-    auto store_x = [&](int s, float *dst, const float4 (&r)[XU]) __attribute__((always_inline)) {
+    auto store_x = [&](int s, float *dst, float4 (&r)[XU]) __attribute__((always_inline)) {
+        if (s * 256 + xd >= p.K)                  // K % 16 == 0: a float4 is in or out
 #pragma unroll
-        for (int u = 0; u < XU; ++u) {
-            const int i = tid + u * kM32NT;
-            const bool ok = n0 + (i >> 6) < p.B && s * 256 + 4 * (i & 63) < p.K;   // K % 16 == 0
-            reinterpret_cast<float4 *>(dst + (i >> 6) * kM32XS)[i & 63] =
-                ok ? r[u] : make_float4(0.f, 0.f, 0.f, 0.f);
-        }
+            for (int u = 0; u < XU; ++u) r[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (int u = 0; u < XU; ++u)
+            reinterpret_cast<float4 *>(dst + ((tid >> 6) + 8 * u) * kM32XS)[tid & 63] = r[u];
     };
     float4 x0[XU], xr[XU];
     load_x(0, x0);
