@@ -438,8 +438,9 @@ def bench_sustained(b, handles, base, wbytes):
 def bench_batched(b, handles, base, wbytes, args):
     """LUT-GEMV 2560->6912 at batch 8, 16, 32 and 64,
     fp32 and bf16 activations, over the headline's instances (flushed before
-    each pass).  From 9 tokens the call runs as x . W^T on fp32 MFMA
-    (lut_mm_kernel), below that the in-place LUT kernel (lut_dec_kernel).
+    each pass).  From 17 tokens the call runs as x . W^T on bf16 MFMA over
+    exact bf16 pieces (lut_mm32_kernel), from 9 on fp32 MFMA (lut_mm_kernel),
+    below that the in-place LUT kernel (lut_dec_kernel).
     CPU: the reference engine at 8 and 64 tokens (it loops tokens)."""
     res = {}
     n = max(MIN_KERNEL_LAUNCHES, min(args.steps, 400))
