@@ -293,10 +293,11 @@ __global__ __launch_bounds__(MmShape<RT>::kNT) __attribute__((amdgpu_waves_per_e
 
 // ---- 32-row x 32-token tiles on bf16 MFMA
 //
-// lut_mm32_kernel: workgroup = 32 rows x 32 TT tokens, 8 waves: wave q
-// computes the 32 x 32 tiles of the TT token tiles over groups 2q, 2q + 1 of
-// every 16-group input slice (each A operand serves every token tile), on
-// v_mfma_f32_32x32x16_bf16 (one 16-dimension group per MFMA):
+// lut_mm32_kernel: workgroup = 32 RT rows x 32 TT tokens (RT TT <= 2), 8 waves:
+// wave q computes the RT x TT 32 x 32 tiles over groups 2q, 2q + 1 of every
+// 16-group input slice (each A operand serves every token tile, each B operand
+// every row tile), on v_mfma_f32_32x32x16_bf16 (one 16-dimension group per
+// MFMA):
 //   A[m][k] = C[code(m, g)][k]  (the codebook's exact bf16 pieces, staged in LDS),
 //   B[k][n] = x_n[16 g + k]     (x staged per slice in LDS as fp32, split into
 //                                exact bf16 pieces at use; bf16 activations are
@@ -304,32 +305,33 @@ __global__ __launch_bounds__(MmShape<RT>::kNT) __attribute__((amdgpu_waves_per_e
 // with the six products a_i b_j, i + j <= 4, of fp32 inputs (x split by
 // truncation, split3_trunc: the three left out are below 2^-22 of |a b|) or
 // the three a_i b of bf16 inputs, all accumulated in fp32 (mfma32_bf16x3's
-// operand layout).  A 32 x 32 tile reads 3 KB of A and 1-3 KB
-// of B per group for 16384 multiply-adds, against 2 KB per 4096 for the 16 x 16
-// fp32 tiles of lut_mm_kernel.  The x slices are staged through a register ring
-// one slice ahead; codes kPF slices ahead.
+// operand layout).  A 32 x 32 tile reads 3 KB of A and 1-3 KB of B per group
+// for 16384 multiply-adds, against 2 KB per 4096 for the 16 x 16 fp32 tiles
+// of lut_mm_kernel.  Every workgroup splits the x of its tokens for itself: two
+// row tiles per workgroup halve that work per row.  The x slices are staged
+// through a register ring one slice ahead; codes kM32PF slices ahead.
 //
-// The input parts' partial tiles meet in LDS at the end, added in part order;
-// wave q then finishes the RV = 16 / KP values r = RV q .. RV q + RV - 1 of its
-// lanes (rows 8 (r / 4) + 4 h + r % 4 of token n, h = lane / 32, n = lane %
-// 32).  The CSR outliers are added slice by slice from the staged x (entries
-// in LDS, sorted by column; thread tid takes row tid / 16 for tokens tid % 16
-// + 16 k), or from memory when the workgroup's rows hold more than kM32Csr
-// entries; their sums reach the epilogue through LDS.  Epilogue
+// The 8 waves' partial tiles meet in LDS at the end, added in wave order; wave
+// q then finishes the values r = 2q, 2q + 1 of its lanes in every tile (rows
+// 8 (r / 4) + 4 h + r % 4 of token n, h = lane / 32, n = lane % 32).  The CSR
+// outliers are added slice by slice from the staged x (entries in LDS, sorted
+// by column; thread tid takes row tid / TPR for tokens tid % TPR + TPR k), or
+// from memory when the workgroup's rows hold more than the staging holds;
+// their sums reach the epilogue through LDS.  Epilogue
 // (s_m * sum + bias) + outliers.
 namespace {
 constexpr int kM32XS = 260;      // floats per staged x row (256 + pad: conflict-free b128 reads)
-constexpr int kM32Csr = 512;     // CSR entries staged per workgroup
 constexpr int kM32PF = 4;        // slices of codes in flight
 constexpr int kM32NT = 512;      // threads: 8 waves
+// above 32 tokens: two row tiles per workgroup (else two token tiles)
+template <typename T> constexpr bool kM32RowPairs = std::is_same<T, float>::value;
 }  // namespace
 
 // Exact three-way bf16 split of 8 fp32 values by truncation: v = p0 + p1 + p2,
 // p0 = v with its low 16 bits cleared, p1 the same of v - p0, p2 = v - p0 - p1
 // (the remainders are exact in fp32; p2 has at most 8 significant bits, a
-// bf16 value).  |p1| < 2^-7 |v|, |p2| < 2^-15 |v|.  Five operations per value
-// (two of them packing): the operand split that every workgroup repeats for
-// its x slices.
+// bf16 value).  |p1| < 2^-7 |v|, |p2| < 2^-15 |v|.  About five operations per
+// value (1.5 of them packing).
 __device__ __forceinline__ void split3_trunc(const float (&v)[8], bf16x8_t (&p)[3]) {
     uint32_t w[3][4];
 #pragma unroll
@@ -349,27 +351,33 @@ __device__ __forceinline__ void split3_trunc(const float (&v)[8], bf16x8_t (&p)[
     for (int k = 0; k < 3; ++k) __builtin_memcpy(&p[k], w[k], sizeof(bf16x8_t));
 }
 
-template <typename T, int TT>
+template <typename T, int RT, int TT>
 __global__ __launch_bounds__(kM32NT) void lut_mm32_kernel(MmParams p) {
-    constexpr int KP = 8;                         // input parts, one wave each
+    constexpr int KP = kM32NT / 64;               // input parts, one wave each
     constexpr int GPS = 16 / KP;                  // groups per slice per wave
     constexpr int RV = 16 / KP;                   // tile values a wave finishes
-    constexpr int NTOK = 32 * TT;
+    constexpr int NROW = 32 * RT, NTOK = 32 * TT;
     constexpr int XU = NTOK * 64 / kM32NT;        // float4 of a slice's x per thread
+    constexpr int NC = 512 * RT;                  // CSR entries staged per workgroup
+    constexpr int TPR = kM32NT / NROW;            // outlier threads per row
+    constexpr int NOT = NTOK / TPR;               // tokens per outlier thread
     constexpr bool BF = !std::is_same<T, float>::value;
-    __shared__ bf16x8_t cb3s[256 * 2 * 3];        // [centroid][half][piece]
+    static_assert(RT * TT <= 2 && GPS == 2, "tile shapes");
+    __shared__ bf16x8_t cb3s[256 * 2 * 3];        // [centroid][half][piece]; the outlier sums at the end
     __shared__ __align__(16) float xs[2][NTOK * kM32XS];   // x slices; the partial tiles at the end
-    __shared__ unsigned short lcol[kM32Csr];
-    __shared__ float lval[kM32Csr];
-    static_assert(TT * KP * 16 * 64 <= NTOK * kM32XS && 32 * NTOK <= NTOK * kM32XS,
-                  "partial tiles and outlier sums fit the x buffers");
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    const int q = w;
+    __shared__ unsigned short lcol[NC];
+    __shared__ float lval[NC];
+    static_assert(RT * TT * KP * 16 * 64 <= 2 * NTOK * kM32XS &&
+                      NROW * NTOK * sizeof(float) <= sizeof(cb3s),
+                  "partial tiles and outlier sums fit the staging buffers");
+    const int tid = threadIdx.x, lane = tid & 63, q = tid >> 6;
     const int h = lane >> 5, n = lane & 31;
-    const int m0 = blockIdx.x * 32;
+    const int m0 = blockIdx.x * NROW;
     const int n0 = blockIdx.y * NTOK;
-    const int row = min(m0 + n, p.Mp - 1);        // the lane's A row (rows past M: never stored)
-    auto row_of = [&](int r) { return 8 * (r >> 2) + 4 * h + (r & 3); };   // tile row of value r
+    int arow[RT];                                 // the lane's A rows (rows past M: never stored)
+#pragma unroll
+    for (int r = 0; r < RT; ++r) arow[r] = min(m0 + 32 * r + n, p.Mp - 1);
+    auto row_of = [&](int v) { return 8 * (v >> 2) + 4 * h + (v & 3); };   // tile row of value v
 
     // ---- round trip 1: the codebook pieces, x slices 0 and 1, the CSR ranges, codes
     constexpr int CBU = 256 * 2 * 3 / kM32NT;
@@ -401,45 +409,50 @@ __global__ __launch_bounds__(kM32NT) void lut_mm32_kernel(MmParams p) {
     float4 x0[XU], xr[XU];
     load_x(0, x0);
     load_x(min(1, p.S - 1), xr);
-    // outliers: thread tid adds those of row ro = tid / 16 for tokens
-    // tid % 16 + 16 k, k < NOT
-    constexpr int NOT = NTOK / 16;
-    const int ro = tid >> 4, to = tid & 15;
+    // outliers: thread tid adds those of row ro = tid / TPR for tokens
+    // tid % TPR + TPR k, k < NOT
+    const int ro = tid / TPR, to = tid % TPR;
     int e_lo = 0, e_hi = 0, j = 0, je = 0;
     if (p.rowp) {
         e_lo = gld(p.rowp + m0);
-        e_hi = gld(p.rowp + min(m0 + 32, p.M));
+        e_hi = gld(p.rowp + min(m0 + NROW, p.M));
         j = gld(p.rowp + min(m0 + ro, p.M - 1));
         je = m0 + ro < p.M ? gld(p.rowp + m0 + ro + 1) : j;
     }
-    uint32_t cr[kM32PF];   // codes of slices s .. s + kM32PF - 1, slot s % kM32PF
-    auto load_codes = [&](int s) __attribute__((always_inline)) {
-        const uint8_t *src = p.codes + ((size_t)s * p.Mp + row) * 16 + GPS * q;
-        if constexpr (GPS == 4) return gld(reinterpret_cast<const uint32_t *>(src));
-        else return (uint32_t)gld(reinterpret_cast<const unsigned short *>(src));
+    uint32_t cr[kM32PF][RT];   // codes of slices s .. s + kM32PF - 1, slot s % kM32PF
+    auto load_codes = [&](int s, int r) __attribute__((always_inline)) {
+        return (uint32_t)gld(reinterpret_cast<const unsigned short *>(
+            p.codes + ((size_t)s * p.Mp + arow[r]) * 16 + GPS * q));
     };
 #pragma unroll
-    for (int u = 0; u < kM32PF; ++u) cr[u] = load_codes(min(u, p.S - 1));
+    for (int u = 0; u < kM32PF; ++u)
+#pragma unroll
+        for (int r = 0; r < RT; ++r) cr[u][r] = load_codes(min(u, p.S - 1), r);
     // ---- round trip 2: the CSR entries of the workgroup's rows into LDS when they fit
-    const bool staged = e_hi - e_lo <= kM32Csr;
+    const bool staged = e_hi - e_lo <= NC;
     if (p.rowp && staged && e_hi > e_lo) {
-        const int e = min(e_lo + tid, e_hi - 1);
-        const int c = gld(p.col + e);
-        const float v = gld(p.val + e);
-        if (e_lo + tid < e_hi) {
-            lcol[tid] = (unsigned short)c;
-            lval[tid] = v;
+#pragma unroll
+        for (int u = 0; u < NC / kM32NT; ++u) {
+            const int i = tid + u * kM32NT;
+            const int e = min(e_lo + i, e_hi - 1);
+            const int c = gld(p.col + e);
+            const float v = gld(p.val + e);
+            if (e_lo + i < e_hi) {
+                lcol[i] = (unsigned short)c;
+                lval[i] = v;
+            }
         }
     }
-    static_assert(kM32Csr == kM32NT, "one staged entry per thread");
 #pragma unroll
     for (int u = 0; u < CBU; ++u) cb3s[tid + u * kM32NT] = c3[u];
     store_x(0, xs[0], x0);
     __syncthreads();
 
-    f32x16_t acc[TT];
+    f32x16_t acc[RT][TT];
 #pragma unroll
-    for (int t = 0; t < TT; ++t) acc[t] = f32x16_t{};
+    for (int r = 0; r < RT; ++r)
+#pragma unroll
+        for (int t = 0; t < TT; ++t) acc[r][t] = f32x16_t{};
     float o[NOT];
 #pragma unroll
     for (int k = 0; k < NOT; ++k) o[k] = 0.f;
@@ -451,15 +464,20 @@ __global__ __launch_bounds__(kM32NT) void lut_mm32_kernel(MmParams p) {
     // unconditionally (clamped to the last slice), so the loop body has one
     // path and the wait counts of the rings stay exact across its back edge.
     auto slice = [&](const int s, const int u) __attribute__((always_inline)) {
-        const uint32_t cw = cr[u];
 #pragma unroll
         for (int i = 0; i < GPS; ++i) {
             const int g = GPS * q + i;
-            const uint32_t code = (cw >> (8 * i)) & 0xffu;
-            const bf16x8_t *ap = cb3s + (code * 2 + h) * 3;
-            const bf16x8_t a0 = ap[0], a1 = ap[1], a2 = ap[2];
+            bf16x8_t a[RT][3];
 #pragma unroll
-            for (int t = 0; t < TT; ++t) {            // each A operand serves every token tile
+            for (int r = 0; r < RT; ++r) {
+                const uint32_t code = (cr[u][r] >> (8 * i)) & 0xffu;
+                const bf16x8_t *ap = cb3s + (code * 2 + h) * 3;
+                a[r][0] = ap[0];
+                a[r][1] = ap[1];
+                a[r][2] = ap[2];
+            }
+#pragma unroll
+            for (int t = 0; t < TT; ++t) {
                 const float *xt = xs[s & 1] + (32 * t + n) * kM32XS + 16 * g + 8 * h;
                 const float4 xa = *reinterpret_cast<const float4 *>(xt);
                 const float4 xb = *reinterpret_cast<const float4 *>(xt + 4);
@@ -468,18 +486,24 @@ __global__ __launch_bounds__(kM32NT) void lut_mm32_kernel(MmParams p) {
                     bf16x8_t b;
 #pragma unroll
                     for (int e = 0; e < 8; ++e) b[e] = (__bf16)xv[e];   // exact: bf16 values
-                    acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a2, b, acc[t], 0, 0, 0);
-                    acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, b, acc[t], 0, 0, 0);
-                    acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, b, acc[t], 0, 0, 0);
+#pragma unroll
+                    for (int r = 0; r < RT; ++r) {
+                        acc[r][t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[r][2], b, acc[r][t], 0, 0, 0);
+                        acc[r][t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[r][1], b, acc[r][t], 0, 0, 0);
+                        acc[r][t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[r][0], b, acc[r][t], 0, 0, 0);
+                    }
                 } else {
                     bf16x8_t b[3];
                     split3_trunc(xv, b);
-                    acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, b[2], acc[t], 0, 0, 0);
-                    acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, b[1], acc[t], 0, 0, 0);
-                    acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a2, b[0], acc[t], 0, 0, 0);
-                    acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, b[1], acc[t], 0, 0, 0);
-                    acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, b[0], acc[t], 0, 0, 0);
-                    acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, b[0], acc[t], 0, 0, 0);
+#pragma unroll
+                    for (int r = 0; r < RT; ++r) {
+                        acc[r][t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[r][0], b[2], acc[r][t], 0, 0, 0);
+                        acc[r][t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[r][1], b[1], acc[r][t], 0, 0, 0);
+                        acc[r][t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[r][2], b[0], acc[r][t], 0, 0, 0);
+                        acc[r][t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[r][0], b[1], acc[r][t], 0, 0, 0);
+                        acc[r][t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[r][1], b[0], acc[r][t], 0, 0, 0);
+                        acc[r][t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[r][0], b[0], acc[r][t], 0, 0, 0);
+                    }
                 }
             }
         }
@@ -496,7 +520,7 @@ __global__ __launch_bounds__(kM32NT) void lut_mm32_kernel(MmParams p) {
                 float vv[kOutPass];
 #pragma unroll
                 for (int k = 0; k < kOutPass; ++k) {
-                    const int e = min(j + k, kM32Csr - 1);
+                    const int e = min(j + k, NC - 1);
                     c[k] = lcol[e];
                     vv[k] = lval[e];
                 }
@@ -507,9 +531,9 @@ __global__ __launch_bounds__(kM32NT) void lut_mm32_kernel(MmParams p) {
                     in = in && j + k < je && c[k] < lim;
                     const int cc = in ? c[k] : s * 256;
 #pragma unroll
-                    for (int u = 0; u < NOT; ++u) {
-                        const float xv = xsl[16 * u * kM32XS + cc];
-                        if (in) o[u] += vv[k] * xv;
+                    for (int v = 0; v < NOT; ++v) {
+                        const float xv = xsl[TPR * v * kM32XS + cc];
+                        if (in) o[v] += vv[k] * xv;
                     }
                     took += in ? 1 : 0;
                 }
@@ -521,7 +545,8 @@ __global__ __launch_bounds__(kM32NT) void lut_mm32_kernel(MmParams p) {
         // reload, never read), then the rings refilled
         store_x(min(s + 1, p.S - 1), xs[(s + 1) & 1], xr);
         load_x(min(s + 2, p.S - 1), xr);
-        cr[u] = load_codes(min(s + kM32PF, p.S - 1));
+#pragma unroll
+        for (int r = 0; r < RT; ++r) cr[u][r] = load_codes(min(s + kM32PF, p.S - 1), r);
         __syncthreads();   // slice s + 1 staged; slice s's reads done before it is overwritten
     };
     int s0 = 0;
@@ -536,53 +561,65 @@ __global__ __launch_bounds__(kM32NT) void lut_mm32_kernel(MmParams p) {
     // ---- a dense-outlier block: the row's entries and x from memory
     if (p.rowp && !staged && m0 + ro < p.M)
 #pragma unroll
-        for (int u = 0; u < NOT; ++u) {
-            const int nn = n0 + to + 16 * u;
+        for (int v = 0; v < NOT; ++v) {
+            const int nn = n0 + to + TPR * v;
             if (nn >= p.B) continue;
             const T *xn = static_cast<const T *>(p.x) + (size_t)nn * p.K;
-            for (int e = j; e < je; ++e) o[u] += gld(p.val + e_lo + e) * load_act(xn, gld(p.col + e_lo + e));
+            for (int e = j; e < je; ++e) o[v] += gld(p.val + e_lo + e) * load_act(xn, gld(p.col + e_lo + e));
         }
-    // ---- the input parts' partial tiles and the outlier sums through LDS
-    // (the x buffers are free: the last slice ended with a barrier); the
-    // partial tiles are summed in part order
-    float *red = &xs[0][0];                       // [TT][KP][16][64]
-    float *osum = &xs[1][0];                      // [32 rows][NTOK tokens]
+    // ---- the waves' partial tiles and the outlier sums through LDS (the
+    // staging buffers are free: the last slice ended with a barrier); the
+    // partial tiles are summed in wave order
+    float *red = &xs[0][0];                       // [RT][TT][KP][16][64]
+    float *osum = reinterpret_cast<float *>(cb3s);   // [NROW][NTOK]
 #pragma unroll
-    for (int t = 0; t < TT; ++t)
+    for (int r = 0; r < RT; ++r)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) red[((t * KP + q) * 16 + r) * 64 + lane] = acc[t][r];
+        for (int t = 0; t < TT; ++t)
 #pragma unroll
-    for (int u = 0; u < NOT; ++u) osum[ro * NTOK + to + 16 * u] = o[u];
+            for (int v = 0; v < 16; ++v) red[(((r * TT + t) * KP + q) * 16 + v) * 64 + lane] = acc[r][t][v];
+#pragma unroll
+    for (int v = 0; v < NOT; ++v) osum[ro * NTOK + to + TPR * v] = o[v];
     __syncthreads();
 #pragma unroll
-    for (int i = 0; i < RV; ++i) {
-        const int r = RV * q + i;
-        const int m = m0 + row_of(r);
-        if (m >= p.M) continue;
-        const float sc = gld(p.scales + m);
-        const float bs = p.bias ? gld(p.bias + m) : 0.f;
+    for (int r = 0; r < RT; ++r)
 #pragma unroll
-        for (int t = 0; t < TT; ++t) {
-            const int nn = n0 + 32 * t + n;
-            if (nn >= p.B) continue;
-            float sum = red[((t * KP) * 16 + r) * 64 + lane];
+        for (int i = 0; i < RV; ++i) {
+            const int v = RV * q + i;
+            const int mr = 32 * r + row_of(v);            // row within the workgroup
+            const int m = m0 + mr;
+            if (m >= p.M) continue;
+            const float sc = gld(p.scales + m);
+            const float bs = p.bias ? gld(p.bias + m) : 0.f;
 #pragma unroll
-            for (int qq = 1; qq < KP; ++qq) sum += red[((t * KP + qq) * 16 + r) * 64 + lane];
-            float yv = sum * sc;
-            if (p.bias) yv += bs;
-            store_act(static_cast<T *>(p.y) + (size_t)nn * p.M, (size_t)m, yv + osum[row_of(r) * NTOK + 32 * t + n]);
+            for (int t = 0; t < TT; ++t) {
+                const int nn = n0 + 32 * t + n;
+                if (nn >= p.B) continue;
+                const float *rt = red + ((r * TT + t) * KP * 16 + v) * 64 + lane;
+                float sum = rt[0];
+#pragma unroll
+                for (int qq = 1; qq < KP; ++qq) sum += rt[qq * 16 * 64];
+                float yv = sum * sc;
+                if (p.bias) yv += bs;
+                store_act(static_cast<T *>(p.y) + (size_t)nn * p.M, (size_t)m,
+                          yv + osum[mr * NTOK + 32 * t + n]);
+            }
         }
-    }
 }
 
+// Tile shape by batch: one 32 x 32 tile per workgroup up to 32 tokens; above,
+// two tiles per workgroup: two row tiles for fp32 x (each workgroup splits
+// half as much x per row), two token tiles for bf16 x (no split: each A
+// operand serves both).
 template <typename T>
-static void launch_mm32_t(const MmParams &p, int tt, hipStream_t st) {
-    if (tt == 1)
-        OJX_LAUNCH((lut_mm32_kernel<T, 1>), dim3((p.M + 31) / 32, (p.B + 31) / 32), dim3(kM32NT), 0,
-                   st, p);
+static void launch_mm32_t(const MmParams &p, hipStream_t st) {
+    const int gx1 = (p.M + 31) / 32, gx2 = (p.M + 63) / 64;
+    if (p.B <= 32)
+        OJX_LAUNCH((lut_mm32_kernel<T, 1, 1>), dim3(gx1, (p.B + 31) / 32), dim3(kM32NT), 0, st, p);
+    else if (kM32RowPairs<T>)
+        OJX_LAUNCH((lut_mm32_kernel<T, 2, 1>), dim3(gx2, (p.B + 31) / 32), dim3(kM32NT), 0, st, p);
     else
-        OJX_LAUNCH((lut_mm32_kernel<T, 2>), dim3((p.M + 31) / 32, (p.B + 63) / 64), dim3(kM32NT), 0,
-                   st, p);
+        OJX_LAUNCH((lut_mm32_kernel<T, 1, 2>), dim3(gx1, (p.B + 63) / 64), dim3(kM32NT), 0, st, p);
 }
 
 // Row tiles per workgroup by batch: small batches take one tile per
@@ -611,11 +648,10 @@ int launch_mm(const MmParams &p, int dtype, hipStream_t st) {
     }
     if (p.B >= kMm32MinBatch && p.cb3 &&
         (dtype == OJASX_DTYPE_F32 || reinterpret_cast<uintptr_t>(p.x) % 8 == 0)) {
-        const int tt = p.B > 32 ? 2 : 1;
         if (dtype == OJASX_DTYPE_F32)
-            launch_mm32_t<float>(p, tt, st);
+            launch_mm32_t<float>(p, st);
         else
-            launch_mm32_t<__hip_bfloat16>(p, tt, st);
+            launch_mm32_t<__hip_bfloat16>(p, st);
         OJX_HIP(hipGetLastError());
         return OJASX_OK;
     }
