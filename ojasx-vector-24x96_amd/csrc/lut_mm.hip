@@ -637,8 +637,11 @@ static void launch_mm_t(const MmParams &p, int rt, int gy, hipStream_t st) {
         OJX_LAUNCH((lut_mm_kernel<T, 4>), dim3((p.M + 63) / 64, gy), dim3(MmShape<4>::kNT), 0, st, p);
 }
 
-// From this many tokens the 32 x 32 bf16-MFMA tiles run (lut_mm32_kernel).
-constexpr int kMm32MinBatch = 17;
+// From this many tokens the 32 x 32 bf16-MFMA tiles run (lut_mm32_kernel):
+// fp32 x from 17 (at 9-16 the 16 x 16 fp32 tiles are faster: 17.6-18.0 vs
+// 18.4-18.7 us at 2560->6912), bf16 x from 9 (16.9-17.0 vs 17.4-17.9 us).
+constexpr int kMm32MinBatchF32 = 17;
+constexpr int kMm32MinBatchBF16 = 9;
 
 int launch_mm(const MmParams &p, int dtype, hipStream_t st) {
     const int gy = (p.B + kMmTok - 1) / kMmTok;
@@ -646,8 +649,9 @@ int launch_mm(const MmParams &p, int dtype, hipStream_t st) {
         set_error("batch %d too large for the MFMA path", p.B);
         return OJASX_ERR_INVALID;
     }
-    if (p.B >= kMm32MinBatch && p.cb3 &&
-        (dtype == OJASX_DTYPE_F32 || reinterpret_cast<uintptr_t>(p.x) % 8 == 0)) {
+    if (p.cb3 && (dtype == OJASX_DTYPE_F32 ? p.B >= kMm32MinBatchF32
+                                           : p.B >= kMm32MinBatchBF16 &&
+                                                 reinterpret_cast<uintptr_t>(p.x) % 8 == 0)) {
         if (dtype == OJASX_DTYPE_F32)
             launch_mm32_t<float>(p, st);
         else

@@ -120,7 +120,9 @@ def test_baseline_configs_fp32(pkg, dev, M, K, B):
     (517, 3072, 31, 1, 0.0038),    # two row tiles, 12 slices
     (257, 9728, 65, 0, 0.0038),    # 38 slices (a tail of 2); five 16-token tiles, the last of 1
     (64, 176, 100, 0, 0.02),       # 11 groups in one slice; 100 tokens
-    (40, 2560, 128, 1, 0.0038)])   # eight full 16-token tiles
+    (40, 2560, 128, 1, 0.0038),    # eight full 16-token tiles
+    (333, 2000, 9, 1, 0.0038),     # bf16 from 9 tokens on 32 x 32 tiles (9 of 32 tokens)
+    (1000, 2560, 57, 0, 0.0038)])  # fp32 two row tiles: a ragged 64-row block and token tile
 def test_mfma_batched_shapes(pkg, dev, M, K, B, dt, density):
     """Many tokens (x . W^T on MFMA): ragged rows, tokens and slices, bias,
     outliers given with each row's columns shuffled (the handle sorts them),
