@@ -363,7 +363,12 @@ __global__ __launch_bounds__(kM32NT) void lut_mm32_kernel(MmParams p) {
     constexpr int NOT = NTOK / TPR;               // tokens per outlier thread
     constexpr bool BF = !std::is_same<T, float>::value;
     static_assert(RT * TT <= 2 && GPS == 2, "tile shapes");
-    __shared__ bf16x8_t cb3s[256 * 2 * 3];        // [centroid][half][piece]; the outlier sums at the end
+    // [centroid][half][piece], 16-byte units: 7 per centroid where the LDS
+    // allows (112-byte rows put 16 lanes' random rows over all 16 four-bank
+    // groups instead of 8: 16.9 -> 16.2 us for bf16 x at 16 tokens), else 6;
+    // the outlier sums at the end
+    constexpr int CBS = TT == 2 ? 6 : 7;
+    __shared__ bf16x8_t cb3s[256 * CBS];
     __shared__ __align__(16) float xs[2][NTOK * kM32XS];   // x slices; the partial tiles at the end
     __shared__ unsigned short lcol[NC];
     __shared__ float lval[NC];
@@ -444,7 +449,10 @@ __global__ __launch_bounds__(kM32NT) void lut_mm32_kernel(MmParams p) {
         }
     }
 #pragma unroll
-    for (int u = 0; u < CBU; ++u) cb3s[tid + u * kM32NT] = c3[u];
+    for (int u = 0; u < CBU; ++u) {
+        const int i = tid + u * kM32NT;
+        cb3s[(i / 6) * CBS + i % 6] = c3[u];
+    }
     store_x(0, xs[0], x0);
     __syncthreads();
 
@@ -471,7 +479,7 @@ __global__ __launch_bounds__(kM32NT) void lut_mm32_kernel(MmParams p) {
 #pragma unroll
             for (int r = 0; r < RT; ++r) {
                 const uint32_t code = (cr[u][r] >> (8 * i)) & 0xffu;
-                const bf16x8_t *ap = cb3s + (code * 2 + h) * 3;
+                const bf16x8_t *ap = cb3s + code * CBS + h * 3;
                 a[r][0] = ap[0];
                 a[r][1] = ap[1];
                 a[r][2] = ap[2];
