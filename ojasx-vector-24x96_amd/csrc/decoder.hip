@@ -502,7 +502,7 @@ struct Decoder {
                               &l.ks, &l.vc, &l.vs})
                 b->release();
         for (DevBuf *b : {&final_norm, &emb, &cos_t, &sin_t, &bt, &x, &qkv, &attn, &gu, &logits,
-                          &part_o, &part_ml, &state, &tokens})
+                          &arg_part, &part_o, &part_ml, &state, &tokens})
             b->release();
     }
 
