@@ -128,9 +128,11 @@ OJASX_API int ojasx_linear_forward_grouped_device(const OjasxLinearHandle *handl
 OJASX_API int ojasx_build_lut_device(const void *x, const float *codebook, int batch_size,
                                      int groups, int block_dim, int codebook_size, float *lut,
                                      int dtype, void *stream);
-/* Bytes the forward reads per call that are weights: packed codes, outlier
- * stream, codebook, scales, bias (no reference counterpart; for roofline
- * accounting). */
+/* Bytes the batch-1 forward reads per call that are weights: packed codes,
+ * outlier stream (16-bit columns and fp32 values, 6 bytes per entry, where
+ * in_features <= 65536; plus the row pointers), codebook, scales, bias (no
+ * reference counterpart; for roofline accounting).  The batched kernels (9
+ * tokens and more) read 32-bit columns: 2 more bytes per outlier. */
 OJASX_API size_t ojasx_linear_device_weight_bytes(OjasxLinearHandle handle);
 
 /* ---- KV cache (ref.h:96-120) ------------------------------------------ */

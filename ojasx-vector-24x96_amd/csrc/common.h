@@ -113,6 +113,7 @@ struct GroupItem {
     const float *bias;        // [M] or null
     const int *rowp;          // [M+1] or null
     const int *col;
+    const uint16_t *col16;    // the same columns in 16 bits (in_features <= 65536), or null
     const float *val;
     const float *x;           // [K], 16-byte aligned
     float *y;                 // [M]

@@ -182,7 +182,7 @@ struct BankBlock {
     const float *scales;        // [M]
     const float *bias;          // [M] or null
     const int *rowp;            // [M + 1] or null
-    const int *col;
+    const uint16_t *col;        // [nnz] 16-bit columns (K <= 16384 here)
     const float *val;
     const void *x;              // XS_F32: [K] fp32; XS_BF16: [K] bf16; XS_SWIGLU: [2K] fp32
     float *y;                   // [M]
@@ -381,7 +381,7 @@ __global__ __launch_bounds__(kBNT) void lut_bank_kernel(const GroupItem *__restr
     extern __shared__ float xs[];                    // [32 S][kXRow]: x pieces (B operands, outliers)
     const int2 wk = work[blockIdx.x];
     const GroupItem it = items[wk.x];
-    const BankBlock bb{it.codes_b, static_cast<const v8bf *>(it.cb3), it.scales, it.bias, it.rowp, it.col, it.val,
+    const BankBlock bb{it.codes_b, static_cast<const v8bf *>(it.cb3), it.scales, it.bias, it.rowp, it.col16, it.val,
                        it.x, it.y, it.K, it.M, wk.y};
     bank_block<XS_F32>(bb, L, xs);
 }

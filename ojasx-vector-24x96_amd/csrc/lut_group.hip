@@ -95,13 +95,13 @@ __global__ __launch_bounds__(kTNT) void lut_tall_rms_kernel(GroupItem it, const 
             float v[4];
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
-                c[u] = gld(it.col + j + u);
+                c[u] = gld(it.col16 + j + u);
                 v[u] = gld(it.val + j + u);
             }
 #pragma unroll
             for (int u = 0; u < 4; ++u) o += v[u] * xs[c[u]];
         }
-        for (; j < j1; ++j) o += gld(it.val + j) * xs[gld(it.col + j)];
+        for (; j < j1; ++j) o += gld(it.val + j) * xs[gld(it.col16 + j)];
     }
     float y = (acc[0] * rn) * sc;
     if (it.bias) y += bs;
@@ -155,6 +155,10 @@ struct GroupWork {
 };
 static thread_local GroupWork t_group;
 
+// An item runs on the bank kernel when its staged input fits the LDS; the
+// kernel reads the 16-bit copy of the outlier columns.
+static bool on_bank(const GroupItem &it) { return bank_fits(it.K) && (!it.rowp || it.col16); }
+
 }  // namespace ojx
 
 extern "C" {
@@ -187,7 +191,7 @@ OJASX_API int ojasx_linear_forward_grouped_device(const OjasxLinearHandle *handl
         }
         it.x = xs[i];
         it.y = ys[i];
-        if (bank_fits(it.K)) max_K = std::max(max_K, it.K);
+        if (on_bank(it)) max_K = std::max(max_K, it.K);
         else wide.push_back(i);
     }
     hipStream_t st = static_cast<hipStream_t>(stream);
@@ -201,13 +205,13 @@ OJASX_API int ojasx_linear_forward_grouped_device(const OjasxLinearHandle *handl
     // the bank kernel's work list: every 512-row block of every other item, item-major
     int n_work = 0;
     for (int i = 0; i < count; ++i)
-        if (bank_fits(host[i].K)) n_work += (host[i].M + kBankRows - 1) / kBankRows;
+        if (on_bank(host[i])) n_work += (host[i].M + kBankRows - 1) / kBankRows;
     const size_t bytes = item_bytes + sizeof(int2) * (size_t)n_work;
     gw.host.resize(bytes);
     host = reinterpret_cast<GroupItem *>(gw.host.data());
     int2 *wl = reinterpret_cast<int2 *>(gw.host.data() + item_bytes);
     for (int i = 0, t = 0; i < count; ++i)
-        if (bank_fits(host[i].K))
+        if (on_bank(host[i]))
             for (int b = 0; b < host[i].M; b += kBankRows) wl[t++] = make_int2(i, b);
     void *staged = nullptr;
     rc = gw.ring.stage(gw.host.data(), bytes, true, st, &staged);

@@ -249,7 +249,7 @@ struct DecParams {
     const float *scales;    // [M]
     const float *bias;      // [M] or null
     const int *rowp;        // [M+1] (null: no outliers)
-    const int *col;         // [nnz]
+    const uint16_t *col;    // [nnz] 16-bit columns (the staged x bounds K far below 65536)
     const float *val;       // [nnz]
     const void *x;          // [B][xrow], 16-byte aligned (fp32) / 8-byte (bf16)
     void *y;                // [B][M]
@@ -588,11 +588,11 @@ struct Linear {
     int K = 0, M = 0, D = 0, Kcb = 0, G = 0, S = 0, Mp = 0;
     bool has_bias = false;
     size_t nnz = 0;
-    DevBuf codes, codes_b, codebook, cb3, scales, bias, rowp, col, val;
+    DevBuf codes, codes_b, codebook, cb3, scales, bias, rowp, col, col16, val;
     DevBuf lut, xstage, ystage;
     ~Linear() {
-        for (DevBuf *b : {&codes, &codes_b, &codebook, &cb3, &scales, &bias, &rowp, &col, &val, &lut,
-                          &xstage, &ystage})
+        for (DevBuf *b : {&codes, &codes_b, &codebook, &cb3, &scales, &bias, &rowp, &col, &col16,
+                          &val, &lut, &xstage, &ystage})
             b->release();
     }
 };
@@ -656,7 +656,7 @@ int launch_dec(Linear *L, const void *x, void *y, int B, size_t lds, hipStream_t
     dp.scales = L->scales.as<float>();
     dp.bias = L->has_bias ? L->bias.as<float>() : nullptr;
     dp.rowp = L->nnz ? L->rowp.as<int>() : nullptr;
-    dp.col = L->col.as<int>();
+    dp.col = L->col16.as<uint16_t>();
     dp.val = L->val.as<float>();
     dp.x = x;
     dp.y = y;
@@ -699,6 +699,7 @@ template <typename T>
 int try_dec(Linear *L, const void *x, void *y, int B, hipStream_t st, const Fuse &f = Fuse{}) {
     const size_t align = sizeof(T) == 4 ? 16 : 8;
     if (L->D != 16 || (reinterpret_cast<uintptr_t>(x) % align)) return 1;
+    if (L->nnz && !L->col16.ptr) return 1;   // the kernel reads the 16-bit columns
     // tokens per workgroup: all of them up to 8 (the codebook staged and the
     // codes read once per row block), fewer where the staged x does not fit
     // the LDS beside the per-wave partials (2 x 16 waves x 32 rows x bt floats)
@@ -846,6 +847,7 @@ int linear_items(const void *h, GroupItem *it) {
     it->bias = L->has_bias ? L->bias.as<float>() : nullptr;
     it->rowp = L->nnz ? L->rowp.as<int>() : nullptr;
     it->col = L->col.as<int>();
+    it->col16 = L->nnz ? L->col16.as<uint16_t>() : nullptr;
     it->val = L->val.as<float>();
     it->K = L->K;
     it->M = L->M;
@@ -894,7 +896,7 @@ static int fused_forward(void *h, const float *x, float *y, int pro, const float
     const bool tall_fits = (size_t)L->S * 256 * sizeof(float) + 2 * 16 * 260 * sizeof(float) +
                                64 <= kMaxLds;
     if (pro == kProRms && !res && L->D == 16 && L->M >= kTallMinRows && tall_fits &&
-        !(reinterpret_cast<uintptr_t>(x) & 15)) {
+        (!L->nnz || L->col16.ptr) && !(reinterpret_cast<uintptr_t>(x) & 15)) {
         GroupItem it{};
         int rc = linear_items(h, &it);
         if (rc) return rc;
@@ -1063,6 +1065,14 @@ OJASX_API int ojasx_set_linear_outliers(OjasxLinearHandle handle, int nnz, const
     int rc = upload(L->rowp, row_ptrs, (size_t)(L->M + 1) * sizeof(int));
     if (!rc) rc = upload(L->col, cs.data(), (size_t)nnz * sizeof(int));
     if (!rc) rc = upload(L->val, vs.data(), (size_t)nnz * sizeof(float));
+    // 16-bit columns for the grouped kernel: 6 instead of 8 bytes per entry
+    // where the outliers are a bandwidth term of their own
+    if (!rc && L->K <= 65536) {
+        std::vector<uint16_t> c16(cs.begin(), cs.end());
+        rc = upload(L->col16, c16.data(), (size_t)nnz * sizeof(uint16_t));
+    } else if (!rc) {
+        L->col16.release();
+    }
     if (rc) return rc;
     L->nnz = (size_t)nnz;
     return OJASX_OK;
@@ -1168,7 +1178,9 @@ OJASX_API size_t ojasx_linear_device_weight_bytes(OjasxLinearHandle handle) {
     const Linear *L = static_cast<const Linear *>(handle);
     size_t b = (size_t)L->M * L->G + (size_t)L->Kcb * L->D * 4 + (size_t)L->M * 4;
     if (L->has_bias) b += (size_t)L->M * 4;
-    if (L->nnz) b += L->nnz * 8 + (size_t)(L->M + 1) * 4;
+    // outliers as the batch-1 and grouped kernels read them: 16-bit columns
+    // and fp32 values (the batched MFMA kernels read 32-bit columns)
+    if (L->nnz) b += L->nnz * (L->col16.ptr ? 6 : 8) + (size_t)(L->M + 1) * 4;
     return b;
 }
 
