@@ -299,8 +299,8 @@ def make_instances(b, M, K, n, seed, csr=True):
         if csr:
             assert L.ojasx_set_linear_outliers(h, vl.size, p(rp), p(cl), p(vl)) == 0
         hs.append(h)
-    base["nnz"] = vl.size if csr else 0
         wbytes = L.ojasx_linear_device_weight_bytes(h)
+    base["nnz"] = vl.size if csr else 0
     return hs, base, wbytes
 
 

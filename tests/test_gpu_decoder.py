@@ -46,7 +46,10 @@ def make_linear(pkg, r, M, K, density=0.0038, scales="u"):
                                          # workgroup; the 64-VGPR build (641 workgroups)
                                          (19456, 2560, 3, False), (700, 2560, 3, False),
                                          (9002, 1024, 3, False), (16384, 256, 3, False),
-                                         (20482, 64, 3, False), (12290, 9728, 3, False)])
+                                         (20482, 64, 3, False), (12290, 9728, 3, False),
+                                         # 2048 .. 4095 rows: 8 - 15 rows per workgroup
+                                         (2560, 9728, 0, True), (2050, 2560, 1, False),
+                                         (3001, 4096, 2, True), (4000, 512, 1, True)])
 def test_fused_linear(pkg, dev, M, K, pro, res):
     import torch
     r = np.random.default_rng(M + K + pro)

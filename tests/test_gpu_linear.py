@@ -87,7 +87,11 @@ def test_reference_t2(pkg):
                                    # batch 1, tall: 3 / 4 / 5 row tiles per workgroup
                                    # (48- and 80-row workgroups end past the padded rows)
                                    (9000, 1024, 1), (12289, 256, 1), (19456, 2560, 1),
-                                   (20481, 64, 1)])   # past 5 tiles: 32-row workgroups
+                                   (20481, 64, 1),    # past 5 tiles: 32-row workgroups
+                                   # batch 1, 2048 .. 4095 rows: ceil(M / 256) rows per
+                                   # workgroup (8 - 15), the last workgroup ragged
+                                   (2048, 512, 1), (2049, 1024, 1), (3001, 2560, 1),
+                                   (4095, 256, 1)])
 def test_integer_inputs_bit_exact(pkg, dev, M, K, B):
     import torch
     c = integer_case(M * 7 + B, M=M, K=K, B=B)
