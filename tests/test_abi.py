@@ -64,3 +64,17 @@ def test_metadata_without_gpu(pkg):
 def test_library_has_gfx950_code_object(pkg):
     data = open(pkg._lib.LIB_PATH, "rb").read()
     assert b"gfx950" in data
+
+
+def test_bench_and_entry_compile_and_refuse_several_gpus():
+    """bench.py and __graft_entry__.py parse, and bench.py --gpus 2 exits with
+    its one-GPU message before touching torch or a device."""
+    import py_compile
+    import subprocess
+    import sys
+    for f in ("bench.py", "__graft_entry__.py"):
+        py_compile.compile(os.path.join(ROOT, f), doraise=True)
+    p = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"],
+                       capture_output=True, text=True, timeout=60)
+    assert p.returncode == 2
+    assert "measures one GPU" in p.stderr
