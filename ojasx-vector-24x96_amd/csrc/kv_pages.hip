@@ -145,21 +145,25 @@ struct EncodeParams {
     int Hkv, hd, D, G, P, num_pages;
 };
 
+// Workgroup (token i, kv head h, z): z = 0 encodes the token's K row, z = 1
+// its V row (two workgroups per token and head: each runs half the nearest-
+// centroid work, and the two chains run side by side).
 template <int DT>
 __global__ __launch_bounds__(kNT) void kv_encode_append_kernel(EncodeParams p) {
-    extern __shared__ float xs[];                // [2][hd]: k / s_k, v / s_v
-    const int i = blockIdx.x, h = blockIdx.y;
-    float kreg[DT > 0 ? DT : 1], vreg[DT > 0 ? DT : 1];
-    const float *kcb = p.kcb ? p.kcb + (size_t)h * 256 * p.D : nullptr;
-    const float *vcb = p.vcb ? p.vcb + (size_t)h * 256 * p.D : nullptr;
-    if (kcb) enc_load_centroids<DT>(kcb, vcb, kreg, vreg);
+    extern __shared__ float xs[];                // [hd]: the row / its scale
+    const int i = blockIdx.x, h = blockIdx.y, kv = blockIdx.z;
+    float creg[DT > 0 ? DT : 1];
+    const float *cb = kv ? p.vcb : p.kcb;
+    if (cb) {
+        cb += (size_t)h * 256 * p.D;
+        enc_load_centroid<DT>(cb, creg);
+    }
     const int slot = p.slots[i];
     if (slot < 0 || slot / p.P >= p.num_pages) return;   // skipped slot; workgroup-uniform
     const int page = slot / p.P;
     const size_t row = ((size_t)page * p.Hkv + h) * p.P + (slot - page * p.P);
-    encode_kv_token<DT>(p.k + ((size_t)i * p.Hkv + h) * p.hd, p.v + ((size_t)i * p.Hkv + h) * p.hd,
-                        kcb, vcb, kreg, vreg, p.hd, p.D, p.G, p.kc + row * p.G, p.vc + row * p.G,
-                        p.ks + row, p.vs + row, xs);
+    encode_row<DT>((kv ? p.v : p.k) + ((size_t)i * p.Hkv + h) * p.hd, cb, creg, p.hd, p.D, p.G,
+                   (kv ? p.vc : p.kc) + row * p.G, (kv ? p.vs : p.ks) + row, xs);
 }
 
 }  // namespace ojx
@@ -268,8 +272,8 @@ OJASX_API int ojasx_kv_encode_append_device(const float *k, const float *v, int 
                    v_scales, num_kv_heads, head_dim, block_dim, head_dim / block_dim, page_size,
                    num_pages};
     hipStream_t st = static_cast<hipStream_t>(stream);
-    const size_t lds = (size_t)2 * head_dim * sizeof(float);
-    const dim3 grid(num_tokens, num_kv_heads);
+    const size_t lds = (size_t)head_dim * sizeof(float);
+    const dim3 grid(num_tokens, num_kv_heads, 2);   // z: K, then V
     const bool reg16 = block_dim == 16 && k_codebook &&
                        (reinterpret_cast<uintptr_t>(k_codebook) & 15) == 0 &&
                        (reinterpret_cast<uintptr_t>(v_codebook) & 15) == 0;
