@@ -213,7 +213,11 @@ def check_encoded(bufs, k, v, slots, P, want_k, want_v):
 
 
 @pytest.mark.parametrize("Hkv,hd,D,aligned", [(8, 128, 16, True), (2, 64, 8, True),
-                                               (3, 128, 16, False), (1, 96, 32, True)])
+                                               (3, 128, 16, False), (1, 96, 32, True),
+                                               # groups past one batch of 8: 16, 12 (a
+                                               # partial second batch) and 64 (the most)
+                                               (2, 128, 8, True), (1, 96, 8, False),
+                                               (1, 1024, 16, True)])
 def test_encode_append_codebook_bit_exact(pkg, dev, Hkv, hd, D, aligned):
     """Nearest-centroid codes and scales bit-exact against the oracle, tokens
     scattered through a slot mapping that also skips tokens (-1 and a slot past
